@@ -1,0 +1,182 @@
+"""Paged decode attention benchmark on one MI355X.
+
+A step is one batched paged decode attention launch (decode kernel plus the
+split merge) over the Llama-3.2-1B attention shape: 64 sequences, 32 query /
+8 KV heads, head_dim 64, f32 KV, contexts uniform in [128, 4096], 16-token
+blocks scattered over a 65,536-block pool.  Inputs (K/V blocks, block tables,
+queries) are resident in HBM before the timed region.
+
+Prints one JSON line: value = algorithmic bytes moved per step / step time
+(GB/s), plus decode tokens/s, the roofline of the decode kernel from HIP events
+around its own launches, and the reference CPU path timed on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+METRIC = "paged decode attn: achieved HBM GB/s (% of peak) + decode tokens/s, 1 MI355X"
+MODEL_LAYERS = {"llama-3.2-1b-decode-64x[128,4096]": 16, "smollm2-135m-decode-1x512": 30,
+                "llama-3-8b-q8_0-decode-16x32768": 32}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, seconds_cap=30.0):
+    """The reference's fused_paged_attention (oracle/_ref, built from the
+    reference headers) on one host thread over the same workload; the C
+    restatement of the oracle when _ref was not built."""
+    import numpy as np
+
+    from oracle import pyoracle
+    from tvara_amd import workloads
+
+    kind = "reference" if pyoracle.ref_available() else "port"
+    make = pyoracle.RefCache if kind == "reference" else pyoracle.Cache
+    g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)
+    cache = make(*g)
+    seqs = workloads.fill_decode(cache, w)
+    q = w.queries()
+    times, done_seqs = [], 0
+    t_all = time.perf_counter()
+    for rep in range(3):
+        t0 = time.perf_counter()
+        n = 0
+        for i, s in enumerate(seqs):
+            cache.fused_paged_attention(q[i], s, 0, w.heads, w.context)
+            n += 1
+            if time.perf_counter() - t_all > seconds_cap:
+                break
+        times.append((time.perf_counter() - t0, n))
+        if time.perf_counter() - t_all > seconds_cap:
+            break
+    # median per-sequence-batch time scaled to the whole batch
+    per_pass = sorted(t * len(seqs) / n for t, n in times)[len(times) // 2]
+    done_seqs = times[-1][1]
+    value = w.kv_bytes() / per_pass / 1e9
+    del cache
+    return {
+        "value": round(value, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"{len(times)} pass(es) of fused_paged_attention over {done_seqs} of {len(seqs)} sequences, "
+                  f"1 thread, median scaled to the batch; {per_pass * 1e3:.1f} ms per batch, "
+                  f"{len(seqs) / per_pass:.1f} decode tokens/s",
+        "ms_per_step": round(per_pass * 1e3, 3),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c5"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--split-tokens", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the path shards by sequence or KV head with no exchange; see the design notes)", file=sys.stderr)
+        sys.exit(2)
+    if args.split_tokens:
+        os.environ["TVARA_SPLIT_TOKENS"] = str(args.split_tokens)
+
+    import numpy as np
+    import torch
+
+    from tvara_amd import attention, kv, workloads
+
+    w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5}[args.workload]()
+    log(f"workload {w.name}: {w.sequences} sequences, {w.total_tokens} tokens")
+    g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)
+    cache = kv.PagedCache(*g, fmt=kv.Q8_0 if w.q8 else kv.F32)
+    t0 = time.perf_counter()
+    seqs = workloads.fill_decode(cache, w)
+    cache.synchronize()
+    log(f"filled in {time.perf_counter() - t0:.1f}s")
+    q = torch.from_numpy(w.queries()).cuda()
+    out = torch.empty_like(q)
+    plan = attention.DecodePlan(cache, seqs, w.heads, w.context)
+    log(f"plan: split {plan.split_tokens} tokens, {plan.items} work items")
+    for _ in range(args.warmup):
+        plan.launch(0, q.data_ptr(), out.data_ptr())
+    plan.check()
+    torch.cuda.synchronize()
+
+    attention.profile_reset()
+    attention.profile_enable(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        plan.launch(0, q.data_ptr(), out.data_ptr())
+    stop.record()
+    torch.cuda.synchronize()
+    attention.profile_enable(False)
+    plan.check()
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    kern_ms, launches = attention.profile_read("paged_decode")
+    merge_ms, merges = attention.profile_read("paged_decode_merge")
+    kernel_avg_ms = kern_ms / max(launches, 1)
+    log(f"step {ms_per_step * 1e3:.1f} us; decode kernel {kernel_avg_ms * 1e3:.1f} us x{launches}; "
+        f"merge {merge_ms / max(merges, 1) * 1e3:.1f} us x{merges}")
+    assert np.isfinite(out.cpu().numpy()).all()
+
+    kv_bytes = w.kv_bytes()
+    step_bytes = kv_bytes + w.qo_bytes() + w.table_bytes()
+    gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    kernel_gbs = (kv_bytes + w.qo_bytes() // 2 + w.table_bytes()) / (kernel_avg_ms * 1e-3) / 1e9
+    tokens_per_s = w.sequences / (ms_per_step * 1e-3)
+    layers = MODEL_LAYERS.get(w.name, 1)
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0" if w.q8 else "f32",
+        "data": "synthetic: K/V/q ~ N(0,1) from a seeded splitmix64 stream, blocks at a seeded permutation",
+        "config": {"workload": w.name, "sequences": w.sequences, "heads": w.heads, "kv_heads": w.kv_heads,
+                   "head_dim": w.head_dim, "tokens_per_block": w.tokens_per_block, "total_tokens": w.total_tokens,
+                   "pool_blocks": w.pool_blocks, "split_tokens": plan.split_tokens, "work_items": plan.items},
+        "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "decode_tokens_per_s": round(tokens_per_s, 1),
+        "model_decode_tokens_per_s": round(tokens_per_s / layers, 1),
+        "model_layers": layers,
+        "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "paged_decode", "kernel_avg_us": round(kernel_avg_ms * 1e3, 3),
+                     "algorithmic_bytes": kv_bytes + w.qo_bytes() // 2 + w.table_bytes()},
+    }
+    del plan, cache, q, out
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        result["cpu_baseline"] = cpu_baseline(w)
+        log(f"cpu baseline in {time.perf_counter() - t0:.1f}s")
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,218 @@
+/*
+ * tvara_capi.h -- C ABI of the MI355X paged KV cache and paged attention
+ * library (libtvara_capi.so, hand-written HIP for gfx950).
+ *
+ * The reference exposes this path only through its in-process C++ API
+ * (core/include/tvara/kv.hpp, core/include/tvara/attention.hpp); its C ABI
+ * (core/include/tvara/c_api.h:13-24) reaches it through the model executor.
+ * The entry points below are the additive exports that a Tvara build binds for
+ * the path itself: each one names the reference interface it replaces.
+ *
+ * Conventions (mirroring core/src/c_api.cpp:66-107):
+ *   - every call clears a thread-local message; on failure it returns a
+ *     negative status (or NULL / 0 for constructors and id-returning calls)
+ *     and tvara_last_error() describes it;
+ *   - the status distinguishes the reference's exception classes;
+ *   - host pointers passed in are consumed before the call returns unless a
+ *     call says otherwise; device pointers are HBM addresses on the current
+ *     HIP device;
+ *   - a cache handle is single-owner, like PagedCache (docs/kv-cache.md): the
+ *     caller serialises calls on one handle;
+ *   - device work is issued on the handle's stream (the null stream unless
+ *     tvara_kv_set_stream was called); calls that return host data
+ *     synchronise that stream.
+ */
+#ifndef TVARA_CAPI_H
+#define TVARA_CAPI_H
+#include <stddef.h>
+#include <stdint.h>
+
+#define TVARA_API __attribute__((visibility("default")))
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define TVARA_OK 0
+#define TVARA_ERROR (-1)     /* std::runtime_error or a HIP failure */
+#define TVARA_INVALID (-2)   /* std::invalid_argument */
+#define TVARA_EXHAUSTED (-3) /* tvara::CacheExhausted (kv.hpp:34) */
+#define TVARA_LOGIC (-4)     /* std::logic_error (audit invariants, kv.hpp:61-64, 138-146) */
+
+/* KV storage formats of a cache */
+#define TVARA_KV_F32 0  /* f32 blocks, byte-identical to the reference block layout (kv.hpp:30-33) */
+#define TVARA_KV_Q8_0 1 /* Q8_0 groups (quant.hpp:40-49) of the same element order */
+
+/* attention precisions for tvara_attn_prefill */
+#define TVARA_ATTN_F32 0  /* reference semantics: one fused_paged_attention per row */
+#define TVARA_ATTN_BF16 1 /* bf16 MFMA tiles, f32 accumulation */
+
+typedef struct tvara_kv_cache tvara_kv_cache;
+typedef struct tvara_attn_plan tvara_attn_plan;
+
+/* BlockHandle (kv.hpp:35) */
+typedef struct {
+    uint64_t id;
+    uint64_t generation;
+} tvara_kv_handle;
+
+/* c_api.h:17 -- thread-local message of the last failed call */
+TVARA_API const char* tvara_last_error(void);
+/* Status of the last failed call on this thread (TVARA_OK after a success);
+ * lets callers of the NULL- or 0-returning entry points tell the exception
+ * classes apart.  No reference counterpart: the reference throws in C++. */
+TVARA_API int tvara_last_status(void);
+
+/* ------------------------------------------------------------------ caches */
+
+/* PagedCache(CacheGeometry) (kv.hpp:80) with BlockPool's constructor
+ * (kv.hpp:39-43) and CacheGeometry::validate (kv.hpp:24-28).  The block pool
+ * is one HBM allocation.  format: TVARA_KV_F32 or TVARA_KV_Q8_0 (head_dim a
+ * multiple of 32).  NULL on failure. */
+TVARA_API tvara_kv_cache* tvara_kv_cache_create(size_t layers, size_t kv_heads, size_t head_dim,
+                                                size_t tokens_per_block, size_t max_blocks, int format);
+TVARA_API void tvara_kv_cache_destroy(tvara_kv_cache* cache);
+/* Bytes of one block in the reference's element order: f32 blocks are
+ * CacheGeometry::elements_per_block (kv.hpp:18-23) floats; Q8_0 blocks are 34
+ * bytes per 32 elements. */
+TVARA_API size_t tvara_kv_block_bytes(tvara_kv_cache* cache);
+/* Issue device work on `stream` (a hipStream_t; NULL = null stream). */
+TVARA_API int tvara_kv_set_stream(tvara_kv_cache* cache, void* stream);
+/* Wait for the handle's stream. */
+TVARA_API int tvara_kv_synchronize(tvara_kv_cache* cache);
+
+/* ---------------------------------------------------------------- the pool */
+
+/* BlockPool::allocate (kv.hpp:44-50): LIFO free list, refs=1, ++generation,
+ * the block reads as zeros. */
+TVARA_API int tvara_kv_pool_allocate(tvara_kv_cache* cache, tvara_kv_handle* out);
+/* BlockPool::retain (kv.hpp:56) */
+TVARA_API int tvara_kv_pool_retain(tvara_kv_cache* cache, tvara_kv_handle handle);
+/* BlockPool::release and BlockPool::free (kv.hpp:51, 57) */
+TVARA_API int tvara_kv_pool_release(tvara_kv_cache* cache, tvara_kv_handle handle);
+/* BlockPool::references (kv.hpp:58) */
+TVARA_API int tvara_kv_pool_references(tvara_kv_cache* cache, tvara_kv_handle handle, size_t* out);
+/* BlockPool::references_by_id (kv.hpp:59) */
+TVARA_API int tvara_kv_pool_references_by_id(tvara_kv_cache* cache, size_t id, size_t* out);
+/* BlockPool::available (kv.hpp:55); 0 for a null handle */
+TVARA_API size_t tvara_kv_pool_available(tvara_kv_cache* cache);
+/* BlockPool::audit (kv.hpp:61-64) */
+TVARA_API int tvara_kv_pool_audit(tvara_kv_cache* cache);
+/* Exact allocator state (no reference counterpart: the pool keeps it private):
+ * refs[max_blocks], generations[max_blocks] and the free list in the order
+ * allocate() would pop it.  Any pointer may be NULL. */
+TVARA_API int tvara_kv_pool_state(tvara_kv_cache* cache, size_t* refs, uint64_t* generations,
+                                  size_t* free_pop_order, size_t* free_count);
+/* BlockPool::data (kv.hpp:52-53): copy a live block out, `bytes` must equal
+ * tvara_kv_block_bytes.  Q8_0 blocks come out as canonical 34-byte groups
+ * (little-endian fp16 d, 32 int8). */
+TVARA_API int tvara_kv_block_read(tvara_kv_cache* cache, tvara_kv_handle handle, void* out, size_t bytes);
+/* Writes through BlockPool::data's mutable span (kv.hpp:52), as the
+ * reference's tests do (tests/core/prefill_t173.cpp:6, prefill_t174.cpp:5);
+ * byte range of the canonical block image. */
+TVARA_API int tvara_kv_block_write(tvara_kv_cache* cache, tvara_kv_handle handle, size_t offset,
+                                   const void* data, size_t bytes);
+/* On-device 64-bit checksums of live blocks' canonical images:
+ * sum over 32-bit words w_i of mix64(i << 32 | w_i) mod 2^64, mix64 being the
+ * splitmix64 finaliser.  No reference counterpart; used to compare whole pools. */
+TVARA_API int tvara_kv_block_checksums(tvara_kv_cache* cache, const tvara_kv_handle* handles, size_t count,
+                                       uint64_t* out);
+
+/* -------------------------------------------------------------- the tables */
+
+/* PagedCache::create_sequence (kv.hpp:81); 0 on failure */
+TVARA_API uint64_t tvara_kv_sequence_create(tvara_kv_cache* cache);
+/* PagedCache::sequence (kv.hpp:82-84): length and block handles; `blocks` may
+ * be NULL to query the count. */
+TVARA_API int tvara_kv_sequence(tvara_kv_cache* cache, uint64_t sequence, size_t* length, tvara_kv_handle* blocks,
+                                size_t capacity, size_t* count);
+/* Live sequence ids in ascending order (the keys of PagedCache::sequences_). */
+TVARA_API int tvara_kv_sequence_ids(tvara_kv_cache* cache, uint64_t* ids, size_t capacity, size_t* count);
+/* PagedCache::physical_block (kv.hpp:85-87) */
+TVARA_API int tvara_kv_physical_block(tvara_kv_cache* cache, uint64_t sequence, size_t position,
+                                      tvara_kv_handle* out);
+/* PagedCache::append (kv.hpp:91-108): keys and values are host f32
+ * [layers * kv_width]; copy-on-write of a shared partial tail block. */
+TVARA_API int tvara_kv_append(tvara_kv_cache* cache, uint64_t sequence, const float* keys, const float* values);
+/* `count` appends, in order, one token per listed sequence:
+ * keys/values are f32 [count][layers * kv_width] (device pointers when
+ * `device_ptrs` is nonzero); a sequence may appear more than once.  On
+ * failure of append k, appends 0..k-1 stay applied (as a loop over
+ * PagedCache::append would leave them), append k changes nothing, and
+ * *applied = k. */
+TVARA_API int tvara_kv_append_batch(tvara_kv_cache* cache, const uint64_t* sequences, size_t count,
+                                    const float* keys, const float* values, int device_ptrs, size_t* applied);
+/* `count` consecutive appends to one sequence (a prompt's K/V) */
+TVARA_API int tvara_kv_append_tokens(tvara_kv_cache* cache, uint64_t sequence, const float* keys,
+                                     const float* values, size_t count, int device_ptrs, size_t* applied);
+/* PagedCache::read (kv.hpp:110-113): kv_width floats of one position */
+TVARA_API int tvara_kv_read(tvara_kv_cache* cache, uint64_t sequence, size_t layer, size_t position, int value,
+                            float* out);
+/* PagedCache::read_all (kv.hpp:114-119): [length][kv_width] floats */
+TVARA_API int tvara_kv_read_all(tvara_kv_cache* cache, uint64_t sequence, size_t layer, int value, float* out,
+                                size_t capacity);
+/* PagedCache::drop (kv.hpp:121) */
+TVARA_API int tvara_kv_drop(tvara_kv_cache* cache, uint64_t sequence);
+/* PagedCache::fork (kv.hpp:123-129); 0 on failure */
+TVARA_API uint64_t tvara_kv_fork(tvara_kv_cache* cache, uint64_t sequence);
+/* PagedCache::truncate (kv.hpp:131-136) */
+TVARA_API int tvara_kv_truncate(tvara_kv_cache* cache, uint64_t sequence, size_t length);
+/* PagedCache::audit (kv.hpp:138-146); external may be NULL (count 0) */
+TVARA_API int tvara_kv_audit(tvara_kv_cache* cache, const size_t* external, size_t count);
+/* PagedCache::import_sequence (kv.hpp:149-159) from a snapshot's handles; 0 on failure */
+TVARA_API uint64_t tvara_kv_import_sequence(tvara_kv_cache* cache, const tvara_kv_handle* blocks,
+                                            size_t block_count, size_t source_length, size_t length);
+
+/* --------------------------------------------------------------- attention */
+
+/* `count` calls of fused_paged_attention (attention.hpp:57-83), one per listed
+ * sequence, in one launch: q f32 [count][heads * head_dim]; tail_keys /
+ * tail_values f32 [count][kv_width] or both NULL (the current token's
+ * uncommitted K/V, paged_model.hpp:22); visible [count] or NULL (no cap);
+ * out f32 [count][heads * head_dim].  `context` is ModelConfig::context.
+ * Synchronous; a non-finite score fails with TVARA_INVALID as
+ * OnlineAttention::update does (attention.hpp:11). */
+TVARA_API int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t layer,
+                                size_t heads, size_t context, const float* q, const float* tail_keys,
+                                const float* tail_values, const size_t* visible, float* out, int device_ptrs);
+/* `count` calls of fused_prompt_attention (attention.hpp:85-89): queries for
+ * sequence i are rows start[i] .. start[i]+rows[i]-1, packed one sequence
+ * after the other, f32 [sum rows][heads * head_dim]; out likewise.
+ * precision TVARA_ATTN_F32 keeps the reference's semantics; TVARA_ATTN_BF16
+ * runs the causal tiles on MFMA with bf16 operands and f32 accumulation. */
+TVARA_API int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t layer,
+                                 size_t heads, size_t context, const size_t* start, const size_t* rows,
+                                 const float* queries, float* out, int precision, int device_ptrs);
+
+/* A decode plan keeps the listed sequences' block tables resident in HBM so
+ * that repeated launches (the same batch over several layers, or timing)
+ * upload nothing.  It records the cache's mutation count; launching it after
+ * the cache changed fails with TVARA_INVALID. */
+TVARA_API tvara_attn_plan* tvara_attn_plan_create(tvara_kv_cache* cache, const uint64_t* sequences, size_t count,
+                                                  size_t heads, size_t context, const size_t* visible,
+                                                  int with_tail);
+/* Asynchronous decode over device buffers (q, optional tails, out) on `stream`
+ * (NULL = the cache's stream). */
+TVARA_API int tvara_attn_plan_decode(tvara_attn_plan* plan, size_t layer, const float* q, const float* tail_keys,
+                                     const float* tail_values, float* out, void* stream);
+/* Synchronise the plan's last launch and report a non-finite score. */
+TVARA_API int tvara_attn_plan_check(tvara_attn_plan* plan);
+/* Work decomposition of the plan: split length in tokens, work items, KV bytes
+ * one launch reads (algorithmic). */
+TVARA_API int tvara_attn_plan_info(tvara_attn_plan* plan, size_t* split_tokens, size_t* items, size_t* kv_bytes);
+TVARA_API void tvara_attn_plan_destroy(tvara_attn_plan* plan);
+
+/* ----------------------------------------------------------------- timing */
+
+/* When enabled, every kernel launch of the library is bracketed by HIP events
+ * on its stream; tvara_profile_read synchronises and returns, per kernel name
+ * prefix, the summed milliseconds and launch count since the last reset. */
+TVARA_API int tvara_profile_enable(int enabled);
+TVARA_API int tvara_profile_read(const char* kernel, double* milliseconds, size_t* launches);
+TVARA_API int tvara_profile_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,226 @@
+"""Paged decode attention on the GPU against the oracle (the reference's fused
+paged attention restated in FP64).  Bar: |gpu - ref| <= 1e-4 * (1 + |ref|)
+for f32 blocks (the tolerance form of tests/core/prefill_support.hpp:7-9)."""
+
+import sys
+
+import numpy as np
+import pytest
+
+import refmath
+from tvara_amd import attention, synth, workloads
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+def build_pair(device, oracle, w, fmt=None):
+    g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)
+    dev = device.PagedCache(*g, fmt=fmt if fmt is not None else device.F32)
+    ref = oracle.Cache(*g)
+    ds = workloads.fill_decode(dev, w)
+    rs = workloads.fill_decode(ref, w)
+    assert ds == rs
+    return dev, ref, ds
+
+
+def oracle_rows(ref, seqs, q, w, **kw):
+    return np.stack([ref.fused_paged_attention(q[i], s, 0, w.heads, w.context, **kw) for i, s in enumerate(seqs)])
+
+
+def test_c1_smollm2_shape(device, oracle):
+    w = workloads.decode_c1()
+    say("decode", w.name)
+    dev, ref, seqs = build_pair(device, oracle, w)
+    assert dev.state() == ref.state()  # the seeded placement reproduced exactly
+    q = w.queries()
+    got = attention.decode_batch(dev, q, seqs, 0, w.heads, w.context)
+    want = oracle_rows(ref, seqs, q, w)
+    assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+def test_c2_llama32_batch(device, oracle):
+    w = workloads.decode_c2()
+    say("decode", w.name, "tokens", w.total_tokens)
+    dev, ref, seqs = build_pair(device, oracle, w)
+    q = w.queries()
+    got = attention.decode_batch(dev, q, seqs, 0, w.heads, w.context)
+    want = oracle_rows(ref, seqs, q, w)
+    assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+    # the same through a resident plan on device buffers, launched twice
+    import torch
+
+    plan = attention.DecodePlan(dev, seqs, w.heads, w.context)
+    dq = torch.from_numpy(q).cuda()
+    out = torch.empty_like(dq)
+    for _ in range(2):
+        out.zero_()
+        plan.launch(0, dq.data_ptr(), out.data_ptr())
+        plan.check()
+        assert np.array_equal(out.cpu().numpy(), got)
+
+
+def _single(device, oracle, heads, kv_heads, dim, tpb, length, seed, tail=False, visible=None, fmt=None,
+            layers=1, layer=0):
+    g = (layers, kv_heads, dim, tpb, length // tpb + 3)
+    dev = device.PagedCache(*g, fmt=fmt if fmt is not None else device.F32)
+    ref = oracle.Cache(*g)
+    w = layers * kv_heads * dim
+    k = synth.normal(seed, "k", length * w).reshape(length, w)
+    v = synth.normal(seed, "v", length * w).reshape(length, w)
+    if fmt == device.Q8_0:  # the oracle holds the dequantised values
+        k = oracle.dequantize_q8_0(oracle.quantize_q8_0(k)).reshape(length, w)
+        v = oracle.dequantize_q8_0(oracle.quantize_q8_0(v)).reshape(length, w)
+    sd, sr = dev.create_sequence(), ref.create_sequence()
+    dev.append_many(sd, k, v)
+    ref.append_many(sr, k, v)
+    q = synth.normal(seed, "q", heads * dim)
+    kw = {}
+    if tail:
+        kw = {"tail_key": synth.normal(seed, "tk", kv_heads * dim), "tail_value": synth.normal(seed, "tv", kv_heads * dim)}
+    if visible is not None:
+        kw["visible"] = visible
+    got = attention.fused_paged_attention(q, dev, sd, layer, heads, 1 << 20, **kw)
+    want = ref.fused_paged_attention(q, sr, layer, heads, 1 << 20, **kw)
+    return got, want
+
+
+@pytest.mark.parametrize("dim,kv_heads,group", [(64, 8, 1), (64, 8, 2), (64, 3, 3), (64, 2, 4), (128, 8, 4),
+                                                (128, 2, 8), (128, 4, 5), (8, 1, 8), (32, 2, 2), (16, 4, 1)])
+@pytest.mark.parametrize("length", [1, 15, 16, 17, 100, 1031])
+def test_shapes_and_gqa_ratios(device, oracle, dim, kv_heads, group, length):
+    say("decode shape", dim, kv_heads, group, length)
+    got, want = _single(device, oracle, kv_heads * group, kv_heads, dim, 16, length, seed=dim + length)
+    assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+@pytest.mark.parametrize("tpb", [7, 5, 4, 32, 1])
+def test_block_sizes(device, oracle, tpb):
+    # block sizes that do not divide the length (prefill_t171.cpp, prefill_t180.cpp)
+    for dim in (8, 64):
+        got, want = _single(device, oracle, 4, 2, dim, tpb, 53, seed=tpb)
+        assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+@pytest.mark.parametrize("dim", [8, 64, 128])
+def test_tail_and_visible(device, oracle, dim):
+    for length, visible in [(0, None), (53, None), (53, 54), (53, 20), (300, 1), (300, 299)]:
+        say("tail", dim, length, visible)
+        got, want = _single(device, oracle, 8, 2, dim, 16, max(length, 0), seed=3, tail=True, visible=visible) \
+            if length else (None, None)
+        if length == 0:  # an empty cache with a tail attends to the tail alone
+            g = (1, 2, dim, 16, 4)
+            dev = device.PagedCache(*g)
+            s = dev.create_sequence()
+            tv = synth.normal(4, "tv", 2 * dim)
+            out = attention.fused_paged_attention(synth.normal(4, "q", 8 * dim), dev, s, 0, 8, 64,
+                                                  synth.normal(4, "tk", 2 * dim), tv)
+            assert np.array_equal(out.reshape(8, dim), np.repeat(tv.reshape(2, dim), 4, axis=0))
+            continue
+        assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+def test_layers(device, oracle):
+    for layer in range(3):
+        got, want = _single(device, oracle, 8, 4, 64, 16, 77, seed=layer, layers=3, layer=layer)
+        assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+def test_long_contexts(device, oracle):
+    # fused vs reference through 8192 positions (prefill_t177.cpp)
+    for length in (127, 1024, 4097, 8192):
+        for dim in (16, 64):
+            got, want = _single(device, oracle, 4, 2, dim, 16, length, seed=length)
+            assert refmath.close(got, want, TOL), (length, dim, refmath.max_rel(got, want))
+
+
+def test_nan_poisoned_unused_slots(device, oracle):
+    # NaN in unused tail slots and junk in recycled blocks never leak (prefill_t174.cpp)
+    for dim in (8, 64):
+        for length in (1, 15, 16, 17, 31, 32, 33):
+            g = (1, 2, dim, 16, 8)
+            dev = device.PagedCache(*g)
+            old = dev.create_sequence()
+            junk = synth.signal(2 * dim, 100)
+            dev.append_many(old, np.tile(junk, (48, 1)), np.tile(junk, (48, 1)))
+            dev.drop(old)
+            s = dev.create_sequence()
+            k = synth.signal(length * 2 * dim).reshape(length, 2 * dim)
+            v = synth.signal(length * 2 * dim, 2).reshape(length, 2 * dim)
+            dev.append_many(s, k, v)
+            h = dev.physical_block(s, length - 1)
+            for slot in range(length % 16 or 16, 16):
+                for kind in (0, 1):
+                    dev.block_write(h, dev.kv_offset(0, kind, slot), np.full(2 * dim, np.nan, np.float32))
+            q = synth.signal(4 * dim, 3)
+            got = attention.fused_paged_attention(q, dev, s, 0, 4, 128)
+            assert refmath.close(got, refmath.attention(q, k, v, 4, 2, dim), TOL)
+            dev.audit()
+
+
+def test_rejections(device):
+    dev = device.PagedCache(1, 2, 64, 16, 8)
+    s = dev.create_sequence()
+    x = synth.normal(1, "x", 10 * 128).reshape(10, 128)
+    dev.append_many(s, x, x)
+    q = synth.normal(1, "q", 4 * 64)
+    with pytest.raises(device.InvalidArgument):  # empty attention
+        attention.fused_paged_attention(q, dev, s, 0, 4, 64, visible=0)
+    with pytest.raises(device.InvalidArgument):  # length beyond context
+        attention.fused_paged_attention(q, dev, s, 0, 4, 8)
+    with pytest.raises(device.InvalidArgument):  # heads not a multiple of kv heads
+        attention.fused_paged_attention(synth.normal(1, "q3", 3 * 64), dev, s, 0, 3, 64)
+    with pytest.raises(device.InvalidArgument):  # bad layer
+        attention.fused_paged_attention(q, dev, s, 1, 4, 64)
+    with pytest.raises(device.InvalidArgument):  # unknown sequence
+        attention.fused_paged_attention(q, dev, 99, 0, 4, 64)
+    with pytest.raises(device.InvalidArgument):  # non-finite score (attention.hpp:11)
+        attention.fused_paged_attention(np.full_like(q, np.inf), dev, s, 0, 4, 64)
+    # the error flag is cleared: a valid call after it succeeds
+    assert np.isfinite(attention.fused_paged_attention(q, dev, s, 0, 4, 64)).all()
+    plan = attention.DecodePlan(dev, [s], 4, 64)
+    dev.append(s, x[0], x[0])
+    import torch
+
+    dq = torch.from_numpy(q).cuda()
+    with pytest.raises(device.InvalidArgument):  # the cache changed under the plan
+        plan.launch(0, dq.data_ptr(), dq.data_ptr())
+
+
+def test_huge_scores_stay_finite(device, oracle):
+    # scores near 1e4 (prefill_t170.cpp:4): the running maximum must move
+    g = (1, 2, 64, 16, 8)
+    dev, ref = device.PagedCache(*g), oracle.Cache(*g)
+    sd, sr = dev.create_sequence(), ref.create_sequence()
+    k = synth.normal(2, "k", 60 * 128).reshape(60, 128) * np.float32(300.0)
+    v = synth.normal(2, "v", 60 * 128).reshape(60, 128)
+    dev.append_many(sd, k, v)
+    ref.append_many(sr, k, v)
+    q = synth.normal(2, "q", 4 * 64)
+    got = attention.fused_paged_attention(q, dev, sd, 0, 4, 64)
+    want = ref.fused_paged_attention(q, sr, 0, 4, 64)
+    assert np.isfinite(got).all() and refmath.close(got, want, TOL)
+
+
+def test_prompt_chunk_f32(device, oracle):
+    # fused_prompt_attention (prefill_t173.cpp): rows see their own prefix only
+    g = (1, 1, 8, 7, 20)
+    dev, ref = device.PagedCache(*g), oracle.Cache(*g)
+    sd, sr = dev.create_sequence(), ref.create_sequence()
+    k = synth.signal(39 * 8).reshape(39, 8)
+    v = synth.signal(39 * 8, 2).reshape(39, 8)
+    dev.append_many(sd, k, v)
+    ref.append_many(sr, k, v)
+    qs = synth.signal(13 * 32, 3)
+    got = attention.fused_prompt_attention(qs, dev, sd, 0, 11, 13, 4, 128)
+    want = ref.fused_prompt_attention(qs, sr, 0, 11, 13, 4, 128)
+    assert refmath.close(got, want, TOL)
+    h = dev.physical_block(sd, 38)
+    dev.block_write(h, 0, np.full(dev.elements_per_block, 99999, np.float32))
+    assert np.array_equal(attention.fused_prompt_attention(qs, dev, sd, 0, 11, 13, 4, 128), got)
+    with pytest.raises(device.InvalidArgument):
+        attention.fused_prompt_attention(qs, dev, sd, 0, 30, 13, 4, 128)

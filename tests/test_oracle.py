@@ -1,0 +1,238 @@
+"""Pins the C oracle (oracle/tvara_oracle.c) without trusting it: the
+reference's own known-answer tests restated, float64 brute force, closed forms
+and numpy's IEEE rounding routines.  CPU only."""
+
+import numpy as np
+import pytest
+
+import kv_cases
+import refmath
+from tvara_amd import synth
+
+
+@pytest.mark.parametrize("case", kv_cases.CASES, ids=lambda f: f.__name__)
+def test_kv_known_answers(oracle, case):
+    case(lambda *g: oracle.Cache(*g), (oracle.InvalidArgument, oracle.CacheExhausted))
+
+
+def _filled(oracle, heads, kv_heads, dim, tpb, positions, seed=7, scale=1.0, max_blocks=None):
+    nb = max_blocks or (positions // tpb + 4)
+    c = oracle.Cache(1, kv_heads, dim, tpb, nb)
+    s = c.create_sequence()
+    w = kv_heads * dim
+    k = synth.normal(seed, "k", positions * w).reshape(positions, w) * np.float32(scale)
+    v = synth.normal(seed, "v", positions * w).reshape(positions, w)
+    c.append_many(s, k, v)
+    q = synth.normal(seed, "q", heads * dim)
+    return c, s, q, k, v
+
+
+@pytest.mark.parametrize("kv_heads", [1, 2, 4, 8])
+def test_fused_attention_vs_float64(oracle, kv_heads):
+    # GQA ratios 8/4/2/1 (tests/core/prefill_t172.cpp:3-4), 67 positions, 16-token blocks
+    c, s, q, k, v = _filled(oracle, 8, kv_heads, 8, 16, 67)
+    out = c.fused_paged_attention(q, s, 0, 8, 128)
+    ref = refmath.attention(q, k, v, 8, kv_heads, 8)
+    assert refmath.close(out, ref, 1e-6)
+
+
+@pytest.mark.parametrize("tpb,positions", [(7, 53), (5, 23), (16, 1), (16, 15), (16, 16), (16, 17), (16, 33)])
+def test_fused_attention_block_shapes(oracle, tpb, positions):
+    # block sizes that do not divide the length (prefill_t171.cpp, prefill_t180.cpp)
+    c, s, q, k, v = _filled(oracle, 4, 2, 8, tpb, positions)
+    assert refmath.close(c.fused_paged_attention(q, s, 0, 4, 256), refmath.attention(q, k, v, 4, 2, 8), 1e-6)
+
+
+def test_tail_equals_append(oracle):
+    # the uncommitted tail is the last position (prefill_t171.cpp:6)
+    c, s, q, k, v = _filled(oracle, 4, 2, 8, 7, 53)
+    tk, tv = synth.signal(16, 4), synth.signal(16, 5)
+    out = c.fused_paged_attention(q, s, 0, 4, 128, tk, tv)
+    ref = refmath.attention(q, np.vstack([k, tk]), np.vstack([v, tv]), 4, 2, 8)
+    assert refmath.close(out, ref, 1e-6)
+    c.append(s, tk, tv)
+    assert np.array_equal(c.fused_paged_attention(q, s, 0, 4, 128), out)
+
+
+def test_visible_cap_and_chunk(oracle):
+    # fused_prompt_attention rows are fused attention with visible=start+i+1 (attention.hpp:88)
+    c, s, _, k, v = _filled(oracle, 4, 1, 8, 7, 39)
+    qs = synth.signal(13 * 32, 3)
+    out = c.fused_prompt_attention(qs, s, 0, 11, 13, 4, 128).reshape(13, 32)
+    for i in range(13):
+        ref = refmath.attention(qs[i * 32 : (i + 1) * 32], k[: 12 + i], v[: 12 + i], 4, 1, 8)
+        assert refmath.close(out[i], ref, 1e-6)
+    # future slots do not leak (prefill_t173.cpp:6)
+    h = c.physical_block(s, 38)
+    c.block_write(h, 0, np.full(c.elements_per_block, 99999, np.float32))
+    assert np.array_equal(c.fused_prompt_attention(qs, s, 0, 11, 13, 4, 128).reshape(13, 32), out)
+    with pytest.raises(oracle.InvalidArgument):
+        c.fused_prompt_attention(qs, s, 0, 30, 13, 4, 128)
+
+
+def test_known_answers(oracle):
+    c, s, q, k, v = _filled(oracle, 4, 2, 8, 16, 40)
+    # q = 0 gives the mean of V (test_model.cpp:46-51 style closed form)
+    out = c.fused_paged_attention(np.zeros_like(q), s, 0, 4, 128).reshape(4, 8)
+    mean = v.reshape(40, 2, 8).astype(np.float64).mean(axis=0)
+    assert refmath.close(out, np.repeat(mean, 2, axis=0), 1e-6)
+    # one position gives V
+    one = c.fused_paged_attention(q, s, 0, 4, 128, visible=1).reshape(4, 8)
+    assert np.array_equal(one, np.repeat(v[0].reshape(2, 8), 2, axis=0))
+    # scores near 1e4 stay finite (prefill_t170.cpp:4)
+    big, bs, bq, bk, bv = _filled(oracle, 4, 2, 8, 16, 20, scale=4000.0)
+    assert np.isfinite(big.fused_paged_attention(bq, bs, 0, 4, 128)).all()
+
+
+def test_nan_poisoned_tail_slots(oracle):
+    # unused slots poisoned with NaN and recycled junk blocks never leak (prefill_t174.cpp)
+    for length in (1, 15, 16, 17, 31, 32, 33):
+        c = oracle.Cache(1, 2, 8, 16, 8)
+        old = c.create_sequence()
+        junk = synth.signal(16, 100)
+        for _ in range(48):
+            c.append(old, junk, junk)
+        c.drop(old)
+        s = c.create_sequence()
+        k = synth.signal(length * 16).reshape(length, 16)
+        v = synth.signal(length * 16, 2).reshape(length, 16)
+        c.append_many(s, k, v)
+        h = c.physical_block(s, length - 1)
+        if length % 16:
+            for slot in range(length % 16, 16):
+                c.block_write(h, c.kv_offset(0, 0, slot), np.full(16, np.nan, np.float32))
+        q = synth.signal(32, 3)
+        assert refmath.close(c.fused_paged_attention(q, s, 0, 4, 128), refmath.attention(q, k, v, 4, 2, 8), 1e-6)
+        c.audit()
+
+
+def test_rejections(oracle):
+    c, s, q, _, _ = _filled(oracle, 4, 2, 8, 16, 10)
+    with pytest.raises(oracle.InvalidArgument):  # empty attention
+        c.fused_paged_attention(q, s, 0, 4, 128, visible=0)
+    with pytest.raises(oracle.InvalidArgument):  # length above context
+        c.fused_paged_attention(q, s, 0, 4, 8)
+    with pytest.raises(oracle.InvalidArgument):  # non-finite score (attention.hpp:11)
+        c.fused_paged_attention(np.full_like(q, np.inf), s, 0, 4, 128)
+    with pytest.raises(oracle.InvalidArgument):  # bad layer
+        c.fused_paged_attention(q, s, 1, 4, 128)
+
+
+def test_dot_orders_agree(oracle):
+    # the AVX2 summation order vs the scalar double dot (prefill_t175.cpp: < 1e-9 relative)
+    import ctypes as C
+
+    lib = oracle.oracle_lib()
+    for dim in (2, 6, 8, 14, 32, 64, 128):
+        x, y = synth.signal(dim, 7), synth.signal(dim, 11)
+        px, py = x.ctypes.data_as(C.POINTER(C.c_float)), y.ctypes.data_as(C.POINTER(C.c_float))
+        lib.tvo_set_dot_mode(0)
+        a = lib.tvo_attention_dot(px, py, dim)
+        lib.tvo_set_dot_mode(1)
+        b = lib.tvo_attention_dot(px, py, dim)
+        lib.tvo_set_dot_mode(0)
+        assert abs(a - b) < 1e-9 * (1 + abs(a))
+        assert abs(a - float(np.dot(x.astype(np.float64), y.astype(np.float64)))) < 1e-9 * (1 + abs(a))
+
+
+# ------------------------------------------------------------------- Q8_0
+
+
+def test_half_to_float_known_answers(oracle):
+    # tests/core/test_quant.cpp:16-22
+    assert oracle.half_to_float(0x3C00) == 1.0 and oracle.half_to_float(0xC000) == -2.0
+    assert oracle.half_to_float(1) == np.ldexp(1.0, -24)
+    assert oracle.half_to_float(0x7BFF) == 65504.0
+    assert np.isinf(oracle.half_to_float(0x7C00)) and np.isnan(oracle.half_to_float(0x7E00))
+    assert np.signbit(oracle.half_to_float(0x8000))
+
+
+def test_half_to_float_exhaustive(oracle):
+    bits = np.arange(65536, dtype=np.uint16)
+    expect = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.half_to_float(int(b)) for b in bits], np.float32)
+    finite = ~np.isnan(expect)
+    assert np.array_equal(got[finite].view(np.uint32), expect[finite].view(np.uint32))
+    assert np.isnan(got[~finite]).all()
+
+
+def test_double_to_half_matches_numpy(oracle):
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([
+        rng.standard_normal(4000) * 10.0 ** rng.integers(-9, 6, 4000),
+        np.ldexp(np.arange(1, 2048, dtype=np.float64), -34),  # subnormal halves and ties
+        [0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e10, 2.0**-25, 2.0**-25 * 1.0000001, 2.0**-24 * 1.5],
+    ])
+    for x in xs:
+        assert oracle.double_to_half(float(x)) == int(np.asarray(x, dtype="<f2").view(np.uint16)), x
+
+
+def test_dequantize_known_answers(oracle):
+    # tests/core/test_quant.cpp:23-29 and :135-138
+    raw = np.zeros(34, np.uint8)
+    raw[0:2] = np.array([0x3800], np.uint16).view(np.uint8)
+    raw[2:] = (np.arange(32) - 16).astype(np.int8).view(np.uint8)
+    assert np.array_equal(oracle.dequantize_q8_0(raw), 0.5 * (np.arange(32) - 16).astype(np.float32))
+    zero = np.zeros(34, np.uint8)
+    assert not oracle.dequantize_q8_0(zero).any()
+    zero[0:2] = np.array([0x3C00], np.uint16).view(np.uint8)
+    zero[2], zero[3] = 128, 127
+    out = oracle.dequantize_q8_0(zero)
+    assert out[0] == -128 and out[1] == 127
+    with pytest.raises(oracle.InvalidArgument):
+        oracle.dequantize_q8_0(zero[:33])
+
+
+def _numpy_q8_0(block):
+    """The expression of tools/make_api_fixture.py:131-137, evaluated by numpy."""
+    scale = float(np.max(np.abs(block))) / 127
+    quant = np.zeros(32, dtype=np.int8) if scale == 0 else np.clip(np.round(block / scale), -127, 127).astype(np.int8)
+    return np.asarray(scale, dtype="<f2").tobytes() + quant.tobytes()
+
+
+def test_q8_0_encoder_matches_numpy(oracle):
+    blocks = [synth.normal(9, "q8", 32 * 400).reshape(400, 32)]
+    ties = np.linspace(-127, 127, 32, dtype=np.float32) / np.float32(127) * np.float32(3)  # exact .5 ties
+    half = (np.arange(32, dtype=np.float32) - 15.5) * np.float32(0.25)
+    blocks.append(np.stack([ties, half, np.zeros(32, np.float32), np.full(32, -1e-30, np.float32)]))
+    for b in np.concatenate(blocks):
+        b = np.ascontiguousarray(b, np.float32)
+        assert bytes(oracle.quantize_q8_0(b)) == _numpy_q8_0(b)
+
+
+def test_q8_0_round_trip_bound(oracle):
+    # |x - dequantize(encode(x))| <= scale/2 plus the f16 rounding of the scale
+    x = synth.normal(11, "rt", 32 * 256)
+    raw = oracle.quantize_q8_0(x)
+    y = oracle.dequantize_q8_0(raw)
+    scale = np.abs(x.reshape(-1, 32)).max(axis=1) / 127
+    bound = scale / 2 + 127 * scale * 2.0**-11
+    assert np.all(np.abs(x - y).reshape(-1, 32) <= bound[:, None] * (1 + 1e-6))
+
+
+def test_synth_is_deterministic():
+    a = synth.normal(3, "x", 1001)
+    assert np.array_equal(a, synth.normal(3, "x", 1001))
+    assert not np.array_equal(a, synth.normal(4, "x", 1001))
+    assert np.allclose(a.mean(), 0, atol=0.1) and np.allclose(a.std(), 1, atol=0.1)
+    p = synth.permutation(5, "p", 1000)
+    assert sorted(p.tolist()) == list(range(1000))
+    u = synth.integers(2, "ctx", 1000, 128, 4096)
+    assert u.min() >= 128 and u.max() <= 4096
+    # a slice of a stream regenerates independently
+    assert np.array_equal(synth.bits(1, "s", 10, 5), synth.bits(1, "s", 15)[5:])
+
+
+def test_checksum_definition(oracle):
+    w = np.arange(10, dtype=np.uint32)
+    mask = (1 << 64) - 1
+
+    def mix(z):
+        z ^= z >> 30
+        z = (z * 0xBF58476D1CE4E5B9) & mask
+        z ^= z >> 27
+        z = (z * 0x94D049BB133111EB) & mask
+        return z ^ (z >> 31)
+
+    expect = sum(mix((i << 32) | int(x)) for i, x in enumerate(w)) & mask
+    assert oracle.checksum_words(w) == expect

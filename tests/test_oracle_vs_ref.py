@@ -1,0 +1,54 @@
+"""The oracle against the reference's own code compiled from its headers
+(oracle/_ref/libtvara_ref.so).  Skipped where the reference tree is absent."""
+
+import numpy as np
+import pytest
+
+import kv_cases
+from tvara_amd import synth
+
+
+@pytest.mark.parametrize("case", kv_cases.CASES, ids=lambda f: f.__name__)
+def test_reference_passes_restated_cases(ref, case):
+    # the restated known-answer cases hold for the reference itself
+    case(lambda *g: ref.RefCache(*g), (ref.InvalidArgument, ref.CacheExhausted))
+
+
+@pytest.mark.parametrize("geometry,seed", [((2, 2, 4, 4, 12), 1), ((1, 1, 2, 3, 9), 2), ((3, 1, 4, 5, 20), 3),
+                                           ((1, 2, 8, 16, 6), 4)])
+def test_state_machine_matches_reference(ref, geometry, seed):
+    layers, kv_heads, dim, tpb, _ = geometry
+    n = kv_cases.random_ops(ref.Cache(*geometry), ref.RefCache(*geometry), 300, seed, layers * kv_heads * dim, tpb)
+    assert n >= 1
+
+
+@pytest.mark.parametrize("heads,kv_heads,dim,tpb,positions", [(9, 3, 64, 16, 512), (8, 2, 32, 7, 200),
+                                                              (4, 4, 16, 5, 61), (32, 8, 64, 16, 300)])
+def test_attention_matches_reference(ref, heads, kv_heads, dim, tpb, positions):
+    nb = positions // tpb + 2
+    o, r = ref.Cache(1, kv_heads, dim, tpb, nb), ref.RefCache(1, kv_heads, dim, tpb, nb)
+    so, sr = o.create_sequence(), r.create_sequence()
+    w = kv_heads * dim
+    k = synth.normal(1, "k", positions * w)
+    v = synth.normal(1, "v", positions * w)
+    o.append_many(so, k, v)
+    r.append_many(sr, k, v)
+    q = synth.normal(1, "q", heads * dim)
+    tk, tv = synth.normal(1, "tk", w), synth.normal(1, "tv", w)
+    for kwargs in ({}, {"tail_key": tk, "tail_value": tv}, {"visible": positions // 3}):
+        a = o.fused_paged_attention(q, so, 0, heads, 4096, **kwargs)
+        b = r.fused_paged_attention(q, sr, 0, heads, 4096, **kwargs)
+        assert np.max(np.abs(a - b)) <= 2e-7 * (1 + np.abs(b).max())
+    qs = synth.normal(2, "qs", 5 * heads * dim)
+    a = o.fused_prompt_attention(qs, so, 0, positions - 5, 5, heads, 4096)
+    b = r.fused_prompt_attention(qs, sr, 0, positions - 5, 5, heads, 4096)
+    assert np.max(np.abs(a - b)) <= 2e-7 * (1 + np.abs(b).max())
+
+
+def test_q8_0_dequantize_matches_reference(ref):
+    raw = np.frombuffer(synth.bits(3, "raw", 34 * 64 // 8).tobytes(), np.uint8)[: 34 * 64].copy()
+    raw.reshape(64, 34)[:, 1] &= 0x7B  # keep the scales finite
+    assert np.array_equal(ref.dequantize_q8_0(raw), ref.ref_dequantize_q8_0(raw))
+    for h in range(0, 65536, 7):
+        a, b = ref.half_to_float(h), ref.ref_half_to_float(h)
+        assert (np.isnan(a) and np.isnan(b)) or np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)

@@ -1,0 +1,496 @@
+// Exported C ABI of libtvara_capi (declared in include/tvara_capi.h).  Error
+// convention of core/src/c_api.cpp:66-107: each call clears a thread-local
+// message, catches every exception and returns a status naming its class.
+#include "tvara_capi.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kv_cache.hpp"
+
+using tvara_amd::AttnPlan;
+using tvara_amd::DeviceCache;
+using tvara_amd::Geometry;
+using tvara_amd::Handle;
+
+struct tvara_kv_cache {
+    DeviceCache cache;
+    tvara_kv_cache(const Geometry& g, int format) : cache(g, format) {}
+};
+
+struct tvara_attn_plan {
+    AttnPlan plan;
+    size_t context = 0;
+};
+
+namespace tvara_amd {
+void profile_enable(bool on);
+void profile_read(const char* prefix, double* ms, size_t* launches);
+void profile_reset();
+}  // namespace tvara_amd
+
+namespace {
+thread_local std::string error_message;
+thread_local int error_status = TVARA_OK;
+
+int failed(int status, const char* what) {
+    error_message = what;
+    error_status = status;
+    return status;
+}
+
+template <class F>
+int guard(F&& f) {
+    error_message.clear();
+    error_status = TVARA_OK;
+    try {
+        f();
+        return TVARA_OK;
+    } catch (const tvara_amd::CacheExhausted& e) {
+        return failed(TVARA_EXHAUSTED, e.what());
+    } catch (const std::invalid_argument& e) {
+        return failed(TVARA_INVALID, e.what());
+    } catch (const std::logic_error& e) {
+        return failed(TVARA_LOGIC, e.what());
+    } catch (const std::exception& e) {
+        return failed(TVARA_ERROR, e.what());
+    } catch (...) {
+        return failed(TVARA_ERROR, "unknown native error");
+    }
+}
+
+DeviceCache& live(tvara_kv_cache* c) {
+    if (!c) throw std::invalid_argument("closed KV cache");
+    return c->cache;
+}
+
+Handle handle(tvara_kv_handle h) { return Handle{static_cast<size_t>(h.id), h.generation}; }
+tvara_kv_handle exported(Handle h) { return tvara_kv_handle{h.id, h.generation}; }
+
+// ModelConfig::validate (model.hpp:13-19), the part attention depends on
+void check_config(const DeviceCache& c, size_t heads, size_t context) {
+    const Geometry& g = c.geometry();
+    if (!heads || !context || heads % g.kv_heads || g.head_dim % 2 || heads > 65535)
+        throw std::invalid_argument("invalid native model configuration");
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Rows of fused_paged_attention calls (attention.hpp:57-83) for `count`
+// sequences: the argument checks of attention.hpp:59-63 and the visible cap.
+void decode_rows(const DeviceCache& c, const uint64_t* seqs, size_t count, size_t context, bool tail,
+                 const size_t* visible, std::vector<uint64_t>& seq_of_row, std::vector<size_t>& cached,
+                 std::vector<uint8_t>& tail_rows) {
+    for (size_t i = 0; i < count; ++i) {
+        const size_t length = c.sequence(seqs[i]).length;
+        if (length > context || (tail && length == context)) throw std::invalid_argument("invalid fused attention shape");
+        const size_t total = length + (tail ? 1 : 0);
+        const size_t vis = visible ? std::min(visible[i], total) : total;
+        if (!vis) throw std::invalid_argument("empty fused attention");
+        if (length > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
+            throw std::invalid_argument("sequence too long for the device kernels");
+        seq_of_row.push_back(seqs[i]);
+        cached.push_back(std::min(vis, length));
+        tail_rows.push_back(vis > length ? 1 : 0);
+    }
+}
+
+// device copies of host arrays for the synchronous attention entry points
+struct Staged {
+    std::vector<void*> owned;
+    ~Staged() {
+        for (void* p : owned) (void)hipFree(p);
+    }
+    const float* in(const float* host, size_t n) {
+        if (!host) return nullptr;
+        void* d = nullptr;
+        TVARA_HIP(hipMalloc(&d, std::max<size_t>(n, 1) * sizeof(float)));
+        owned.push_back(d);
+        TVARA_HIP(hipMemcpy(d, host, n * sizeof(float), hipMemcpyHostToDevice));
+        return static_cast<const float*>(d);
+    }
+    float* out(size_t n) {
+        void* d = nullptr;
+        TVARA_HIP(hipMalloc(&d, std::max<size_t>(n, 1) * sizeof(float)));
+        owned.push_back(d);
+        return static_cast<float*>(d);
+    }
+};
+}  // namespace
+
+extern "C" {
+
+const char* tvara_last_error(void) { return error_message.c_str(); }
+
+int tvara_last_status(void) { return error_status; }
+
+tvara_kv_cache* tvara_kv_cache_create(size_t layers, size_t kv_heads, size_t head_dim, size_t tokens_per_block,
+                                      size_t max_blocks, int format) {
+    tvara_kv_cache* out = nullptr;
+    guard([&] {
+        Geometry g{layers, kv_heads, head_dim, tokens_per_block, max_blocks};
+        out = new tvara_kv_cache(g, format);
+    });
+    return out;
+}
+
+void tvara_kv_cache_destroy(tvara_kv_cache* cache) { delete cache; }
+
+size_t tvara_kv_block_bytes(tvara_kv_cache* cache) {
+    size_t n = 0;
+    guard([&] { n = live(cache).canonical_block_bytes(); });
+    return n;
+}
+
+int tvara_kv_set_stream(tvara_kv_cache* cache, void* stream) {
+    return guard([&] { live(cache).set_stream(static_cast<hipStream_t>(stream)); });
+}
+
+int tvara_kv_synchronize(tvara_kv_cache* cache) {
+    return guard([&] {
+        live(cache).flush();
+        live(cache).synchronize();
+    });
+}
+
+int tvara_kv_pool_allocate(tvara_kv_cache* cache, tvara_kv_handle* out) {
+    return guard([&] {
+        if (!out) throw std::invalid_argument("null handle output");
+        *out = exported(live(cache).allocate());
+    });
+}
+
+int tvara_kv_pool_retain(tvara_kv_cache* cache, tvara_kv_handle h) {
+    return guard([&] { live(cache).retain(handle(h)); });
+}
+
+int tvara_kv_pool_release(tvara_kv_cache* cache, tvara_kv_handle h) {
+    return guard([&] { live(cache).release(handle(h)); });
+}
+
+int tvara_kv_pool_references(tvara_kv_cache* cache, tvara_kv_handle h, size_t* out) {
+    return guard([&] { *out = live(cache).references(handle(h)); });
+}
+
+int tvara_kv_pool_references_by_id(tvara_kv_cache* cache, size_t id, size_t* out) {
+    return guard([&] { *out = live(cache).references_by_id(id); });
+}
+
+size_t tvara_kv_pool_available(tvara_kv_cache* cache) {
+    size_t n = 0;
+    guard([&] { n = live(cache).available(); });
+    return n;
+}
+
+int tvara_kv_pool_audit(tvara_kv_cache* cache) {
+    return guard([&] { live(cache).pool_audit(); });
+}
+
+int tvara_kv_pool_state(tvara_kv_cache* cache, size_t* refs, uint64_t* generations, size_t* free_pop_order,
+                        size_t* free_count) {
+    return guard([&] { live(cache).pool_state(refs, generations, free_pop_order, free_count); });
+}
+
+int tvara_kv_block_read(tvara_kv_cache* cache, tvara_kv_handle h, void* out, size_t bytes) {
+    return guard([&] { live(cache).block_read(handle(h), out, bytes); });
+}
+
+int tvara_kv_block_write(tvara_kv_cache* cache, tvara_kv_handle h, size_t offset, const void* data, size_t bytes) {
+    return guard([&] { live(cache).block_write(handle(h), offset, data, bytes); });
+}
+
+int tvara_kv_block_checksums(tvara_kv_cache* cache, const tvara_kv_handle* handles, size_t count, uint64_t* out) {
+    return guard([&] {
+        if (count && (!handles || !out)) throw std::invalid_argument("null checksum buffers");
+        std::vector<Handle> hs(count);
+        for (size_t i = 0; i < count; ++i) hs[i] = handle(handles[i]);
+        live(cache).checksums(hs.data(), count, out);
+    });
+}
+
+uint64_t tvara_kv_sequence_create(tvara_kv_cache* cache) {
+    uint64_t id = 0;
+    guard([&] { id = live(cache).create_sequence(); });
+    return id;
+}
+
+int tvara_kv_sequence(tvara_kv_cache* cache, uint64_t sequence, size_t* length, tvara_kv_handle* blocks,
+                      size_t capacity, size_t* count) {
+    return guard([&] {
+        const auto& t = live(cache).sequence(sequence);
+        if (length) *length = t.length;
+        if (count) *count = t.blocks.size();
+        if (blocks) {
+            if (capacity < t.blocks.size()) throw std::invalid_argument("block list buffer too small");
+            for (size_t i = 0; i < t.blocks.size(); ++i) blocks[i] = exported(t.blocks[i]);
+        }
+    });
+}
+
+int tvara_kv_sequence_ids(tvara_kv_cache* cache, uint64_t* ids, size_t capacity, size_t* count) {
+    return guard([&] {
+        auto v = live(cache).sequence_ids();
+        if (count) *count = v.size();
+        if (ids) {
+            if (capacity < v.size()) throw std::invalid_argument("id buffer too small");
+            std::copy(v.begin(), v.end(), ids);
+        }
+    });
+}
+
+int tvara_kv_physical_block(tvara_kv_cache* cache, uint64_t sequence, size_t position, tvara_kv_handle* out) {
+    return guard([&] { *out = exported(live(cache).physical_block(sequence, position)); });
+}
+
+int tvara_kv_append(tvara_kv_cache* cache, uint64_t sequence, const float* keys, const float* values) {
+    return guard([&] { live(cache).append_batch(&sequence, 1, keys, values, false); });
+}
+
+int tvara_kv_append_batch(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, const float* keys,
+                          const float* values, int device_ptrs, size_t* applied) {
+    size_t done = 0;
+    const int rc = guard([&] { live(cache).append_batch(sequences, count, keys, values, device_ptrs != 0, &done); });
+    if (applied) *applied = done;
+    return rc;
+}
+
+int tvara_kv_append_tokens(tvara_kv_cache* cache, uint64_t sequence, const float* keys, const float* values,
+                           size_t count, int device_ptrs, size_t* applied) {
+    return tvara_kv_append_batch(cache, std::vector<uint64_t>(count, sequence).data(), count, keys, values,
+                                 device_ptrs, applied);
+}
+
+int tvara_kv_read(tvara_kv_cache* cache, uint64_t sequence, size_t layer, size_t position, int value, float* out) {
+    return guard([&] {
+        if (!out) throw std::invalid_argument("null output");
+        live(cache).read(sequence, layer, position, value != 0, out);
+    });
+}
+
+int tvara_kv_read_all(tvara_kv_cache* cache, uint64_t sequence, size_t layer, int value, float* out,
+                      size_t capacity) {
+    return guard([&] { live(cache).read_all(sequence, layer, value != 0, out, out ? capacity : 0); });
+}
+
+int tvara_kv_drop(tvara_kv_cache* cache, uint64_t sequence) {
+    return guard([&] { live(cache).drop(sequence); });
+}
+
+uint64_t tvara_kv_fork(tvara_kv_cache* cache, uint64_t sequence) {
+    uint64_t id = 0;
+    guard([&] { id = live(cache).fork(sequence); });
+    return id;
+}
+
+int tvara_kv_truncate(tvara_kv_cache* cache, uint64_t sequence, size_t length) {
+    return guard([&] { live(cache).truncate(sequence, length); });
+}
+
+int tvara_kv_audit(tvara_kv_cache* cache, const size_t* external, size_t count) {
+    return guard([&] { live(cache).audit(external, external ? count : 0); });
+}
+
+uint64_t tvara_kv_import_sequence(tvara_kv_cache* cache, const tvara_kv_handle* blocks, size_t block_count,
+                                  size_t source_length, size_t length) {
+    uint64_t id = 0;
+    guard([&] {
+        if (block_count && !blocks) throw std::invalid_argument("null snapshot blocks");
+        std::vector<Handle> hs(block_count);
+        for (size_t i = 0; i < block_count; ++i) hs[i] = handle(blocks[i]);
+        id = live(cache).import_sequence(hs.data(), block_count, source_length, length);
+    });
+    return id;
+}
+
+int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t layer, size_t heads,
+                      size_t context, const float* q, const float* tail_keys, const float* tail_values,
+                      const size_t* visible, float* out, int device_ptrs) {
+    return guard([&] {
+        auto& c = live(cache);
+        check_config(c, heads, context);
+        if (!count) return;
+        if (!sequences || !q || !out || (tail_keys == nullptr) != (tail_values == nullptr))
+            throw std::invalid_argument("invalid fused attention shape");
+        if (layer >= c.geometry().layers) throw std::invalid_argument("invalid fused attention shape");
+        const bool tail = tail_keys != nullptr;
+        std::vector<uint64_t> seq_of_row;
+        std::vector<size_t> cached;
+        std::vector<uint8_t> tails;
+        decode_rows(c, sequences, count, context, tail, visible, seq_of_row, cached, tails);
+        AttnPlan plan;
+        plan.build(&c, seq_of_row, cached, tails, static_cast<int>(heads), 0);
+        const size_t hidden = heads * c.geometry().head_dim, kvw = c.geometry().kv_width();
+        if (device_ptrs) {
+            if (!aligned16(q) || !aligned16(out) || (tail && (!aligned16(tail_keys) || !aligned16(tail_values))))
+                throw std::invalid_argument("device buffers must be 16-byte aligned");
+            plan.launch(static_cast<int>(layer), q, tail_keys, tail_values, out, c.stream());
+            plan.check();
+            return;
+        }
+        Staged st;
+        const float* dq = st.in(q, count * hidden);
+        const float* dk = st.in(tail_keys, count * kvw);
+        const float* dv = st.in(tail_values, count * kvw);
+        float* dout = st.out(count * hidden);
+        plan.launch(static_cast<int>(layer), dq, dk, dv, dout, c.stream());
+        plan.check();
+        TVARA_HIP(hipMemcpy(out, dout, count * hidden * sizeof(float), hipMemcpyDeviceToHost));
+    });
+}
+
+int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t layer, size_t heads,
+                       size_t context, const size_t* start, const size_t* rows, const float* queries, float* out,
+                       int precision, int device_ptrs) {
+    return guard([&] {
+        auto& c = live(cache);
+        check_config(c, heads, context);
+        if (!count) return;
+        if (!sequences || !start || !rows || !queries || !out) throw std::invalid_argument("invalid causal prompt chunk");
+        if (layer >= c.geometry().layers) throw std::invalid_argument("invalid fused attention shape");
+        if (precision != TVARA_ATTN_F32 && precision != TVARA_ATTN_BF16)
+            throw std::invalid_argument("unknown attention precision");
+        std::vector<uint64_t> seq_of_row;
+        std::vector<size_t> cached;
+        size_t total_rows = 0, max_rows = 0;
+        for (size_t i = 0; i < count; ++i) {
+            const size_t length = c.sequence(sequences[i]).length;
+            // fused_prompt_attention (attention.hpp:85-87)
+            if (!rows[i] || start[i] >= length || rows[i] > length - start[i])
+                throw std::invalid_argument("invalid causal prompt chunk");
+            if (length > context) throw std::invalid_argument("invalid fused attention shape");
+            for (size_t j = 0; j < rows[i]; ++j) {
+                seq_of_row.push_back(sequences[i]);
+                cached.push_back(start[i] + j + 1);
+            }
+            total_rows += rows[i];
+            max_rows = std::max(max_rows, rows[i]);
+        }
+        const size_t hidden = heads * c.geometry().head_dim;
+        Staged st;
+        const float* dq = device_ptrs ? queries : st.in(queries, total_rows * hidden);
+        float* dout = device_ptrs ? out : st.out(total_rows * hidden);
+        if (device_ptrs && (!aligned16(queries) || !aligned16(out)))
+            throw std::invalid_argument("device buffers must be 16-byte aligned");
+        if (precision == TVARA_ATTN_F32) {
+            AttnPlan plan;
+            plan.build(&c, seq_of_row, cached, {}, static_cast<int>(heads), 0);
+            plan.launch(static_cast<int>(layer), dq, nullptr, nullptr, dout, c.stream());
+            plan.check();
+        } else {
+            if (!tvara_amd::prefill_bf16_supported(c.layout(), static_cast<int>(heads / c.geometry().kv_heads)))
+                throw std::invalid_argument("bf16 prefill needs f32 blocks of 16 tokens and head_dim 64 or 128");
+            std::vector<int32_t> tab;
+            std::vector<int4> seqs(count);
+            size_t row0 = 0;
+            for (size_t i = 0; i < count; ++i) {
+                seqs[i] = make_int4(static_cast<int>(tab.size()), static_cast<int>(start[i]),
+                                    static_cast<int>(rows[i]), static_cast<int>(row0));
+                for (const Handle& b : c.sequence(sequences[i]).blocks) tab.push_back(static_cast<int32_t>(b.id));
+                row0 += rows[i];
+            }
+            tvara_amd::DeviceBuffer dtab, dseq, derr;
+            void* pt = dtab.ensure(tab.size() * sizeof(int32_t));
+            void* ps = dseq.ensure(seqs.size() * sizeof(int4));
+            void* pe = derr.ensure(sizeof(int));
+            TVARA_HIP(hipMemcpy(pt, tab.data(), tab.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+            TVARA_HIP(hipMemcpy(ps, seqs.data(), seqs.size() * sizeof(int4), hipMemcpyHostToDevice));
+            TVARA_HIP(hipMemset(pe, 0, sizeof(int)));
+            c.flush();
+            tvara_amd::PrefillArgs a{};
+            a.pool = c.pool();
+            a.lay = c.layout();
+            a.layer = static_cast<int>(layer);
+            a.heads = static_cast<int>(heads);
+            a.group = static_cast<int>(heads / c.geometry().kv_heads);
+            a.tables = static_cast<const int32_t*>(pt);
+            a.seqs = static_cast<const int4*>(ps);
+            a.q = dq;
+            a.out = dout;
+            a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(c.geometry().head_dim)));
+            a.err = static_cast<int*>(pe);
+            tvara_amd::launch_prefill_bf16(a, static_cast<int>(count), static_cast<int>(max_rows), c.stream());
+            int flag = 0;
+            TVARA_HIP(hipMemcpy(&flag, pe, sizeof(int), hipMemcpyDeviceToHost));
+            if (flag) throw std::invalid_argument("invalid online attention input");
+        }
+        if (!device_ptrs)
+            TVARA_HIP(hipMemcpy(out, dout, total_rows * hidden * sizeof(float), hipMemcpyDeviceToHost));
+        else
+            c.synchronize();
+    });
+}
+
+tvara_attn_plan* tvara_attn_plan_create(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t heads,
+                                        size_t context, const size_t* visible, int with_tail) {
+    tvara_attn_plan* out = nullptr;
+    guard([&] {
+        auto& c = live(cache);
+        check_config(c, heads, context);
+        if (!count || !sequences) throw std::invalid_argument("empty attention plan");
+        std::vector<uint64_t> seq_of_row;
+        std::vector<size_t> cached;
+        std::vector<uint8_t> tails;
+        decode_rows(c, sequences, count, context, with_tail != 0, visible, seq_of_row, cached, tails);
+        auto p = std::make_unique<tvara_attn_plan>();
+        p->context = context;
+        p->plan.build(&c, seq_of_row, cached, tails, static_cast<int>(heads), 0);
+        out = p.release();
+    });
+    return out;
+}
+
+int tvara_attn_plan_decode(tvara_attn_plan* plan, size_t layer, const float* q, const float* tail_keys,
+                           const float* tail_values, float* out, void* stream) {
+    return guard([&] {
+        if (!plan) throw std::invalid_argument("null attention plan");
+        if (!q || !out || !aligned16(q) || !aligned16(out)) throw std::invalid_argument("device buffers must be 16-byte aligned");
+        if ((tail_keys && !aligned16(tail_keys)) || (tail_values && !aligned16(tail_values)))
+            throw std::invalid_argument("device buffers must be 16-byte aligned");
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : plan->plan.cache->stream();
+        plan->plan.launch(static_cast<int>(layer), q, tail_keys, tail_values, out, s);
+    });
+}
+
+int tvara_attn_plan_check(tvara_attn_plan* plan) {
+    return guard([&] {
+        if (!plan) throw std::invalid_argument("null attention plan");
+        plan->plan.check();
+    });
+}
+
+int tvara_attn_plan_info(tvara_attn_plan* plan, size_t* split_tokens, size_t* items, size_t* kv_bytes) {
+    return guard([&] {
+        if (!plan) throw std::invalid_argument("null attention plan");
+        if (split_tokens) *split_tokens = static_cast<size_t>(plan->plan.split_tokens);
+        if (items) *items = static_cast<size_t>(plan->plan.items);
+        if (kv_bytes) *kv_bytes = plan->plan.kv_bytes;
+    });
+}
+
+void tvara_attn_plan_destroy(tvara_attn_plan* plan) { delete plan; }
+
+int tvara_profile_enable(int enabled) {
+    return guard([&] { tvara_amd::profile_enable(enabled != 0); });
+}
+
+int tvara_profile_read(const char* kernel, double* milliseconds, size_t* launches) {
+    return guard([&] {
+        double ms = 0;
+        size_t n = 0;
+        tvara_amd::profile_read(kernel, &ms, &n);
+        if (milliseconds) *milliseconds = ms;
+        if (launches) *launches = n;
+    });
+}
+
+int tvara_profile_reset(void) {
+    return guard([&] { tvara_amd::profile_reset(); });
+}
+
+}  // extern "C"

@@ -1,0 +1,115 @@
+// Internal declarations shared by the host allocator, the C ABI and the
+// gfx950 kernels of libtvara_capi.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace tvara_amd {
+
+// tvara::CacheExhausted (kv.hpp:34)
+struct CacheExhausted : std::runtime_error {
+    CacheExhausted() : std::runtime_error("KV cache exhausted") {}
+};
+
+inline void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+#define TVARA_HIP(x) ::tvara_amd::hip_check((x), #x)
+
+enum Format : int { kF32 = 0, kQ8 = 1 };
+
+// Where a (layer, kind, slot, column) element of a block lives in HBM.
+//  f32: the reference layout, ((layer*2+kind)*tpb+slot)*kv_width+column floats
+//       (kv.hpp:30-33), so block bytes are the reference's bytes.
+//  Q8_0: one section per (layer, kind) of `section` bytes: an int8 plane
+//       [tpb][kv_width] followed by an fp16 scale plane [tpb][kv_width/32];
+//       the canonical image is the reference element order cut into 34-byte
+//       groups (little-endian fp16 d, then 32 int8).
+struct BlockLayout {
+    int format;
+    int layers, kv_heads, head_dim, tpb, kv_width;
+    size_t stride;   // bytes between consecutive blocks in the pool (256-aligned)
+    size_t section;  // Q8_0: bytes per (layer, kind) section
+};
+
+// Block initialisation: zero-fill (src < 0, BlockPool::allocate, kv.hpp:48)
+// or whole-block copy (copy-on-write, kv.hpp:99).
+struct BlockInitOp {
+    int64_t dst;
+    int64_t src;
+};
+
+// One appended token: destination block, slot and the row of the input.
+struct RowOp {
+    int32_t block;
+    int32_t slot;
+    int32_t src_row;
+    int32_t pad;
+};
+
+// Decode work: one entry per attention row (a sequence for decode, a
+// (sequence, position) pair for the f32 prompt path); work items split rows
+// into chunks of `split_tokens` cached tokens.
+struct DecodeArgs {
+    const char* pool;
+    BlockLayout lay;
+    int layer;
+    int heads, group;  // query heads, heads per kv head
+    const int32_t* tables;
+    const int4* entries;  // x: table offset, y: cached tokens, z: tail | nsplit<<1, w: first item
+    const int2* items;    // x: row, y: split index
+    int split_tokens;
+    const float* q;
+    const float* tail_k;  // [rows][kv_width] or null
+    const float* tail_v;
+    float* out;
+    float* part_acc;  // [items][heads][head_dim]
+    float* part_ml;   // [items][heads][2]: running max (log2 units), normaliser
+    float qscale;     // log2(e)/sqrt(head_dim)
+    int* err;
+};
+
+struct PrefillArgs {
+    const char* pool;
+    BlockLayout lay;
+    int layer;
+    int heads, group;
+    const int32_t* tables;
+    const int4* seqs;  // x: table offset, y: start, z: rows, w: first query row
+    const float* q;    // [sum rows][heads][head_dim]
+    float* out;
+    float qscale;
+    int* err;
+};
+
+// launchers (kernels.hip)
+void launch_block_init(char* pool, size_t stride, const BlockInitOp* ops, int n, hipStream_t s);
+void launch_append_rows(char* pool, const BlockLayout& lay, const RowOp* ops, int n, const float* keys,
+                        const float* values, hipStream_t s);
+void launch_gather_rows(const char* pool, const BlockLayout& lay, const int2* rows, int n, int layer, int kind,
+                        float* out, hipStream_t s);
+void launch_checksums(const char* pool, const BlockLayout& lay, const int64_t* ids, int n, uint64_t* out,
+                      hipStream_t s);
+void launch_q8_to_canonical(const char* pool, const BlockLayout& lay, int64_t id, uint8_t* out, hipStream_t s);
+void launch_canonical_to_q8(char* pool, const BlockLayout& lay, int64_t id, const uint8_t* in, hipStream_t s);
+// decode.hip
+void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, hipStream_t s);
+int decode_waves(int kv_heads, int group);
+// prefill.hip
+bool prefill_bf16_supported(const BlockLayout& lay, int group);
+void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s);
+
+// kernel timing (profile.cpp)
+struct ProfileScope {
+    ProfileScope(const char* name, hipStream_t s);
+    ~ProfileScope();
+    const char* name;
+    hipStream_t stream;
+    void* begin = nullptr;
+};
+
+}  // namespace tvara_amd

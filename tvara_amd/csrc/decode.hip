@@ -1,0 +1,632 @@
+// Paged decode attention for gfx950: fused_paged_attention
+// (core/include/tvara/attention.hpp:57-83) over f32 or Q8_0 blocks.
+//
+// Work decomposition.  A row (one query vector with `heads` heads) walks its
+// sequence's block table.  The host cuts each row's cached tokens into splits
+// of `split_tokens`; one workgroup handles one split for a group of KV heads,
+// one wave per KV head.  Within a wave, LPT lanes share one token (a "token
+// group") and each lane owns E = head_dim / LPT consecutive-in-memory columns,
+// so one dwordx4 per lane reads whole 64-128 byte row segments and the whole
+// workgroup streams contiguous 2 KiB slot rows of a block.  The G query heads
+// of a GQA group are evaluated on every K/V element loaded (the reference
+// re-reads the rows once per query head, attention.hpp:72).
+//
+// Softmax.  Scores are in log2 units (q is pre-scaled by log2(e)/sqrt(d)).
+// Each lane keeps the running maximum of its head slot; the accumulators are
+// only rescaled when a score exceeds the running maximum by more than
+// kThreshold, so exp2(s - m) stays below 2^kThreshold and the rescale runs a
+// handful of times per split instead of once per tile.
+//
+// Splits are merged by log-sum-exp in merge_kernel.  A non-finite score sets
+// *err, matching OnlineAttention::update's rejection (attention.hpp:11).
+#include "common.hpp"
+#include "q8.hpp"
+
+namespace tvara_amd {
+namespace {
+
+constexpr float kThreshold = 8.0f;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Transpose-reduce: lane c of every LPT-lane group returns the sum over the
+// group of v[c].  Pairings use DPP (quad permutes, half-row mirror).
+template <int LPT>
+__device__ __forceinline__ float transpose_reduce(const float (&v)[LPT], int c);
+
+template <>
+__device__ __forceinline__ float transpose_reduce<4>(const float (&v)[4], int c) {
+    const bool b2 = (c & 2) != 0, b1 = (c & 1) != 0;
+    const float r0 = (b2 ? v[2] : v[0]) + dpp<0x4E>(b2 ? v[0] : v[2]);
+    const float r1 = (b2 ? v[3] : v[1]) + dpp<0x4E>(b2 ? v[1] : v[3]);
+    return (b1 ? r1 : r0) + dpp<0xB1>(b1 ? r0 : r1);
+}
+
+template <>
+__device__ __forceinline__ float transpose_reduce<8>(const float (&v)[8], int c) {
+    const bool b4 = (c & 4) != 0;
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = (b4 ? v[i + 4] : v[i]) + dpp<0x141>(b4 ? v[i] : v[i + 4]);
+    return transpose_reduce<4>(r, c & 3);
+}
+
+// value of lane (token group base + h)
+template <int LPT>
+__device__ __forceinline__ float group_bcast(float v, int h, int lane);
+
+template <>
+__device__ __forceinline__ float group_bcast<4>(float v, int h, int) {
+    switch (h) {
+        case 0: return dpp<0x00>(v);
+        case 1: return dpp<0x55>(v);
+        case 2: return dpp<0xAA>(v);
+        default: return dpp<0xFF>(v);
+    }
+}
+
+template <>
+__device__ __forceinline__ float group_bcast<8>(float v, int h, int lane) {
+    return __shfl(v, (lane & ~7) | h);
+}
+
+__device__ __forceinline__ float wave_max_across(float v, int from) {
+    for (int o = from; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_across(float v, int from) {
+    for (int o = from; o < 64; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+struct RowState {
+    float m = -INFINITY;  // running max of this lane's head slot (log2 units)
+    float l = 0.f;        // partial normaliser of this lane's head slot
+    bool bad = false;
+};
+
+// Online-softmax update for one tile: `s` is this lane's full score for head
+// slot c (valid when `own`); rescales acc when the maximum moves by more than
+// kThreshold; returns p = exp2(s - m).
+template <int G, int LPT, int E>
+__device__ __forceinline__ float softmax_step(float s, bool own, int lane, RowState& st, float (&acc)[G][E]) {
+    s = own ? s : -INFINITY;
+    st.bad |= own && !__builtin_isfinite(s);
+    const bool need = own && (s > st.m + kThreshold);
+    if (__any(need)) {
+        const float mnew = fmaxf(st.m, wave_max_across(s, LPT));
+        const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(st.m - mnew);
+        st.m = mnew;
+        st.l *= alpha;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float ah = group_bcast<LPT>(alpha, h, lane);
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[h][e] *= ah;
+        }
+    }
+    const float p = own ? fast_exp2(s - st.m) : 0.f;
+    st.l += p;
+    return p;
+}
+
+// Reduce the token groups of a wave and write the split's result: the
+// normalised output when the row has one split, otherwise the partial
+// (acc, m, l) for merge_kernel.  `col(h, e4)` is the head-local column of the
+// lane's e4-th float4.
+template <int D, int G, int LPT, int E, class Col>
+__device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G][E], RowState& st, int lane, int wave,
+                                             int nwaves, int kh, int item, int row, int nsplit, Col col) {
+    constexpr int TT = 64 / LPT;
+    extern __shared__ float lds[];
+    const int c = lane & (LPT - 1), tg = lane / LPT;
+    st.l = wave_sum_across(st.l, LPT);
+    float* red = lds + static_cast<size_t>(wave) * 64 * G * E;
+    float* ml = lds + static_cast<size_t>(nwaves) * 64 * G * E + wave * 2 * G;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e4 = 0; e4 < E / 4; ++e4)
+            *reinterpret_cast<float4*>(red + (tg * G + h) * D + col(c, e4)) =
+                make_float4(acc[h][4 * e4], acc[h][4 * e4 + 1], acc[h][4 * e4 + 2], acc[h][4 * e4 + 3]);
+    if (tg == 0 && c < G) {
+        ml[c] = st.m;
+        ml[G + c] = st.l;
+    }
+    __syncthreads();
+    const size_t head0 = static_cast<size_t>(kh) * G;
+    for (int o4 = lane; o4 < G * D / 4; o4 += 64) {
+        float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const float4 x = *reinterpret_cast<const float4*>(red + t * G * D + 4 * o4);
+            sum.x += x.x;
+            sum.y += x.y;
+            sum.z += x.z;
+            sum.w += x.w;
+        }
+        const int h = (4 * o4) / D;
+        if (nsplit == 1) {
+            const float l = ml[G + h];
+            float* o = a.out + (static_cast<size_t>(row) * a.heads + head0) * D + 4 * o4;
+            *reinterpret_cast<float4*>(o) = make_float4(sum.x / l, sum.y / l, sum.z / l, sum.w / l);
+        } else {
+            float* o = a.part_acc + (static_cast<size_t>(item) * a.heads + head0) * D + 4 * o4;
+            *reinterpret_cast<float4*>(o) = sum;
+        }
+    }
+    if (nsplit > 1 && lane < G) {
+        float* o = a.part_ml + (static_cast<size_t>(item) * a.heads + head0 + lane) * 2;
+        o[0] = ml[lane];
+        o[1] = ml[G + lane];
+    }
+    if (__any(st.bad) && lane == 0) *a.err = 1;
+}
+
+// ------------------------------------------------------------- f32 blocks
+
+template <int D, int G, int LPT>
+__global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs a) {
+    constexpr int E = D / LPT, NV = E / 4, TT = 64 / LPT;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int groups = a.lay.kv_heads / nwaves;
+    const int item = static_cast<int>(blockIdx.x) / groups;
+    const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
+    const int2 it = a.items[item];
+    const int4 en = a.entries[it.x];
+    const int nsplit = en.z >> 1;
+    const bool tail = (en.z & 1) && it.y == nsplit - 1;
+    const int t0 = it.y * a.split_tokens;
+    const int t1 = min(t0 + a.split_tokens, en.y);
+    const int c = lane & (LPT - 1), tg = lane / LPT;
+    const int kvw = a.lay.kv_width;
+
+    float q[G][E];
+    {
+        const float* qr = a.q + (static_cast<size_t>(it.x) * a.heads + static_cast<size_t>(kh) * G) * D + 4 * c;
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int m = 0; m < NV; ++m) {
+                const float4 x = *reinterpret_cast<const float4*>(qr + h * D + 4 * LPT * m);
+                q[h][4 * m] = x.x * a.qscale;
+                q[h][4 * m + 1] = x.y * a.qscale;
+                q[h][4 * m + 2] = x.z * a.qscale;
+                q[h][4 * m + 3] = x.w * a.qscale;
+            }
+    }
+    float acc[G][E];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
+    RowState st;
+
+    const float* pool = reinterpret_cast<const float*>(a.pool);
+    const size_t bstride = a.lay.stride / sizeof(float);
+    const int32_t* tab = a.tables + en.x;
+    const size_t koff = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D + 4 * c;
+    const size_t voff = koff + 16 * static_cast<size_t>(kvw);
+
+    auto load = [&](int tb, float4 (&kk)[NV], float4 (&vv)[NV]) -> bool {
+        const bool ok = tb + tg < t1;
+        const int bid = tab[tb >> 4];
+        const float* base = pool + static_cast<size_t>(bid) * bstride + static_cast<size_t>((tb & 15) + tg) * kvw;
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            kk[m] = ok ? *reinterpret_cast<const float4*>(base + koff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+            vv[m] = ok ? *reinterpret_cast<const float4*>(base + voff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        return ok;
+    };
+    auto process = [&](const float4 (&kk)[NV], const float4 (&vv)[NV], bool ok) {
+        float part[LPT];
+#pragma unroll
+        for (int h = 0; h < LPT; ++h) part[h] = 0.f;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float s = 0.f;
+#pragma unroll
+            for (int m = 0; m < NV; ++m) {
+                s = fmaf(q[h][4 * m], kk[m].x, s);
+                s = fmaf(q[h][4 * m + 1], kk[m].y, s);
+                s = fmaf(q[h][4 * m + 2], kk[m].z, s);
+                s = fmaf(q[h][4 * m + 3], kk[m].w, s);
+            }
+            part[h] = s;
+        }
+        const float s = transpose_reduce<LPT>(part, c);
+        const float p = softmax_step<G, LPT, E>(s, ok && c < G, lane, st, acc);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float ph = group_bcast<LPT>(p, h, lane);
+#pragma unroll
+            for (int m = 0; m < NV; ++m) {
+                acc[h][4 * m] = fmaf(ph, vv[m].x, acc[h][4 * m]);
+                acc[h][4 * m + 1] = fmaf(ph, vv[m].y, acc[h][4 * m + 1]);
+                acc[h][4 * m + 2] = fmaf(ph, vv[m].z, acc[h][4 * m + 2]);
+                acc[h][4 * m + 3] = fmaf(ph, vv[m].w, acc[h][4 * m + 3]);
+            }
+        }
+    };
+
+    // two tiles in flight: tile t+2 is requested as soon as tile t is consumed
+    float4 ka[NV], va[NV], kb[NV], vb[NV];
+    bool oka = false, okb = false;
+    if (t0 < t1) oka = load(t0, ka, va);
+    if (t0 + TT < t1) okb = load(t0 + TT, kb, vb);
+    for (int t = t0; t < t1; t += 2 * TT) {
+        process(ka, va, oka);
+        if (t + 2 * TT < t1) oka = load(t + 2 * TT, ka, va);
+        if (t + TT < t1) {
+            process(kb, vb, okb);
+            if (t + 3 * TT < t1) okb = load(t + 3 * TT, kb, vb);
+        }
+    }
+    if (tail) {  // the current token's uncommitted K/V is the last position (attention.hpp:80)
+        const bool ok = tg == 0;
+        const float* tk = a.tail_k + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kh) * D + 4 * c;
+        const float* tv = a.tail_v + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kh) * D + 4 * c;
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            ka[m] = ok ? *reinterpret_cast<const float4*>(tk + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+            va[m] = ok ? *reinterpret_cast<const float4*>(tv + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        process(ka, va, ok);
+    }
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
+                               [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
+}
+
+// ------------------------------------------------------------- Q8_0 blocks
+
+__device__ __forceinline__ void unpack_i8(uint4 w, float (&f)[16]) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            f[4 * j + b] = static_cast<float>(static_cast<int8_t>(static_cast<uint8_t>(words[j] >> (8 * b))));
+}
+
+// Each lane owns 16 consecutive columns (one dwordx4 of int8) = half a Q8_0
+// group, so a token's row of head_dim columns is LPT = head_dim/16 lanes.
+template <int D, int G>
+__global__ __launch_bounds__(256) void decode_q8_kernel(const DecodeArgs a) {
+    constexpr int LPT = D / 16, TT = 64 / LPT, E = 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int groups = a.lay.kv_heads / nwaves;
+    const int item = static_cast<int>(blockIdx.x) / groups;
+    const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
+    const int2 it = a.items[item];
+    const int4 en = a.entries[it.x];
+    const int nsplit = en.z >> 1;
+    const bool tail = (en.z & 1) && it.y == nsplit - 1;
+    const int t0 = it.y * a.split_tokens;
+    const int t1 = min(t0 + a.split_tokens, en.y);
+    const int c = lane & (LPT - 1), tg = lane / LPT;
+    const int kvw = a.lay.kv_width;
+
+    float q[G][E];
+    {
+        const float* qr = a.q + (static_cast<size_t>(it.x) * a.heads + static_cast<size_t>(kh) * G) * D + 16 * c;
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const float4 x = *reinterpret_cast<const float4*>(qr + h * D + 4 * m);
+                q[h][4 * m] = x.x * a.qscale;
+                q[h][4 * m + 1] = x.y * a.qscale;
+                q[h][4 * m + 2] = x.z * a.qscale;
+                q[h][4 * m + 3] = x.w * a.qscale;
+            }
+    }
+    float acc[G][E];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
+    RowState st;
+
+    const int32_t* tab = a.tables + en.x;
+    const size_t sec = a.lay.section;
+    const size_t qcol = static_cast<size_t>(kh) * D + 16 * c;
+    const size_t scol = (static_cast<size_t>(kh) * D + 16 * c) / 32;
+    const size_t plane = static_cast<size_t>(16) * kvw;  // int8 plane bytes of a section
+    const size_t ksec = static_cast<size_t>(a.layer) * 2 * sec, vsec = ksec + sec;
+    const int gpr = kvw / 32;
+
+    struct Tile {
+        uint4 kq, vq;
+        uint16_t ks, vs;
+        bool ok;
+    };
+    auto load = [&](int tb, Tile& x) {
+        x.ok = tb + tg < t1;
+        const int bid = tab[tb >> 4];
+        const int slot = (tb & 15) + tg;
+        const char* base = a.pool + static_cast<size_t>(bid) * a.lay.stride;
+        if (x.ok) {
+            x.kq = *reinterpret_cast<const uint4*>(base + ksec + static_cast<size_t>(slot) * kvw + qcol);
+            x.vq = *reinterpret_cast<const uint4*>(base + vsec + static_cast<size_t>(slot) * kvw + qcol);
+            x.ks = *reinterpret_cast<const uint16_t*>(base + ksec + plane + (static_cast<size_t>(slot) * gpr + scol) * 2);
+            x.vs = *reinterpret_cast<const uint16_t*>(base + vsec + plane + (static_cast<size_t>(slot) * gpr + scol) * 2);
+        } else {
+            x.kq = x.vq = make_uint4(0, 0, 0, 0);
+            x.ks = x.vs = 0;
+        }
+    };
+    auto process_f = [&](const float (&kf)[16], float ks, const float (&vf)[16], float vs, bool ok) {
+        float part[LPT];
+#pragma unroll
+        for (int h = 0; h < LPT; ++h) part[h] = 0.f;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float s = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s = fmaf(q[h][e], kf[e], s);
+            part[h] = s * ks;
+        }
+        const float s = transpose_reduce<LPT>(part, c);
+        const float p = softmax_step<G, LPT, E>(s, ok && c < G, lane, st, acc);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float w = group_bcast<LPT>(p, h, lane) * vs;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[h][e] = fmaf(w, vf[e], acc[h][e]);
+        }
+    };
+    auto process = [&](const Tile& x) {
+        float kf[16], vf[16];
+        unpack_i8(x.kq, kf);
+        unpack_i8(x.vq, vf);
+        process_f(kf, half_bits_to_float(x.ks), vf, half_bits_to_float(x.vs), x.ok);
+    };
+
+    Tile ta, tb2;
+    ta.ok = tb2.ok = false;
+    if (t0 < t1) load(t0, ta);
+    if (t0 + TT < t1) load(t0 + TT, tb2);
+    for (int t = t0; t < t1; t += 2 * TT) {
+        process(ta);
+        if (t + 2 * TT < t1) load(t + 2 * TT, ta);
+        if (t + TT < t1) {
+            process(tb2);
+            if (t + 3 * TT < t1) load(t + 3 * TT, tb2);
+        }
+    }
+    if (tail) {  // the uncommitted token arrives as f32
+        const bool ok = tg == 0;
+        const float* tk = a.tail_k + static_cast<size_t>(it.x) * kvw + qcol;
+        const float* tv = a.tail_v + static_cast<size_t>(it.x) * kvw + qcol;
+        float kf[16], vf[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            kf[e] = ok ? tk[e] : 0.f;
+            vf[e] = ok ? tv[e] : 0.f;
+        }
+        process_f(kf, 1.f, vf, 1.f, ok);
+    }
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
+                               [](int cc, int e4) { return 16 * cc + 4 * e4; });
+}
+
+// --------------------------------------------------- any shape (one wave per head)
+
+__device__ __forceinline__ float element(const DecodeArgs& a, int block, int kind, int slot, int column) {
+    const char* base = a.pool + static_cast<size_t>(block) * a.lay.stride;
+    const int kvw = a.lay.kv_width;
+    if (a.lay.format == kF32)
+        return reinterpret_cast<const float*>(base)[(static_cast<size_t>(a.layer * 2 + kind) * a.lay.tpb + slot) * kvw +
+                                                    column];
+    const char* sec = base + static_cast<size_t>(a.layer * 2 + kind) * a.lay.section;
+    const int8_t qv = reinterpret_cast<const int8_t*>(sec)[static_cast<size_t>(slot) * kvw + column];
+    const uint16_t d = reinterpret_cast<const uint16_t*>(sec + static_cast<size_t>(a.lay.tpb) * kvw)
+        [static_cast<size_t>(slot) * (kvw / 32) + column / 32];
+    return half_bits_to_float(d) * static_cast<float>(qv);
+}
+
+constexpr int kGenericMaxDim = 512;
+
+__global__ __launch_bounds__(64) void decode_generic_kernel(const DecodeArgs a) {
+    __shared__ float qs[kGenericMaxDim];
+    const int lane = threadIdx.x;
+    const int h = blockIdx.y, kh = h / a.group;
+    const int D = a.lay.head_dim, kvw = a.lay.kv_width, tpb = a.lay.tpb;
+    const int2 it = a.items[blockIdx.x];
+    const int4 en = a.entries[it.x];
+    const int nsplit = en.z >> 1;
+    const bool tail = (en.z & 1) && it.y == nsplit - 1;
+    const int t0 = it.y * a.split_tokens;
+    const int t1 = min(t0 + a.split_tokens, en.y);
+    const int ntok = max(t1 - t0, 0) + (tail ? 1 : 0);
+    const int32_t* tab = a.tables + en.x;
+    const float* qr = a.q + (static_cast<size_t>(it.x) * a.heads + h) * D;
+    for (int d = lane; d < D; d += 64) qs[d] = qr[d] * a.qscale;
+    __syncthreads();
+    const float* tk = tail ? a.tail_k + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kh) * D : nullptr;
+    const float* tv = tail ? a.tail_v + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kh) * D : nullptr;
+    float m = -INFINITY, l = 0.f, acc[kGenericMaxDim / 64];
+    for (int i = 0; i < kGenericMaxDim / 64; ++i) acc[i] = 0.f;
+    bool bad = false;
+    for (int base = 0; base < ntok; base += 64) {
+        const int j = base + lane;
+        const bool ok = j < ntok;
+        float s = -INFINITY;
+        if (ok) {
+            s = 0.f;
+            const int p = t0 + j;
+            if (p < t1) {
+                const int bid = tab[p / tpb], slot = p % tpb;
+                for (int d = 0; d < D; ++d) s = fmaf(qs[d], element(a, bid, 0, slot, kh * D + d), s);
+            } else {
+                for (int d = 0; d < D; ++d) s = fmaf(qs[d], tk[d], s);
+            }
+            bad |= !__builtin_isfinite(s);
+        }
+        float mx = s;
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float mnew = fmaxf(m, mx);
+        const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m - mnew);
+        const float pj = ok ? exp2f(s - mnew) : 0.f;
+        float ps = pj;
+        for (int o = 32; o >= 1; o >>= 1) ps += __shfl_xor(ps, o);
+        l = l * alpha + ps;
+        m = mnew;
+        for (int i = 0; i < kGenericMaxDim / 64; ++i) acc[i] *= alpha;
+        const int count = min(64, ntok - base);
+        for (int jj = 0; jj < count; ++jj) {
+            const float w = __shfl(pj, jj);
+            const int p = t0 + base + jj;
+            if (p < t1) {
+                const int bid = tab[p / tpb], slot = p % tpb;
+                for (int i = 0; i * 64 + lane < D; ++i)
+                    acc[i] = fmaf(w, element(a, bid, 1, slot, kh * D + i * 64 + lane), acc[i]);
+            } else {
+                for (int i = 0; i * 64 + lane < D; ++i) acc[i] = fmaf(w, tv[i * 64 + lane], acc[i]);
+            }
+        }
+    }
+    if (nsplit == 1) {
+        float* o = a.out + (static_cast<size_t>(it.x) * a.heads + h) * D;
+        for (int i = 0; i * 64 + lane < D; ++i) o[i * 64 + lane] = acc[i] / l;
+    } else {
+        float* o = a.part_acc + (static_cast<size_t>(blockIdx.x) * a.heads + h) * D;
+        for (int i = 0; i * 64 + lane < D; ++i) o[i * 64 + lane] = acc[i];
+        if (lane == 0) {
+            a.part_ml[(static_cast<size_t>(blockIdx.x) * a.heads + h) * 2] = m;
+            a.part_ml[(static_cast<size_t>(blockIdx.x) * a.heads + h) * 2 + 1] = l;
+        }
+    }
+    if (__any(bad) && lane == 0) *a.err = 1;
+}
+
+// ---------------------------------------------------------- split merge
+
+__global__ __launch_bounds__(64) void merge_kernel(const DecodeArgs a) {
+    const int row = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int4 en = a.entries[row];
+    const int nsplit = en.z >> 1;
+    if (nsplit <= 1) return;
+    const int D = a.lay.head_dim;
+    const float* ml = a.part_ml + (static_cast<size_t>(en.w) * a.heads + h) * 2;
+    const size_t mstep = static_cast<size_t>(a.heads) * 2;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[s * mstep]);
+    float L = 0.f;
+    float acc[kGenericMaxDim / 64];
+    for (int i = 0; i < kGenericMaxDim / 64; ++i) acc[i] = 0.f;
+    const float* pa = a.part_acc + (static_cast<size_t>(en.w) * a.heads + h) * D;
+    const size_t astep = static_cast<size_t>(a.heads) * D;
+    for (int s = 0; s < nsplit; ++s) {
+        const float w = exp2f(ml[s * mstep] - M);
+        L = fmaf(w, ml[s * mstep + 1], L);
+        for (int i = 0; i * 64 + lane < D; ++i) acc[i] = fmaf(w, pa[s * astep + i * 64 + lane], acc[i]);
+    }
+    float* o = a.out + (static_cast<size_t>(row) * a.heads + h) * D;
+    for (int i = 0; i * 64 + lane < D; ++i) o[i * 64 + lane] = acc[i] / L;
+}
+
+template <int D, int G, int LPT>
+void launch_f32(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
+    const size_t lds = (static_cast<size_t>(waves) * 64 * G * (D / LPT) + waves * 2 * G) * sizeof(float);
+    hipLaunchKernelGGL((decode_f32_kernel<D, G, LPT>), dim3(nitems * (a.lay.kv_heads / waves)), dim3(64 * waves), lds,
+                       s, a);
+}
+
+template <int D, int G>
+void launch_q8(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
+    const size_t lds = (static_cast<size_t>(waves) * 64 * G * 16 + waves * 2 * G) * sizeof(float);
+    hipLaunchKernelGGL((decode_q8_kernel<D, G>), dim3(nitems * (a.lay.kv_heads / waves)), dim3(64 * waves), lds, s, a);
+}
+
+template <int D>
+bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
+    constexpr int LPT = D == 64 ? 4 : 8;
+    const int G = a.group;
+    if (G > LPT) return false;
+    if (a.lay.format == kF32) {
+        switch (G) {
+            case 1: launch_f32<D, 1, LPT>(a, nitems, waves, s); return true;
+            case 2: launch_f32<D, 2, LPT>(a, nitems, waves, s); return true;
+            case 3: launch_f32<D, 3, LPT>(a, nitems, waves, s); return true;
+            case 4: launch_f32<D, 4, LPT>(a, nitems, waves, s); return true;
+            default: break;
+        }
+        if constexpr (LPT == 8) {
+            switch (G) {
+                case 5: launch_f32<D, 5, LPT>(a, nitems, waves, s); return true;
+                case 6: launch_f32<D, 6, LPT>(a, nitems, waves, s); return true;
+                case 7: launch_f32<D, 7, LPT>(a, nitems, waves, s); return true;
+                case 8: launch_f32<D, 8, LPT>(a, nitems, waves, s); return true;
+                default: break;
+            }
+        }
+        return false;
+    }
+    switch (G) {
+        case 1: launch_q8<D, 1>(a, nitems, waves, s); return true;
+        case 2: launch_q8<D, 2>(a, nitems, waves, s); return true;
+        case 3: launch_q8<D, 3>(a, nitems, waves, s); return true;
+        case 4: launch_q8<D, 4>(a, nitems, waves, s); return true;
+        default: break;
+    }
+    if constexpr (LPT == 8) {
+        switch (G) {
+            case 5: launch_q8<D, 5>(a, nitems, waves, s); return true;
+            case 6: launch_q8<D, 6>(a, nitems, waves, s); return true;
+            case 7: launch_q8<D, 7>(a, nitems, waves, s); return true;
+            case 8: launch_q8<D, 8>(a, nitems, waves, s); return true;
+            default: break;
+        }
+    }
+    return false;
+}
+
+}  // namespace
+
+// Waves per workgroup: two KV heads (32 KiB of LDS for the end-of-split
+// reduction when G <= 4) when kv_heads is even, else one.  Consecutive
+// workgroups take the KV-head groups of one work item, so the waves reading a
+// block's slot rows run close together.
+int decode_waves(int kv_heads, int group) {
+    if (group > 4) return 1;
+    return kv_heads % 2 ? 1 : 2;
+}
+
+static int waves_for(const DecodeArgs& a) { return decode_waves(a.lay.kv_heads, a.group); }
+
+bool decode_fast_path(const DecodeArgs& a) {
+    return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128) &&
+           a.group <= (a.lay.head_dim == 64 ? 4 : 8);
+}
+
+void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, hipStream_t s) {
+    if (nitems <= 0) return;
+    {
+        ProfileScope p("paged_decode", s);
+        bool done = false;
+        if (decode_fast_path(a)) {
+            const int waves = waves_for(a);
+            done = a.lay.head_dim == 64 ? dispatch_fast<64>(a, nitems, waves, s) : dispatch_fast<128>(a, nitems, waves, s);
+        }
+        if (!done) {
+            if (a.lay.head_dim > kGenericMaxDim) throw std::invalid_argument("head_dim above 512 is not supported");
+            hipLaunchKernelGGL(decode_generic_kernel, dim3(nitems, a.heads), dim3(64), 0, s, a);
+        }
+        TVARA_HIP(hipGetLastError());
+    }
+    if (need_merge) {
+        ProfileScope p("paged_decode_merge", s);
+        hipLaunchKernelGGL(merge_kernel, dim3(nrows, a.heads), dim3(64), 0, s, a);
+        TVARA_HIP(hipGetLastError());
+    }
+}
+
+}  // namespace tvara_amd

@@ -1,0 +1,150 @@
+// Device paged KV cache: the reference's PagedCache/BlockPool rules
+// (core/include/tvara/kv.hpp) kept on the host, block storage in one HBM
+// allocation, and every byte movement done by gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <vector>
+
+#include "common.hpp"
+
+namespace tvara_amd {
+
+// CacheGeometry (kv.hpp:12-29)
+struct Geometry {
+    size_t layers = 1, kv_heads = 1, head_dim = 4, tokens_per_block = 16, max_blocks = 64;
+    size_t kv_width() const;
+    size_t elements_per_block() const;
+    void validate() const;
+};
+
+// BlockHandle (kv.hpp:35)
+struct Handle {
+    size_t id = 0;
+    uint64_t generation = 0;
+};
+
+// BlockTable (kv.hpp:77)
+struct Table {
+    std::vector<Handle> blocks;
+    size_t length = 0;
+};
+
+// Grow-only device buffer.
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    void* ensure(size_t n);
+    ~DeviceBuffer();
+};
+
+// Grow-only pinned host buffer whose reuse waits for the last copy out of it.
+struct PinnedBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;
+    void* acquire(size_t n);
+    void release(hipStream_t s);
+    ~PinnedBuffer();
+};
+
+class DeviceCache {
+public:
+    DeviceCache(const Geometry& g, int format);
+    ~DeviceCache();
+    DeviceCache(const DeviceCache&) = delete;
+    DeviceCache& operator=(const DeviceCache&) = delete;
+
+    const Geometry& geometry() const { return g_; }
+    int format() const { return format_; }
+    const BlockLayout& layout() const { return lay_; }
+    size_t canonical_block_bytes() const;
+    char* pool() const { return pool_; }
+    hipStream_t stream() const { return stream_; }
+    void set_stream(hipStream_t s) { stream_ = s; }
+    uint64_t epoch() const { return epoch_; }
+    void synchronize();
+
+    // BlockPool (kv.hpp:36-75)
+    Handle allocate();
+    void retain(Handle h);
+    void release(Handle h);
+    size_t references(Handle h) const;
+    size_t references_by_id(size_t id) const;
+    size_t available() const { return free_.size(); }
+    void pool_audit() const;
+    void pool_state(size_t* refs, uint64_t* generations, size_t* free_pop_order, size_t* free_count) const;
+    void block_read(Handle h, void* out, size_t bytes);
+    void block_write(Handle h, size_t offset, const void* data, size_t bytes);
+    void checksums(const Handle* handles, size_t n, uint64_t* out);
+
+    // PagedCache (kv.hpp:78-165)
+    uint64_t create_sequence();
+    const Table& sequence(uint64_t id) const;
+    std::vector<uint64_t> sequence_ids() const;
+    Handle physical_block(uint64_t id, size_t position) const;
+    // appends one token to each listed sequence in order; *applied receives the
+    // number applied before the failure of the first one that could not be,
+    // which is rethrown
+    size_t append_batch(const uint64_t* seqs, size_t n, const float* keys, const float* values, bool device,
+                        size_t* applied = nullptr);
+    size_t append_tokens(uint64_t seq, const float* keys, const float* values, size_t count, bool device);
+    void read(uint64_t id, size_t layer, size_t position, bool value, float* out);
+    void read_all(uint64_t id, size_t layer, bool value, float* out, size_t capacity);
+    void drop(uint64_t id);
+    uint64_t fork(uint64_t id);
+    void truncate(uint64_t id, size_t length);
+    void audit(const size_t* external, size_t count) const;
+    uint64_t import_sequence(const Handle* blocks, size_t count, size_t source_length, size_t length);
+
+    // zero-fill blocks handed out by allocate() that are still live
+    void flush();
+    // device scratch owned by the cache
+    DeviceBuffer& scratch(int i) { return scratch_[i]; }
+    PinnedBuffer& pinned(int i) { return pinned_[i]; }
+    int* error_flag() const { return err_; }
+
+private:
+    const Handle& validated(Handle h) const;
+    Handle take_free();  // pop the free list: refs=1, ++generation
+    Table& mutable_sequence(uint64_t id);
+    uint64_t publish(const Handle* blocks, size_t count, size_t length);
+
+    Geometry g_;
+    int format_;
+    BlockLayout lay_{};
+    char* pool_ = nullptr;
+    hipStream_t stream_ = nullptr;
+    uint64_t epoch_ = 0;
+    std::vector<size_t> refs_;
+    std::vector<uint64_t> gens_;
+    std::vector<size_t> free_;
+    std::vector<uint8_t> zero_pending_;
+    std::vector<size_t> zero_list_;
+    std::map<uint64_t, Table> sequences_;
+    uint64_t next_ = 0;
+    DeviceBuffer scratch_[6];
+    PinnedBuffer pinned_[6];
+    int* err_ = nullptr;
+};
+
+// A batch of attention rows with resident block tables.
+struct AttnPlan {
+    DeviceCache* cache = nullptr;
+    uint64_t epoch = 0;
+    int rows = 0, heads = 0, group = 0, items = 0, split_tokens = 0;
+    bool need_merge = false, with_tail = false;
+    size_t kv_bytes = 0;  // algorithmic K/V bytes one launch reads
+    DeviceBuffer tables, entries, items_buf, part_acc, part_ml, err;
+    // Builds the plan for rows reading `cached[r]` tokens of `seq_of_row[r]`,
+    // followed by the row's uncommitted tail token when tail_rows[r] != 0.
+    void build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, const std::vector<size_t>& cached,
+               const std::vector<uint8_t>& tail_rows, int heads, size_t split_override);
+    void launch(int layer, const float* q, const float* tail_k, const float* tail_v, float* out, hipStream_t s);
+    void check();
+};
+
+}  // namespace tvara_amd

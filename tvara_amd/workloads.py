@@ -1,0 +1,186 @@
+"""Synthetic workloads of the paged KV path, shared by the parity tests and
+bench.py.  Inputs come from tvara_amd.synth (counter-based splitmix64), so a
+test can rebuild exactly the bench's data on any backend that has the
+PagedCache method surface.
+
+decode_c1  1 sequence, SmolLM2-135M attention: 9 q / 3 kv heads, d=64, 512
+           cached tokens in 16-token blocks at a seeded permutation of ids.
+decode_c2  64 sequences, Llama-3.2-1B attention: 32 q / 8 kv heads, d=64,
+           contexts uniform in [128, 4096], blocks scattered over a
+           65,536-block pool.
+kv_c3      KV-management stress: 256 sequences share a 1,024-token prefix
+           (22 layers x 8 kv heads x 64), 128 steps of one appended token per
+           sequence, then a seeded 0-64 token rollback per sequence; the
+           unaligned-prefix variant (1,025 tokens) makes step 1 copy-on-write.
+prefill_c4 8 sequences x (2,048 cached + 512-token causal chunk), 32/8 heads, d=64.
+decode_c5  16 sequences x 32,768 tokens, Llama-3-8B attention: 32/8 heads,
+           d=128, Q8_0 blocks.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import synth
+
+
+@dataclass
+class DecodeWorkload:
+    name: str
+    heads: int
+    kv_heads: int
+    head_dim: int
+    lengths: list
+    pool_blocks: int
+    seed: int
+    tokens_per_block: int = 16
+    layers: int = 1
+    q8: bool = False
+    context: int = 1 << 20
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def kv_width(self):
+        return self.kv_heads * self.head_dim
+
+    @property
+    def sequences(self):
+        return len(self.lengths)
+
+    @property
+    def total_tokens(self):
+        return int(sum(self.lengths))
+
+    def kv_bytes(self):
+        """Algorithmic K+V bytes one decode launch reads."""
+        per_element = 34 / 32 if self.q8 else 4
+        return int(self.total_tokens * self.kv_width * 2 * per_element)
+
+    def qo_bytes(self):
+        return self.sequences * self.heads * self.head_dim * 4 * 2
+
+    def table_bytes(self):
+        return sum((n + self.tokens_per_block - 1) // self.tokens_per_block for n in self.lengths) * 4
+
+    def keys(self, i):
+        n = self.lengths[i]
+        return synth.normal(self.seed, f"k{i}", n * self.kv_width).reshape(n, self.kv_width)
+
+    def values(self, i):
+        n = self.lengths[i]
+        return synth.normal(self.seed, f"v{i}", n * self.kv_width).reshape(n, self.kv_width)
+
+    def queries(self):
+        return synth.normal(self.seed, "q", self.sequences * self.heads * self.head_dim).reshape(
+            self.sequences, self.heads * self.head_dim)
+
+    def placement(self):
+        return synth.permutation(self.seed, "blocks", self.pool_blocks)
+
+
+def decode_c1():
+    return DecodeWorkload("smollm2-135m-decode-1x512", 9, 3, 64, [512], 64, seed=1, context=2048)
+
+
+def decode_c2(sequences=64):
+    lengths = synth.integers(2, "ctx", 64, 128, 4096)[:sequences].tolist()
+    return DecodeWorkload("llama-3.2-1b-decode-64x[128,4096]", 32, 8, 64, lengths, 65536, seed=2, context=8192)
+
+
+def decode_c5(sequences=16, length=32768):
+    blocks = sequences * length // 16
+    return DecodeWorkload("llama-3-8b-q8_0-decode-16x32768", 32, 8, 128, [length] * sequences, blocks + 64, seed=5,
+                          q8=True, context=1 << 17)
+
+
+def place_blocks(cache, order):
+    """Make the pool hand out block ids in `order`: allocate every block, then
+    release them in reverse (the LIFO free list pops the last release first)."""
+    handles = {}
+    for _ in range(cache.max_blocks):
+        h = cache.allocate()
+        handles[h[0]] = h
+    for i in reversed(list(order)):
+        cache.release(handles[int(i)])
+
+
+def fill_decode(cache, w: DecodeWorkload, progress=None):
+    """Create one sequence per length and append its K/V; returns the ids."""
+    place_blocks(cache, w.placement())
+    seqs = []
+    for i in range(w.sequences):
+        s = cache.create_sequence()
+        cache.append_many(s, w.keys(i), w.values(i))
+        seqs.append(s)
+        if progress:
+            progress(i)
+    return seqs
+
+
+# ------------------------------------------------------------------- KV stress
+
+@dataclass
+class KVStress:
+    name: str
+    sequences: int = 256
+    prefix: int = 1024
+    steps: int = 128
+    max_rollback: int = 64
+    layers: int = 22
+    kv_heads: int = 8
+    head_dim: int = 64
+    tokens_per_block: int = 16
+    seed: int = 3
+
+    @property
+    def width(self):
+        return self.layers * self.kv_heads * self.head_dim
+
+    def max_blocks(self):
+        tpb = self.tokens_per_block
+        prefix_blocks = (self.prefix + tpb - 1) // tpb
+        own = (self.prefix + self.steps + tpb - 1) // tpb - self.prefix // tpb
+        return prefix_blocks + self.sequences * own + 8
+
+    def tokens(self, tag, n):
+        """n rows of `width` floats in [1, 2) (bit patterns from the stream)."""
+        bits = synth.bits(self.seed, tag, (n * self.width + 1) // 2)
+        words = np.empty(2 * bits.size, np.uint32)
+        words[0::2] = (bits & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+        words[1::2] = (bits >> np.uint64(32)).astype(np.uint32)
+        words = (words[: n * self.width] >> np.uint32(9)) | np.uint32(0x3F800000)
+        return words.view(np.float32).reshape(n, self.width)
+
+    def rollback(self):
+        return synth.integers(self.seed, "rollback", self.sequences, 0, self.max_rollback).tolist()
+
+
+def kv_c3(unaligned=False, **kw):
+    if unaligned:
+        kw.setdefault("prefix", 1025)
+    return KVStress("kv-stress-256x(1024+128)-22l" + ("-cow" if unaligned else ""), **kw)
+
+
+def run_kv_stress(cache, w: KVStress, on_phase=None):
+    """The stress on one cache; on_phase(name, seqs) is called after each phase."""
+    src = cache.create_sequence()
+    k = w.tokens("prefix-k", w.prefix)
+    v = w.tokens("prefix-v", w.prefix)
+    cache.append_many(src, k, v)
+    seqs = [cache.fork(src) for _ in range(w.sequences)]
+    cache.drop(src)
+    if on_phase:
+        on_phase("fork", seqs)
+    for step in range(w.steps):
+        k = w.tokens(f"step{step}-k", w.sequences)
+        v = w.tokens(f"step{step}-v", w.sequences)
+        cache.append_batch(seqs, k, v)
+        if on_phase:
+            on_phase(f"step{step}", seqs)
+    for s, r in zip(seqs, w.rollback()):
+        cache.truncate(s, cache.length(s) - r)
+    if on_phase:
+        on_phase("rollback", seqs)
+    return seqs
