@@ -96,9 +96,8 @@ def main():
         os.environ["TVARA_SPLIT_TOKENS"] = str(args.split_tokens)
 
     import numpy as np
-    import torch
 
-    from tvara_amd import attention, kv, workloads
+    from tvara_amd import attention, hip, kv, workloads
 
     w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5}[args.workload]()
     log(f"workload {w.name}: {w.sequences} sequences, {w.total_tokens} tokens")
@@ -108,33 +107,35 @@ def main():
     seqs = workloads.fill_decode(cache, w)
     cache.synchronize()
     log(f"filled in {time.perf_counter() - t0:.1f}s")
-    q = torch.from_numpy(w.queries()).cuda()
-    out = torch.empty_like(q)
+    q = hip.DeviceArray.from_numpy(w.queries())
+    out = hip.DeviceArray(q.shape)
     plan = attention.DecodePlan(cache, seqs, w.heads, w.context)
     log(f"plan: split {plan.split_tokens} tokens, {plan.items} work items")
     for _ in range(args.warmup):
-        plan.launch(0, q.data_ptr(), out.data_ptr())
+        plan.launch(0, q.ptr, out.ptr)
     plan.check()
-    torch.cuda.synchronize()
+    hip.synchronize()
 
+    # the timed region: K launches on the cache's stream (the null stream),
+    # bracketed by device synchronisation and HIP events on that stream
     attention.profile_reset()
     attention.profile_enable(True)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    start, stop = hip.Event(), hip.Event()
+    hip.synchronize()
     start.record()
     for _ in range(args.steps):
-        plan.launch(0, q.data_ptr(), out.data_ptr())
+        plan.launch(0, q.ptr, out.ptr)
     stop.record()
-    torch.cuda.synchronize()
+    hip.synchronize()
     attention.profile_enable(False)
     plan.check()
-    ms_per_step = start.elapsed_time(stop) / args.steps
+    ms_per_step = start.elapsed_ms(stop) / args.steps
     kern_ms, launches = attention.profile_read("paged_decode")
     merge_ms, merges = attention.profile_read("paged_decode_merge")
     kernel_avg_ms = kern_ms / max(launches, 1)
     log(f"step {ms_per_step * 1e3:.1f} us; decode kernel {kernel_avg_ms * 1e3:.1f} us x{launches}; "
         f"merge {merge_ms / max(merges, 1) * 1e3:.1f} us x{merges}")
-    assert np.isfinite(out.cpu().numpy()).all()
+    assert np.isfinite(out.numpy()).all()
 
     kv_bytes = w.kv_bytes()
     step_bytes = kv_bytes + w.qo_bytes() + w.table_bytes()
@@ -168,7 +169,6 @@ def main():
                      "algorithmic_bytes": kv_bytes + w.qo_bytes() // 2 + w.table_bytes()},
     }
     del plan, cache, q, out
-    torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
         result["cpu_baseline"] = cpu_baseline(w)

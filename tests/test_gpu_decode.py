@@ -52,16 +52,16 @@ def test_c2_llama32_batch(device, oracle):
     want = oracle_rows(ref, seqs, q, w)
     assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
     # the same through a resident plan on device buffers, launched twice
-    import torch
+    from tvara_amd import hip
 
     plan = attention.DecodePlan(dev, seqs, w.heads, w.context)
-    dq = torch.from_numpy(q).cuda()
-    out = torch.empty_like(dq)
+    dq = hip.DeviceArray.from_numpy(q)
+    out = hip.DeviceArray(q.shape)
     for _ in range(2):
-        out.zero_()
-        plan.launch(0, dq.data_ptr(), out.data_ptr())
+        out.zero()
+        plan.launch(0, dq.ptr, out.ptr)
         plan.check()
-        assert np.array_equal(out.cpu().numpy(), got)
+        assert np.array_equal(out.numpy(), got)
 
 
 def _single(device, oracle, heads, kv_heads, dim, tpb, length, seed, tail=False, visible=None, fmt=None,
@@ -184,11 +184,11 @@ def test_rejections(device):
     assert np.isfinite(attention.fused_paged_attention(q, dev, s, 0, 4, 64)).all()
     plan = attention.DecodePlan(dev, [s], 4, 64)
     dev.append(s, x[0], x[0])
-    import torch
+    from tvara_amd import hip
 
-    dq = torch.from_numpy(q).cuda()
+    dq = hip.DeviceArray.from_numpy(q)
     with pytest.raises(device.InvalidArgument):  # the cache changed under the plan
-        plan.launch(0, dq.data_ptr(), dq.data_ptr())
+        plan.launch(0, dq.ptr, dq.ptr)
 
 
 def test_huge_scores_stay_finite(device, oracle):
