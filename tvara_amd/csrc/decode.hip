@@ -19,6 +19,9 @@
 //
 // Splits are merged by log-sum-exp in merge_kernel.  A non-finite score sets
 // *err, matching OnlineAttention::update's rejection (attention.hpp:11).
+#include <algorithm>
+#include <cstdlib>
+
 #include "common.hpp"
 #include "q8.hpp"
 
@@ -118,47 +121,62 @@ __device__ __forceinline__ float softmax_step(float s, bool own, int lane, RowSt
 
 // Reduce the token groups of a wave and write the split's result: the
 // normalised output when the row has one split, otherwise the partial
-// (acc, m, l) for merge_kernel.  `col(h, e4)` is the head-local column of the
-// lane's e4-th float4.
+// (acc, m, l).  The last workgroup to finish a row's splits (an atomic count
+// per row and KV-head group, after a device-scope release of the partials)
+// merges them by log-sum-exp and resets the count for the next launch.
+// `col(c, e4)` is the head-local column of lane slot c's e4-th float4.
 template <int D, int G, int LPT, int E, class Col>
 __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G][E], RowState& st, int lane, int wave,
-                                             int nwaves, int kh, int item, int row, int nsplit, Col col) {
-    constexpr int TT = 64 / LPT;
+                                             int nwaves, int kh, int item, int row, int nsplit, int first_item,
+                                             Col col) {
     extern __shared__ float lds[];
-    const int c = lane & (LPT - 1), tg = lane / LPT;
+    __shared__ int last_split;
+    const int c = lane & (LPT - 1);
     st.l = wave_sum_across(st.l, LPT);
-    float* red = lds + static_cast<size_t>(wave) * 64 * G * E;
-    float* ml = lds + static_cast<size_t>(nwaves) * 64 * G * E + wave * 2 * G;
+    // token groups sharing a 16-lane row are summed with DPP row rotates, so
+    // only the four row sums go through LDS
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int e4 = 0; e4 < E / 4; ++e4)
-            *reinterpret_cast<float4*>(red + (tg * G + h) * D + col(c, e4)) =
-                make_float4(acc[h][4 * e4], acc[h][4 * e4 + 1], acc[h][4 * e4 + 2], acc[h][4 * e4 + 3]);
-    if (tg == 0 && c < G) {
+        for (int e = 0; e < E; ++e) {
+            float v = acc[h][e];
+            v += dpp<0x128>(v);             // row_ror:8
+            if constexpr (LPT == 4) v += dpp<0x124>(v);  // row_ror:4
+            acc[h][e] = v;
+        }
+    float* red = lds + static_cast<size_t>(wave) * 4 * G * D;
+    float* ml = lds + static_cast<size_t>(nwaves) * 4 * G * D + wave * 2 * G;
+    if ((lane & 15) < LPT) {
+        const int row = lane >> 4;
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int e4 = 0; e4 < E / 4; ++e4)
+                *reinterpret_cast<float4*>(red + (row * G + h) * D + col(c, e4)) =
+                    make_float4(acc[h][4 * e4], acc[h][4 * e4 + 1], acc[h][4 * e4 + 2], acc[h][4 * e4 + 3]);
+    }
+    if (lane < G) {
         ml[c] = st.m;
         ml[G + c] = st.l;
     }
     __syncthreads();
     const size_t head0 = static_cast<size_t>(kh) * G;
+    float* out = a.out + (static_cast<size_t>(row) * a.heads + head0) * D;
     for (int o4 = lane; o4 < G * D / 4; o4 += 64) {
         float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
+        for (int t = 0; t < 4; ++t) {
             const float4 x = *reinterpret_cast<const float4*>(red + t * G * D + 4 * o4);
             sum.x += x.x;
             sum.y += x.y;
             sum.z += x.z;
             sum.w += x.w;
         }
-        const int h = (4 * o4) / D;
         if (nsplit == 1) {
-            const float l = ml[G + h];
-            float* o = a.out + (static_cast<size_t>(row) * a.heads + head0) * D + 4 * o4;
-            *reinterpret_cast<float4*>(o) = make_float4(sum.x / l, sum.y / l, sum.z / l, sum.w / l);
+            const float l = ml[G + (4 * o4) / D];
+            *reinterpret_cast<float4*>(out + 4 * o4) = make_float4(sum.x / l, sum.y / l, sum.z / l, sum.w / l);
         } else {
-            float* o = a.part_acc + (static_cast<size_t>(item) * a.heads + head0) * D + 4 * o4;
-            *reinterpret_cast<float4*>(o) = sum;
+            *reinterpret_cast<float4*>(a.part_acc + (static_cast<size_t>(item) * a.heads + head0) * D + 4 * o4) = sum;
         }
     }
     if (nsplit > 1 && lane < G) {
@@ -167,12 +185,42 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
         o[1] = ml[G + lane];
     }
     if (__any(st.bad) && lane == 0) *a.err = 1;
+    if (nsplit == 1) return;
+    const int groups = a.lay.kv_heads / nwaves;
+    int* count = a.counters + static_cast<size_t>(row) * groups + kh / nwaves;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last_split = atomicAdd(count, 1) == nsplit - 1;
+    __syncthreads();
+    if (!last_split) return;
+    __threadfence();
+    const size_t step = static_cast<size_t>(a.heads);
+    for (int o4 = lane; o4 < G * D / 4; o4 += 64) {
+        const size_t h = head0 + (4 * o4) / D;
+        const float* pm = a.part_ml + (static_cast<size_t>(first_item) * step + h) * 2;
+        float M = -INFINITY;
+        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pm[s * step * 2]);
+        float L = 0.f;
+        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float* pa = a.part_acc + (static_cast<size_t>(first_item) * step + head0) * D + 4 * o4;
+        for (int s = 0; s < nsplit; ++s) {
+            const float w = fast_exp2(pm[s * step * 2] - M);
+            L = fmaf(w, pm[s * step * 2 + 1], L);
+            const float4 x = *reinterpret_cast<const float4*>(pa + s * step * D);
+            O.x = fmaf(w, x.x, O.x);
+            O.y = fmaf(w, x.y, O.y);
+            O.z = fmaf(w, x.z, O.z);
+            O.w = fmaf(w, x.w, O.w);
+        }
+        *reinterpret_cast<float4*>(out + 4 * o4) = make_float4(O.x / L, O.y / L, O.z / L, O.w / L);
+    }
+    if (threadIdx.x == 0) *count = 0;
 }
 
 // ------------------------------------------------------------- f32 blocks
 
 template <int D, int G, int LPT>
-__global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
     constexpr int E = D / LPT, NV = E / 4, TT = 64 / LPT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int groups = a.lay.kv_heads / nwaves;
@@ -214,8 +262,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs a) {
     const size_t koff = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D + 4 * c;
     const size_t voff = koff + 16 * static_cast<size_t>(kvw);
 
-    auto load = [&](int tb, float4 (&kk)[NV], float4 (&vv)[NV]) -> bool {
-        const bool ok = tb + tg < t1;
+    auto load = [&](int tb, float4 (&kk)[NV], float4 (&vv)[NV], bool ok) {
         const int bid = tab[tb >> 4];
         const float* base = pool + static_cast<size_t>(bid) * bstride + static_cast<size_t>((tb & 15) + tg) * kvw;
 #pragma unroll
@@ -223,7 +270,6 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs a) {
             kk[m] = ok ? *reinterpret_cast<const float4*>(base + koff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
             vv[m] = ok ? *reinterpret_cast<const float4*>(base + voff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        return ok;
     };
     auto process = [&](const float4 (&kk)[NV], const float4 (&vv)[NV], bool ok) {
         float part[LPT];
@@ -256,18 +302,24 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs a) {
         }
     };
 
-    // two tiles in flight: tile t+2 is requested as soon as tile t is consumed
+    // Full tiles stream with two in flight (tile i+2 is requested as soon as
+    // tile i is consumed) and unmasked loads; a partial last tile is masked.
+    const int nfull = max(t1 - t0, 0) / TT;
     float4 ka[NV], va[NV], kb[NV], vb[NV];
-    bool oka = false, okb = false;
-    if (t0 < t1) oka = load(t0, ka, va);
-    if (t0 + TT < t1) okb = load(t0 + TT, kb, vb);
-    for (int t = t0; t < t1; t += 2 * TT) {
-        process(ka, va, oka);
-        if (t + 2 * TT < t1) oka = load(t + 2 * TT, ka, va);
-        if (t + TT < t1) {
-            process(kb, vb, okb);
-            if (t + 3 * TT < t1) okb = load(t + 3 * TT, kb, vb);
+    if (nfull > 0) load(t0, ka, va, true);
+    if (nfull > 1) load(t0 + TT, kb, vb, true);
+    for (int i = 0; i < nfull; i += 2) {
+        process(ka, va, true);
+        if (i + 2 < nfull) load(t0 + (i + 2) * TT, ka, va, true);
+        if (i + 1 < nfull) {
+            process(kb, vb, true);
+            if (i + 3 < nfull) load(t0 + (i + 3) * TT, kb, vb, true);
         }
+    }
+    if (t0 + nfull * TT < t1) {
+        const bool ok = t0 + nfull * TT + tg < t1;
+        load(t0 + nfull * TT, ka, va, ok);
+        process(ka, va, ok);
     }
     if (tail) {  // the current token's uncommitted K/V is the last position (attention.hpp:80)
         const bool ok = tg == 0;
@@ -280,7 +332,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(const DecodeArgs a) {
         }
         process(ka, va, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit, en.w,
                                [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
 }
 
@@ -298,7 +350,7 @@ __device__ __forceinline__ void unpack_i8(uint4 w, float (&f)[16]) {
 // Each lane owns 16 consecutive columns (one dwordx4 of int8) = half a Q8_0
 // group, so a token's row of head_dim columns is LPT = head_dim/16 lanes.
 template <int D, int G>
-__global__ __launch_bounds__(256) void decode_q8_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
     constexpr int LPT = D / 16, TT = 64 / LPT, E = 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int groups = a.lay.kv_heads / nwaves;
@@ -347,12 +399,12 @@ __global__ __launch_bounds__(256) void decode_q8_kernel(const DecodeArgs a) {
         uint16_t ks, vs;
         bool ok;
     };
-    auto load = [&](int tb, Tile& x) {
-        x.ok = tb + tg < t1;
+    auto load = [&](int tb, Tile& x, bool ok) {
+        x.ok = ok;
         const int bid = tab[tb >> 4];
         const int slot = (tb & 15) + tg;
         const char* base = a.pool + static_cast<size_t>(bid) * a.lay.stride;
-        if (x.ok) {
+        if (ok) {
             x.kq = *reinterpret_cast<const uint4*>(base + ksec + static_cast<size_t>(slot) * kvw + qcol);
             x.vq = *reinterpret_cast<const uint4*>(base + vsec + static_cast<size_t>(slot) * kvw + qcol);
             x.ks = *reinterpret_cast<const uint16_t*>(base + ksec + plane + (static_cast<size_t>(slot) * gpr + scol) * 2);
@@ -389,17 +441,21 @@ __global__ __launch_bounds__(256) void decode_q8_kernel(const DecodeArgs a) {
         process_f(kf, half_bits_to_float(x.ks), vf, half_bits_to_float(x.vs), x.ok);
     };
 
+    const int nfull = max(t1 - t0, 0) / TT;
     Tile ta, tb2;
-    ta.ok = tb2.ok = false;
-    if (t0 < t1) load(t0, ta);
-    if (t0 + TT < t1) load(t0 + TT, tb2);
-    for (int t = t0; t < t1; t += 2 * TT) {
+    if (nfull > 0) load(t0, ta, true);
+    if (nfull > 1) load(t0 + TT, tb2, true);
+    for (int i = 0; i < nfull; i += 2) {
         process(ta);
-        if (t + 2 * TT < t1) load(t + 2 * TT, ta);
-        if (t + TT < t1) {
+        if (i + 2 < nfull) load(t0 + (i + 2) * TT, ta, true);
+        if (i + 1 < nfull) {
             process(tb2);
-            if (t + 3 * TT < t1) load(t + 3 * TT, tb2);
+            if (i + 3 < nfull) load(t0 + (i + 3) * TT, tb2, true);
         }
+    }
+    if (t0 + nfull * TT < t1) {
+        load(t0 + nfull * TT, ta, t0 + nfull * TT + tg < t1);
+        process(ta);
     }
     if (tail) {  // the uncommitted token arrives as f32
         const bool ok = tg == 0;
@@ -413,7 +469,7 @@ __global__ __launch_bounds__(256) void decode_q8_kernel(const DecodeArgs a) {
         }
         process_f(kf, 1.f, vf, 1.f, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit, en.w,
                                [](int cc, int e4) { return 16 * cc + 4 * e4; });
 }
 
@@ -535,14 +591,14 @@ __global__ __launch_bounds__(64) void merge_kernel(const DecodeArgs a) {
 
 template <int D, int G, int LPT>
 void launch_f32(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
-    const size_t lds = (static_cast<size_t>(waves) * 64 * G * (D / LPT) + waves * 2 * G) * sizeof(float);
+    const size_t lds = (static_cast<size_t>(waves) * 4 * G * D + waves * 2 * G) * sizeof(float);
     hipLaunchKernelGGL((decode_f32_kernel<D, G, LPT>), dim3(nitems * (a.lay.kv_heads / waves)), dim3(64 * waves), lds,
                        s, a);
 }
 
 template <int D, int G>
 void launch_q8(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
-    const size_t lds = (static_cast<size_t>(waves) * 64 * G * 16 + waves * 2 * G) * sizeof(float);
+    const size_t lds = (static_cast<size_t>(waves) * 4 * G * D + waves * 2 * G) * sizeof(float);
     hipLaunchKernelGGL((decode_q8_kernel<D, G>), dim3(nitems * (a.lay.kv_heads / waves)), dim3(64 * waves), lds, s, a);
 }
 
@@ -596,8 +652,12 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
 // workgroups take the KV-head groups of one work item, so the waves reading a
 // block's slot rows run close together.
 int decode_waves(int kv_heads, int group) {
-    if (group > 4) return 1;
-    return kv_heads % 2 ? 1 : 2;
+    int w = 4;
+    if (const char* env = std::getenv("TVARA_DECODE_WAVES")) w = std::atoi(env);
+    if (group > 4) w = std::min(w, 2);
+    w = std::max(1, std::min(w, 8));
+    while (w > 1 && kv_heads % w) w /= 2;
+    return w;
 }
 
 static int waves_for(const DecodeArgs& a) { return decode_waves(a.lay.kv_heads, a.group); }
@@ -609,20 +669,21 @@ bool decode_fast_path(const DecodeArgs& a) {
 
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, hipStream_t s) {
     if (nitems <= 0) return;
+    bool fused = false;  // the fast kernels merge their own splits
     {
         ProfileScope p("paged_decode", s);
-        bool done = false;
         if (decode_fast_path(a)) {
             const int waves = waves_for(a);
-            done = a.lay.head_dim == 64 ? dispatch_fast<64>(a, nitems, waves, s) : dispatch_fast<128>(a, nitems, waves, s);
+            fused = a.lay.head_dim == 64 ? dispatch_fast<64>(a, nitems, waves, s)
+                                         : dispatch_fast<128>(a, nitems, waves, s);
         }
-        if (!done) {
+        if (!fused) {
             if (a.lay.head_dim > kGenericMaxDim) throw std::invalid_argument("head_dim above 512 is not supported");
             hipLaunchKernelGGL(decode_generic_kernel, dim3(nitems, a.heads), dim3(64), 0, s, a);
         }
         TVARA_HIP(hipGetLastError());
     }
-    if (need_merge) {
+    if (need_merge && !fused) {
         ProfileScope p("paged_decode_merge", s);
         hipLaunchKernelGGL(merge_kernel, dim3(nrows, a.heads), dim3(64), 0, s, a);
         TVARA_HIP(hipGetLastError());
