@@ -69,7 +69,6 @@ struct DecodeArgs {
     float* out;
     float* part_acc;  // [items][heads][head_dim]
     float* part_ml;   // [items][heads][2]: running max (log2 units), normaliser
-    int* counters;    // [rows][kv head groups]: finished splits, back to 0 after the merge
     float qscale;     // log2(e)/sqrt(head_dim)
     int* err;
 };

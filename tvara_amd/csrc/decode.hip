@@ -121,16 +121,15 @@ __device__ __forceinline__ float softmax_step(float s, bool own, int lane, RowSt
 
 // Reduce the token groups of a wave and write the split's result: the
 // normalised output when the row has one split, otherwise the partial
-// (acc, m, l).  The last workgroup to finish a row's splits (an atomic count
-// per row and KV-head group, after a device-scope release of the partials)
-// merges them by log-sum-exp and resets the count for the next launch.
-// `col(c, e4)` is the head-local column of lane slot c's e4-th float4.
+// (acc, m, l) that merge_kernel combines.  (Merging in the last workgroup to
+// finish a row needs a device-scope release per workgroup; on gfx950 each one
+// writes back the XCD's L2 and they serialise, which costs far more than a
+// second launch.)  `col(c, e4)` is the head-local column of lane slot c's
+// e4-th float4.
 template <int D, int G, int LPT, int E, class Col>
 __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G][E], RowState& st, int lane, int wave,
-                                             int nwaves, int kh, int item, int row, int nsplit, int first_item,
-                                             Col col) {
+                                             int nwaves, int kh, int item, int row, int nsplit, Col col) {
     extern __shared__ float lds[];
-    __shared__ int last_split;
     const int c = lane & (LPT - 1);
     st.l = wave_sum_across(st.l, LPT);
     // token groups sharing a 16-lane row are summed with DPP row rotates, so
@@ -185,36 +184,6 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
         o[1] = ml[G + lane];
     }
     if (__any(st.bad) && lane == 0) *a.err = 1;
-    if (nsplit == 1) return;
-    const int groups = a.lay.kv_heads / nwaves;
-    int* count = a.counters + static_cast<size_t>(row) * groups + kh / nwaves;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last_split = atomicAdd(count, 1) == nsplit - 1;
-    __syncthreads();
-    if (!last_split) return;
-    __threadfence();
-    const size_t step = static_cast<size_t>(a.heads);
-    for (int o4 = lane; o4 < G * D / 4; o4 += 64) {
-        const size_t h = head0 + (4 * o4) / D;
-        const float* pm = a.part_ml + (static_cast<size_t>(first_item) * step + h) * 2;
-        float M = -INFINITY;
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pm[s * step * 2]);
-        float L = 0.f;
-        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float* pa = a.part_acc + (static_cast<size_t>(first_item) * step + head0) * D + 4 * o4;
-        for (int s = 0; s < nsplit; ++s) {
-            const float w = fast_exp2(pm[s * step * 2] - M);
-            L = fmaf(w, pm[s * step * 2 + 1], L);
-            const float4 x = *reinterpret_cast<const float4*>(pa + s * step * D);
-            O.x = fmaf(w, x.x, O.x);
-            O.y = fmaf(w, x.y, O.y);
-            O.z = fmaf(w, x.z, O.z);
-            O.w = fmaf(w, x.w, O.w);
-        }
-        *reinterpret_cast<float4*>(out + 4 * o4) = make_float4(O.x / L, O.y / L, O.z / L, O.w / L);
-    }
-    if (threadIdx.x == 0) *count = 0;
 }
 
 // ------------------------------------------------------------- f32 blocks
@@ -332,7 +301,7 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
         }
         process(ka, va, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit, en.w,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
                                [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
 }
 
@@ -469,7 +438,7 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
         }
         process_f(kf, 1.f, vf, 1.f, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit, en.w,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
                                [](int cc, int e4) { return 16 * cc + 4 * e4; });
 }
 
@@ -565,28 +534,39 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(const DecodeArgs a) 
 
 // ---------------------------------------------------------- split merge
 
+// Log-sum-exp merge of a row's split partials, one wave per (row, head):
+// lanes first hold one split each for the maxima and normalisers, then one
+// column each while every split's partial is loaded back to back.
 __global__ __launch_bounds__(64) void merge_kernel(const DecodeArgs a) {
     const int row = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int4 en = a.entries[row];
     const int nsplit = en.z >> 1;
     if (nsplit <= 1) return;
     const int D = a.lay.head_dim;
-    const float* ml = a.part_ml + (static_cast<size_t>(en.w) * a.heads + h) * 2;
-    const size_t mstep = static_cast<size_t>(a.heads) * 2;
+    const size_t step = static_cast<size_t>(a.heads);
+    const float* ml = a.part_ml + (static_cast<size_t>(en.w) * step + h) * 2;
+    const float* pa = a.part_acc + (static_cast<size_t>(en.w) * step + h) * D;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[s * mstep]);
+    for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, ml[s * step * 2]);
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
     float L = 0.f;
-    float acc[kGenericMaxDim / 64];
-    for (int i = 0; i < kGenericMaxDim / 64; ++i) acc[i] = 0.f;
-    const float* pa = a.part_acc + (static_cast<size_t>(en.w) * a.heads + h) * D;
-    const size_t astep = static_cast<size_t>(a.heads) * D;
-    for (int s = 0; s < nsplit; ++s) {
-        const float w = exp2f(ml[s * mstep] - M);
-        L = fmaf(w, ml[s * mstep + 1], L);
-        for (int i = 0; i * 64 + lane < D; ++i) acc[i] = fmaf(w, pa[s * astep + i * 64 + lane], acc[i]);
-    }
+    for (int s = lane; s < nsplit; s += 64) L += fast_exp2(ml[s * step * 2] - M) * ml[s * step * 2 + 1];
+    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
     float* o = a.out + (static_cast<size_t>(row) * a.heads + h) * D;
-    for (int i = 0; i * 64 + lane < D; ++i) o[i * 64 + lane] = acc[i] / L;
+    for (int d = lane; d < D; d += 64) {
+        float acc = 0.f;
+        int s = 0;
+        for (; s + 4 <= nsplit; s += 4) {
+            const float x0 = pa[(s + 0) * step * D + d], x1 = pa[(s + 1) * step * D + d];
+            const float x2 = pa[(s + 2) * step * D + d], x3 = pa[(s + 3) * step * D + d];
+            acc = fmaf(fast_exp2(ml[(s + 0) * step * 2] - M), x0, acc);
+            acc = fmaf(fast_exp2(ml[(s + 1) * step * 2] - M), x1, acc);
+            acc = fmaf(fast_exp2(ml[(s + 2) * step * 2] - M), x2, acc);
+            acc = fmaf(fast_exp2(ml[(s + 3) * step * 2] - M), x3, acc);
+        }
+        for (; s < nsplit; ++s) acc = fmaf(fast_exp2(ml[s * step * 2] - M), pa[s * step * D + d], acc);
+        o[d] = acc / L;
+    }
 }
 
 template <int D, int G, int LPT>
@@ -669,21 +649,21 @@ bool decode_fast_path(const DecodeArgs& a) {
 
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, hipStream_t s) {
     if (nitems <= 0) return;
-    bool fused = false;  // the fast kernels merge their own splits
     {
         ProfileScope p("paged_decode", s);
+        bool done = false;
         if (decode_fast_path(a)) {
             const int waves = waves_for(a);
-            fused = a.lay.head_dim == 64 ? dispatch_fast<64>(a, nitems, waves, s)
-                                         : dispatch_fast<128>(a, nitems, waves, s);
+            done = a.lay.head_dim == 64 ? dispatch_fast<64>(a, nitems, waves, s)
+                                        : dispatch_fast<128>(a, nitems, waves, s);
         }
-        if (!fused) {
+        if (!done) {
             if (a.lay.head_dim > kGenericMaxDim) throw std::invalid_argument("head_dim above 512 is not supported");
             hipLaunchKernelGGL(decode_generic_kernel, dim3(nitems, a.heads), dim3(64), 0, s, a);
         }
         TVARA_HIP(hipGetLastError());
     }
-    if (need_merge && !fused) {
+    if (need_merge) {
         ProfileScope p("paged_decode_merge", s);
         hipLaunchKernelGGL(merge_kernel, dim3(nrows, a.heads), dim3(64), 0, s, a);
         TVARA_HIP(hipGetLastError());

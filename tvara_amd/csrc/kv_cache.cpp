@@ -566,9 +566,6 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     if (need_merge) {
         part_acc.ensure(static_cast<size_t>(items) * heads * g.head_dim * sizeof(float));
         part_ml.ensure(static_cast<size_t>(items) * heads * 2 * sizeof(float));
-        const size_t n = static_cast<size_t>(rows) * g.kv_heads * sizeof(int);
-        counters.ensure(n);
-        TVARA_HIP(hipMemset(counters.ptr, 0, n));
     }
     err.ensure(sizeof(int));
     TVARA_HIP(hipMemset(err.ptr, 0, sizeof(int)));
@@ -596,7 +593,6 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.out = out;
     a.part_acc = static_cast<float*>(part_acc.ptr);
     a.part_ml = static_cast<float*>(part_ml.ptr);
-    a.counters = static_cast<int*>(counters.ptr);
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
     a.err = static_cast<int*>(err.ptr);
     launch_decode(a, items, rows, need_merge, s);

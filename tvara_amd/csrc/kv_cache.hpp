@@ -138,7 +138,7 @@ struct AttnPlan {
     int rows = 0, heads = 0, group = 0, items = 0, split_tokens = 0;
     bool need_merge = false, with_tail = false;
     size_t kv_bytes = 0;  // algorithmic K/V bytes one launch reads
-    DeviceBuffer tables, entries, items_buf, part_acc, part_ml, counters, err;
+    DeviceBuffer tables, entries, items_buf, part_acc, part_ml, err;
     // Builds the plan for rows reading `cached[r]` tokens of `seq_of_row[r]`,
     // followed by the row's uncommitted tail token when tail_rows[r] != 0.
     void build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, const std::vector<size_t>& cached,
