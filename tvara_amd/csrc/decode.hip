@@ -37,6 +37,9 @@ __device__ __forceinline__ float dpp(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// K/V rows (non-temporal loads measured no faster on MI355X)
+__device__ __forceinline__ float4 stream_load(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
 // Transpose-reduce: lane c of every LPT-lane group returns the sum over the
 // group of v[c].  Pairings use DPP (quad permutes, half-row mirror).
 template <int LPT>
@@ -188,7 +191,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
 
 // ------------------------------------------------------------- f32 blocks
 
-template <int D, int G, int LPT>
+template <int D, int G, int LPT, int NB>
 __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
     constexpr int E = D / LPT, NV = E / 4, TT = 64 / LPT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
@@ -236,8 +239,8 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
         const float* base = pool + static_cast<size_t>(bid) * bstride + static_cast<size_t>((tb & 15) + tg) * kvw;
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
-            kk[m] = ok ? *reinterpret_cast<const float4*>(base + koff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
-            vv[m] = ok ? *reinterpret_cast<const float4*>(base + voff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+            kk[m] = ok ? stream_load(base + koff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+            vv[m] = ok ? stream_load(base + voff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     auto process = [&](const float4 (&kk)[NV], const float4 (&vv)[NV], bool ok) {
@@ -271,20 +274,24 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
         }
     };
 
-    // Full tiles stream with two in flight (tile i+2 is requested as soon as
+    // Full tiles stream with NB in flight (tile i+NB is requested as soon as
     // tile i is consumed) and unmasked loads; a partial last tile is masked.
     const int nfull = max(t1 - t0, 0) / TT;
-    float4 ka[NV], va[NV], kb[NV], vb[NV];
-    if (nfull > 0) load(t0, ka, va, true);
-    if (nfull > 1) load(t0 + TT, kb, vb, true);
-    for (int i = 0; i < nfull; i += 2) {
-        process(ka, va, true);
-        if (i + 2 < nfull) load(t0 + (i + 2) * TT, ka, va, true);
-        if (i + 1 < nfull) {
-            process(kb, vb, true);
-            if (i + 3 < nfull) load(t0 + (i + 3) * TT, kb, vb, true);
+    float4 kbuf[NB][NV], vbuf[NB][NV];
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+        if (j < nfull) load(t0 + j * TT, kbuf[j], vbuf[j], true);
+    for (int i = 0; i < nfull; i += NB) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            if (i + j < nfull) {
+                process(kbuf[j], vbuf[j], true);
+                if (i + j + NB < nfull) load(t0 + (i + j + NB) * TT, kbuf[j], vbuf[j], true);
+            }
         }
     }
+    float4 (&ka)[NV] = kbuf[0];
+    float4 (&va)[NV] = vbuf[0];
     if (t0 + nfull * TT < t1) {
         const bool ok = t0 + nfull * TT + tg < t1;
         load(t0 + nfull * TT, ka, va, ok);
@@ -534,9 +541,12 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(const DecodeArgs a) 
 
 // ---------------------------------------------------------- split merge
 
-// Log-sum-exp merge of a row's split partials, one wave per (row, head):
-// lanes first hold one split each for the maxima and normalisers, then one
-// column each while every split's partial is loaded back to back.
+// Log-sum-exp merge of a row's split partials, one wave per (row, head).
+// Lane s holds split s's maximum and normaliser; every split's partial column
+// is requested before any arithmetic waits, so the merge costs about one
+// memory round trip.
+constexpr int kMergeSplits = 32;
+
 __global__ __launch_bounds__(64) void merge_kernel(const DecodeArgs a) {
     const int row = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int4 en = a.entries[row];
@@ -546,25 +556,41 @@ __global__ __launch_bounds__(64) void merge_kernel(const DecodeArgs a) {
     const size_t step = static_cast<size_t>(a.heads);
     const float* ml = a.part_ml + (static_cast<size_t>(en.w) * step + h) * 2;
     const float* pa = a.part_acc + (static_cast<size_t>(en.w) * step + h) * D;
+    float* o = a.out + (static_cast<size_t>(row) * a.heads + h) * D;
+    if (nsplit <= kMergeSplits && nsplit <= 64 && D <= 128) {
+        float x[2][kMergeSplits];
+#pragma unroll
+        for (int s = 0; s < kMergeSplits; ++s)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                x[i][s] = (s < nsplit && lane + 64 * i < D) ? pa[s * step * D + lane + 64 * i] : 0.f;
+        const float ms = lane < nsplit ? ml[lane * step * 2] : -INFINITY;
+        const float ls = lane < nsplit ? ml[lane * step * 2 + 1] : 0.f;
+        float M = ms;
+        for (int k = 32; k >= 1; k >>= 1) M = fmaxf(M, __shfl_xor(M, k));
+        const float ws = lane < nsplit ? fast_exp2(ms - M) : 0.f;
+        float L = ws * ls;
+        for (int k = 32; k >= 1; k >>= 1) L += __shfl_xor(L, k);
+        float acc[2] = {0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < kMergeSplits; ++s) {
+            const float w = __shfl(ws, s);
+            acc[0] = fmaf(w, x[0][s], acc[0]);
+            acc[1] = fmaf(w, x[1][s], acc[1]);
+        }
+        for (int i = 0; i < 2; ++i)
+            if (lane + 64 * i < D) o[lane + 64 * i] = acc[i] / L;
+        return;
+    }
     float M = -INFINITY;
     for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, ml[s * step * 2]);
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    for (int k = 32; k >= 1; k >>= 1) M = fmaxf(M, __shfl_xor(M, k));
     float L = 0.f;
     for (int s = lane; s < nsplit; s += 64) L += fast_exp2(ml[s * step * 2] - M) * ml[s * step * 2 + 1];
-    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
-    float* o = a.out + (static_cast<size_t>(row) * a.heads + h) * D;
+    for (int k = 32; k >= 1; k >>= 1) L += __shfl_xor(L, k);
     for (int d = lane; d < D; d += 64) {
         float acc = 0.f;
-        int s = 0;
-        for (; s + 4 <= nsplit; s += 4) {
-            const float x0 = pa[(s + 0) * step * D + d], x1 = pa[(s + 1) * step * D + d];
-            const float x2 = pa[(s + 2) * step * D + d], x3 = pa[(s + 3) * step * D + d];
-            acc = fmaf(fast_exp2(ml[(s + 0) * step * 2] - M), x0, acc);
-            acc = fmaf(fast_exp2(ml[(s + 1) * step * 2] - M), x1, acc);
-            acc = fmaf(fast_exp2(ml[(s + 2) * step * 2] - M), x2, acc);
-            acc = fmaf(fast_exp2(ml[(s + 3) * step * 2] - M), x3, acc);
-        }
-        for (; s < nsplit; ++s) acc = fmaf(fast_exp2(ml[s * step * 2] - M), pa[s * step * D + d], acc);
+        for (int s = 0; s < nsplit; ++s) acc = fmaf(fast_exp2(ml[s * step * 2] - M), pa[s * step * D + d], acc);
         o[d] = acc / L;
     }
 }
@@ -572,8 +598,10 @@ __global__ __launch_bounds__(64) void merge_kernel(const DecodeArgs a) {
 template <int D, int G, int LPT>
 void launch_f32(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
     const size_t lds = (static_cast<size_t>(waves) * 4 * G * D + waves * 2 * G) * sizeof(float);
-    hipLaunchKernelGGL((decode_f32_kernel<D, G, LPT>), dim3(nitems * (a.lay.kv_heads / waves)), dim3(64 * waves), lds,
-                       s, a);
+    const dim3 grid(nitems * (a.lay.kv_heads / waves)), block(64 * waves);
+    // two tiles in flight: a third needs more than the 256 VGPRs that keep two
+    // waves per SIMD, and measured slower
+    hipLaunchKernelGGL((decode_f32_kernel<D, G, LPT, 2>), grid, block, lds, s, a);
 }
 
 template <int D, int G>
@@ -627,10 +655,11 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
 
 }  // namespace
 
-// Waves per workgroup: two KV heads (32 KiB of LDS for the end-of-split
-// reduction when G <= 4) when kv_heads is even, else one.  Consecutive
-// workgroups take the KV-head groups of one work item, so the waves reading a
-// block's slot rows run close together.
+// Waves per workgroup (one per KV head): four when kv_heads allows (measured
+// best for GQA 32/8 on MI355X: a workgroup streams 1 KiB of every 2 KiB slot
+// row), at most two for groups above four query heads.  Consecutive
+// workgroups take the KV-head groups of one work item.  TVARA_DECODE_WAVES
+// overrides it for tuning.
 int decode_waves(int kv_heads, int group) {
     int w = 4;
     if (const char* env = std::getenv("TVARA_DECODE_WAVES")) w = std::atoi(env);

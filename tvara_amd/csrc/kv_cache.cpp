@@ -528,14 +528,15 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     }
     if (tab.size() > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
         throw std::invalid_argument("attention batch too large");
-    // split length: enough work items to give every CU several workgroups
+    // split length: about 1,536 workgroups per launch, six per CU (measured
+    // best on the 64-sequence Llama-3.2-1B batch: 192 tokens)
     size_t split = split_override;
     if (!split) {
         if (const char* env = std::getenv("TVARA_SPLIT_TOKENS")) split = std::strtoull(env, nullptr, 10);
     }
     if (!split) {
         const size_t groups = g.kv_heads / static_cast<size_t>(decode_waves(static_cast<int>(g.kv_heads), group));
-        split = round_up(std::max<size_t>(1, total * groups / 2048), 16);
+        split = round_up(std::max<size_t>(1, total * groups / 1536), 16);
         split = std::clamp<size_t>(split, 64, 4096);
     }
     split = round_up(std::max<size_t>(split, 16), 16);
