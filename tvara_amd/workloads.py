@@ -119,6 +119,68 @@ def fill_decode(cache, w: DecodeWorkload, progress=None):
     return seqs
 
 
+# ------------------------------------------------------------------- prefill
+
+@dataclass
+class PrefillWorkload:
+    """Chunked prefill: each sequence holds `prefix` cached tokens plus a
+    `chunk`-token causal chunk whose K/V are appended first; chunk row i sees
+    positions 0 .. prefix+i."""
+    name: str
+    sequences: int = 8
+    prefix: int = 2048
+    chunk: int = 512
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 64
+    tokens_per_block: int = 16
+    seed: int = 4
+    context: int = 8192
+
+    @property
+    def kv_width(self):
+        return self.kv_heads * self.head_dim
+
+    @property
+    def total(self):
+        return self.prefix + self.chunk
+
+    def pool_blocks(self):
+        return self.sequences * ((self.total + self.tokens_per_block - 1) // self.tokens_per_block) + 8
+
+    def keys(self, i):
+        return synth.normal(self.seed, f"k{i}", self.total * self.kv_width).reshape(self.total, self.kv_width)
+
+    def values(self, i):
+        return synth.normal(self.seed, f"v{i}", self.total * self.kv_width).reshape(self.total, self.kv_width)
+
+    def chunk_queries(self, i):
+        n = self.chunk * self.heads * self.head_dim
+        return synth.normal(self.seed, f"q{i}", n).reshape(self.chunk, self.heads * self.head_dim)
+
+    def flops(self):
+        """QK^T and PV multiply-adds over the causal chunk, 2 flops each."""
+        pairs = self.chunk * self.prefix + self.chunk * (self.chunk + 1) // 2
+        return 4 * self.head_dim * pairs * self.heads * self.sequences
+
+    def bytes(self):
+        qo = 2 * self.sequences * self.chunk * self.heads * self.head_dim * 4
+        return qo + self.sequences * self.total * self.kv_width * 2 * 4
+
+
+def prefill_c4(**kw):
+    return PrefillWorkload("llama-3.2-1b-chunked-prefill-8x(2048+512)", **kw)
+
+
+def fill_prefill(cache, w: PrefillWorkload):
+    seqs = []
+    for i in range(w.sequences):
+        s = cache.create_sequence()
+        cache.append_many(s, w.keys(i), w.values(i))
+        seqs.append(s)
+    return seqs
+
+
 # ------------------------------------------------------------------- KV stress
 
 @dataclass
