@@ -1,13 +1,256 @@
-// Paged chunked-prefill attention on MFMA (placeholder until the bf16 tile
-// kernel lands; the f32 path of tvara_attn_prefill does not use this file).
+// Paged chunked-prefill attention on CDNA4 MFMA: the causal chunk of
+// fused_prompt_attention (core/include/tvara/attention.hpp:85-89), with bf16
+// operands and f32 accumulation.
+//
+// A workgroup takes 4 waves x 32 query rows of one (sequence, KV head); a row
+// is one (chunk position, query head of the GQA group), so the G heads that
+// share a KV head share every K/V tile.  Key tiles of 64 positions (4 paged
+// blocks) are read from the f32 pool, rounded to bf16 and staged in
+// double-buffered LDS: K as [key][d], V transposed as [d][key].
+//
+// Each wave computes S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A = K from
+// LDS, B = Q^T held in registers), so the score of row r and key k sits in the
+// lane that owns row r: lane l holds rows 16*nt + l%16 and keys
+// 16*mt + 4*(l/16) + i.  Those registers are exactly the B operand of
+// O^T = V^T P^T when the 32-key K dimension of the second product is ordered
+// {4g..4g+3, 16+4g..16+4g+3} for lane group g, so P never leaves registers;
+// the A operand (V^T) is read from LDS in the same key order.  Online softmax
+// runs in log2 units with the lazy rescale of the decode kernels; the causal
+// mask is applied on tiles that reach past a row's own position.
 #include "common.hpp"
 
 namespace tvara_amd {
+namespace {
 
-bool prefill_bf16_supported(const BlockLayout&, int) { return false; }
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-void launch_prefill_bf16(const PrefillArgs&, int, int, hipStream_t) {
-    throw std::runtime_error("bf16 prefill is not available in this build");
+constexpr float kThreshold = 8.0f;
+constexpr int kWaves = 4, kRows = 32, kKeys = 64;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ bf16x4 to_bf16(float4 v) {
+    const f32x4 f = {v.x, v.y, v.z, v.w};
+    return __builtin_convertvector(f, bf16x4);
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void prefill_bf16_kernel(const PrefillArgs a) {
+    constexpr int PW = kRows / G;        // chunk positions per wave
+    constexpr int QT = kWaves * PW;      // chunk positions per workgroup
+    constexpr int KC = D / 32;           // K-dimension chunks of S^T
+    constexpr int DT = D / 16;           // output column tiles
+    constexpr int KSTR = D + 8;          // LDS row pitch of K (bf16), padded
+    constexpr int VSTR = kKeys + 8;      // LDS row pitch of V^T (bf16), padded
+    static_assert(D == 64, "the staging map covers 64 columns");
+    __shared__ __attribute__((aligned(16))) __bf16 klds[2][kKeys * KSTR];
+    __shared__ __attribute__((aligned(16))) __bf16 vlds[2][D * VSTR];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int kh = blockIdx.y;
+    const int4 sd = a.seqs[blockIdx.z];  // table offset, start, rows, first query row
+    const int start = sd.y, nrows = sd.z;
+    const int q0 = blockIdx.x * QT;
+    if (q0 >= nrows) return;  // the whole workgroup: grid.x covers the longest chunk
+    const int kmax = start + min(q0 + QT, nrows);  // keys this workgroup reads: [0, kmax)
+    const int ntiles = (kmax + kKeys - 1) / kKeys;
+    const int pw0 = q0 + wave * PW;
+    const int wave_kmax = pw0 < nrows ? start + min(pw0 + PW, nrows) : 0;
+    const int kvw = a.lay.kv_width;
+    const int32_t* tab = a.tables + sd.x;
+    const float* pool = reinterpret_cast<const float*>(a.pool);
+    const size_t bstride = a.lay.stride / sizeof(float);
+    const size_t koff = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D;
+    const size_t voff = koff + 16 * static_cast<size_t>(kvw);
+
+    // Q^T as the B operand: row n = 16*nt + r16, columns 32*kc + 8*g .. +7
+    bf16x8 qop[2][KC];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const int r = 16 * nt + r16, pos = pw0 + r / G, head = kh * G + r % G;
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+            float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+            if (pos < nrows) {
+                const float* qp = a.q + (static_cast<size_t>(sd.w + pos) * a.heads + head) * D + 32 * kc + 8 * g;
+                x0 = *reinterpret_cast<const float4*>(qp);
+                x1 = *reinterpret_cast<const float4*>(qp + 4);
+            }
+            const float s = a.qscale;
+            const bf16x4 lo = to_bf16(make_float4(x0.x * s, x0.y * s, x0.z * s, x0.w * s));
+            const bf16x4 hi = to_bf16(make_float4(x1.x * s, x1.y * s, x1.z * s, x1.w * s));
+            qop[nt][kc] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+    }
+
+    // staging map: thread -> 4 consecutive keys (one block) x 4 columns
+    const int key4 = tid & 15, col = 4 * (tid >> 4);
+    float4 kreg[4], vreg[4];
+    auto gload = [&](int kt) {
+        const int kb = kt * kKeys + 4 * key4;
+        const int bid = kb < kmax ? tab[kb >> 4] : 0;
+        const float* base = pool + static_cast<size_t>(bid) * bstride + static_cast<size_t>(kb & 15) * kvw + col;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = kb + j < kmax;  // keys past the chunk's reach are never read
+            kreg[j] = ok ? *reinterpret_cast<const float4*>(base + j * kvw + koff) : make_float4(0.f, 0.f, 0.f, 0.f);
+            vreg[j] = ok ? *reinterpret_cast<const float4*>(base + j * kvw + voff) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<bf16x4*>(&klds[buf][(4 * key4 + j) * KSTR + col]) = to_bf16(kreg[j]);
+        const float4 v0 = vreg[0], v1 = vreg[1], v2 = vreg[2], v3 = vreg[3];
+        *reinterpret_cast<bf16x4*>(&vlds[buf][(col + 0) * VSTR + 4 * key4]) = to_bf16(make_float4(v0.x, v1.x, v2.x, v3.x));
+        *reinterpret_cast<bf16x4*>(&vlds[buf][(col + 1) * VSTR + 4 * key4]) = to_bf16(make_float4(v0.y, v1.y, v2.y, v3.y));
+        *reinterpret_cast<bf16x4*>(&vlds[buf][(col + 2) * VSTR + 4 * key4]) = to_bf16(make_float4(v0.z, v1.z, v2.z, v3.z));
+        *reinterpret_cast<bf16x4*>(&vlds[buf][(col + 3) * VSTR + 4 * key4]) = to_bf16(make_float4(v0.w, v1.w, v2.w, v3.w));
+    };
+
+    f32x4 acc[DT][2];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt][0] = acc[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
+    int lim[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) lim[nt] = start + pw0 + (16 * nt + r16) / G;  // last visible key of the row
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < ntiles) gload(kt + 1);
+        const int kbase = kt * kKeys;
+        if (kbase < wave_kmax) {
+            f32x4 s[4][2];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) s[mt][0] = s[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    const bf16x8 kop =
+                        *reinterpret_cast<const bf16x8*>(&klds[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
+                    s[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[0][kc], s[mt][0], 0, 0, 0);
+                    s[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[1][kc], s[mt][1], 0, 0, 0);
+                }
+            const bool diag = kbase + kKeys - 1 > start + pw0;
+            float rmax[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float v = s[mt][nt][i];
+                        if (diag && kbase + 16 * mt + 4 * g + i > lim[nt]) v = -INFINITY;
+                        s[mt][nt][i] = v;
+                        mx = fmaxf(mx, v);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                rmax[nt] = mx;
+            }
+            if (__any(rmax[0] > m[0] + kThreshold || rmax[1] > m[1] + kThreshold)) {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    const float mnew = fmaxf(m[nt], rmax[nt]);
+                    const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m[nt] - mnew);
+                    m[nt] = mnew;
+                    lsum[nt] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) acc[dt][nt] *= alpha;
+                }
+            }
+            // P^T as the B operand of O^T = V^T P^T: keys {4g+i, 16+4g+i} of each 32-key half
+            bf16x8 pop[2][2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                float p[4][4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float v = s[mt][nt][i];
+                        p[mt][i] = v == -INFINITY ? 0.f : fast_exp2(v - m[nt]);
+                        lsum[nt] += p[mt][i];
+                    }
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) {
+                    const bf16x4 lo = to_bf16(make_float4(p[2 * kc][0], p[2 * kc][1], p[2 * kc][2], p[2 * kc][3]));
+                    const bf16x4 hi =
+                        to_bf16(make_float4(p[2 * kc + 1][0], p[2 * kc + 1][1], p[2 * kc + 1][2], p[2 * kc + 1][3]));
+                    pop[nt][kc] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+            }
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const __bf16* vrow = &vlds[buf][(16 * dt + r16) * VSTR + 32 * kc + 4 * g];
+                    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
+                    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 16);
+                    const bf16x8 vop = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[0][kc], acc[dt][0], 0, 0, 0);
+                    acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[1][kc], acc[dt][1], 0, 0, 0);
+                }
+        }
+        if (kt + 1 < ntiles) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    bool bad = false;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        float l = lsum[nt];
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        const int r = 16 * nt + r16, pos = pw0 + r / G, head = kh * G + r % G;
+        if (pos >= nrows) continue;
+        float* o = a.out + (static_cast<size_t>(sd.w + pos) * a.heads + head) * D + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const f32x4 v = acc[dt][nt] / l;
+            bad |= !__builtin_isfinite(v[0]) || !__builtin_isfinite(v[1]) || !__builtin_isfinite(v[2]) ||
+                   !__builtin_isfinite(v[3]);
+            *reinterpret_cast<float4*>(o + 16 * dt) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    if (__any(bad) && lane == 0) *a.err = 1;
+}
+
+template <int G>
+void launch_g(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
+    constexpr int QT = kWaves * (kRows / G);
+    const dim3 grid((max_rows + QT - 1) / QT, a.lay.kv_heads, nseqs);
+    hipLaunchKernelGGL((prefill_bf16_kernel<64, G>), grid, dim3(64 * kWaves), 0, s, a);
+}
+
+}  // namespace
+
+bool prefill_bf16_supported(const BlockLayout& lay, int group) {
+    return lay.format == kF32 && lay.tpb == 16 && lay.head_dim == 64 &&
+           (group == 1 || group == 2 || group == 4 || group == 8);
+}
+
+void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
+    if (!prefill_bf16_supported(a.lay, a.group))
+        throw std::invalid_argument("bf16 prefill needs f32 blocks of 16 tokens, head_dim 64, GQA group 1/2/4/8");
+    if (nseqs <= 0 || max_rows <= 0) return;
+    ProfileScope p("paged_prefill_bf16", s);
+    switch (a.group) {
+        case 1: launch_g<1>(a, nseqs, max_rows, s); break;
+        case 2: launch_g<2>(a, nseqs, max_rows, s); break;
+        case 4: launch_g<4>(a, nseqs, max_rows, s); break;
+        default: launch_g<8>(a, nseqs, max_rows, s); break;
+    }
+    TVARA_HIP(hipGetLastError());
 }
 
 }  // namespace tvara_amd
