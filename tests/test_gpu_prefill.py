@@ -3,17 +3,24 @@ fused_prompt_attention (attention.hpp:85-89, FP64).
 
 f32 path: |gpu - ref| <= 1e-4 * (1 + |ref|).
 
-bf16 MFMA path.  q·log2(e)/sqrt(d), K, V and the probabilities P are rounded
+bf16 MFMA path.  q*log2(e)/sqrt(d), K, V and the probabilities P are rounded
 to bf16 (unit roundoff u = 2^-9); products and sums are f32.  To first order
 the output error of one row is
-    sum_t w_t (dv_t + v_t dp_t + (v_t - o) ds_t)
-with |dv_t| <= u|v_t|, |dp_t| <= u and a score error ds_t whose typical size
-is u*sqrt(2*sum_i (q_i k_i)^2 / d) ~ 2^-9 for N(0,1) inputs at d = 64.  The
-rounding errors are independent across keys, so with n_eff effective keys the
-row error is ~ u * |v| * sqrt(3 / n_eff); with |v| <= 5 and n_eff >= 1 the
-elementwise worst case stays below 1e-2, and over a whole batch the RMS is
-two orders smaller.  Bar: max |gpu - ref| <= 1e-2 * (1 + |ref|) and
-RMS(gpu - ref) <= 1e-3.
+    sum_t w_t * (dv_t + v_t * dp_t + (v_t - o) * ds_t)
+with |dv_t| <= u|v_t|, |dp_t| <= u, and a score error ds_t (natural-log units)
+that is a sum of d independent rounding terms, so its standard deviation is
+    sigma_s = u / sqrt(3) * sqrt(2 * sum_i (q_i k_i)^2) / sqrt(d)  ~ 2^-9 * 0.8
+for N(0,1) inputs at d = 64.  The three terms are independent across keys:
+  * a row with few visible keys keeps them whole: with |v| <= 5 (the largest of
+    ~10^6 N(0,1) draws) and |v - o| <= 10, a 4-sigma score error gives
+    10 * 4 * 1.6e-3 + 2 * 5 * u ~ 8e-2 in the worst element, and the batch RMS
+    is ~ |v| * sigma_s ~ 2e-3;
+  * a row of the chunked-prefill shape sees >= 2,049 keys; N(0,1) scores give
+    n_eff = n / e >= 750 effective keys, so every term shrinks by
+    1/sqrt(n_eff) < 0.04: the worst element stays below 1e-2 and the RMS below
+    1e-3.
+Bars: short rows  max |gpu - ref| <= 8e-2 * (1 + |ref|), RMS <= 2e-3;
+      long rows   max |gpu - ref| <= 1e-2 * (1 + |ref|), RMS <= 1e-3.
 """
 
 import sys
@@ -26,17 +33,18 @@ from tvara_amd import attention, synth, workloads
 
 pytestmark = pytest.mark.gpu
 TOL_F32 = 1e-4
-TOL_BF16_MAX, TOL_BF16_RMS = 1e-2, 1e-3
+SHORT_ROWS = (8e-2, 2e-3)
+LONG_ROWS = (1e-2, 1e-3)
 
 
 def say(*a):
     print(*a, flush=True, file=sys.stderr)
 
 
-def bf16_ok(got, want):
+def bf16_ok(got, want, bars):
     d = np.asarray(got, np.float64) - np.asarray(want, np.float64)
     rms = float(np.sqrt(np.mean(d * d)))
-    return refmath.close(got, want, TOL_BF16_MAX) and rms <= TOL_BF16_RMS, (refmath.max_rel(got, want), rms)
+    return refmath.close(got, want, bars[0]) and rms <= bars[1], (refmath.max_rel(got, want), rms)
 
 
 def build(device, oracle, heads, kv_heads, dim, specs, seed, tpb=16):
@@ -70,7 +78,7 @@ def test_bf16_small_shapes(device, oracle, group):
     want = np.concatenate([ref.fused_prompt_attention(q, s, 0, st, c, heads, 4096).reshape(c, -1)
                            for q, s, st, c in zip(qs, rs, starts, counts)])
     assert refmath.close(f32, want, TOL_F32), refmath.max_rel(f32, want)
-    ok, err = bf16_ok(got, want)
+    ok, err = bf16_ok(got, want, SHORT_ROWS)
     assert ok, err
 
 
@@ -98,11 +106,13 @@ def test_bf16_c4_shape(device, oracle):
         ref.drop(s)
     want = np.stack(want)
     assert refmath.close(np.stack(fsel), want, TOL_F32), refmath.max_rel(np.stack(fsel), want)
-    ok, err = bf16_ok(np.stack(gsel), want)
+    ok, err = bf16_ok(np.stack(gsel), want, LONG_ROWS)
     assert ok, err
+    say("c4 bf16 vs oracle (max rel, rms):", err)
     # over the whole batch the bf16 path tracks the f32 path
-    ok, err = bf16_ok(got, f32)
+    ok, err = bf16_ok(got, f32, LONG_ROWS)
     assert ok, err
+    say("c4 bf16 vs f32 path (max rel, rms):", err)
 
 
 def test_bf16_rejections(device):
