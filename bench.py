@@ -8,7 +8,9 @@ queries) are resident in HBM before the timed region.
 
 Prints one JSON line: value = algorithmic bytes moved per step / step time
 (GB/s), plus decode tokens/s, the roofline of the decode kernel from HIP events
-around its own launches, and the reference CPU path timed on this host.
+around its own launches (a second pass of the same steps, so the event packets
+stay out of the throughput region), and the reference CPU path timed on this
+host.
 """
 
 from __future__ import annotations
@@ -82,6 +84,51 @@ def cpu_baseline(w, seconds_cap=30.0):
 MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16
 
 
+def timed_steps(call, steps):
+    """ms per step over `steps` back-to-back calls, bracketed by device
+    synchronisation and HIP events on the library's stream (the null stream)."""
+    from tvara_amd import hip
+
+    start, stop = hip.Event(), hip.Event()
+    hip.synchronize()
+    start.record()
+    for _ in range(steps):
+        call()
+    stop.record()
+    hip.synchronize()
+    return start.elapsed_ms(stop) / steps
+
+
+def kernel_times(call, steps, names):
+    """Average duration of each named kernel over `steps` more calls, from the
+    HIP event pair the library records around its own launches (kept out of
+    the throughput region: the extra event packets add gaps between launches)."""
+    from tvara_amd import attention, hip
+
+    attention.profile_reset()
+    attention.profile_enable(True)
+    hip.synchronize()
+    for _ in range(steps):
+        call()
+    hip.synchronize()
+    attention.profile_enable(False)
+    out = {}
+    for n in names:
+        ms, k = attention.profile_read(n)
+        out[n] = (ms / max(k, 1), k)
+    return out
+
+
+def hbm_traffic(workload, kernel):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (profiles/hbm_traffic.json, written from those runs), or None."""
+    f = ROOT / "profiles" / "hbm_traffic.json"
+    if not f.exists():
+        return None
+    entry = json.loads(f.read_text()).get(f"{workload}/{kernel}")
+    return None if entry is None else int(entry["bytes_per_launch"])
+
+
 def bench_prefill(args):
     """Chunked prefill, 8 x (2,048 cached + 512 causal chunk), 32/8 heads, d=64:
     the bf16 MFMA kernel's TFLOP/s over the algorithmic 77.3 GFLOP."""
@@ -98,19 +145,8 @@ def bench_prefill(args):
                                                   [w.chunk] * w.sequences, 0, w.heads, w.context, "bf16")
     for _ in range(args.warmup):
         call()
-    attention.profile_reset()
-    attention.profile_enable(True)
-    start, stop = hip.Event(), hip.Event()
-    hip.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        call()
-    stop.record()
-    hip.synchronize()
-    attention.profile_enable(False)
-    ms_per_step = start.elapsed_ms(stop) / args.steps
-    kern_ms, n = attention.profile_read("paged_prefill_bf16")
-    kernel_ms = kern_ms / max(n, 1)
+    ms_per_step = timed_steps(call, args.steps)
+    kernel_ms, _ = kernel_times(call, args.steps, ["paged_prefill_bf16"])["paged_prefill_bf16"]
     assert np.isfinite(out.numpy()).all()
     tfs = w.flops() / (kernel_ms * 1e-3) / 1e12
     log(f"prefill kernel {kernel_ms * 1e3:.1f} us, call {ms_per_step * 1e3:.1f} us, {tfs:.1f} TFLOP/s")
@@ -122,7 +158,8 @@ def bench_prefill(args):
         "config": {"workload": w.name, "sequences": w.sequences, "prefix": w.prefix, "chunk": w.chunk,
                    "heads": w.heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim},
         "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
-                     "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4), "traffic": None, "kernel": "paged_prefill_bf16",
+                     "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
+                     "traffic": hbm_traffic(w.name, "paged_prefill_bf16"), "kernel": "paged_prefill_bf16",
                      "kernel_avg_us": round(kernel_ms * 1e3, 3), "algorithmic_flops": w.flops()},
         "cpu_baseline": None,
     }), flush=True)
@@ -131,11 +168,14 @@ def bench_prefill(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first run 3 device-to-device copies of this many MiB (a known-size kernel that "
+                         "calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -148,6 +188,13 @@ def main():
 
     from tvara_amd import attention, hip, kv, workloads
 
+    if args.copy_mib:
+        a, b = hip.DeviceArray((args.copy_mib << 18,)), hip.DeviceArray((args.copy_mib << 18,))
+        for _ in range(3):
+            hip.copy(b.ptr, a.ptr, a.nbytes)
+        hip.synchronize()
+        log(f"copied {args.copy_mib} MiB x3")
+        del a, b
     if args.workload == "c4":
         return bench_prefill(args)
     w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5}[args.workload]()
@@ -167,25 +214,15 @@ def main():
     plan.check()
     hip.synchronize()
 
-    # the timed region: K launches on the cache's stream (the null stream),
-    # bracketed by device synchronisation and HIP events on that stream
-    attention.profile_reset()
-    attention.profile_enable(True)
-    start, stop = hip.Event(), hip.Event()
-    hip.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        plan.launch(0, q.ptr, out.ptr)
-    stop.record()
-    hip.synchronize()
-    attention.profile_enable(False)
+    # the timed region: K launches on the cache's stream (the null stream)
+    step = lambda: plan.launch(0, q.ptr, out.ptr)  # noqa: E731
+    ms_per_step = timed_steps(step, args.steps)
     plan.check()
-    ms_per_step = start.elapsed_ms(stop) / args.steps
-    kern_ms, launches = attention.profile_read("paged_decode")
-    merge_ms, merges = attention.profile_read("paged_decode_merge")
-    kernel_avg_ms = kern_ms / max(launches, 1)
+    kt = kernel_times(step, args.steps, ["paged_decode", "paged_decode_merge"])
+    kernel_avg_ms, launches = kt["paged_decode"]
+    merge_ms, merges = kt["paged_decode_merge"]
     log(f"step {ms_per_step * 1e3:.1f} us; decode kernel {kernel_avg_ms * 1e3:.1f} us x{launches}; "
-        f"merge {merge_ms / max(merges, 1) * 1e3:.1f} us x{merges}")
+        f"merge {merge_ms * 1e3:.1f} us x{merges}")
     assert np.isfinite(out.numpy()).all()
 
     kv_bytes = w.kv_bytes()
@@ -215,7 +252,7 @@ def main():
         "model_decode_tokens_per_s": round(tokens_per_s / layers, 1),
         "model_layers": layers,
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(w.name, "paged_decode"),
                      "kernel": "paged_decode", "kernel_avg_us": round(kernel_avg_ms * 1e3, 3),
                      "algorithmic_bytes": kv_bytes + w.qo_bytes() // 2 + w.table_bytes()},
     }

@@ -98,6 +98,50 @@ def test_shapes_and_gqa_ratios(device, oracle, dim, kv_heads, group, length):
     assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
 
 
+# Q8_0 groups of 32 columns never straddle a head: head_dim is a multiple of 32
+Q8_SHAPES = [(64, 8, 1), (64, 8, 2), (64, 3, 3), (64, 2, 4), (128, 8, 4), (128, 2, 8), (128, 4, 5), (32, 2, 2),
+             (32, 1, 8)]
+
+
+@pytest.mark.parametrize("dim,kv_heads,group", Q8_SHAPES)
+@pytest.mark.parametrize("length", [1, 17, 1031, 20000])
+def test_q8_shapes(device, oracle, dim, kv_heads, group, length):
+    # Q8_0 blocks against the oracle holding the dequantised values; the
+    # 20,000-token row is cut into hundreds of splits (several merge passes)
+    say("decode q8", dim, kv_heads, group, length)
+    got, want = _single(device, oracle, kv_heads * group, kv_heads, dim, 16, length, seed=dim + length, tail=True,
+                        fmt=device.Q8_0)
+    assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+def test_c5_q8_full_batch(device, oracle):
+    # the whole 16 x 32,768-token Q8_0 batch in one launch; rows 0 and 15
+    # against the oracle on the dequantised values, and against the original
+    # f32 values within the quantisation bar (2e-3)
+    w = workloads.decode_c5()
+    say("decode", w.name)
+    dev = device.PagedCache(1, w.kv_heads, w.head_dim, 16, w.pool_blocks, fmt=device.Q8_0)
+    seqs = workloads.fill_decode(dev, w)
+    q = w.queries()
+    got = attention.decode_batch(dev, q, seqs, 0, w.heads, w.context)
+    for i in (0, w.sequences - 1):
+        k, v = w.keys(i), w.values(i)
+        n = len(k)
+        ref = oracle.Cache(1, w.kv_heads, w.head_dim, 16, n // 16 + 1)
+        s = ref.create_sequence()
+        ref.append_many(s, oracle.dequantize_q8_0(oracle.quantize_q8_0(k)).reshape(n, -1),
+                        oracle.dequantize_q8_0(oracle.quantize_q8_0(v)).reshape(n, -1))
+        want = ref.fused_paged_attention(q[i], s, 0, w.heads, w.context)
+        assert refmath.close(got[i], want, TOL), (i, refmath.max_rel(got[i], want))
+        exact = oracle.Cache(1, w.kv_heads, w.head_dim, 16, n // 16 + 1)
+        s = exact.create_sequence()
+        exact.append_many(s, k, v)
+        orig = exact.fused_paged_attention(q[i], s, 0, w.heads, w.context)
+        assert refmath.close(got[i], orig, 2e-3), (i, refmath.max_rel(got[i], orig))
+        say("row", i, "vs dequantised", refmath.max_rel(got[i], want), "vs f32", refmath.max_rel(got[i], orig))
+        del ref, exact
+
+
 @pytest.mark.parametrize("tpb", [7, 5, 4, 32, 1])
 def test_block_sizes(device, oracle, tpb):
     # block sizes that do not divide the length (prefill_t171.cpp, prefill_t180.cpp)

@@ -21,6 +21,7 @@
 // *err, matching OnlineAttention::update's rejection (attention.hpp:11).
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.hpp"
 #include "q8.hpp"
@@ -76,9 +77,14 @@ __device__ __forceinline__ float group_bcast<4>(float v, int h, int) {
     }
 }
 
+// Eight-lane groups: broadcast lane h%4 within every quad, then copy the
+// quad that holds lane h onto the other quad of its group (row_shr:4 writes
+// banks 1 and 3 from banks 0 and 2; row_shl:4 the reverse).
 template <>
-__device__ __forceinline__ float group_bcast<8>(float v, int h, int lane) {
-    return __shfl(v, (lane & ~7) | h);
+__device__ __forceinline__ float group_bcast<8>(float v, int h, int) {
+    const int b = __builtin_bit_cast(int, group_bcast<4>(v, h & 3, 0));
+    if (h < 4) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, 0x114, 0xF, 0xA, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, 0x104, 0xF, 0x5, false));
 }
 
 __device__ __forceinline__ float wave_max_across(float v, int from) {
@@ -314,13 +320,32 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
 
 // ------------------------------------------------------------- Q8_0 blocks
 
+// Signed byte B of w to float in one instruction (SDWA byte select with sign
+// extension); the compiler's own lowering takes a shift, a bit-field extract
+// and a conversion.
+template <int B>
+__device__ __forceinline__ float sbyte_to_float(uint32_t w) {
+    float r;
+    if constexpr (B == 0)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+    else if constexpr (B == 1)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+    else if constexpr (B == 2)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+    return r;
+}
+
 __device__ __forceinline__ void unpack_i8(uint4 w, float (&f)[16]) {
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-            f[4 * j + b] = static_cast<float>(static_cast<int8_t>(static_cast<uint8_t>(words[j] >> (8 * b))));
+    for (int j = 0; j < 4; ++j) {
+        f[4 * j] = sbyte_to_float<0>(words[j]);
+        f[4 * j + 1] = sbyte_to_float<1>(words[j]);
+        f[4 * j + 2] = sbyte_to_float<2>(words[j]);
+        f[4 * j + 3] = sbyte_to_float<3>(words[j]);
+    }
 }
 
 // Each lane owns 16 consecutive columns (one dwordx4 of int8) = half a Q8_0
@@ -417,17 +442,23 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
         process_f(kf, half_bits_to_float(x.ks), vf, half_bits_to_float(x.vs), x.ok);
     };
 
+    // Two tiles in flight.  The prefetches are unconditional (past the last
+    // full tile they re-read it and the result is masked out): a conditional
+    // load lets the compiler pull the byte unpacking up to the load, which then
+    // has to wait for the data at once.
     const int nfull = max(t1 - t0, 0) / TT;
+    const int last = max(nfull - 1, 0);
     Tile ta, tb2;
-    if (nfull > 0) load(t0, ta, true);
-    if (nfull > 1) load(t0 + TT, tb2, true);
+    if (nfull > 0) {
+        load(t0, ta, true);
+        load(t0 + min(1, last) * TT, tb2, true);
+    }
     for (int i = 0; i < nfull; i += 2) {
         process(ta);
-        if (i + 2 < nfull) load(t0 + (i + 2) * TT, ta, true);
-        if (i + 1 < nfull) {
-            process(tb2);
-            if (i + 3 < nfull) load(t0 + (i + 3) * TT, tb2, true);
-        }
+        load(t0 + min(i + 2, last) * TT, ta, true);
+        tb2.ok = i + 1 < nfull;
+        process(tb2);
+        load(t0 + min(i + 3, last) * TT, tb2, true);
     }
     if (t0 + nfull * TT < t1) {
         load(t0 + nfull * TT, ta, t0 + nfull * TT + tg < t1);
@@ -541,58 +572,124 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(const DecodeArgs a) 
 
 // ---------------------------------------------------------- split merge
 
-// Log-sum-exp merge of a row's split partials, one wave per (row, head).
-// Lane s holds split s's maximum and normaliser; every split's partial column
-// is requested before any arithmetic waits, so the merge costs about one
-// memory round trip.
-constexpr int kMergeSplits = 32;
-
-__global__ __launch_bounds__(64) void merge_kernel(const DecodeArgs a) {
+// Log-sum-exp merge of a row's split partials, one 256-lane workgroup per
+// (row, head).  The partial row of a split is cut into `nu` units of V floats;
+// lane (r, u) takes unit u (and u + 64, ... when nu > 64) of splits r, r + R,
+// ... where R = 256 / min(64, nu), U splits at a time with every load issued
+// before the first is used, so a row of up to R * U splits costs one memory
+// round trip.  Each lane keeps an online maximum over its splits; the R lanes
+// of a unit are combined through LDS.
+template <int V, int UPL, int U>
+__global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
+    using T = typename std::conditional<V == 4, float4, float>::type;
+    __shared__ float sm[256], sl[256];
+    __shared__ T sa[256][UPL];
     const int row = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int4 en = a.entries[row];
     const int nsplit = en.z >> 1;
     if (nsplit <= 1) return;
-    const int D = a.lay.head_dim;
+    const int D = a.lay.head_dim, nu = D / V;
+    const int lpr = min(64, nu), R = 256 / lpr;
+    const int u0 = lane % lpr, r = lane / lpr;
     const size_t step = static_cast<size_t>(a.heads);
     const float* ml = a.part_ml + (static_cast<size_t>(en.w) * step + h) * 2;
     const float* pa = a.part_acc + (static_cast<size_t>(en.w) * step + h) * D;
-    float* o = a.out + (static_cast<size_t>(row) * a.heads + h) * D;
-    if (nsplit <= kMergeSplits && nsplit <= 64 && D <= 128) {
-        float x[2][kMergeSplits];
-#pragma unroll
-        for (int s = 0; s < kMergeSplits; ++s)
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                x[i][s] = (s < nsplit && lane + 64 * i < D) ? pa[s * step * D + lane + 64 * i] : 0.f;
-        const float ms = lane < nsplit ? ml[lane * step * 2] : -INFINITY;
-        const float ls = lane < nsplit ? ml[lane * step * 2 + 1] : 0.f;
-        float M = ms;
-        for (int k = 32; k >= 1; k >>= 1) M = fmaxf(M, __shfl_xor(M, k));
-        const float ws = lane < nsplit ? fast_exp2(ms - M) : 0.f;
-        float L = ws * ls;
-        for (int k = 32; k >= 1; k >>= 1) L += __shfl_xor(L, k);
-        float acc[2] = {0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < kMergeSplits; ++s) {
-            const float w = __shfl(ws, s);
-            acc[0] = fmaf(w, x[0][s], acc[0]);
-            acc[1] = fmaf(w, x[1][s], acc[1]);
+
+    auto zero = [] {
+        if constexpr (V == 4) return make_float4(0.f, 0.f, 0.f, 0.f);
+        else return 0.f;
+    };
+    auto axpy = [](float w, const T& x, T& y) {
+        if constexpr (V == 4) {
+            y.x = fmaf(w, x.x, y.x);
+            y.y = fmaf(w, x.y, y.y);
+            y.z = fmaf(w, x.z, y.z);
+            y.w = fmaf(w, x.w, y.w);
+        } else {
+            y = fmaf(w, x, y);
         }
-        for (int i = 0; i < 2; ++i)
-            if (lane + 64 * i < D) o[lane + 64 * i] = acc[i] / L;
-        return;
+    };
+    float M = -INFINITY, L = 0.f;
+    T acc[UPL];
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) acc[j] = zero();
+    for (int s0 = 0; s0 < nsplit; s0 += R * U) {
+        float m[U], l[U];
+        T x[U][UPL];
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const int sp = s0 + k * R + r;
+            const bool ok = r < R && sp < nsplit;
+            m[k] = ok ? ml[sp * step * 2] : -INFINITY;
+            l[k] = ok ? ml[sp * step * 2 + 1] : 0.f;
+#pragma unroll
+            for (int j = 0; j < UPL; ++j) {
+                const int u = u0 + 64 * j;
+                x[k][j] = ok && u < nu ? *reinterpret_cast<const T*>(pa + sp * step * D + u * V) : zero();
+            }
+        }
+        float mc = M;
+#pragma unroll
+        for (int k = 0; k < U; ++k) mc = fmaxf(mc, m[k]);
+        if (mc != -INFINITY) {  // this lane holds a split
+            const float sc = fast_exp2(M - mc);  // 0 while M is still -inf
+            L *= sc;
+#pragma unroll
+            for (int j = 0; j < UPL; ++j) {
+                T z = zero();
+                axpy(sc, acc[j], z);
+                acc[j] = z;
+            }
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                const float w = fast_exp2(m[k] - mc);  // 0 for an empty slot
+                L = fmaf(w, l[k], L);
+#pragma unroll
+                for (int j = 0; j < UPL; ++j) axpy(w, x[k][j], acc[j]);
+            }
+            M = mc;
+        }
     }
-    float M = -INFINITY;
-    for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, ml[s * step * 2]);
-    for (int k = 32; k >= 1; k >>= 1) M = fmaxf(M, __shfl_xor(M, k));
-    float L = 0.f;
-    for (int s = lane; s < nsplit; s += 64) L += fast_exp2(ml[s * step * 2] - M) * ml[s * step * 2 + 1];
-    for (int k = 32; k >= 1; k >>= 1) L += __shfl_xor(L, k);
-    for (int d = lane; d < D; d += 64) {
-        float acc = 0.f;
-        for (int s = 0; s < nsplit; ++s) acc = fmaf(fast_exp2(ml[s * step * 2] - M), pa[s * step * D + d], acc);
-        o[d] = acc / L;
+    sm[lane] = M;
+    sl[lane] = L;
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) sa[lane][j] = acc[j];
+    __syncthreads();
+    if (r != 0) return;
+    float Mt = M;
+    for (int rr = 1; rr < R; ++rr) Mt = fmaxf(Mt, sm[rr * lpr + u0]);
+    float Lt = 0.f;
+    T at[UPL];
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) at[j] = zero();
+    for (int rr = 0; rr < R; ++rr) {
+        const int src = rr * lpr + u0;
+        const float w = sm[src] == -INFINITY ? 0.f : fast_exp2(sm[src] - Mt);
+        Lt = fmaf(w, sl[src], Lt);
+#pragma unroll
+        for (int j = 0; j < UPL; ++j) axpy(w, sa[src][j], at[j]);
     }
+    const float inv = 1.f / Lt;
+    float* o = a.out + (static_cast<size_t>(row) * a.heads + h) * D;
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+        const int u = u0 + 64 * j;
+        if (u >= nu) break;
+        T y = zero();
+        axpy(inv, at[j], y);
+        *reinterpret_cast<T*>(o + u * V) = y;
+    }
+}
+
+void launch_merge(const DecodeArgs& a, int nrows, hipStream_t s) {
+    const int D = a.lay.head_dim;
+    const dim3 grid(nrows, a.heads), block(256);
+    if (D % 4 == 0 && D <= 256)
+        hipLaunchKernelGGL((merge_kernel<4, 1, 8>), grid, block, 0, s, a);
+    else if (D % 4 == 0)
+        hipLaunchKernelGGL((merge_kernel<4, 2, 8>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((merge_kernel<1, 8, 4>), grid, block, 0, s, a);
 }
 
 template <int D, int G, int LPT>
@@ -694,7 +791,7 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
     }
     if (need_merge) {
         ProfileScope p("paged_decode_merge", s);
-        hipLaunchKernelGGL(merge_kernel, dim3(nrows, a.heads), dim3(64), 0, s, a);
+        launch_merge(a, nrows, s);
         TVARA_HIP(hipGetLastError());
     }
 }

@@ -50,6 +50,11 @@ def synchronize():
     check(runtime().hipDeviceSynchronize())
 
 
+def copy(dst, src, nbytes):
+    """Device-to-device copy of nbytes (the runtime's copy kernel)."""
+    check(runtime().hipMemcpy(dst, src, nbytes, D2D))
+
+
 def device_count():
     n = C.c_int(0)
     rc = runtime().hipGetDeviceCount(C.byref(n))
