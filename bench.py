@@ -141,12 +141,17 @@ def bench_prefill(args):
     seqs = workloads.fill_prefill(cache, w)
     q = hip.DeviceArray.from_numpy(np.concatenate([w.chunk_queries(i) for i in range(w.sequences)]))
     out = hip.DeviceArray(q.shape)
-    call = lambda: attention.prefill_batch_device(cache, q.ptr, out.ptr, seqs, [w.prefix] * w.sequences,  # noqa: E731
-                                                  [w.chunk] * w.sequences, 0, w.heads, w.context, "bf16")
+    # one plan per prompt chunk (as an executor keeps it for every layer); a
+    # step is one launch of it
+    plan = attention.PrefillPlan(cache, seqs, [w.prefix] * w.sequences, [w.chunk] * w.sequences, w.heads, w.context,
+                                 "bf16")
+    call = lambda: plan.launch(0, q.ptr, out.ptr)  # noqa: E731
     for _ in range(args.warmup):
         call()
+    plan.check()
     ms_per_step = timed_steps(call, args.steps)
     kernel_ms, _ = kernel_times(call, args.steps, ["paged_prefill_bf16"])["paged_prefill_bf16"]
+    plan.check()
     assert np.isfinite(out.numpy()).all()
     tfs = w.flops() / (kernel_ms * 1e-3) / 1e12
     log(f"prefill kernel {kernel_ms * 1e3:.1f} us, call {ms_per_step * 1e3:.1f} us, {tfs:.1f} TFLOP/s")

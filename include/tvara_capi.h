@@ -50,6 +50,7 @@ extern "C" {
 
 typedef struct tvara_kv_cache tvara_kv_cache;
 typedef struct tvara_attn_plan tvara_attn_plan;
+typedef struct tvara_prefill_plan tvara_prefill_plan;
 
 /* BlockHandle (kv.hpp:35) */
 typedef struct {
@@ -202,6 +203,22 @@ TVARA_API int tvara_attn_plan_check(tvara_attn_plan* plan);
  * one launch reads (algorithmic). */
 TVARA_API int tvara_attn_plan_info(tvara_attn_plan* plan, size_t* split_tokens, size_t* items, size_t* kv_bytes);
 TVARA_API void tvara_attn_plan_destroy(tvara_attn_plan* plan);
+
+/* A chunked-prefill plan: tvara_attn_prefill's work (fused_prompt_attention,
+ * attention.hpp:85-89, for each sequence's rows start[i] .. start[i]+rows[i]-1)
+ * with the block tables resident, so one plan per prompt chunk serves every
+ * layer.  Launches take device pointers, run asynchronously on `stream` (NULL:
+ * the cache's stream) and fail with TVARA_INVALID once the cache has changed
+ * since the plan was made.  No counterpart in the reference, which recomputes
+ * the block walk per call. */
+TVARA_API tvara_prefill_plan* tvara_prefill_plan_create(tvara_kv_cache* cache, const uint64_t* sequences,
+                                                        size_t count, size_t heads, size_t context,
+                                                        const size_t* start, const size_t* rows, int precision);
+TVARA_API int tvara_prefill_plan_launch(tvara_prefill_plan* plan, size_t layer, const float* queries, float* out,
+                                        void* stream);
+/* Synchronise the plan's last launch and report a non-finite score. */
+TVARA_API int tvara_prefill_plan_check(tvara_prefill_plan* plan);
+TVARA_API void tvara_prefill_plan_destroy(tvara_prefill_plan* plan);
 
 /* ----------------------------------------------------------------- timing */
 

@@ -115,6 +115,38 @@ def test_bf16_c4_shape(device, oracle):
     say("c4 bf16 vs f32 path (max rel, rms):", err)
 
 
+@pytest.mark.parametrize("precision", ["bf16", "f32"])
+def test_prefill_plan_matches_call(device, oracle, precision):
+    # a resident plan launched on two layers gives the one-shot call's bytes,
+    # and refuses to run once the cache has changed
+    from tvara_amd import hip
+
+    heads, kv_heads, dim = 8, 2, 64
+    specs = [(137, 100, 37), (64, 0, 64), (20, 3, 17)]
+    g = (2, kv_heads, dim, 16, 40)
+    dev = device.PagedCache(*g)
+    w = 2 * kv_heads * dim
+    ds, qs = [], []
+    for i, (n, _, rows) in enumerate(specs):
+        s = dev.create_sequence()
+        dev.append_many(s, synth.normal(9, f"k{i}", n * w).reshape(n, w), synth.normal(9, f"v{i}", n * w).reshape(n, w))
+        ds.append(s)
+        qs.append(synth.normal(9, f"q{i}", rows * heads * dim).reshape(rows, heads * dim))
+    q = np.concatenate(qs)
+    starts, counts = [st for _, st, _ in specs], [r for _, _, r in specs]
+    plan = attention.PrefillPlan(dev, ds, starts, counts, heads, 4096, precision)
+    dq, out = hip.DeviceArray.from_numpy(q), hip.DeviceArray(q.shape)
+    for layer in (1, 0):
+        want = attention.prefill_batch(dev, q, ds, starts, counts, layer, heads, 4096, precision=precision)
+        out.zero()
+        plan.launch(layer, dq.ptr, out.ptr)
+        plan.check()
+        assert np.array_equal(out.numpy(), want.reshape(q.shape))
+    dev.append(ds[0], synth.normal(9, "x", w), synth.normal(9, "y", w))
+    with pytest.raises(device.InvalidArgument):
+        plan.launch(0, dq.ptr, out.ptr)
+
+
 def test_bf16_rejections(device):
     dev = device.PagedCache(1, 2, 128, 16, 8)
     s = dev.create_sequence()

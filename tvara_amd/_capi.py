@@ -69,6 +69,10 @@ SIGNATURES = {
     "tvara_attn_plan_check": (C.c_int, [_vp]),
     "tvara_attn_plan_info": (C.c_int, [_vp, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),
     "tvara_attn_plan_destroy": (None, [_vp]),
+    "tvara_prefill_plan_create": (_vp, [_vp, C.POINTER(_u64), _sz, _sz, _sz, C.POINTER(_sz), C.POINTER(_sz), C.c_int]),
+    "tvara_prefill_plan_launch": (C.c_int, [_vp, _sz, _vp, _vp, _vp]),
+    "tvara_prefill_plan_check": (C.c_int, [_vp]),
+    "tvara_prefill_plan_destroy": (None, [_vp]),
     "tvara_profile_enable": (C.c_int, [C.c_int]),
     "tvara_profile_read": (C.c_int, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(_sz)]),
     "tvara_profile_reset": (C.c_int, []),

@@ -129,6 +129,41 @@ class DecodePlan:
         self.close()
 
 
+class PrefillPlan:
+    """Resident block tables for one chunked-prefill batch (tvara_prefill_plan_*):
+    sequence i attends its rows starts[i] .. starts[i] + counts[i] - 1."""
+
+    def __init__(self, cache, seqs, starts, counts, heads, context, precision="bf16"):
+        self.cache = cache
+        self.lib = cache.lib
+        seqs = np.ascontiguousarray(seqs, dtype=np.uint64).reshape(-1)
+        starts = np.ascontiguousarray(starts, dtype=np.uint64).reshape(-1)
+        counts = np.ascontiguousarray(counts, dtype=np.uint64).reshape(-1)
+        if not (seqs.size == starts.size == counts.size):
+            raise ValueError("seqs, starts and counts differ in length")
+        self.rows = int(counts.sum())
+        self.h = self.lib.tvara_prefill_plan_create(cache.h, seqs.ctypes.data_as(C.POINTER(C.c_uint64)), seqs.size,
+                                                    heads, context, starts.ctypes.data_as(C.POINTER(_sz)),
+                                                    counts.ctypes.data_as(C.POINTER(_sz)), _PRECISION[precision])
+        if not self.h:
+            _capi.raise_last()
+
+    def launch(self, layer, q_ptr, out_ptr, stream=None):
+        """Asynchronous launch over device pointers (ints)."""
+        _capi.check(self.lib.tvara_prefill_plan_launch(self.h, layer, q_ptr, out_ptr, stream))
+
+    def check(self):
+        _capi.check(self.lib.tvara_prefill_plan_check(self.h))
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.tvara_prefill_plan_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
 def profile_enable(on=True):
     _capi.check(_capi.lib().tvara_profile_enable(int(on)))
 

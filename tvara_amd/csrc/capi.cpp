@@ -29,6 +29,10 @@ struct tvara_attn_plan {
     size_t context = 0;
 };
 
+struct tvara_prefill_plan {
+    tvara_amd::PrefillPlan plan;
+};
+
 namespace tvara_amd {
 void profile_enable(bool on);
 void profile_read(const char* prefix, double* ms, size_t* launches);
@@ -355,70 +359,17 @@ int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t 
         if (layer >= c.geometry().layers) throw std::invalid_argument("invalid fused attention shape");
         if (precision != TVARA_ATTN_F32 && precision != TVARA_ATTN_BF16)
             throw std::invalid_argument("unknown attention precision");
-        std::vector<uint64_t> seq_of_row;
-        std::vector<size_t> cached;
-        size_t total_rows = 0, max_rows = 0;
-        for (size_t i = 0; i < count; ++i) {
-            const size_t length = c.sequence(sequences[i]).length;
-            // fused_prompt_attention (attention.hpp:85-87)
-            if (!rows[i] || start[i] >= length || rows[i] > length - start[i])
-                throw std::invalid_argument("invalid causal prompt chunk");
-            if (length > context) throw std::invalid_argument("invalid fused attention shape");
-            for (size_t j = 0; j < rows[i]; ++j) {
-                seq_of_row.push_back(sequences[i]);
-                cached.push_back(start[i] + j + 1);
-            }
-            total_rows += rows[i];
-            max_rows = std::max(max_rows, rows[i]);
-        }
+        tvara_amd::PrefillPlan plan;
+        plan.build(&c, sequences, count, heads, context, start, rows, precision);
+        const size_t total_rows = plan.total_rows;
         const size_t hidden = heads * c.geometry().head_dim;
+        if (device_ptrs && (!aligned16(queries) || !aligned16(out)))
+            throw std::invalid_argument("device buffers must be 16-byte aligned");
         Staged st;
         const float* dq = device_ptrs ? queries : st.in(queries, total_rows * hidden);
         float* dout = device_ptrs ? out : st.out(total_rows * hidden);
-        if (device_ptrs && (!aligned16(queries) || !aligned16(out)))
-            throw std::invalid_argument("device buffers must be 16-byte aligned");
-        if (precision == TVARA_ATTN_F32) {
-            AttnPlan plan;
-            plan.build(&c, seq_of_row, cached, {}, static_cast<int>(heads), 0);
-            plan.launch(static_cast<int>(layer), dq, nullptr, nullptr, dout, c.stream());
-            plan.check();
-        } else {
-            if (!tvara_amd::prefill_bf16_supported(c.layout(), static_cast<int>(heads / c.geometry().kv_heads)))
-                throw std::invalid_argument("bf16 prefill needs f32 blocks of 16 tokens and head_dim 64 or 128");
-            std::vector<int32_t> tab;
-            std::vector<int4> seqs(count);
-            size_t row0 = 0;
-            for (size_t i = 0; i < count; ++i) {
-                seqs[i] = make_int4(static_cast<int>(tab.size()), static_cast<int>(start[i]),
-                                    static_cast<int>(rows[i]), static_cast<int>(row0));
-                for (const Handle& b : c.sequence(sequences[i]).blocks) tab.push_back(static_cast<int32_t>(b.id));
-                row0 += rows[i];
-            }
-            tvara_amd::DeviceBuffer dtab, dseq, derr;
-            void* pt = dtab.ensure(tab.size() * sizeof(int32_t));
-            void* ps = dseq.ensure(seqs.size() * sizeof(int4));
-            void* pe = derr.ensure(sizeof(int));
-            TVARA_HIP(hipMemcpy(pt, tab.data(), tab.size() * sizeof(int32_t), hipMemcpyHostToDevice));
-            TVARA_HIP(hipMemcpy(ps, seqs.data(), seqs.size() * sizeof(int4), hipMemcpyHostToDevice));
-            TVARA_HIP(hipMemset(pe, 0, sizeof(int)));
-            c.flush();
-            tvara_amd::PrefillArgs a{};
-            a.pool = c.pool();
-            a.lay = c.layout();
-            a.layer = static_cast<int>(layer);
-            a.heads = static_cast<int>(heads);
-            a.group = static_cast<int>(heads / c.geometry().kv_heads);
-            a.tables = static_cast<const int32_t*>(pt);
-            a.seqs = static_cast<const int4*>(ps);
-            a.q = dq;
-            a.out = dout;
-            a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(c.geometry().head_dim)));
-            a.err = static_cast<int*>(pe);
-            tvara_amd::launch_prefill_bf16(a, static_cast<int>(count), static_cast<int>(max_rows), c.stream());
-            int flag = 0;
-            TVARA_HIP(hipMemcpy(&flag, pe, sizeof(int), hipMemcpyDeviceToHost));
-            if (flag) throw std::invalid_argument("invalid online attention input");
-        }
+        plan.launch(static_cast<int>(layer), dq, dout, c.stream());
+        plan.check();
         if (!device_ptrs)
             TVARA_HIP(hipMemcpy(out, dout, total_rows * hidden * sizeof(float), hipMemcpyDeviceToHost));
         else
@@ -474,6 +425,39 @@ int tvara_attn_plan_info(tvara_attn_plan* plan, size_t* split_tokens, size_t* it
 }
 
 void tvara_attn_plan_destroy(tvara_attn_plan* plan) { delete plan; }
+
+tvara_prefill_plan* tvara_prefill_plan_create(tvara_kv_cache* cache, const uint64_t* sequences, size_t count,
+                                              size_t heads, size_t context, const size_t* start, const size_t* rows,
+                                              int precision) {
+    tvara_prefill_plan* out = nullptr;
+    guard([&] {
+        auto& c = live(cache);
+        check_config(c, heads, context);
+        auto p = std::make_unique<tvara_prefill_plan>();
+        p->plan.build(&c, sequences, count, heads, context, start, rows, precision);
+        out = p.release();
+    });
+    return out;
+}
+
+int tvara_prefill_plan_launch(tvara_prefill_plan* plan, size_t layer, const float* queries, float* out, void* stream) {
+    return guard([&] {
+        if (!plan) throw std::invalid_argument("null attention plan");
+        if (!queries || !out || !aligned16(queries) || !aligned16(out))
+            throw std::invalid_argument("device buffers must be 16-byte aligned");
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : plan->plan.cache->stream();
+        plan->plan.launch(static_cast<int>(layer), queries, out, s);
+    });
+}
+
+int tvara_prefill_plan_check(tvara_prefill_plan* plan) {
+    return guard([&] {
+        if (!plan) throw std::invalid_argument("null attention plan");
+        plan->plan.check();
+    });
+}
+
+void tvara_prefill_plan_destroy(tvara_prefill_plan* plan) { delete plan; }
 
 int tvara_profile_enable(int enabled) {
     return guard([&] { tvara_amd::profile_enable(enabled != 0); });

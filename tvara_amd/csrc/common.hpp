@@ -1,6 +1,7 @@
 // Internal declarations shared by the host allocator, the C ABI and the
 // gfx950 kernels of libtvara_capi.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -54,6 +55,10 @@ struct RowOp {
 // Decode work: one entry per attention row (a sequence for decode, a
 // (sequence, position) pair for the f32 prompt path); work items split rows
 // into chunks of `split_tokens` cached tokens.
+// longest split a decode work item covers: 64 blocks of 16 tokens (the
+// kernels hold a split's block ids one per lane of a wave)
+constexpr size_t kMaxSplitTokens = 1024;
+
 struct DecodeArgs {
     const char* pool;
     BlockLayout lay;
@@ -98,18 +103,24 @@ void launch_q8_to_canonical(const char* pool, const BlockLayout& lay, int64_t id
 void launch_canonical_to_q8(char* pool, const BlockLayout& lay, int64_t id, const uint8_t* in, hipStream_t s);
 // decode.hip
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, hipStream_t s);
-int decode_waves(int kv_heads, int group);
+int decode_waves(int kv_heads, int group, int format, int head_dim);
 // prefill.hip
 bool prefill_bf16_supported(const BlockLayout& lay, int group);
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s);
 
 // kernel timing (profile.cpp)
-struct ProfileScope {
-    ProfileScope(const char* name, hipStream_t s);
-    ~ProfileScope();
-    const char* name;
-    hipStream_t stream;
-    void* begin = nullptr;
-};
+// Per-kernel timing for tvara_profile_*: while enabled, every launch made
+// through launch() carries a start/stop event pair that the runtime stamps
+// with the kernel's own start and end.
+bool profile_events(hipEvent_t* start, hipEvent_t* stop);
+void profile_record(const char* name, hipEvent_t start, hipEvent_t stop);
+
+template <class Kernel, class... Args>
+void launch(const char* name, Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+    hipEvent_t start = nullptr, stop = nullptr;
+    const bool timed = profile_events(&start, &stop);
+    hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), s, start, stop, 0, args...);
+    if (timed) profile_record(name, start, stop);
+}
 
 }  // namespace tvara_amd

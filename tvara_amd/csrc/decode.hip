@@ -137,7 +137,7 @@ __device__ __forceinline__ float softmax_step(float s, bool own, int lane, RowSt
 // e4-th float4.
 template <int D, int G, int LPT, int E, class Col>
 __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G][E], RowState& st, int lane, int wave,
-                                             int nwaves, int kh, int item, int row, int nsplit, Col col) {
+                                             int nwaves, int kh, int item, int row, int first, int nsplit, Col col) {
     extern __shared__ float lds[];
     const int c = lane & (LPT - 1);
     st.l = wave_sum_across(st.l, LPT);
@@ -220,11 +220,13 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
         for (int h = 0; h < G; ++h)
 #pragma unroll
             for (int m = 0; m < NV; ++m) {
+                // scaled in the score, not here: a use of q before the first
+                // tile would make the prologue wait for every tile load
                 const float4 x = *reinterpret_cast<const float4*>(qr + h * D + 4 * LPT * m);
-                q[h][4 * m] = x.x * a.qscale;
-                q[h][4 * m + 1] = x.y * a.qscale;
-                q[h][4 * m + 2] = x.z * a.qscale;
-                q[h][4 * m + 3] = x.w * a.qscale;
+                q[h][4 * m] = x.x;
+                q[h][4 * m + 1] = x.y;
+                q[h][4 * m + 2] = x.z;
+                q[h][4 * m + 3] = x.w;
             }
     }
     float acc[G][E];
@@ -236,12 +238,16 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
 
     const float* pool = reinterpret_cast<const float*>(a.pool);
     const size_t bstride = a.lay.stride / sizeof(float);
+    // the split's block ids, one per lane (a split spans at most 64 blocks);
+    // a tile's id is read from the owning lane, so the loop issues no table loads
     const int32_t* tab = a.tables + en.x;
+    const int nblk = (t1 - t0 + 15) >> 4;
+    const int bids = lane < nblk ? tab[(t0 >> 4) + lane] : 0;
     const size_t koff = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D + 4 * c;
     const size_t voff = koff + 16 * static_cast<size_t>(kvw);
 
     auto load = [&](int tb, float4 (&kk)[NV], float4 (&vv)[NV], bool ok) {
-        const int bid = tab[tb >> 4];
+        const int bid = __builtin_amdgcn_readlane(bids, (tb - t0) >> 4);
         const float* base = pool + static_cast<size_t>(bid) * bstride + static_cast<size_t>((tb & 15) + tg) * kvw;
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
@@ -265,7 +271,7 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
             }
             part[h] = s;
         }
-        const float s = transpose_reduce<LPT>(part, c);
+        const float s = transpose_reduce<LPT>(part, c) * a.qscale;
         const float p = softmax_step<G, LPT, E>(s, ok && c < G, lane, st, acc);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
@@ -282,22 +288,30 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
 
     // Full tiles stream with NB in flight (tile i+NB is requested as soon as
     // tile i is consumed) and unmasked loads; a partial last tile is masked.
+    // The prefetches are unconditional: past the last full tile they re-read
+    // it and the result is masked out.  (A conditional prefetch leaves a phi
+    // at the join whose register copies wait for the load just issued.)
     const int nfull = max(t1 - t0, 0) / TT;
-    float4 kbuf[NB][NV], vbuf[NB][NV];
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-        if (j < nfull) load(t0 + j * TT, kbuf[j], vbuf[j], true);
-    for (int i = 0; i < nfull; i += NB) {
+    if (nfull > 0) {
+        const int last = nfull - 1;
+        float4 kbuf[NB][NV], vbuf[NB][NV];
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            if (i + j < nfull) {
-                process(kbuf[j], vbuf[j], true);
-                if (i + j + NB < nfull) load(t0 + (i + j + NB) * TT, kbuf[j], vbuf[j], true);
+            load(t0 + min(j, last) * TT, kbuf[j], vbuf[j], true);
+            asm volatile("" ::: "memory");  // issue order = use order
+        }
+        for (int i = 0; i < nfull; i += NB) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                process(kbuf[j], vbuf[j], i + j < nfull);
+                load(t0 + min(i + j + NB, last) * TT, kbuf[j], vbuf[j], true);
+                // keep the prefetch here: without this the compiler sinks it
+                // past the next tile's wait and only one tile is in flight
+                asm volatile("" ::: "memory");
             }
         }
     }
-    float4 (&ka)[NV] = kbuf[0];
-    float4 (&va)[NV] = vbuf[0];
+    float4 ka[NV], va[NV];
     if (t0 + nfull * TT < t1) {
         const bool ok = t0 + nfull * TT + tg < t1;
         load(t0 + nfull * TT, ka, va, ok);
@@ -314,7 +328,7 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
         }
         process(ka, va, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, item - it.y, nsplit,
                                [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
 }
 
@@ -387,7 +401,11 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
         for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
     RowState st;
 
+    // the split's block ids, one per lane (a split spans at most 64 blocks);
+    // a tile's id is read from the owning lane, so the loop issues no table loads
     const int32_t* tab = a.tables + en.x;
+    const int nblk = (t1 - t0 + 15) >> 4;
+    const int bids = lane < nblk ? tab[(t0 >> 4) + lane] : 0;
     const size_t sec = a.lay.section;
     const size_t qcol = static_cast<size_t>(kh) * D + 16 * c;
     const size_t scol = (static_cast<size_t>(kh) * D + 16 * c) / 32;
@@ -402,7 +420,7 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
     };
     auto load = [&](int tb, Tile& x, bool ok) {
         x.ok = ok;
-        const int bid = tab[tb >> 4];
+        const int bid = __builtin_amdgcn_readlane(bids, (tb - t0) >> 4);
         const int slot = (tb & 15) + tg;
         const char* base = a.pool + static_cast<size_t>(bid) * a.lay.stride;
         if (ok) {
@@ -451,14 +469,18 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
     Tile ta, tb2;
     if (nfull > 0) {
         load(t0, ta, true);
+        asm volatile("" ::: "memory");  // issue order = use order
         load(t0 + min(1, last) * TT, tb2, true);
+        asm volatile("" ::: "memory");
     }
     for (int i = 0; i < nfull; i += 2) {
         process(ta);
         load(t0 + min(i + 2, last) * TT, ta, true);
+        asm volatile("" ::: "memory");  // keep the prefetch ahead of the next tile's wait
         tb2.ok = i + 1 < nfull;
         process(tb2);
         load(t0 + min(i + 3, last) * TT, tb2, true);
+        asm volatile("" ::: "memory");
     }
     if (t0 + nfull * TT < t1) {
         load(t0 + nfull * TT, ta, t0 + nfull * TT + tg < t1);
@@ -476,7 +498,7 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
         }
         process_f(kf, 1.f, vf, 1.f, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, item - it.y, nsplit,
                                [](int cc, int e4) { return 16 * cc + 4 * e4; });
 }
 
@@ -685,11 +707,11 @@ void launch_merge(const DecodeArgs& a, int nrows, hipStream_t s) {
     const int D = a.lay.head_dim;
     const dim3 grid(nrows, a.heads), block(256);
     if (D % 4 == 0 && D <= 256)
-        hipLaunchKernelGGL((merge_kernel<4, 1, 8>), grid, block, 0, s, a);
+        launch("paged_decode_merge", merge_kernel<4, 1, 8>, grid, block, 0, s, a);
     else if (D % 4 == 0)
-        hipLaunchKernelGGL((merge_kernel<4, 2, 8>), grid, block, 0, s, a);
+        launch("paged_decode_merge", merge_kernel<4, 2, 8>, grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((merge_kernel<1, 8, 4>), grid, block, 0, s, a);
+        launch("paged_decode_merge", merge_kernel<1, 8, 4>, grid, block, 0, s, a);
 }
 
 template <int D, int G, int LPT>
@@ -698,13 +720,14 @@ void launch_f32(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
     const dim3 grid(nitems * (a.lay.kv_heads / waves)), block(64 * waves);
     // two tiles in flight: a third needs more than the 256 VGPRs that keep two
     // waves per SIMD, and measured slower
-    hipLaunchKernelGGL((decode_f32_kernel<D, G, LPT, 2>), grid, block, lds, s, a);
+    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2>, grid, block, lds, s, a);
 }
 
 template <int D, int G>
 void launch_q8(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
     const size_t lds = (static_cast<size_t>(waves) * 4 * G * D + waves * 2 * G) * sizeof(float);
-    hipLaunchKernelGGL((decode_q8_kernel<D, G>), dim3(nitems * (a.lay.kv_heads / waves)), dim3(64 * waves), lds, s, a);
+    launch("paged_decode", decode_q8_kernel<D, G>, dim3(nitems * (a.lay.kv_heads / waves)), dim3(64 * waves), lds, s,
+           a);
 }
 
 template <int D>
@@ -752,21 +775,25 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
 
 }  // namespace
 
-// Waves per workgroup (one per KV head): four when kv_heads allows (measured
-// best for GQA 32/8 on MI355X: a workgroup streams 1 KiB of every 2 KiB slot
-// row), at most two for groups above four query heads.  Consecutive
-// workgroups take the KV-head groups of one work item.  TVARA_DECODE_WAVES
-// overrides it for tuning.
-int decode_waves(int kv_heads, int group) {
-    int w = 4;
+// Waves per workgroup (one per KV head), measured on MI355X: eight for f32
+// blocks (a workgroup streams whole 2 KiB slot rows; about one workgroup per
+// CU is best), four for Q8_0 (more, shorter workgroups hide its longer
+// per-tile arithmetic), at most two for groups above four query heads; a
+// divisor of kv_heads whose reduction buffers fit 64 KiB of LDS.
+// TVARA_DECODE_WAVES overrides it for tuning.
+int decode_waves(int kv_heads, int group, int format, int head_dim) {
+    int w = format == kF32 ? 8 : 4;
     if (const char* env = std::getenv("TVARA_DECODE_WAVES")) w = std::atoi(env);
     if (group > 4) w = std::min(w, 2);
     w = std::max(1, std::min(w, 8));
-    while (w > 1 && kv_heads % w) w /= 2;
+    auto lds = [&](int n) { return static_cast<size_t>(n) * (4 * group * head_dim + 2 * group) * sizeof(float); };
+    while (w > 1 && (kv_heads % w || lds(w) > 65536)) --w;
     return w;
 }
 
-static int waves_for(const DecodeArgs& a) { return decode_waves(a.lay.kv_heads, a.group); }
+static int waves_for(const DecodeArgs& a) {
+    return decode_waves(a.lay.kv_heads, a.group, a.lay.format, a.lay.head_dim);
+}
 
 bool decode_fast_path(const DecodeArgs& a) {
     return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128) &&
@@ -776,7 +803,6 @@ bool decode_fast_path(const DecodeArgs& a) {
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, hipStream_t s) {
     if (nitems <= 0) return;
     {
-        ProfileScope p("paged_decode", s);
         bool done = false;
         if (decode_fast_path(a)) {
             const int waves = waves_for(a);
@@ -785,12 +811,11 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
         }
         if (!done) {
             if (a.lay.head_dim > kGenericMaxDim) throw std::invalid_argument("head_dim above 512 is not supported");
-            hipLaunchKernelGGL(decode_generic_kernel, dim3(nitems, a.heads), dim3(64), 0, s, a);
+            launch("paged_decode", decode_generic_kernel, dim3(nitems, a.heads), dim3(64), 0, s, a);
         }
         TVARA_HIP(hipGetLastError());
     }
     if (need_merge) {
-        ProfileScope p("paged_decode_merge", s);
         launch_merge(a, nrows, s);
         TVARA_HIP(hipGetLastError());
     }

@@ -134,6 +134,9 @@ DeviceCache::DeviceCache(const Geometry& g, int format) : g_(g), format_(format)
         lay_.stride = round_up(2 * g_.layers * lay_.section, 256);
     }
     if (lay_.stride > kMax / g_.max_blocks) throw std::invalid_argument("KV capacity overflow");
+    int dev = 0;
+    TVARA_HIP(hipGetDevice(&dev));
+    TVARA_HIP(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
     TVARA_HIP(hipMalloc(&pool_, lay_.stride * g_.max_blocks));
     TVARA_HIP(hipMalloc(&err_, sizeof(int)));
     TVARA_HIP(hipMemset(err_, 0, sizeof(int)));
@@ -528,18 +531,33 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     }
     if (tab.size() > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
         throw std::invalid_argument("attention batch too large");
-    // split length: about 1,536 workgroups per launch, six per CU (measured
-    // best on the 64-sequence Llama-3.2-1B batch: 192 tokens)
+    // Split length: the shortest (a multiple of 16 from 64 to 1,024 tokens)
+    // whose launch fits the workgroup budget -- one workgroup per CU for f32
+    // blocks, four for Q8_0 (measured best on MI355X: the 64-sequence
+    // Llama-3.2-1B batch and the 16 x 32,768 Llama-3-8B Q8_0 batch).
     size_t split = split_override;
     if (!split) {
         if (const char* env = std::getenv("TVARA_SPLIT_TOKENS")) split = std::strtoull(env, nullptr, 10);
     }
     if (!split) {
-        const size_t groups = g.kv_heads / static_cast<size_t>(decode_waves(static_cast<int>(g.kv_heads), group));
-        split = round_up(std::max<size_t>(1, total * groups / 1536), 16);
-        split = std::clamp<size_t>(split, 64, 4096);
+        const size_t groups = g.kv_heads / static_cast<size_t>(decode_waves(static_cast<int>(g.kv_heads), group,
+                                                                             c->format(), static_cast<int>(g.head_dim)));
+        const size_t budget = static_cast<size_t>(c->compute_units()) * (c->format() == kF32 ? 1 : 4);
+        auto workgroups = [&](size_t sp) {
+            size_t n = 0;
+            for (size_t len : cached) n += std::max<size_t>(1, (len + sp - 1) / sp);
+            return n * groups;
+        };
+        size_t lo = 4, hi = kMaxSplitTokens / 16;  // in units of 16 tokens
+        while (lo < hi) {
+            const size_t mid = (lo + hi) / 2;
+            if (workgroups(mid * 16) <= budget) hi = mid;
+            else lo = mid + 1;
+        }
+        split = lo * 16;
     }
-    split = round_up(std::max<size_t>(split, 16), 16);
+    // the decode kernels keep a split's block ids in one register per lane
+    split = std::min(round_up(std::max<size_t>(split, 16), 16), kMaxSplitTokens);
     split_tokens = static_cast<int>(split);
     std::vector<int4> ent(rows);
     std::vector<int2> its;
@@ -600,6 +618,103 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
 }
 
 void AttnPlan::check() {
+    int flag = 0;
+    TVARA_HIP(hipDeviceSynchronize());
+    TVARA_HIP(hipMemcpy(&flag, err.ptr, sizeof(int), hipMemcpyDeviceToHost));
+    if (flag) {
+        TVARA_HIP(hipMemset(err.ptr, 0, sizeof(int)));
+        throw std::invalid_argument("invalid online attention input");
+    }
+}
+
+void PrefillPlan::build(DeviceCache* c, const uint64_t* sequences, size_t n, size_t h, size_t context,
+                        const size_t* start, const size_t* rows, int prec) {
+    cache = c;
+    const Geometry& g = c->geometry();
+    if (!sequences || !start || !rows || !n) throw std::invalid_argument("invalid causal prompt chunk");
+    if (prec != 0 && prec != 1) throw std::invalid_argument("unknown attention precision");
+    if (n > static_cast<size_t>(std::numeric_limits<int>::max())) throw std::invalid_argument("attention batch too large");
+    heads = static_cast<int>(h);
+    group = static_cast<int>(h / g.kv_heads);
+    count = static_cast<int>(n);
+    precision = prec;
+    std::vector<uint64_t> seq_of_row;
+    std::vector<size_t> cached;
+    total_rows = 0;
+    max_rows = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const size_t length = c->sequence(sequences[i]).length;
+        // fused_prompt_attention (attention.hpp:85-87)
+        if (!rows[i] || start[i] >= length || rows[i] > length - start[i])
+            throw std::invalid_argument("invalid causal prompt chunk");
+        if (length > context) throw std::invalid_argument("invalid fused attention shape");
+        if (prec == 0) {
+            for (size_t j = 0; j < rows[i]; ++j) {
+                seq_of_row.push_back(sequences[i]);
+                cached.push_back(start[i] + j + 1);
+            }
+        }
+        total_rows += rows[i];
+        max_rows = std::max(max_rows, static_cast<int>(std::min<size_t>(rows[i], std::numeric_limits<int>::max())));
+    }
+    if (total_rows > static_cast<size_t>(std::numeric_limits<int>::max()))
+        throw std::invalid_argument("attention batch too large");
+    if (prec == 0) {
+        rows_plan.build(c, seq_of_row, cached, {}, heads, 0);
+        epoch = rows_plan.epoch;
+        return;
+    }
+    if (!prefill_bf16_supported(c->layout(), group))
+        throw std::invalid_argument("bf16 prefill needs f32 blocks of 16 tokens, head_dim 64, GQA group 1/2/4/8");
+    std::vector<int32_t> tab;
+    std::vector<int4> sq(n);
+    size_t row0 = 0;
+    for (size_t i = 0; i < n; ++i) {
+        sq[i] = make_int4(static_cast<int>(tab.size()), static_cast<int>(start[i]), static_cast<int>(rows[i]),
+                          static_cast<int>(row0));
+        for (const Handle& b : c->sequence(sequences[i]).blocks) tab.push_back(static_cast<int32_t>(b.id));
+        row0 += rows[i];
+    }
+    if (tab.size() > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
+        throw std::invalid_argument("attention batch too large");
+    void* pt = tables.ensure(std::max<size_t>(tab.size() * sizeof(int32_t), 16));
+    void* ps = seqs.ensure(sq.size() * sizeof(int4));
+    void* pe = err.ensure(sizeof(int));
+    TVARA_HIP(hipMemcpy(pt, tab.data(), tab.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+    TVARA_HIP(hipMemcpy(ps, sq.data(), sq.size() * sizeof(int4), hipMemcpyHostToDevice));
+    TVARA_HIP(hipMemset(pe, 0, sizeof(int)));
+    epoch = c->epoch();
+}
+
+void PrefillPlan::launch(int layer, const float* q, float* out, hipStream_t s) {
+    if (layer < 0 || static_cast<size_t>(layer) >= cache->geometry().layers)
+        throw std::invalid_argument("invalid fused attention shape");
+    if (precision == 0) {
+        rows_plan.launch(layer, q, nullptr, nullptr, out, s);
+        return;
+    }
+    if (cache->epoch() != epoch) throw std::invalid_argument("attention plan is stale: the cache changed");
+    cache->flush();
+    PrefillArgs a{};
+    a.pool = cache->pool();
+    a.lay = cache->layout();
+    a.layer = layer;
+    a.heads = heads;
+    a.group = group;
+    a.tables = static_cast<const int32_t*>(tables.ptr);
+    a.seqs = static_cast<const int4*>(seqs.ptr);
+    a.q = q;
+    a.out = out;
+    a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
+    a.err = static_cast<int*>(err.ptr);
+    launch_prefill_bf16(a, count, max_rows, s);
+}
+
+void PrefillPlan::check() {
+    if (precision == 0) {
+        rows_plan.check();
+        return;
+    }
     int flag = 0;
     TVARA_HIP(hipDeviceSynchronize());
     TVARA_HIP(hipMemcpy(&flag, err.ptr, sizeof(int), hipMemcpyDeviceToHost));

@@ -66,6 +66,7 @@ public:
     hipStream_t stream() const { return stream_; }
     void set_stream(hipStream_t s) { stream_ = s; }
     uint64_t epoch() const { return epoch_; }
+    int compute_units() const { return cus_; }
     void synchronize();
 
     // BlockPool (kv.hpp:36-75)
@@ -119,6 +120,7 @@ private:
     char* pool_ = nullptr;
     hipStream_t stream_ = nullptr;
     uint64_t epoch_ = 0;
+    int cus_ = 256;
     std::vector<size_t> refs_;
     std::vector<uint64_t> gens_;
     std::vector<size_t> free_;
@@ -144,6 +146,24 @@ struct AttnPlan {
     void build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, const std::vector<size_t>& cached,
                const std::vector<uint8_t>& tail_rows, int heads, size_t split_override);
     void launch(int layer, const float* q, const float* tail_k, const float* tail_v, float* out, hipStream_t s);
+    void check();
+};
+
+// Chunked-prefill plan: sequences[i] attends its prompt rows start[i] ..
+// start[i] + rows[i] - 1 causally (fused_prompt_attention,
+// attention.hpp:85-89).  precision 0 = f32 rows through the decode kernels,
+// 1 = the bf16 MFMA tile kernel.  Block tables stay resident, so a plan built
+// once per chunk serves every layer.
+struct PrefillPlan {
+    DeviceCache* cache = nullptr;
+    uint64_t epoch = 0;
+    int heads = 0, group = 0, count = 0, max_rows = 0, precision = 0;
+    size_t total_rows = 0;
+    AttnPlan rows_plan;
+    DeviceBuffer tables, seqs, err;
+    void build(DeviceCache* c, const uint64_t* sequences, size_t count, size_t heads, size_t context,
+               const size_t* start, const size_t* rows, int precision);
+    void launch(int layer, const float* q, float* out, hipStream_t s);
     void check();
 };
 

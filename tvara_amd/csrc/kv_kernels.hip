@@ -207,12 +207,11 @@ constexpr int kMaxGridY = 65535;
 
 void launch_block_init(char* pool, size_t stride, const BlockInitOp* ops, int n, hipStream_t s) {
     if (n <= 0) return;
-    ProfileScope p("kv_block_init", s);
     const size_t units = stride / 16;
     const unsigned gx = static_cast<unsigned>(std::min<size_t>((units + kThreads - 1) / kThreads, 512));
     for (int base = 0; base < n; base += kMaxGridY) {
         const int count = std::min(kMaxGridY, n - base);
-        hipLaunchKernelGGL(block_init_kernel, dim3(gx, count), dim3(kThreads), 0, s, pool, stride, ops + base);
+        launch("kv_block_init", block_init_kernel, dim3(gx, count), dim3(kThreads), 0, s, pool, stride, ops + base);
     }
     TVARA_HIP(hipGetLastError());
 }
@@ -220,16 +219,15 @@ void launch_block_init(char* pool, size_t stride, const BlockInitOp* ops, int n,
 void launch_append_rows(char* pool, const BlockLayout& lay, const RowOp* ops, int n, const float* keys,
                         const float* values, hipStream_t s) {
     if (n <= 0) return;
-    ProfileScope p("kv_append_rows", s);
     const int threads = lay.format == kF32 ? (lay.kv_width >= 1024 ? 256 : 128) : 256;
     for (int base = 0; base < n; base += kMaxGridY) {
         const int count = std::min(kMaxGridY, n - base);
         if (lay.format == kF32)
-            hipLaunchKernelGGL(append_rows_f32_kernel, dim3(lay.layers * 2, count), dim3(threads), 0, s, pool, lay,
-                               ops + base, keys, values);
+            launch("kv_append_rows", append_rows_f32_kernel, dim3(lay.layers * 2, count), dim3(threads), 0, s, pool,
+                   lay, ops + base, keys, values);
         else
-            hipLaunchKernelGGL(append_rows_q8_kernel, dim3(lay.layers * 2, count), dim3(threads), 0, s, pool, lay,
-                               ops + base, keys, values);
+            launch("kv_append_rows", append_rows_q8_kernel, dim3(lay.layers * 2, count), dim3(threads), 0, s, pool,
+                   lay, ops + base, keys, values);
     }
     TVARA_HIP(hipGetLastError());
 }
@@ -237,26 +235,24 @@ void launch_append_rows(char* pool, const BlockLayout& lay, const RowOp* ops, in
 void launch_gather_rows(const char* pool, const BlockLayout& lay, const int2* rows, int n, int layer, int kind,
                         float* out, hipStream_t s) {
     if (n <= 0) return;
-    ProfileScope p("kv_gather_rows", s);
-    hipLaunchKernelGGL(gather_rows_kernel, dim3(n), dim3(128), 0, s, pool, lay, rows, layer, kind, out);
+    launch("kv_gather_rows", gather_rows_kernel, dim3(n), dim3(128), 0, s, pool, lay, rows, layer, kind, out);
     TVARA_HIP(hipGetLastError());
 }
 
 void launch_checksums(const char* pool, const BlockLayout& lay, const int64_t* ids, int n, uint64_t* out,
                       hipStream_t s) {
     if (n <= 0) return;
-    ProfileScope p("kv_checksum", s);
-    hipLaunchKernelGGL(checksum_kernel, dim3(n), dim3(kThreads), 0, s, pool, lay, ids, out);
+    launch("kv_checksum", checksum_kernel, dim3(n), dim3(kThreads), 0, s, pool, lay, ids, out);
     TVARA_HIP(hipGetLastError());
 }
 
 void launch_q8_to_canonical(const char* pool, const BlockLayout& lay, int64_t id, uint8_t* out, hipStream_t s) {
-    hipLaunchKernelGGL(q8_to_canonical_kernel, dim3(64), dim3(kThreads), 0, s, pool, lay, id, out);
+    launch("kv_q8_to_canonical", q8_to_canonical_kernel, dim3(64), dim3(kThreads), 0, s, pool, lay, id, out);
     TVARA_HIP(hipGetLastError());
 }
 
 void launch_canonical_to_q8(char* pool, const BlockLayout& lay, int64_t id, const uint8_t* in, hipStream_t s) {
-    hipLaunchKernelGGL(canonical_to_q8_kernel, dim3(64), dim3(kThreads), 0, s, pool, lay, id, in);
+    launch("kv_canonical_to_q8", canonical_to_q8_kernel, dim3(64), dim3(kThreads), 0, s, pool, lay, id, in);
     TVARA_HIP(hipGetLastError());
 }
 

@@ -229,7 +229,7 @@ template <int G>
 void launch_g(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     constexpr int QT = kWaves * (kRows / G);
     const dim3 grid((max_rows + QT - 1) / QT, a.lay.kv_heads, nseqs);
-    hipLaunchKernelGGL((prefill_bf16_kernel<64, G>), grid, dim3(64 * kWaves), 0, s, a);
+    launch("paged_prefill_bf16", prefill_bf16_kernel<64, G>, grid, dim3(64 * kWaves), 0, s, a);
 }
 
 }  // namespace
@@ -243,7 +243,6 @@ void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStrea
     if (!prefill_bf16_supported(a.lay, a.group))
         throw std::invalid_argument("bf16 prefill needs f32 blocks of 16 tokens, head_dim 64, GQA group 1/2/4/8");
     if (nseqs <= 0 || max_rows <= 0) return;
-    ProfileScope p("paged_prefill_bf16", s);
     switch (a.group) {
         case 1: launch_g<1>(a, nseqs, max_rows, s); break;
         case 2: launch_g<2>(a, nseqs, max_rows, s); break;

@@ -1,9 +1,11 @@
-// Per-kernel HIP-event timing for the library's own launches.
+// Per-kernel timing of the library's own launches: start/stop events that the
+// runtime stamps with each kernel's execution (hipExtLaunchKernel).
 #include <hip/hip_runtime.h>
 
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -35,22 +37,20 @@ void drain() {
 }
 }  // namespace
 
-ProfileScope::ProfileScope(const char* n, hipStream_t s) : name(n), stream(s) {
+bool profile_events(hipEvent_t* start, hipEvent_t* stop) {
     std::lock_guard<std::mutex> lock(mutex);
-    if (!enabled) return;
-    hipEvent_t e;
-    TVARA_HIP(hipEventCreate(&e));
-    TVARA_HIP(hipEventRecord(e, s));
-    begin = e;
+    if (!enabled) return false;
+    TVARA_HIP(hipEventCreate(start));
+    if (hipEventCreate(stop) != hipSuccess) {
+        (void)hipEventDestroy(*start);
+        throw std::runtime_error("hipEventCreate failed");
+    }
+    return true;
 }
 
-ProfileScope::~ProfileScope() {
-    if (!begin) return;
+void profile_record(const char* name, hipEvent_t start, hipEvent_t stop) {
     std::lock_guard<std::mutex> lock(mutex);
-    hipEvent_t e;
-    if (hipEventCreate(&e) != hipSuccess) return;
-    if (hipEventRecord(e, stream) != hipSuccess) return;
-    pending.push_back({name, static_cast<hipEvent_t>(begin), e});
+    pending.push_back({name, start, stop});
 }
 
 void profile_enable(bool on) {
