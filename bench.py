@@ -229,6 +229,15 @@ def main():
     log(f"step {ms_per_step * 1e3:.1f} us; decode kernel {kernel_avg_ms * 1e3:.1f} us x{launches}; "
         f"merge {merge_ms * 1e3:.1f} us x{merges}")
     assert np.isfinite(out.numpy()).all()
+    # the same batch through the host-buffer entry point (queries in and
+    # outputs out over PCIe, block tables uploaded per call): reported beside
+    # the value, never as it
+    qh = w.queries()
+    attention.decode_batch(cache, qh, seqs, 0, w.heads, w.context)
+    t0 = time.perf_counter()
+    for _ in range(20):
+        attention.decode_batch(cache, qh, seqs, 0, w.heads, w.context)
+    host_ms = (time.perf_counter() - t0) / 20 * 1e3
 
     kv_bytes = w.kv_bytes()
     step_bytes = kv_bytes + w.qo_bytes() + w.table_bytes()
@@ -256,6 +265,7 @@ def main():
         "decode_tokens_per_s": round(tokens_per_s, 1),
         "model_decode_tokens_per_s": round(tokens_per_s / layers, 1),
         "model_layers": layers,
+        "host_buffers_ms_per_step": round(host_ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(w.name, "paged_decode"),
                      "kernel": "paged_decode", "kernel_avg_us": round(kernel_avg_ms * 1e3, 3),
