@@ -170,12 +170,126 @@ def bench_prefill(args):
     }), flush=True)
 
 
+def bench_kv(args, cow):
+    """KV-management stress: 256 sequences forked from a shared 1,024-token
+    (or 1,025-token, copy-on-write) prefix, 22 layers x 8 x 64 f32; a step is
+    one batched append of one token to every sequence (host bookkeeping, the
+    zero-fill / copy-on-write launch and the row-copy launch).  K/V rows are
+    resident in HBM.  Bytes per step: the rows written, plus a block's zero
+    fill for every new block and a read and a write of a block for every
+    copy-on-write."""
+    import numpy as np
+
+    from tvara_amd import hip, kv, workloads
+
+    w = workloads.kv_c3(unaligned=cow)
+    cache = kv.PagedCache(w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.max_blocks())
+    width = w.layers * w.kv_heads * w.head_dim
+    block_bytes = w.tokens_per_block * width * 2 * 4
+    row_bytes = width * 2 * 4
+    # four distinct step batches, used in turn (the contents do not change the work)
+    batches = [(hip.DeviceArray.from_numpy(w.tokens(f"step{i}-k", w.sequences)),
+                hip.DeviceArray.from_numpy(w.tokens(f"step{i}-v", w.sequences))) for i in range(4)]
+    steps_k = [batches[i % 4][0] for i in range(w.steps)]
+    steps_v = [batches[i % 4][1] for i in range(w.steps)]
+    pk, pv = w.tokens("prefix-k", w.prefix), w.tokens("prefix-v", w.prefix)
+
+    def step_bytes(i):
+        length = w.prefix + i
+        slot = length % w.tokens_per_block
+        if slot == 0:
+            extra = w.sequences * block_bytes  # new tail blocks, zero-filled
+        elif i == 0:
+            extra = (w.sequences - 1) * 2 * block_bytes  # shared tail copied for all but the last appender
+        else:
+            extra = 0
+        return w.sequences * row_bytes + extra
+
+    def setup():
+        src = cache.create_sequence()
+        cache.append_many(src, pk, pv)
+        seqs = [cache.fork(src) for _ in range(w.sequences)]
+        cache.drop(src)
+        cache.synchronize()
+        return seqs
+
+    def run_pass(seqs, first, count, timed):
+        start, stop = hip.Event(), hip.Event()
+        hip.synchronize()
+        start.record()
+        for i in range(first, first + count):
+            cache.append_batch_device(seqs, steps_k[i].ptr, steps_v[i].ptr)
+        stop.record()
+        hip.synchronize()
+        return start.elapsed_ms(stop)
+
+    # warm-up: whole passes, untimed
+    for _ in range(max(1, args.warmup // w.steps)):
+        seqs = setup()
+        run_pass(seqs, 0, w.steps, False)
+        for s in seqs:
+            cache.drop(s)
+    total_ms, done, nbytes = 0.0, 0, 0
+    while done < args.steps:
+        seqs = setup()
+        n = min(w.steps, args.steps - done)
+        total_ms += run_pass(seqs, 0, n, True)
+        nbytes += sum(step_bytes(i) for i in range(n))
+        done += n
+        for s, r in zip(seqs, w.rollback()):  # speculative rollback (metadata only)
+            cache.truncate(s, cache.length(s) - r)
+        cache.audit()
+        for s in seqs:
+            cache.drop(s)
+    ms_per_step = total_ms / done
+    gbs = nbytes / (total_ms * 1e-3) / 1e9
+    log(f"{w.name}: {ms_per_step * 1e3:.1f} us per step, {gbs:.1f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the reference's PagedCache (oracle/_ref) on one host thread: one fork
+        # of the prefix and the first 32 append steps
+        from oracle import pyoracle
+
+        kind = "reference" if pyoracle.ref_available() else "port"
+        ref = (pyoracle.RefCache if kind == "reference" else pyoracle.Cache)(
+            w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.max_blocks())
+        src = ref.create_sequence()
+        ref.append_many(src, pk, pv)
+        rseqs = [ref.fork(src) for _ in range(w.sequences)]
+        ref.drop(src)
+        hk = [w.tokens(f"step{i}-k", w.sequences) for i in range(4)]
+        hv = [w.tokens(f"step{i}-v", w.sequences) for i in range(4)]
+        n_cpu = 32
+        t0 = time.perf_counter()
+        for i in range(n_cpu):
+            ref.append_batch(rseqs, hk[i % 4], hv[i % 4])
+        cpu_s = (time.perf_counter() - t0) / n_cpu
+        cpu_bytes = sum(step_bytes(i) for i in range(n_cpu)) / n_cpu
+        cpu = {"value": round(cpu_bytes / cpu_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+               "sample": f"{n_cpu} append steps of 256 tokens after one fork of the prefix, 1 thread; "
+                         f"{cpu_s * 1e3:.2f} ms per step", "ms_per_step": round(cpu_s * 1e3, 4)}
+        del ref
+    print(json.dumps({
+        "metric": "paged KV management stress: us per append step + GB/s, 1 MI355X", "value": round(gbs, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": done, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: K/V rows from a seeded splitmix64 stream (floats in [1, 2))",
+        "config": {"workload": w.name, "sequences": w.sequences, "prefix": w.prefix, "steps_per_pass": w.steps,
+                   "layers": w.layers, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
+                   "tokens_per_block": w.tokens_per_block},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "kv_append (step)",
+                     "algorithmic_bytes_per_step": round(nbytes / done)},
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c5"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c3cow", "c4", "c5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -202,6 +316,8 @@ def main():
         del a, b
     if args.workload == "c4":
         return bench_prefill(args)
+    if args.workload in ("c3", "c3cow"):
+        return bench_kv(args, args.workload == "c3cow")
     w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5}[args.workload]()
     log(f"workload {w.name}: {w.sequences} sequences, {w.total_tokens} tokens")
     g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)

@@ -48,6 +48,7 @@ extern "C" {
 #define TVARA_ATTN_F32 0  /* reference semantics: one fused_paged_attention per row */
 #define TVARA_ATTN_BF16 1 /* bf16 MFMA tiles, f32 accumulation */
 
+typedef struct tvara_model tvara_model;
 typedef struct tvara_kv_cache tvara_kv_cache;
 typedef struct tvara_attn_plan tvara_attn_plan;
 typedef struct tvara_prefill_plan tvara_prefill_plan;
@@ -60,6 +61,38 @@ typedef struct {
 
 /* c_api.h:17 -- thread-local message of the last failed call */
 TVARA_API const char* tvara_last_error(void);
+
+/* ---- model-level exports: the reference's 11 (c_api.h:13-24), same
+ * signatures, return conventions (NULL / 0 / -1 with tvara_last_error set),
+ * messages and per-handle lock (c_api.cpp:35-78).  The model runs on the GPU:
+ * GGUF weights dequantised to f32 in HBM, every layer of a token on device,
+ * the KV cache in this library's paged pool. */
+
+/* tvara_model_open (c_api.cpp:36-40): load a Llama GGUF file; the KV pool holds
+ * max_blocks blocks of block_tokens tokens */
+TVARA_API tvara_model* tvara_model_open(const char* utf8_path, size_t max_blocks, size_t block_tokens);
+/* c_api.cpp:42 */
+TVARA_API void tvara_model_close(tvara_model* model);
+/* c_api.cpp:43-44: 0 and "closed model" for a NULL handle */
+TVARA_API size_t tvara_model_vocab_size(tvara_model* model);
+TVARA_API size_t tvara_model_context_size(tvara_model* model);
+/* c_api.cpp:46: the GGUF metadata as one JSON object, owned by the handle */
+TVARA_API const char* tvara_model_metadata(tvara_model* model);
+/* c_api.cpp:47-50: a new empty sequence (ids from 1), 0 on failure */
+TVARA_API uint64_t tvara_sequence_create(tvara_model* model);
+/* c_api.cpp:51-55 (PagedModelExecutor::decode, paged_model.hpp:12-28): logits
+ * (count == vocab) of `token` at the end of `sequence`; its K/V are appended
+ * only when every layer succeeded */
+TVARA_API int tvara_sequence_decode(tvara_model* model, uint64_t sequence, uint32_t token, float* logits,
+                                    size_t count);
+/* c_api.cpp:56-59 */
+TVARA_API int tvara_sequence_drop(tvara_model* model, uint64_t sequence);
+/* c_api.cpp:61-73: token_count decodes (count == token_count * vocab); all
+ * tokens are checked first and a failure truncates back to the entry length */
+TVARA_API int tvara_sequence_decode_batch(tvara_model* model, uint64_t sequence, const uint32_t* tokens,
+                                          size_t token_count, float* logits, size_t count);
+/* c_api.cpp:76-78 (PagedCache::truncate, kv.hpp:131-136) */
+TVARA_API int tvara_sequence_truncate(tvara_model* model, uint64_t sequence, size_t length);
 /* Status of the last failed call on this thread (TVARA_OK after a success);
  * lets callers of the NULL- or 0-returning entry points tell the exception
  * classes apart.  No reference counterpart: the reference throws in C++. */

@@ -1,0 +1,173 @@
+"""The model-level exports on the GPU against the reference's own C ABI
+(core/src/c_api.cpp + its CPU executor, built into oracle/_ref) on the same
+synthetic GGUF files: logits of every decoded token, metadata JSON, and the
+sequence semantics of decode_batch (rollback), truncate, drop and the error
+paths (c_api.cpp:35-78, paged_model.hpp:12-28).
+
+Logit bar: |gpu - ref| <= 1e-4 * (1 + |ref|) per element.  Derivation: the
+matvecs and RMSNorm accumulate in double and round once as the reference
+does, RoPE uses the host's cos/sin exactly as rotary() computes them, and
+weights dequantise to the reference's floats; what differs is the attention
+(f32 online softmax against the reference's FP64, within 1e-6 relative,
+tests/test_gpu_decode.py) and expf in the SwiGLU gate (within 2 ulp).  Those
+relative errors of ~1e-6 per layer pass through the remaining matvecs with a
+gain of order one for these 1/sqrt(fan-in)-scaled weights, so a few layers
+stay near 1e-5 of the logit scale -- a tenth of the bar.
+"""
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import gguf_fixture as gf
+from tvara_amd import native
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+REF = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "libtvara_ref_capi.so"
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+@pytest.fixture(scope="module")
+def ref_capi():
+    if not REF.exists():
+        pytest.skip("reference C ABI not built (make -C oracle ref)")
+    return str(REF)
+
+
+def close(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return bool(np.all(np.abs(got - want) <= TOL * (1 + np.abs(want)))), float(
+        np.max(np.abs(got - want) / (1 + np.abs(want))))
+
+
+SPECS = {
+    "f32-gqa": dict(),
+    "f16-split-tied": dict(matrix_type=gf.T_F16, embed_type=gf.T_F16, norm_type=gf.T_F16, rope_layout="split",
+                           output=False),
+    "q8_0-gqa4": dict(matrix_type=gf.T_Q8_0, heads=8, kv_heads=2, hidden=128, intermediate=256),
+    "q4_0-mha": dict(matrix_type=gf.T_Q4_0, heads=4, kv_heads=4, rope_layout="interleaved"),
+    "q4_k-256": dict(matrix_type=gf.T_Q4_K, hidden=256, intermediate=512, heads=4, kv_heads=1, layers=3),
+}
+
+
+@pytest.mark.parametrize("name", list(SPECS))
+def test_logits_match_reference(tmp_path, ref_capi, name):
+    spec = gf.LlamaSpec(**SPECS[name])
+    path = spec.write(tmp_path / f"{name}.gguf")
+    say("model", name)
+    mine = native.NativeModel(path, max_blocks=32, block_tokens=4)
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=32, block_tokens=4)
+    assert (mine.vocab_size, mine.context_size) == (ref.vocab_size, ref.context_size)
+    assert mine.metadata_json() == ref.metadata_json()
+    sm, sr = mine.new_sequence(), ref.new_sequence()
+    assert sm == sr
+    tokens = [int(t) for t in np.random.default_rng(1).integers(0, spec.vocab, 40)]
+    worst = 0.0
+    for t in tokens[:13]:  # token by token, across block boundaries (4-token blocks)
+        ok, err = close(mine.logits(sm, t), ref.logits(sr, t))
+        worst = max(worst, err)
+        assert ok, (name, t, err)
+    got, want = mine.decode_batch(sm, tokens[13:20]), ref.decode_batch(sr, tokens[13:20])
+    ok, err = close(got, want)
+    assert ok, err
+    worst = max(worst, err)
+    # speculative rollback: truncate and continue with other tokens
+    mine.truncate(sm, 15)
+    ref.truncate(sr, 15)
+    got, want = mine.decode_batch(sm, tokens[20:28]), ref.decode_batch(sr, tokens[20:28])
+    ok, err = close(got, want)
+    assert ok, err
+    worst = max(worst, err)
+    # a second sequence interleaved with the first
+    s2m, s2r = mine.new_sequence(), ref.new_sequence()
+    for t in tokens[28:34]:
+        ok, err = close(mine.logits(s2m, t), ref.logits(s2r, t))
+        assert ok, err
+        ok, err = close(mine.logits(sm, t), ref.logits(sr, t))
+        assert ok, err
+    mine.drop_sequence(s2m)
+    ref.drop_sequence(s2r)
+    say(name, "worst relative logit error", worst)
+    mine.close()
+    ref.close()
+
+
+def errors(model, fn, *args):
+    try:
+        fn(*args)
+    except RuntimeError as e:
+        return str(e)
+    return None
+
+
+def test_sequence_semantics_match_reference(tmp_path, ref_capi):
+    spec = gf.LlamaSpec(context=24)
+    path = spec.write(tmp_path / "m.gguf")
+    # a 5-block pool of 4-token blocks: 20 tokens fit
+    mine = native.NativeModel(path, max_blocks=5, block_tokens=4)
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=5, block_tokens=4)
+    sm, sr = mine.new_sequence(), ref.new_sequence()
+    first = list(range(1, 11))
+    ok, err = close(mine.decode_batch(sm, first), ref.decode_batch(sr, first))
+    assert ok, err
+    # a batch that exhausts the pool midway fails and leaves the sequence at its entry length
+    more = list(range(20, 32))
+    em, er = errors(mine, mine.decode_batch, sm, more), errors(ref, ref.decode_batch, sr, more)
+    assert em == er and em is not None, (em, er)
+    ok, err = close(mine.logits(sm, 5), ref.logits(sr, 5))  # continues from length 10
+    assert ok, err
+    # a token outside the vocabulary anywhere in a batch: nothing is decoded
+    bad = [1, 2, spec.vocab]
+    assert errors(mine, mine.decode_batch, sm, bad) == errors(ref, ref.decode_batch, sr, bad) == "invalid batch token"
+    ok, err = close(mine.logits(sm, 6), ref.logits(sr, 6))
+    assert ok, err
+    # context: 12 cached + 13 > 24
+    long = [3] * 13
+    assert errors(mine, mine.decode_batch, sm, long) == errors(ref, ref.decode_batch, sr, long) == \
+        "batch exceeds context"
+    # unknown sequence, truncate past the end, drop twice
+    for fn_m, fn_r, args in [(mine.logits, ref.logits, (999, 1)), (mine.truncate, ref.truncate, (sm, 100)),
+                             (mine.drop_sequence, ref.drop_sequence, (999,))]:
+        a, b = errors(mine, fn_m, *args), errors(ref, fn_r, *args)
+        assert a == b and a is not None, (a, b)
+    mine.drop_sequence(sm)
+    ref.drop_sequence(sr)
+    assert errors(mine, mine.logits, sm, 1) == errors(ref, ref.logits, sr, 1)
+
+
+def test_context_limit_and_geometry(tmp_path, ref_capi):
+    spec = gf.LlamaSpec(context=6)
+    path = spec.write(tmp_path / "m.gguf")
+    mine = native.NativeModel(path, max_blocks=8, block_tokens=2)
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=8, block_tokens=2)
+    sm, sr = mine.new_sequence(), ref.new_sequence()
+    mine.decode_batch(sm, [1, 2, 3, 4, 5, 6])
+    ref.decode_batch(sr, [1, 2, 3, 4, 5, 6])
+    assert errors(mine, mine.logits, sm, 1) == errors(ref, ref.logits, sr, 1) == \
+        "paged decode exceeds token/context limits"
+    # cache geometry the reference rejects (kv.hpp:24-27)
+    for blocks, tokens in [(0, 16), (2000000, 16), (8, 0)]:
+        lm, lr = native._capi.lib(), native._capi.model_lib(ref_capi)
+        assert not lm.tvara_model_open(str(path).encode(), blocks, tokens)
+        assert not lr.tvara_model_open(str(path).encode(), blocks, tokens)
+        assert lm.tvara_last_error() == lr.tvara_last_error(), (blocks, tokens)
+
+
+def test_nonfinite_weight_rejected(tmp_path, ref_capi):
+    spec = gf.LlamaSpec()
+    tensors = spec.tensors()
+    name, dims, ttype, payload = tensors[3]
+    w = np.frombuffer(payload, "<f4").copy()
+    w[7] = np.inf
+    tensors[3] = (name, dims, ttype, w.tobytes())
+    path = tmp_path / "inf.gguf"
+    gf.write_gguf(path, spec.metadata(), tensors)
+    a = errors(None, native.NativeModel, path)
+    b = errors(None, native.NativeModel, path, ref_capi)
+    assert a == b == "nonfinite model weight"

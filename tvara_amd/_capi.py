@@ -28,6 +28,17 @@ _vp = C.c_void_p
 
 # name -> (restype, argtypes); every export of include/tvara_capi.h
 SIGNATURES = {
+    # model-level exports (c_api.h:13-24)
+    "tvara_model_open": (_vp, [C.c_char_p, _sz, _sz]),
+    "tvara_model_close": (None, [_vp]),
+    "tvara_model_vocab_size": (_sz, [_vp]),
+    "tvara_model_context_size": (_sz, [_vp]),
+    "tvara_model_metadata": (C.c_char_p, [_vp]),
+    "tvara_sequence_create": (_u64, [_vp]),
+    "tvara_sequence_decode": (C.c_int, [_vp, _u64, C.c_uint32, _fp, _sz]),
+    "tvara_sequence_drop": (C.c_int, [_vp, _u64]),
+    "tvara_sequence_decode_batch": (C.c_int, [_vp, _u64, C.POINTER(C.c_uint32), _sz, _fp, _sz]),
+    "tvara_sequence_truncate": (C.c_int, [_vp, _u64, _sz]),
     "tvara_last_error": (C.c_char_p, []),
     "tvara_last_status": (C.c_int, []),
     "tvara_kv_cache_create": (_vp, [_sz, _sz, _sz, _sz, _sz, C.c_int]),
@@ -129,6 +140,23 @@ def lib(explicit=None):
             return handle
         _lib = handle
     return _lib
+
+
+MODEL_EXPORTS = ("tvara_last_error", "tvara_model_open", "tvara_model_close", "tvara_model_vocab_size",
+                 "tvara_model_context_size", "tvara_model_metadata", "tvara_sequence_create", "tvara_sequence_decode",
+                 "tvara_sequence_drop", "tvara_sequence_decode_batch", "tvara_sequence_truncate")
+
+
+def model_lib(explicit=None):
+    """A library with the 11 model-level exports bound (this one by default, or
+    any build of that ABI given by path)."""
+    if not explicit:
+        return lib()
+    handle = C.CDLL(str(Path(explicit).resolve()))
+    for name in MODEL_EXPORTS:
+        fn = getattr(handle, name)
+        fn.restype, fn.argtypes = SIGNATURES[name]
+    return handle
 
 
 def last_error() -> str:

@@ -9,10 +9,12 @@
 #include <cstring>
 #include <limits>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "kv_cache.hpp"
+#include "model.hpp"
 
 using tvara_amd::AttnPlan;
 using tvara_amd::DeviceCache;
@@ -27,6 +29,13 @@ struct tvara_kv_cache {
 struct tvara_attn_plan {
     AttnPlan plan;
     size_t context = 0;
+};
+
+// the handle of the model-level exports (c_api.cpp:6-13): the executor and one
+// mutex held for every call that touches sequences
+struct tvara_model {
+    std::unique_ptr<tvara_amd::DeviceModel> model;
+    std::mutex mutex;
 };
 
 struct tvara_prefill_plan {
@@ -458,6 +467,152 @@ int tvara_prefill_plan_check(tvara_prefill_plan* plan) {
 }
 
 void tvara_prefill_plan_destroy(tvara_prefill_plan* plan) { delete plan; }
+
+// ------------------------------------------------------- model-level exports
+// c_api.cpp:35-78: return conventions (nullptr / 0 / -1), messages and the
+// per-handle lock are the reference's.
+
+tvara_model* tvara_model_open(const char* path, size_t blocks, size_t tokens) {
+    error_message.clear();
+    error_status = TVARA_OK;
+    try {
+        if (!path || !*path) throw std::invalid_argument("empty model path");
+        auto m = std::make_unique<tvara_model>();
+        m->model = std::make_unique<tvara_amd::DeviceModel>(path, blocks, tokens);
+        return m.release();
+    } catch (const std::exception& e) {
+        failed(TVARA_ERROR, e.what());
+        return nullptr;
+    } catch (...) {
+        failed(TVARA_ERROR, "unknown native error");
+        return nullptr;
+    }
+}
+
+void tvara_model_close(tvara_model* model) { delete model; }
+
+size_t tvara_model_vocab_size(tvara_model* model) {
+    if (!model) {
+        failed(TVARA_ERROR, "closed model");
+        return 0;
+    }
+    return model->model->config().vocab;
+}
+
+size_t tvara_model_context_size(tvara_model* model) {
+    if (!model) {
+        failed(TVARA_ERROR, "closed model");
+        return 0;
+    }
+    return model->model->config().context;
+}
+
+const char* tvara_model_metadata(tvara_model* model) {
+    if (!model) {
+        failed(TVARA_ERROR, "closed model");
+        return nullptr;
+    }
+    return model->model->metadata().c_str();
+}
+
+uint64_t tvara_sequence_create(tvara_model* model) {
+    error_message.clear();
+    error_status = TVARA_OK;
+    try {
+        if (!model) throw std::invalid_argument("closed model");
+        std::lock_guard<std::mutex> lock(model->mutex);
+        return model->model->cache().create_sequence();
+    } catch (const std::exception& e) {
+        failed(TVARA_ERROR, e.what());
+        return 0;
+    } catch (...) {
+        failed(TVARA_ERROR, "unknown native error");
+        return 0;
+    }
+}
+
+int tvara_sequence_decode(tvara_model* model, uint64_t sequence, uint32_t token, float* logits, size_t count) {
+    error_message.clear();
+    error_status = TVARA_OK;
+    try {
+        if (!model || !logits || count != model->model->config().vocab)
+            throw std::invalid_argument("invalid logit output buffer");
+        std::lock_guard<std::mutex> lock(model->mutex);
+        model->model->decode(sequence, token, logits);
+        return 0;
+    } catch (const std::exception& e) {
+        failed(TVARA_ERROR, e.what());
+        return -1;
+    } catch (...) {
+        failed(TVARA_ERROR, "unknown native error");
+        return -1;
+    }
+}
+
+int tvara_sequence_drop(tvara_model* model, uint64_t sequence) {
+    error_message.clear();
+    error_status = TVARA_OK;
+    try {
+        if (!model) throw std::invalid_argument("closed model");
+        std::lock_guard<std::mutex> lock(model->mutex);
+        model->model->cache().drop(sequence);
+        return 0;
+    } catch (const std::exception& e) {
+        failed(TVARA_ERROR, e.what());
+        return -1;
+    } catch (...) {
+        failed(TVARA_ERROR, "unknown native error");
+        return -1;
+    }
+}
+
+int tvara_sequence_decode_batch(tvara_model* model, uint64_t sequence, const uint32_t* tokens, size_t token_count,
+                                float* logits, size_t count) {
+    error_message.clear();
+    error_status = TVARA_OK;
+    try {
+        if (!model || (!tokens && token_count) || (!logits && count)) throw std::invalid_argument("invalid batch buffers");
+        const size_t vocab = model->model->config().vocab;
+        if (token_count > std::numeric_limits<size_t>::max() / vocab || count != token_count * vocab)
+            throw std::invalid_argument("invalid batch dimensions");
+        std::lock_guard<std::mutex> lock(model->mutex);
+        auto& cache = model->model->cache();
+        const size_t length = cache.sequence(sequence).length;
+        if (token_count > model->model->config().context - length) throw std::invalid_argument("batch exceeds context");
+        for (size_t i = 0; i < token_count; ++i)
+            if (tokens[i] >= vocab) throw std::invalid_argument("invalid batch token");
+        try {
+            for (size_t i = 0; i < token_count; ++i) model->model->decode(sequence, tokens[i], logits + i * vocab);
+        } catch (...) {
+            cache.truncate(sequence, length);  // no partial batch stays in the cache (c_api.cpp:68-70)
+            throw;
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        failed(TVARA_ERROR, e.what());
+        return -1;
+    } catch (...) {
+        failed(TVARA_ERROR, "unknown batch error");
+        return -1;
+    }
+}
+
+int tvara_sequence_truncate(tvara_model* model, uint64_t sequence, size_t length) {
+    error_message.clear();
+    error_status = TVARA_OK;
+    try {
+        if (!model) throw std::invalid_argument("closed model");
+        std::lock_guard<std::mutex> lock(model->mutex);
+        model->model->cache().truncate(sequence, length);
+        return 0;
+    } catch (const std::exception& e) {
+        failed(TVARA_ERROR, e.what());
+        return -1;
+    } catch (...) {
+        failed(TVARA_ERROR, "unknown truncate error");
+        return -1;
+    }
+}
 
 int tvara_profile_enable(int enabled) {
     return guard([&] { tvara_amd::profile_enable(enabled != 0); });

@@ -1,0 +1,191 @@
+// Llama decode executor on the GPU (see model.hpp).
+#include "model.hpp"
+
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+
+#include "gguf.hpp"
+
+namespace tvara_amd {
+
+void ModelConfig::validate() const {
+    // ModelConfig::validate (model.hpp:12-18)
+    if (!vocab || !hidden || !intermediate || !layers || !heads || !kv_heads || !context || hidden % heads ||
+        heads % kv_heads || (hidden / heads) % 2 || !std::isfinite(rms_epsilon) || rms_epsilon <= 0 ||
+        !std::isfinite(rope_theta) || rope_theta <= 0)
+        throw std::invalid_argument("invalid native model configuration");
+}
+
+namespace {
+
+size_t elements(const gguf::TensorInfo& t) {
+    size_t n = 1;
+    for (uint64_t d : t.dims) n *= static_cast<size_t>(d);
+    return n;
+}
+
+float* at(DeviceBuffer& b, size_t offset_floats) { return static_cast<float*>(b.ptr) + offset_floats; }
+
+}  // namespace
+
+DeviceModel::DeviceModel(const std::string& path, size_t max_blocks, size_t block_tokens) {
+    gguf::ModelFile file(path);
+    const gguf::Document& doc = file.document();
+    const gguf::LlamaShape shape = gguf::llama_shape(doc);
+    gguf::validate_llama_tensors(doc, shape);
+    cfg_.vocab = shape.vocab;
+    cfg_.hidden = shape.hidden;
+    cfg_.intermediate = shape.intermediate;
+    cfg_.layers = shape.layers;
+    cfg_.heads = shape.heads;
+    cfg_.kv_heads = shape.kv_heads;
+    cfg_.context = shape.context;
+    cfg_.rms_epsilon = static_cast<float>(shape.rms_epsilon);
+    cfg_.rope_theta = static_cast<float>(shape.rope_theta);
+    if (auto it = doc.metadata.find("tvara.rope.layout"); it != doc.metadata.end()) {
+        auto layout = std::get_if<std::string>(&it->second.data);
+        if (!layout || (*layout != "split" && *layout != "interleaved")) throw std::invalid_argument("invalid RoPE layout");
+        cfg_.interleaved_rope = *layout == "interleaved";
+    }
+    cfg_.validate();
+    const ModelConfig& c = cfg_;
+    const size_t H = c.hidden, I = c.intermediate, KV = c.kv_width();
+
+    // weights: every tensor dequantised to f32 in HBM, as load_weights does
+    // on the host (model.hpp:119-134,156-169); fused row blocks Wq|Wk|Wv and
+    // Wgate|Wup feed one matvec launch each
+    DeviceBuffer staging;
+    bad_.ensure(sizeof(int));
+    TVARA_HIP(hipMemset(bad_.ptr, 0, sizeof(int)));
+    auto load = [&](const std::string& name, float* dst) {
+        const gguf::TensorInfo& t = file.tensor(name);
+        const size_t n = elements(t), bytes = gguf::tensor_bytes(t);
+        const uint8_t* src = file.payload(t);
+        if (t.type == gguf::kF32) {
+            TVARA_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+            launch_dequant(t.type, nullptr, n, dst, static_cast<int*>(bad_.ptr), nullptr);
+        } else {
+            void* raw = staging.ensure(bytes);
+            TVARA_HIP(hipMemcpy(raw, src, bytes, hipMemcpyHostToDevice));
+            launch_dequant(t.type, static_cast<const uint8_t*>(raw), n, dst, static_cast<int*>(bad_.ptr), nullptr);
+        }
+        TVARA_HIP(hipDeviceSynchronize());
+    };
+    embedding_.ensure(c.vocab * H * sizeof(float));
+    load("token_embd.weight", at(embedding_, 0));
+    final_norm_.ensure(H * sizeof(float));
+    load("output_norm.weight", at(final_norm_, 0));
+    if (doc.tensors.count("output.weight")) {
+        has_output_ = true;
+        output_.ensure(c.vocab * H * sizeof(float));
+        load("output.weight", at(output_, 0));
+    }
+    layers_.resize(c.layers);
+    for (size_t i = 0; i < c.layers; ++i) {
+        const std::string p = "blk." + std::to_string(i) + ".";
+        Layer& L = layers_[i];
+        L.attn_norm.ensure(H * sizeof(float));
+        load(p + "attn_norm.weight", at(L.attn_norm, 0));
+        L.ffn_norm.ensure(H * sizeof(float));
+        load(p + "ffn_norm.weight", at(L.ffn_norm, 0));
+        L.qkv.ensure((H + 2 * KV) * H * sizeof(float));
+        load(p + "attn_q.weight", at(L.qkv, 0));
+        load(p + "attn_k.weight", at(L.qkv, H * H));
+        load(p + "attn_v.weight", at(L.qkv, (H + KV) * H));
+        L.out.ensure(H * H * sizeof(float));
+        load(p + "attn_output.weight", at(L.out, 0));
+        L.gate_up.ensure(2 * I * H * sizeof(float));
+        load(p + "ffn_gate.weight", at(L.gate_up, 0));
+        load(p + "ffn_up.weight", at(L.gate_up, I * H));
+        L.down.ensure(H * I * sizeof(float));
+        load(p + "ffn_down.weight", at(L.down, 0));
+    }
+    int bad = 0;
+    TVARA_HIP(hipMemcpy(&bad, bad_.ptr, sizeof(int), hipMemcpyDeviceToHost));
+    if (bad) throw std::invalid_argument("nonfinite model weight");
+
+    // the executor's cache (paged_model.hpp:8-9)
+    Geometry g;
+    g.layers = c.layers;
+    g.kv_heads = c.kv_heads;
+    g.head_dim = c.head_dim();
+    g.tokens_per_block = block_tokens;
+    g.max_blocks = max_blocks;
+    cache_ = std::make_unique<DeviceCache>(g, kF32);
+
+    x_.ensure(H * sizeof(float));
+    norm_.ensure(H * sizeof(float));
+    q_.ensure(H * sizeof(float));
+    kall_.ensure(c.layers * KV * sizeof(float));
+    vall_.ensure(c.layers * KV * sizeof(float));
+    attn_.ensure(H * sizeof(float));
+    gate_.ensure(I * sizeof(float));
+    up_.ensure(I * sizeof(float));
+    logits_.ensure(c.vocab * sizeof(float));
+    rope_.ensure(c.head_dim() * sizeof(float));
+    metadata_ = gguf::metadata_json(doc);
+}
+
+void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
+    const ModelConfig& c = cfg_;
+    const size_t position = cache_->sequence(sequence).length;
+    if (token >= c.vocab || position >= c.context)
+        throw std::invalid_argument("paged decode exceeds token/context limits");
+    hipStream_t s = cache_->stream();
+    const int H = static_cast<int>(c.hidden), I = static_cast<int>(c.intermediate);
+    const int KV = static_cast<int>(c.kv_width()), D = static_cast<int>(c.head_dim());
+    float* x = at(x_, 0);
+    float* norm = at(norm_, 0);
+    float* q = at(q_, 0);
+    float* attn = at(attn_, 0);
+    float* gate = at(gate_, 0);
+    float* up = at(up_, 0);
+
+    TVARA_HIP(hipMemcpyAsync(x, at(embedding_, token * c.hidden), c.hidden * sizeof(float), hipMemcpyDeviceToDevice, s));
+    // (cos, sin) of this position, computed as rotary() does (model.hpp:66-68)
+    auto* cs = static_cast<float*>(rope_host_.acquire(c.head_dim() * sizeof(float)));
+    for (int i = 0; i < D / 2; ++i) {
+        const float angle =
+            static_cast<float>(position) / std::pow(c.rope_theta, static_cast<float>(2 * i) / static_cast<float>(D));
+        cs[2 * i] = std::cos(angle);
+        cs[2 * i + 1] = std::sin(angle);
+    }
+    TVARA_HIP(hipMemcpyAsync(rope_.ptr, cs, c.head_dim() * sizeof(float), hipMemcpyHostToDevice, s));
+    rope_host_.release(s);
+
+    // attention rows: the cached tokens plus this token as the tail
+    // (paged_model.hpp:22; attention.hpp:80)
+    AttnPlan plan;
+    plan.build(cache_.get(), {sequence}, {position}, {1}, static_cast<int>(c.heads), 0);
+
+    for (size_t l = 0; l < c.layers; ++l) {
+        Layer& L = layers_[l];
+        float* kl = at(kall_, l * c.kv_width());
+        float* vl = at(vall_, l * c.kv_width());
+        launch_rmsnorm(x, at(L.attn_norm, 0), norm, H, c.rms_epsilon, s);
+        const MatvecSegment qkv[3] = {{q, H, nullptr}, {kl, KV, nullptr}, {vl, KV, nullptr}};
+        launch_matvec(at(L.qkv, 0), H + 2 * KV, H, norm, qkv, 3, s);
+        launch_rope(q, static_cast<int>(c.heads), kl, static_cast<int>(c.kv_heads), D, at(rope_, 0), c.interleaved_rope,
+                    s);
+        plan.launch(static_cast<int>(l), q, kl, vl, attn, s);
+        const MatvecSegment o[1] = {{x, H, x}};
+        launch_matvec(at(L.out, 0), H, H, attn, o, 1, s);
+        launch_rmsnorm(x, at(L.ffn_norm, 0), norm, H, c.rms_epsilon, s);
+        const MatvecSegment gu[2] = {{gate, I, nullptr}, {up, I, nullptr}};
+        launch_matvec(at(L.gate_up, 0), 2 * I, H, norm, gu, 2, s);
+        launch_swiglu(gate, up, I, s);
+        const MatvecSegment d[1] = {{x, H, x}};
+        launch_matvec(at(L.down, 0), H, I, gate, d, 1, s);
+    }
+    launch_rmsnorm(x, at(final_norm_, 0), norm, H, c.rms_epsilon, s);
+    const MatvecSegment lg[1] = {{at(logits_, 0), static_cast<int>(c.vocab), nullptr}};
+    launch_matvec(has_output_ ? at(output_, 0) : at(embedding_, 0), static_cast<int>(c.vocab), H, norm, lg, 1, s);
+    plan.check();  // a non-finite score fails the token before anything is appended
+    // the token's K/V for every layer, appended after all layers succeeded
+    // (paged_model.hpp:27)
+    cache_->append_batch(&sequence, 1, at(kall_, 0), at(vall_, 0), true);
+    TVARA_HIP(hipMemcpy(logits_host, logits_.ptr, c.vocab * sizeof(float), hipMemcpyDeviceToHost));
+}
+
+}  // namespace tvara_amd

@@ -1,0 +1,71 @@
+// Llama decode executor over the device KV cache: the state behind the
+// model-level C exports (core/include/tvara/c_api.h:13-24), restating
+// PagedModelExecutor (core/include/tvara/paged_model.hpp:6-34) with weights
+// in HBM and every step of a token on the GPU.
+#pragma once
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "kv_cache.hpp"
+
+namespace tvara_amd {
+
+// output rows of one matvec launch that go to one buffer (as residual + y
+// when `residual` is set)
+struct MatvecSegment {
+    float* out;
+    int rows;
+    const float* residual;
+};
+
+void launch_dequant(uint32_t type, const uint8_t* raw, size_t n, float* out, int* bad, hipStream_t s);
+void launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t s);
+void launch_matvec(const float* w, int rows, int cols, const float* v, const MatvecSegment* seg, int nseg,
+                   hipStream_t s);
+void launch_rope(float* q, int qheads, float* k, int kheads, int dim, const float* cs, bool interleaved,
+                 hipStream_t s);
+void launch_swiglu(float* gate, const float* up, int n, hipStream_t s);
+
+// ModelConfig (model.hpp:9-22)
+struct ModelConfig {
+    size_t vocab = 0, hidden = 0, intermediate = 0, layers = 0, heads = 0, kv_heads = 0, context = 0;
+    float rms_epsilon = 1e-6f, rope_theta = 10000.f;
+    bool interleaved_rope = true;
+    void validate() const;
+    size_t head_dim() const { return hidden / heads; }
+    size_t kv_width() const { return head_dim() * kv_heads; }
+};
+
+class DeviceModel {
+public:
+    // load_weights (model.hpp:140-170) + the executor's cache (paged_model.hpp:8-9)
+    DeviceModel(const std::string& path, size_t max_blocks, size_t block_tokens);
+    const ModelConfig& config() const { return cfg_; }
+    DeviceCache& cache() { return *cache_; }
+    const std::string& metadata() const { return metadata_; }
+    // PagedModelExecutor::decode (paged_model.hpp:12-28): logits of `token`
+    // at the end of `sequence`, whose K/V are then appended
+    void decode(uint64_t sequence, size_t token, float* logits_host);
+
+private:
+    struct Layer {
+        DeviceBuffer attn_norm, ffn_norm, qkv, out, gate_up, down;
+    };
+    void upload(const std::string& name, DeviceBuffer& dst, size_t offset_floats, const void* file_payload,
+                const void* info);
+
+    ModelConfig cfg_;
+    std::string metadata_;
+    std::unique_ptr<DeviceCache> cache_;
+    DeviceBuffer embedding_, output_, final_norm_;
+    bool has_output_ = false;
+    std::vector<Layer> layers_;
+    // per-token work buffers
+    DeviceBuffer x_, norm_, q_, kall_, vall_, attn_, gate_, up_, logits_, rope_, bad_;
+    PinnedBuffer rope_host_;
+};
+
+}  // namespace tvara_amd
