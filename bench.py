@@ -284,12 +284,108 @@ def bench_kv(args, cow):
     }), flush=True)
 
 
+def bench_model(args):
+    """Decode through the model-level C ABI on a Llama-3.2-1B-shaped GGUF file
+    with random Q8_0 weights (tied embedding): one sequence token by token
+    (tvara_sequence_decode), and 64 sequences stepping together
+    (tvara_sequences_decode) after a 128-token prompt each.  A step is one
+    decode of every sequence in the batch."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from tvara_amd import gguf_writer, native
+
+    spec = gguf_writer.llama32_1b()
+    tmp = Path(tempfile.mkdtemp(prefix="tvara-model-"))
+    try:
+        t0 = time.perf_counter()
+        path = spec.write(tmp / "llama32-1b-q8_0.gguf")
+        log(f"wrote {path.stat().st_size / 1e9:.2f} GB GGUF in {time.perf_counter() - t0:.1f}s")
+        nseq, prompt = 64, 128
+        t0 = time.perf_counter()
+        m = native.NativeModel(path, max_blocks=nseq * ((prompt + args.steps + args.warmup + 64) // 16 + 1) + 64,
+                               block_tokens=16)
+        log(f"loaded in {time.perf_counter() - t0:.1f}s")
+        rng = np.random.default_rng(3)
+        # one sequence, token by token
+        s1 = m.new_sequence()
+        for t in rng.integers(0, spec.vocab, 8):
+            m.logits(s1, int(t))
+        single_steps = min(args.steps, 64)
+        toks = rng.integers(0, spec.vocab, single_steps)
+        t0 = time.perf_counter()
+        for t in toks:
+            m.logits(s1, int(t))
+        single_s = (time.perf_counter() - t0) / single_steps
+        m.drop_sequence(s1)
+        # a batch of sequences
+        seqs = [m.new_sequence() for _ in range(nseq)]
+        for _ in range(prompt):
+            m.decode_sequences(seqs, rng.integers(0, spec.vocab, nseq))
+        for _ in range(args.warmup):
+            m.decode_sequences(seqs, rng.integers(0, spec.vocab, nseq))
+        steps = [rng.integers(0, spec.vocab, nseq) for _ in range(args.steps)]
+        t0 = time.perf_counter()
+        for st in steps:
+            logits = m.decode_sequences(seqs, st)
+        batch_s = (time.perf_counter() - t0) / args.steps
+        assert np.isfinite(logits).all()
+        m.close()
+        weights = spec.vocab * spec.hidden + spec.layers * (
+            spec.hidden * (spec.hidden * 2 + 2 * spec.hidden // spec.heads * spec.kv_heads) +
+            3 * spec.hidden * spec.intermediate)
+        weight_bytes = 4 * weights  # the weights as the kernels read them (f32 in HBM)
+        tps = nseq / batch_s
+        log(f"single sequence {single_s * 1e3:.2f} ms/token; {nseq} sequences {batch_s * 1e3:.2f} ms/step, "
+            f"{tps:.0f} tokens/s")
+        cpu = None
+        if not args.no_cpu_baseline:
+            from oracle import pyoracle
+
+            if pyoracle.ref_available():
+                refso = ROOT / "oracle" / "_ref" / "libtvara_ref_capi.so"
+                t0 = time.perf_counter()
+                r = native.NativeModel(path, library=str(refso), max_blocks=16, block_tokens=16)
+                log(f"reference loaded in {time.perf_counter() - t0:.1f}s")
+                rs = r.new_sequence()
+                r.logits(rs, 1)
+                t0 = time.perf_counter()
+                for t in (2, 3, 4):
+                    r.logits(rs, t)
+                cpu_s = (time.perf_counter() - t0) / 3
+                r.close()
+                cpu = {"value": round(1 / cpu_s, 4), "unit": "tokens/s", "cores": 1, "kind": "reference",
+                       "sample": f"3 tokens of one sequence through the reference's tvara_sequence_decode (its "
+                                 f"f32 executor on the calling thread); {cpu_s:.2f} s per token",
+                       "s_per_token": round(cpu_s, 4)}
+        print(json.dumps({
+            "metric": "llama-3.2-1b-shaped decode through the model-level C ABI: tokens/s, 1 MI355X",
+            "value": round(tps, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(batch_s * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic: random Q8_0 weights (numpy PCG64), random token ids",
+            "config": {"workload": "llama-3.2-1b-q8_0-decode-64seq", "sequences": nseq, "prompt": prompt,
+                       "layers": spec.layers, "hidden": spec.hidden, "heads": spec.heads,
+                       "kv_heads": spec.kv_heads, "intermediate": spec.intermediate, "vocab": spec.vocab},
+            "single_sequence_ms_per_token": round(single_s * 1e3, 4),
+            "roofline": {"bound": "hbm", "achieved": round(weight_bytes / batch_s / 1e9, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(weight_bytes / batch_s / 1e9 / HBM_PEAK_GBS, 4),
+                         "traffic": None, "kernel": "decode step (weights read once per step)",
+                         "algorithmic_bytes": weight_bytes},
+            "cpu_baseline": cpu,
+        }), flush=True)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c3cow", "c4", "c5"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c3cow", "c4", "c5", "llama1b"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -318,6 +414,8 @@ def main():
         return bench_prefill(args)
     if args.workload in ("c3", "c3cow"):
         return bench_kv(args, args.workload == "c3cow")
+    if args.workload == "llama1b":
+        return bench_model(args)
     w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5}[args.workload]()
     log(f"workload {w.name}: {w.sequences} sequences, {w.total_tokens} tokens")
     g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)

@@ -93,6 +93,16 @@ TVARA_API int tvara_sequence_decode_batch(tvara_model* model, uint64_t sequence,
                                           size_t token_count, float* logits, size_t count);
 /* c_api.cpp:76-78 (PagedCache::truncate, kv.hpp:131-136) */
 TVARA_API int tvara_sequence_truncate(tvara_model* model, uint64_t sequence, size_t length);
+
+/* One decode step for `count` distinct sequences at once: tokens[i] is decoded
+ * at the end of sequences[i] and logits[i*vocab ...] receives its logits, as
+ * tvara_sequence_decode(sequences[i], tokens[i]) would give them (the batched
+ * matvecs accumulate in f32).  Every weight row is read once for the whole
+ * batch.  All or nothing: on failure no sequence changes.  Returns 0 / -1.
+ * Replaces the per-sequence loop of NativeSchedulerBackend.decode_batch
+ * (python/tvara/scheduler.py:201-210); no counterpart in the reference ABI. */
+TVARA_API int tvara_sequences_decode(tvara_model* model, const uint64_t* sequences, const uint32_t* tokens,
+                                     size_t count, float* logits, size_t logits_count);
 /* Status of the last failed call on this thread (TVARA_OK after a success);
  * lets callers of the NULL- or 0-returning entry points tell the exception
  * classes apart.  No reference counterpart: the reference throws in C++. */

@@ -21,7 +21,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-import gguf_fixture as gf
+from tvara_amd import gguf_writer as gf
 from tvara_amd import native
 
 pytestmark = pytest.mark.gpu
@@ -171,3 +171,73 @@ def test_nonfinite_weight_rejected(tmp_path, ref_capi):
     a = errors(None, native.NativeModel, path)
     b = errors(None, native.NativeModel, path, ref_capi)
     assert a == b == "nonfinite model weight"
+
+
+@pytest.mark.parametrize("nseq", [3, 20])
+def test_sequences_decode_matches_serial_reference(tmp_path, ref_capi, nseq):
+    # one pass for many sequences (tvara_sequences_decode) against the
+    # reference decoding each sequence on its own
+    spec = gf.LlamaSpec(matrix_type=gf.T_Q8_0, hidden=128, intermediate=256, heads=8, kv_heads=2)
+    path = spec.write(tmp_path / "m.gguf")
+    mine = native.NativeModel(path, max_blocks=256, block_tokens=4)
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=256, block_tokens=4)
+    rng = np.random.default_rng(nseq)
+    sm = [mine.new_sequence() for _ in range(nseq)]
+    sr = [ref.new_sequence() for _ in range(nseq)]
+    for a, b in zip(sm, sr):  # ragged prompts, 1..9 tokens
+        prompt = [int(t) for t in rng.integers(0, spec.vocab, int(rng.integers(1, 10)))]
+        ok, err = close(mine.decode_batch(a, prompt), ref.decode_batch(b, prompt))
+        assert ok, err
+    worst = 0.0
+    for step in range(4):
+        toks = [int(t) for t in rng.integers(0, spec.vocab, nseq)]
+        got = mine.decode_sequences(sm, toks)
+        for i, (b, t) in enumerate(zip(sr, toks)):
+            ok, err = close(got[i], ref.logits(b, t))
+            worst = max(worst, err)
+            assert ok, (step, i, err)
+    say("sequences_decode", nseq, "worst relative logit error", worst)
+
+
+def test_sequences_decode_all_or_nothing(tmp_path, ref_capi):
+    spec = gf.LlamaSpec(context=12)
+    path = spec.write(tmp_path / "m.gguf")
+    mine = native.NativeModel(path, max_blocks=6, block_tokens=4)
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=6, block_tokens=4)
+    a, b, c = mine.new_sequence(), mine.new_sequence(), mine.new_sequence()
+    ra, rb, rc = ref.new_sequence(), ref.new_sequence(), ref.new_sequence()
+    for s, r, n in [(a, ra, 4), (b, rb, 8), (c, rc, 11)]:
+        ok, err = close(mine.decode_batch(s, list(range(1, n + 1))), ref.decode_batch(r, list(range(1, n + 1))))
+        assert ok, err
+    assert mine.decode_sequences([], []).shape == (0, spec.vocab)
+    # duplicate sequence, a token past the vocabulary, a full context (c at 11 -> 12 ok, then 12 -> fail)
+    assert errors(mine, mine.decode_sequences, [a, a], [1, 2]) == "duplicate sequence in decode batch"
+    assert errors(mine, mine.decode_sequences, [a, b], [1, spec.vocab]) == "paged decode exceeds token/context limits"
+    # the pool: a (4 tokens, 1 block) + b (8, 2) + c (11, 3) = all 6 blocks.  In the
+    # order [c, b, a], c's row fits its tail block and is appended, then b needs a
+    # new block: the pool is exhausted, and c must be rolled back
+    e = errors(mine, mine.decode_sequences, [c, b, a], [5, 6, 7])
+    assert e == errors(ref, ref.logits, rb, 6), e
+    ok, err = close(mine.decode_sequences([c], [5]), ref.logits(rc, 5)[None])  # c continues at 11
+    assert ok, err
+    mine.drop_sequence(a)
+    ref.drop_sequence(ra)
+    ok, err = close(mine.decode_sequences([b], [6]), ref.logits(rb, 6)[None])  # b continues at 8
+    assert ok, err
+    assert errors(mine, mine.decode_sequences, [c, b], [1, 2]) == "paged decode exceeds token/context limits"
+
+
+def test_sequences_decode_odd_width_falls_back(tmp_path, ref_capi):
+    # hidden 40 is not a multiple of the batched kernels' 32-column tiles: the
+    # batch runs sequence by sequence with the same all-or-nothing contract
+    spec = gf.LlamaSpec(hidden=40, intermediate=72, heads=4, kv_heads=2)
+    path = spec.write(tmp_path / "odd.gguf")
+    mine = native.NativeModel(path, max_blocks=32, block_tokens=4)
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=32, block_tokens=4)
+    sm = [mine.new_sequence() for _ in range(3)]
+    sr = [ref.new_sequence() for _ in range(3)]
+    for step in range(3):
+        toks = [step + 1, step + 5, step + 9]
+        got = mine.decode_sequences(sm, toks)
+        ok, err = close(got, np.stack([ref.logits(r, t) for r, t in zip(sr, toks)]))
+        assert ok, err

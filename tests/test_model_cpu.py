@@ -10,11 +10,8 @@ import struct
 import numpy as np
 import pytest
 
-import gguf_fixture as gf
+from tvara_amd import gguf_writer as gf
 from tvara_amd import native
-
-REF_CAPI = None
-
 
 @pytest.fixture(scope="module")
 def ref_capi():
@@ -52,10 +49,6 @@ def test_reference_accepts_q4_k(tmp_path, ref_capi):
     spec = gf.LlamaSpec(matrix_type=gf.T_Q4_K, hidden=256, intermediate=512)
     m = native.NativeModel(spec.write(tmp_path / "k.gguf"), library=ref_capi)
     assert np.isfinite(m.logits(m.new_sequence(), 3)).all()
-
-
-def _spec_file(tmp_path, name, **kw):
-    return gf.LlamaSpec(**kw).write(tmp_path / name)
 
 
 def _meta_file(tmp_path, name, replace=None, drop=(), extra=()):
@@ -147,15 +140,16 @@ def malformed(tmp_path):
     def dup(ts):
         return ts + [ts[0]]
 
+    def grow_last(ts):  # the last tensor claims 64 times its payload
+        return [(n, [d[0] * 64] + d[1:] if n == ts[-1][0] else d, ty, p) for n, d, ty, p in ts]
+
     cases += [
         ("missing tensor", _tensor_file(tmp_path, "af", drop_tensor("blk.1.ffn_down.weight"))),
         ("malformed tensor", _tensor_file(tmp_path, "ag", reshape("blk.0.attn_k.weight", [64, 64]))),
         ("duplicate tensor", _tensor_file(tmp_path, "ah", dup)),
         ("unsupported storage", _tensor_file(tmp_path, "ai", retype("blk.0.attn_q.weight", 3))),
         ("quantized row width", _tensor_file(tmp_path, "aj", retype("blk.0.attn_q.weight", gf.T_Q4_K))),
-        ("payload past end", _tensor_file(tmp_path, "ak", retype("output_norm.weight", gf.T_F32) if False else
-                                          (lambda ts: [(n, [d[0] * 64] + d[1:] if n == ts[-1][0] else d, ty, p)
-                                                       for n, d, ty, p in ts]))),
+        ("payload past end", _tensor_file(tmp_path, "ak", grow_last)),
     ]
     # unaligned offset and overlapping payloads: patch the offset of the first tensor
     path = tmp_path / "al"

@@ -39,6 +39,7 @@ SIGNATURES = {
     "tvara_sequence_drop": (C.c_int, [_vp, _u64]),
     "tvara_sequence_decode_batch": (C.c_int, [_vp, _u64, C.POINTER(C.c_uint32), _sz, _fp, _sz]),
     "tvara_sequence_truncate": (C.c_int, [_vp, _u64, _sz]),
+    "tvara_sequences_decode": (C.c_int, [_vp, C.POINTER(_u64), C.POINTER(C.c_uint32), _sz, _fp, _sz]),
     "tvara_last_error": (C.c_char_p, []),
     "tvara_last_status": (C.c_int, []),
     "tvara_kv_cache_create": (_vp, [_sz, _sz, _sz, _sz, _sz, C.c_int]),

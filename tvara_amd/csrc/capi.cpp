@@ -614,6 +614,30 @@ int tvara_sequence_truncate(tvara_model* model, uint64_t sequence, size_t length
     }
 }
 
+int tvara_sequences_decode(tvara_model* model, const uint64_t* sequences, const uint32_t* tokens, size_t count,
+                           float* logits, size_t logits_count) {
+    error_message.clear();
+    error_status = TVARA_OK;
+    try {
+        if (!model || (count && (!sequences || !tokens || !logits))) throw std::invalid_argument("invalid batch buffers");
+        const size_t vocab = model->model->config().vocab;
+        if (count > std::numeric_limits<size_t>::max() / vocab || logits_count != count * vocab)
+            throw std::invalid_argument("invalid batch dimensions");
+        std::lock_guard<std::mutex> lock(model->mutex);
+        if (count == 1)
+            model->model->decode(sequences[0], tokens[0], logits);
+        else
+            model->model->decode_many(sequences, tokens, count, logits);
+        return 0;
+    } catch (const std::exception& e) {
+        failed(TVARA_ERROR, e.what());
+        return -1;
+    } catch (...) {
+        failed(TVARA_ERROR, "unknown batch error");
+        return -1;
+    }
+}
+
 int tvara_profile_enable(int enabled) {
     return guard([&] { tvara_amd::profile_enable(enabled != 0); });
 }

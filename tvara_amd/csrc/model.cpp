@@ -1,8 +1,10 @@
 // Llama decode executor on the GPU (see model.hpp).
 #include "model.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <limits>
 #include <stdexcept>
 
 #include "gguf.hpp"
@@ -186,6 +188,122 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
     // (paged_model.hpp:27)
     cache_->append_batch(&sequence, 1, at(kall_, 0), at(vall_, 0), true);
     TVARA_HIP(hipMemcpy(logits_host, logits_.ptr, c.vocab * sizeof(float), hipMemcpyDeviceToHost));
+}
+
+void DeviceModel::ensure_batch(size_t n) {
+    if (n <= batch_cap_) return;
+    const ModelConfig& c = cfg_;
+    const size_t H = c.hidden, I = c.intermediate, KV = c.kv_width(), L = c.layers, F = sizeof(float);
+    bx_.ensure(n * H * F);
+    bnorm_.ensure(n * H * F);
+    bq_.ensure(n * H * F);
+    bk_.ensure(L * n * KV * F);
+    bv_.ensure(L * n * KV * F);
+    bkapp_.ensure(n * L * KV * F);
+    bvapp_.ensure(n * L * KV * F);
+    battn_.ensure(n * H * F);
+    bgate_.ensure(n * I * F);
+    bup_.ensure(n * I * F);
+    blogits_.ensure(n * c.vocab * F);
+    brope_.ensure(n * c.head_dim() * F);
+    btok_.ensure(n * sizeof(uint32_t));
+    batch_cap_ = n;
+}
+
+void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens, size_t n, float* logits_host) {
+    if (!n) return;
+    const ModelConfig& c = cfg_;
+    std::vector<uint64_t> seqs(sequences, sequences + n);
+    std::vector<size_t> positions(n);
+    {
+        std::vector<uint64_t> sorted = seqs;
+        std::sort(sorted.begin(), sorted.end());
+        if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end())
+            throw std::invalid_argument("duplicate sequence in decode batch");
+    }
+    for (size_t i = 0; i < n; ++i) {
+        positions[i] = cache_->sequence(seqs[i]).length;
+        if (tokens[i] >= c.vocab || positions[i] >= c.context)
+            throw std::invalid_argument("paged decode exceeds token/context limits");
+    }
+    if (n > static_cast<size_t>(std::numeric_limits<int>::max() / std::max<size_t>(c.vocab, c.hidden)))
+        throw std::invalid_argument("decode batch too large");
+    if (c.hidden % 32 || c.intermediate % 32) {
+        // the batched matvec tiles K by 32: decode the sequences one by one
+        size_t done = 0;
+        try {
+            for (; done < n; ++done) decode(seqs[done], tokens[done], logits_host + done * c.vocab);
+        } catch (...) {
+            for (size_t i = 0; i < done; ++i) cache_->truncate(seqs[i], positions[i]);
+            throw;
+        }
+        return;
+    }
+    ensure_batch(n);
+    hipStream_t s = cache_->stream();
+    const int N = static_cast<int>(n);
+    const int H = static_cast<int>(c.hidden), I = static_cast<int>(c.intermediate);
+    const int KV = static_cast<int>(c.kv_width()), D = static_cast<int>(c.head_dim());
+    float* x = at(bx_, 0);
+    float* norm = at(bnorm_, 0);
+    float* q = at(bq_, 0);
+    float* attn = at(battn_, 0);
+    float* gate = at(bgate_, 0);
+    float* up = at(bup_, 0);
+
+    // tokens and each row's (cos, sin) go up through one pinned staging area
+    const size_t tok_bytes = (n * sizeof(uint32_t) + 15) / 16 * 16;
+    auto* host = static_cast<char*>(bhost_.acquire(tok_bytes + n * c.head_dim() * sizeof(float)));
+    std::memcpy(host, tokens, n * sizeof(uint32_t));
+    auto* cs = reinterpret_cast<float*>(host + tok_bytes);
+    for (size_t j = 0; j < n; ++j)
+        for (int i = 0; i < D / 2; ++i) {
+            const float angle = static_cast<float>(positions[j]) /
+                                std::pow(c.rope_theta, static_cast<float>(2 * i) / static_cast<float>(D));
+            cs[j * D + 2 * i] = std::cos(angle);
+            cs[j * D + 2 * i + 1] = std::sin(angle);
+        }
+    TVARA_HIP(hipMemcpyAsync(btok_.ptr, host, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    TVARA_HIP(hipMemcpyAsync(brope_.ptr, cs, n * c.head_dim() * sizeof(float), hipMemcpyHostToDevice, s));
+    bhost_.release(s);
+    launch_gather_embedding(at(embedding_, 0), static_cast<const uint32_t*>(btok_.ptr), N, H, x, s);
+
+    AttnPlan plan;
+    plan.build(cache_.get(), seqs, positions, std::vector<uint8_t>(n, 1), static_cast<int>(c.heads), 0);
+    for (size_t l = 0; l < c.layers; ++l) {
+        Layer& L = layers_[l];
+        float* kl = at(bk_, l * n * c.kv_width());
+        float* vl = at(bv_, l * n * c.kv_width());
+        launch_rmsnorm(x, at(L.attn_norm, 0), norm, H, c.rms_epsilon, s, N);
+        const MatvecSegment qkv[3] = {{q, H, nullptr}, {kl, KV, nullptr}, {vl, KV, nullptr}};
+        launch_batch_matvec(at(L.qkv, 0), H + 2 * KV, H, norm, N, qkv, 3, bwork_, s);
+        launch_rope(q, static_cast<int>(c.heads), kl, static_cast<int>(c.kv_heads), D, at(brope_, 0),
+                    c.interleaved_rope, s, N);
+        plan.launch(static_cast<int>(l), q, kl, vl, attn, s);
+        const MatvecSegment o[1] = {{x, H, x}};
+        launch_batch_matvec(at(L.out, 0), H, H, attn, N, o, 1, bwork_, s);
+        launch_rmsnorm(x, at(L.ffn_norm, 0), norm, H, c.rms_epsilon, s, N);
+        const MatvecSegment gu[2] = {{gate, I, nullptr}, {up, I, nullptr}};
+        launch_batch_matvec(at(L.gate_up, 0), 2 * I, H, norm, N, gu, 2, bwork_, s);
+        launch_swiglu(gate, up, N * I, s);
+        const MatvecSegment d[1] = {{x, H, x}};
+        launch_batch_matvec(at(L.down, 0), H, I, gate, N, d, 1, bwork_, s);
+    }
+    launch_rmsnorm(x, at(final_norm_, 0), norm, H, c.rms_epsilon, s, N);
+    const MatvecSegment lg[1] = {{at(blogits_, 0), static_cast<int>(c.vocab), nullptr}};
+    launch_batch_matvec(has_output_ ? at(output_, 0) : at(embedding_, 0), static_cast<int>(c.vocab), H, norm, N, lg, 1,
+                        bwork_, s);
+    plan.check();
+    launch_interleave_layers(at(bk_, 0), at(bkapp_, 0), static_cast<int>(c.layers), N, KV, s);
+    launch_interleave_layers(at(bv_, 0), at(bvapp_, 0), static_cast<int>(c.layers), N, KV, s);
+    size_t applied = 0;
+    try {
+        cache_->append_batch(seqs.data(), n, at(bkapp_, 0), at(bvapp_, 0), true, &applied);
+    } catch (...) {
+        for (size_t i = 0; i < applied; ++i) cache_->truncate(seqs[i], positions[i]);  // all or nothing
+        throw;
+    }
+    TVARA_HIP(hipMemcpy(logits_host, blogits_.ptr, n * c.vocab * sizeof(float), hipMemcpyDeviceToHost));
 }
 
 }  // namespace tvara_amd

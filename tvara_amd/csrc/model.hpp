@@ -22,11 +22,19 @@ struct MatvecSegment {
 };
 
 void launch_dequant(uint32_t type, const uint8_t* raw, size_t n, float* out, int* bad, hipStream_t s);
-void launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t s);
+// `rows` rows of a batch, each normalised on its own
+void launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t s, int rows = 1);
 void launch_matvec(const float* w, int rows, int cols, const float* v, const MatvecSegment* seg, int nseg,
                    hipStream_t s);
+// W applied to n vectors x[j] (row-major [n][cols]); segment s of output j at
+// seg[s].out + j * seg[s].rows
+void launch_batch_matvec(const float* w, int rows, int cols, const float* x, int n, const MatvecSegment* seg, int nseg,
+                         DeviceBuffer& work, hipStream_t s);
+void launch_interleave_layers(const float* src, float* dst, int layers, int n, int kv, hipStream_t s);
+void launch_gather_embedding(const float* table, const uint32_t* idx, int n, int h, float* out, hipStream_t s);
+// row j of a batch rotates q + j*qheads*dim and k + j*kheads*dim by cs + j*dim
 void launch_rope(float* q, int qheads, float* k, int kheads, int dim, const float* cs, bool interleaved,
-                 hipStream_t s);
+                 hipStream_t s, int rows = 1);
 void launch_swiglu(float* gate, const float* up, int n, hipStream_t s);
 
 // ModelConfig (model.hpp:9-22)
@@ -49,13 +57,14 @@ public:
     // PagedModelExecutor::decode (paged_model.hpp:12-28): logits of `token`
     // at the end of `sequence`, whose K/V are then appended
     void decode(uint64_t sequence, size_t token, float* logits_host);
+    // one token for each of n distinct sequences in one pass: the logits of n
+    // independent decode() calls; on failure no sequence changes
+    void decode_many(const uint64_t* sequences, const uint32_t* tokens, size_t n, float* logits_host);
 
 private:
     struct Layer {
         DeviceBuffer attn_norm, ffn_norm, qkv, out, gate_up, down;
     };
-    void upload(const std::string& name, DeviceBuffer& dst, size_t offset_floats, const void* file_payload,
-                const void* info);
 
     ModelConfig cfg_;
     std::string metadata_;
@@ -66,6 +75,11 @@ private:
     // per-token work buffers
     DeviceBuffer x_, norm_, q_, kall_, vall_, attn_, gate_, up_, logits_, rope_, bad_;
     PinnedBuffer rope_host_;
+    // batch work buffers, grown to the largest batch seen
+    DeviceBuffer bx_, bnorm_, bq_, bk_, bv_, bkapp_, bvapp_, battn_, bgate_, bup_, blogits_, brope_, btok_, bwork_;
+    PinnedBuffer bhost_;
+    size_t batch_cap_ = 0;
+    void ensure_batch(size_t n);
 };
 
 }  // namespace tvara_amd

@@ -100,6 +100,8 @@ __global__ void q4_k_kernel(const uint8_t* raw, size_t n, float* out, int* bad) 
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const float* w, float* out, int n, float eps) {
     __shared__ double part[1024 / 64];
     __shared__ float inv;
+    x += static_cast<size_t>(blockIdx.x) * n;  // one workgroup per row of a batch
+    out += static_cast<size_t>(blockIdx.x) * n;
     double sum = 0;
     for (int i = threadIdx.x; i < n; i += blockDim.x) sum += static_cast<double>(x[i]) * x[i];
     for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
@@ -158,6 +160,135 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(const MatvecArgs a) {
     out[r] = a.seg[s].residual ? __fadd_rn(a.seg[s].residual[r], y) : y;
 }
 
+// Y[j] = W X[j] for a batch of vectors (one per sequence), as a skinny GEMM:
+// a workgroup owns 64 rows of W and up to 64 vectors; K advances in chunks
+// of 32 columns staged in LDS (W tile [64][32], X tile [64][32], double
+// buffered), and each thread accumulates a 4-row x 4-vector micro-tile in
+// f32.  Every weight is read from HBM once per launch; the X tile comes from
+// L2.
+constexpr int kTileRows = 64, kTileVecs = 64, kTileK = 32;
+
+struct BatchMatvecArgs {
+    const float* w;
+    const float* x;  // [n][cols]
+    int rows, cols, n;
+    MatvecSegment seg[3];  // output j of segment s: seg.out[j * seg.rows + r]
+    int nseg;
+    int chunks_per_split;  // K chunks of kTileK per blockIdx.y
+    float* partial;        // split-K: [gridDim.y][n][rows] partial sums, else null
+};
+
+__global__ __launch_bounds__(256) void batch_matvec_kernel(const BatchMatvecArgs a) {
+    __shared__ float ws[2][kTileRows][kTileK + 4];
+    __shared__ float xs[2][kTileVecs][kTileK + 4];
+    const int t = threadIdx.x;
+    const int row0 = blockIdx.x * kTileRows;
+    // staging map: thread t copies float4 (t % 8) of rows t/8 and t/8 + 32
+    const int sc = (t % 8) * 4, sr = t / 8;
+    // micro-tile: rows 4*(t%16) .. +3, vectors 4*(t/16) .. +3
+    const int mr = (t % 16) * 4, mv = (t / 16) * 4;
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    auto stage = [&](int buf, int k0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = sr + 32 * h;
+            float4 w = make_float4(0.f, 0.f, 0.f, 0.f), x = w;
+            if (row0 + r < a.rows) w = *reinterpret_cast<const float4*>(a.w + static_cast<size_t>(row0 + r) * a.cols + k0 + sc);
+            if (r < a.n) x = *reinterpret_cast<const float4*>(a.x + static_cast<size_t>(r) * a.cols + k0 + sc);
+            *reinterpret_cast<float4*>(&ws[buf][r][sc]) = w;
+            *reinterpret_cast<float4*>(&xs[buf][r][sc]) = x;
+        }
+    };
+    const int kbeg = blockIdx.y * a.chunks_per_split;
+    const int nk = min(a.cols / kTileK - kbeg, a.chunks_per_split);
+    stage(0, kbeg * kTileK);
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+        const int buf = kc & 1;
+        if (kc + 1 < nk) stage(buf ^ 1, (kbeg + kc + 1) * kTileK);
+#pragma unroll
+        for (int k = 0; k < kTileK; k += 4) {
+            float4 w4[4], x4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w4[i] = *reinterpret_cast<const float4*>(&ws[buf][mr + i][k]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) x4[j] = *reinterpret_cast<const float4*>(&xs[buf][mv + j][k]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = fmaf(w4[i].x, x4[j].x, acc[i][j]);
+                    acc[i][j] = fmaf(w4[i].y, x4[j].y, acc[i][j]);
+                    acc[i][j] = fmaf(w4[i].z, x4[j].z, acc[i][j]);
+                    acc[i][j] = fmaf(w4[i].w, x4[j].w, acc[i][j]);
+                }
+        }
+        __syncthreads();
+    }
+    if (a.partial) {  // split-K: the fixed-order sum happens in split_sum_kernel
+        float* p = a.partial + static_cast<size_t>(blockIdx.y) * a.n * a.rows;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (row0 + mr + i < a.rows && mv + j < a.n)
+                    p[static_cast<size_t>(mv + j) * a.rows + row0 + mr + i] = acc[i][j];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = row0 + mr + i;
+        if (row >= a.rows) break;
+        int rr = row, sg = 0;
+        while (sg + 1 < a.nseg && rr >= a.seg[sg].rows) rr -= a.seg[sg++].rows;
+        const MatvecSegment& S = a.seg[sg];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (mv + j >= a.n) break;
+            const size_t at = static_cast<size_t>(mv + j) * S.rows + rr;
+            S.out[at] = S.residual ? __fadd_rn(S.residual[at], acc[i][j]) : acc[i][j];
+        }
+    }
+}
+
+// y[j][r] = sum over splits s (in order) of partial[s][j][r], to the segments
+__global__ void split_sum_kernel(const BatchMatvecArgs a, int splits) {
+    const size_t total = static_cast<size_t>(a.n) * a.rows;
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        float sum = 0.f;
+        for (int sp = 0; sp < splits; ++sp) sum += a.partial[static_cast<size_t>(sp) * total + i];
+        const int j = static_cast<int>(i / a.rows);
+        int rr = static_cast<int>(i % a.rows), sg = 0;
+        while (sg + 1 < a.nseg && rr >= a.seg[sg].rows) rr -= a.seg[sg++].rows;
+        const MatvecSegment& S = a.seg[sg];
+        const size_t at = static_cast<size_t>(j) * S.rows + rr;
+        S.out[at] = S.residual ? __fadd_rn(S.residual[at], sum) : sum;
+    }
+}
+
+// out[j] = table[idx[j]] (embedding rows of a batch)
+__global__ void gather_embedding_kernel(const float* table, const uint32_t* idx, int n, int h, float* out) {
+    const size_t total = static_cast<size_t>(n) * h;
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        out[i] = table[static_cast<size_t>(idx[i / h]) * h + i % h];
+}
+
+// [layers][n][kv] -> [n][layers][kv] (one token row per sequence for the append)
+__global__ void interleave_layers_kernel(const float* src, float* dst, int layers, int n, int kv) {
+    const size_t total = static_cast<size_t>(layers) * n * kv;
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const size_t e = i % kv, j = (i / kv) % n, l = i / (static_cast<size_t>(kv) * n);
+        dst[(j * layers + l) * kv + e] = src[i];
+    }
+}
+
 // ------------------------------------------------------------- RoPE
 
 // rotate pair i of every head of q and k by the (cos, sin) of this position
@@ -166,6 +297,10 @@ __global__ void rope_kernel(float* q, int qheads, float* k, int kheads, int dim,
     const int half = dim / 2;
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (qheads + kheads) * half) return;
+    // row blockIdx.y of a batch: its own position's (cos, sin)
+    q += static_cast<size_t>(blockIdx.y) * qheads * dim;
+    k += static_cast<size_t>(blockIdx.y) * kheads * dim;
+    cs += static_cast<size_t>(blockIdx.y) * dim;
     const int h = t / half, i = t % half;
     float* x = h < qheads ? q + static_cast<size_t>(h) * dim : k + static_cast<size_t>(h - qheads) * dim;
     const int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : i + half;
@@ -211,8 +346,51 @@ void launch_dequant(uint32_t type, const uint8_t* raw, size_t n, float* out, int
     TVARA_HIP(hipGetLastError());
 }
 
-void launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t s) {
-    launch("model_rmsnorm", rmsnorm_kernel, dim3(1), dim3(1024), 0, s, x, w, out, n, eps);
+void launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t s, int rows) {
+    launch("model_rmsnorm", rmsnorm_kernel, dim3(rows), dim3(1024), 0, s, x, w, out, n, eps);
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_batch_matvec(const float* w, int rows, int cols, const float* x, int n, const MatvecSegment* seg, int nseg,
+                         DeviceBuffer& work, hipStream_t s) {
+    if (cols % kTileK) throw std::invalid_argument("batched matvec needs a row width divisible by 32");
+    const int tiles = (rows + kTileRows - 1) / kTileRows, chunks = cols / kTileK;
+    // split K until the launch has about 512 workgroups (two per CU)
+    const int want = std::max(1, std::min(chunks, (512 + tiles - 1) / tiles));
+    const int per = (chunks + want - 1) / want, splits = (chunks + per - 1) / per;
+    for (int j0 = 0; j0 < n; j0 += kTileVecs) {
+        BatchMatvecArgs a{};
+        a.w = w;
+        a.x = x + static_cast<size_t>(j0) * cols;
+        a.rows = rows;
+        a.cols = cols;
+        a.n = std::min(kTileVecs, n - j0);
+        a.nseg = nseg;
+        a.chunks_per_split = per;
+        for (int i = 0; i < nseg; ++i) {
+            a.seg[i] = seg[i];
+            a.seg[i].out = seg[i].out + static_cast<size_t>(j0) * seg[i].rows;
+            if (seg[i].residual) a.seg[i].residual = seg[i].residual + static_cast<size_t>(j0) * seg[i].rows;
+        }
+        if (splits > 1) a.partial = static_cast<float*>(work.ensure(static_cast<size_t>(splits) * a.n * rows * sizeof(float)));
+        launch("model_matvec", batch_matvec_kernel, dim3(tiles, splits), dim3(256), 0, s, a);
+        if (splits > 1)
+            launch("model_matvec_sum", split_sum_kernel, dim3(grid_for(static_cast<size_t>(a.n) * rows)), dim3(kThreads),
+                   0, s, a, splits);
+    }
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_gather_embedding(const float* table, const uint32_t* idx, int n, int h, float* out, hipStream_t s) {
+    launch("model_embedding", gather_embedding_kernel, dim3(grid_for(static_cast<size_t>(n) * h)), dim3(kThreads), 0, s,
+           table, idx, n, h, out);
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_interleave_layers(const float* src, float* dst, int layers, int n, int kv, hipStream_t s) {
+    const size_t total = static_cast<size_t>(layers) * n * kv;
+    launch("model_interleave", interleave_layers_kernel, dim3(grid_for(total)), dim3(kThreads), 0, s, src, dst, layers,
+           n, kv);
     TVARA_HIP(hipGetLastError());
 }
 
@@ -234,10 +412,10 @@ void launch_matvec(const float* w, int rows, int cols, const float* v, const Mat
 }
 
 void launch_rope(float* q, int qheads, float* k, int kheads, int dim, const float* cs, bool interleaved,
-                 hipStream_t s) {
+                 hipStream_t s, int rows) {
     const int n = (qheads + kheads) * (dim / 2);
-    launch("model_rope", rope_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, s, q, qheads, k, kheads,
-           dim, cs, interleaved ? 1 : 0);
+    launch("model_rope", rope_kernel, dim3((n + kThreads - 1) / kThreads, rows), dim3(kThreads), 0, s, q, qheads, k,
+           kheads, dim, cs, interleaved ? 1 : 0);
     TVARA_HIP(hipGetLastError());
 }
 

@@ -1,21 +1,21 @@
-"""Synthetic Llama GGUF files for the model-level tests.
+"""GGUF writer and synthetic Llama models (for the model-level tests and the
+model benchmark).
 
 Writes GGUF v3 (little-endian): header, metadata key/values, tensor infos,
 padding to the alignment, then the tensor payloads at aligned offsets -- the
-layout core/include/tvara/gguf.hpp:43-209 reads.  Weights are random and
-seeded (tvara_amd.synth); every storage type the reference's model loader
-accepts (f32, f16, Q4_0, Q8_0, Q4_K; model.hpp:119-134) can be chosen per
-tensor class.
+layout core/include/tvara/gguf.hpp:43-209 reads.  Synthetic weights are
+random, seeded per tensor (numpy's PCG64 keyed by seed and tensor name); every
+storage type the reference's model loader accepts (f32, f16, Q4_0, Q8_0, Q4_K;
+model.hpp:119-134) can be chosen per tensor class.
 """
 
 from __future__ import annotations
 
 import struct
+import zlib
 from dataclasses import dataclass, field
 
 import numpy as np
-
-from tvara_amd import synth
 
 # GGUF metadata value types
 U8, I8, U16, I16, U32, I32, F32, BOOL, STR, ARR, U64, I64, F64 = range(13)
@@ -44,24 +44,42 @@ def _value(vtype: int, value) -> bytes:
     return struct.pack(_SCALAR[vtype], value)
 
 
+class Lazy:
+    """A payload of known size generated while the file is written."""
+
+    def __init__(self, size, make):
+        self.size, self.make = size, make
+
+    def __call__(self):
+        data = self.make()
+        assert len(data) == self.size
+        return data
+
+
 def write_gguf(path, metadata, tensors, alignment=32, version=3):
     """metadata: list of (key, type, value); tensors: list of (name, dims,
-    storage type, payload bytes), dims fastest-first."""
-    head = b"GGUF" + struct.pack("<IQQ", version, len(tensors), len(metadata))
+    storage type, payload), dims fastest-first; a payload is bytes or a Lazy."""
+    parts = [b"GGUF" + struct.pack("<IQQ", version, len(tensors), len(metadata))]
     for key, vtype, value in metadata:
-        head += _str(key) + struct.pack("<I", vtype) + _value(vtype, value)
-    offset, infos = 0, []
+        parts.append(_str(key) + struct.pack("<I", vtype) + _value(vtype, value))
+    offset = 0
     for name, dims, ttype, payload in tensors:
-        infos.append(_str(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        size = payload.size if isinstance(payload, Lazy) else len(payload)
+        parts.append(_str(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
                      + struct.pack("<IQ", ttype, offset))
-        offset += (len(payload) + alignment - 1) // alignment * alignment
-    head += b"".join(infos)
-    head += b"\0" * ((-len(head)) % alignment)
-    body = b""
-    for _, _, _, payload in tensors:
-        body += payload + b"\0" * ((-len(payload)) % alignment)
+        offset += (size + alignment - 1) // alignment * alignment
+    head = b"".join(parts)
     with open(path, "wb") as f:
-        f.write(head + body)
+        f.write(head + b"\0" * ((-len(head)) % alignment))
+        for _, _, _, payload in tensors:
+            data = payload() if isinstance(payload, Lazy) else payload
+            f.write(data)
+            f.write(b"\0" * ((-len(data)) % alignment))
+
+
+def _payload_size(ttype, dims):
+    n = int(np.prod(dims))
+    return {T_F32: 4 * n, T_F16: 2 * n, T_Q8_0: n // 32 * 34, T_Q4_0: n // 32 * 18, T_Q4_K: n // 256 * 144}[ttype]
 
 
 # ------------------------------------------------------------ payloads
@@ -70,39 +88,36 @@ def _f16_bits(x):
     return np.asarray(x, np.float16).view(np.uint16)
 
 
+def _rng(seed, tag):
+    return np.random.default_rng([seed, zlib.crc32(tag.encode())])
+
+
 def payload(ttype, rows, cols, seed, tag, scale):
     """Random weights of shape [rows][cols] in storage type ttype."""
     n = rows * cols
+    g = _rng(seed, tag)
     if ttype == T_F32:
-        return (synth.normal(seed, tag, n) * np.float32(scale)).astype("<f4").tobytes()
+        return (g.standard_normal(n, np.float32) * np.float32(scale)).astype("<f4").tobytes()
     if ttype == T_F16:
-        return (synth.normal(seed, tag, n) * np.float32(scale)).astype("<f2").tobytes()
-    u = synth.uniform(seed, tag + "/d", n // 32 + 1)
+        return (g.standard_normal(n, np.float32) * np.float32(scale)).astype("<f2").tobytes()
     if ttype == T_Q8_0:
         groups = n // 32
-        d = _f16_bits(scale / 64.0 * (0.5 + u[:groups]))
-        q = (synth.integers(seed, tag + "/q", n, 0, 255) - 127).astype(np.int8).reshape(groups, 32)
-        blk = np.zeros((groups, 34), np.uint8)
-        blk[:, 0:2] = d.astype("<u2").view(np.uint8).reshape(groups, 2)
-        blk[:, 2:] = q.view(np.uint8)
+        blk = np.empty((groups, 34), np.uint8)
+        blk[:, 0:2] = _f16_bits(scale / 64.0 * (0.5 + g.random(groups))).astype("<u2").view(np.uint8).reshape(groups, 2)
+        blk[:, 2:] = g.integers(-127, 128, (groups, 32), dtype=np.int8).view(np.uint8)
         return blk.tobytes()
     if ttype == T_Q4_0:
         groups = n // 32
-        d = _f16_bits(scale / 4.0 * (0.5 + u[:groups]))
-        nib = synth.integers(seed, tag + "/q", groups * 16, 0, 255).astype(np.uint8).reshape(groups, 16)
-        blk = np.zeros((groups, 18), np.uint8)
-        blk[:, 0:2] = d.astype("<u2").view(np.uint8).reshape(groups, 2)
-        blk[:, 2:] = nib
+        blk = np.empty((groups, 18), np.uint8)
+        blk[:, 0:2] = _f16_bits(scale / 4.0 * (0.5 + g.random(groups))).astype("<u2").view(np.uint8).reshape(groups, 2)
+        blk[:, 2:] = g.integers(0, 256, (groups, 16), dtype=np.uint8)
         return blk.tobytes()
     if ttype == T_Q4_K:
         supers = n // 256
-        d = _f16_bits(scale / 256.0 * (0.5 + u[:supers]))
-        dmin = _f16_bits(scale / 512.0 * (0.5 + synth.uniform(seed, tag + "/m", supers)))
-        rest = synth.integers(seed, tag + "/q", supers * 140, 0, 255).astype(np.uint8).reshape(supers, 140)
-        blk = np.zeros((supers, 144), np.uint8)
-        blk[:, 0:2] = d.astype("<u2").view(np.uint8).reshape(supers, 2)
-        blk[:, 2:4] = dmin.astype("<u2").view(np.uint8).reshape(supers, 2)
-        blk[:, 4:] = rest
+        blk = np.empty((supers, 144), np.uint8)
+        blk[:, 0:2] = _f16_bits(scale / 256.0 * (0.5 + g.random(supers))).astype("<u2").view(np.uint8).reshape(supers, 2)
+        blk[:, 2:4] = _f16_bits(scale / 512.0 * (0.5 + g.random(supers))).astype("<u2").view(np.uint8).reshape(supers, 2)
+        blk[:, 4:] = g.integers(0, 256, (supers, 140), dtype=np.uint8)
         return blk.tobytes()
     raise ValueError(ttype)
 
@@ -148,13 +163,14 @@ class LlamaSpec:
         s = self.seed
 
         def norm(name):
-            w = (1.0 + 0.1 * synth.normal(s, name, h)).astype(np.float32)
+            w = (1.0 + 0.1 * _rng(s, name).standard_normal(h)).astype(np.float32)
             if self.norm_type == T_F16:
                 return (name, [h], T_F16, w.astype("<f2").tobytes())
             return (name, [h], T_F32, w.astype("<f4").tobytes())
 
         def mat(name, rows, cols, ttype):
-            return (name, [cols, rows], ttype, payload(ttype, rows, cols, s, name, 1.0 / np.sqrt(cols)))
+            return (name, [cols, rows], ttype,
+                    Lazy(_payload_size(ttype, [cols, rows]), lambda: payload(ttype, rows, cols, s, name, 1.0 / np.sqrt(cols))))
 
         t = [mat("token_embd.weight", v, h, self.embed_type), norm("output_norm.weight")]
         if self.output:
@@ -172,3 +188,12 @@ class LlamaSpec:
     def write(self, path):
         write_gguf(path, self.metadata(), self.tensors())
         return path
+
+
+def llama32_1b(**kw):
+    """The Llama-3.2-1B shape (16 layers, hidden 2048, 32 / 8 heads, FFN 8192,
+    vocabulary 128,256, tied embedding) with random Q8_0 weights."""
+    args = dict(vocab=128256, hidden=2048, intermediate=8192, layers=16, heads=32, kv_heads=8, context=8192,
+                rope_theta=500000.0, output=False, matrix_type=T_Q8_0, embed_type=T_Q8_0, seed=11)
+    args.update(kw)
+    return LlamaSpec(**args)

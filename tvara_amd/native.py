@@ -121,6 +121,23 @@ class NativeModel:
                 self._raise_error()
         return output
 
+    def decode_sequences(self, sequences, tokens):
+        """One token for each of several distinct sequences in one pass
+        (tvara_sequences_decode): logits [len(sequences), vocab]."""
+        seqs = np.ascontiguousarray(sequences, dtype=np.uint64).reshape(-1)
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        if seqs.size != toks.size:
+            raise ValueError("one token per sequence")
+        output = np.empty((seqs.size, self.vocab_size), dtype=np.float32)
+        with self._lock:
+            self._check_open()
+            if self._library.tvara_sequences_decode(self._handle, seqs.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)),
+                                                    toks.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), seqs.size,
+                                                    output.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                                    output.size):
+                self._raise_error()
+        return output
+
     def truncate(self, sequence, length):
         with self._lock:
             self._check_open()
