@@ -52,6 +52,7 @@ typedef struct tvara_model tvara_model;
 typedef struct tvara_kv_cache tvara_kv_cache;
 typedef struct tvara_attn_plan tvara_attn_plan;
 typedef struct tvara_prefill_plan tvara_prefill_plan;
+typedef struct tvara_radix tvara_radix;
 
 /* BlockHandle (kv.hpp:35) */
 typedef struct {
@@ -103,6 +104,56 @@ TVARA_API int tvara_sequence_truncate(tvara_model* model, uint64_t sequence, siz
  * (python/tvara/scheduler.py:201-210); no counterpart in the reference ABI. */
 TVARA_API int tvara_sequences_decode(tvara_model* model, const uint64_t* sequences, const uint32_t* tokens,
                                      size_t count, float* logits, size_t logits_count);
+
+/* The model's KV cache as a tvara_kv_cache handle owned by the model (the
+ * in-process PagedModelExecutor::cache(), paged_model.hpp:10), so every
+ * tvara_kv_* call -- fork (kv.hpp:123-129), snapshots, retain / release,
+ * import_sequence, audit -- and the prefix cache below work on the model's
+ * sequences.  tvara_kv_cache_destroy on it does nothing; it lives until
+ * tvara_model_close.  The caller serialises it with the model's calls.  No
+ * counterpart in the reference ABI, which has no fork
+ * (docs/architecture.md:110). */
+TVARA_API tvara_kv_cache* tvara_model_cache(tvara_model* model);
+
+/* ---- prefix cache: RadixCache (radix.hpp:17-131) over a cache handle, with
+ * its node ids, eviction order and messages.  The tree is host metadata; a
+ * node's KV is a retained snapshot of a sequence's blocks, and reuse imports
+ * it as a new sequence sharing those blocks.  Destroy the tree before its
+ * cache.  Additive: the reference keeps RadixCache in process. */
+/* RadixCache(cache, isolation) (radix.hpp:19-23); isolation must be non-empty */
+TVARA_API tvara_radix* tvara_radix_create(tvara_kv_cache* cache, const char* isolation);
+TVARA_API void tvara_radix_destroy(tvara_radix* radix);
+/* insert (radix.hpp:44-69): the node ending the path, created or split as needed */
+TVARA_API int tvara_radix_insert(tvara_radix* radix, const int32_t* tokens, size_t count, uint64_t* node);
+/* lookup (radix.hpp:29-42): deepest node reached and tokens matched */
+TVARA_API int tvara_radix_lookup(tvara_radix* radix, const int32_t* tokens, size_t count, uint64_t* node,
+                                 size_t* matched);
+/* attach (radix.hpp:72-81): retain `sequence`'s blocks as the node's KV */
+TVARA_API int tvara_radix_attach(tvara_radix* radix, uint64_t node, uint64_t sequence);
+/* reuse (radix.hpp:90-96): a new sequence holding the matched prefix (whole
+ * blocks unless partial) and its length */
+TVARA_API int tvara_radix_reuse(tvara_radix* radix, const int32_t* tokens, size_t count, int partial,
+                                uint64_t* sequence, size_t* length);
+/* pin / unpin / touch (radix.hpp:99-103) */
+TVARA_API int tvara_radix_pin(tvara_radix* radix, uint64_t node);
+TVARA_API int tvara_radix_unpin(tvara_radix* radix, uint64_t node);
+TVARA_API int tvara_radix_touch(tvara_radix* radix, uint64_t node);
+/* eviction_candidate (radix.hpp:106-110): 0 when there is none */
+TVARA_API int tvara_radix_eviction_candidate(tvara_radix* radix, uint64_t* node);
+/* evict_one (radix.hpp:113-117) */
+TVARA_API int tvara_radix_evict_one(tvara_radix* radix, int* evicted);
+/* reset (radix.hpp:119-123) */
+TVARA_API int tvara_radix_reset(tvara_radix* radix);
+/* size (radix.hpp:26) */
+TVARA_API int tvara_radix_size(tvara_radix* radix, size_t* size);
+/* node(id) (radix.hpp:25): parent, edge tokens, pins, access stamp, KV
+ * length and block count (kv_blocks = SIZE_MAX when none is attached),
+ * children */
+TVARA_API int tvara_radix_node(tvara_radix* radix, uint64_t id, uint64_t* parent, int32_t* edge, size_t edge_capacity,
+                               size_t* edge_length, size_t* pins, uint64_t* accessed, size_t* kv_length,
+                               size_t* kv_blocks, size_t* children);
+/* external_references (radix.hpp:83-87): retained count per block id */
+TVARA_API int tvara_radix_external_references(tvara_radix* radix, size_t* counts, size_t capacity);
 /* Status of the last failed call on this thread (TVARA_OK after a success);
  * lets callers of the NULL- or 0-returning entry points tell the exception
  * classes apart.  No reference counterpart: the reference throws in C++. */

@@ -428,6 +428,24 @@ def ref_lib():
         lib.tvr_fused_paged_attention.argtypes = [C.c_void_p, _u64, _sz, _sz, _sz, _fp, _fp, _fp, _sz, C.c_int, _fp]
         lib.tvr_fused_prompt_attention.argtypes = [C.c_void_p, _u64, _sz, _sz, _sz, _sz, _sz, _fp, _fp]
         lib.tvr_grouped_attention.argtypes = [_fp, _fp, _fp, _sz, _sz, _sz, _sz, _sz, _fp]
+        lib.tvr_radix_create.restype = C.c_void_p
+        lib.tvr_radix_create.argtypes = [C.c_void_p, C.c_char_p]
+        lib.tvr_radix_destroy.argtypes = [C.c_void_p]
+        lib.tvr_radix_insert.argtypes = [C.c_void_p, C.POINTER(C.c_int32), _sz, C.POINTER(_u64)]
+        lib.tvr_radix_lookup.argtypes = [C.c_void_p, C.POINTER(C.c_int32), _sz, C.POINTER(_u64), C.POINTER(_sz)]
+        lib.tvr_radix_attach.argtypes = [C.c_void_p, _u64, _u64]
+        lib.tvr_radix_reuse.argtypes = [C.c_void_p, C.POINTER(C.c_int32), _sz, C.c_int, C.POINTER(_u64),
+                                        C.POINTER(_sz)]
+        for name in ("pin", "unpin", "touch"):
+            getattr(lib, "tvr_radix_" + name).argtypes = [C.c_void_p, _u64]
+        lib.tvr_radix_eviction_candidate.argtypes = [C.c_void_p, C.POINTER(_u64)]
+        lib.tvr_radix_evict_one.argtypes = [C.c_void_p, C.POINTER(C.c_int)]
+        lib.tvr_radix_reset.argtypes = [C.c_void_p]
+        lib.tvr_radix_size.argtypes = [C.c_void_p, C.POINTER(_sz)]
+        lib.tvr_radix_node.argtypes = [C.c_void_p, _u64, C.POINTER(_u64), C.POINTER(C.c_int32), _sz, C.POINTER(_sz),
+                                       C.POINTER(_sz), C.POINTER(_u64), C.POINTER(_sz), C.POINTER(_sz),
+                                       C.POINTER(_sz)]
+        lib.tvr_radix_external_references.argtypes = [C.c_void_p, C.POINTER(_sz), _sz]
         lib.tvr_half_to_float.restype = C.c_float
         lib.tvr_half_to_float.argtypes = [C.c_uint16]
         lib.tvr_dequantize_q8_0.argtypes = [C.POINTER(C.c_uint8), _sz, _fp, _sz]
@@ -646,3 +664,101 @@ def ref_dequantize_q8_0(raw: np.ndarray) -> np.ndarray:
     if rc:
         raise _ERRORS.get(rc, OracleError)(ref_lib().tvr_last_error().decode())
     return out
+
+
+class RefRadix:
+    """The reference's RadixCache (core/include/tvara/radix.hpp:17-131) over a
+    RefCache, through oracle/_ref/libtvara_ref.so; same methods and return
+    values as tvara_amd.radix.RadixCache."""
+
+    def __init__(self, cache, isolation):
+        self.cache = cache
+        self.lib = cache.lib
+        self.h = self.lib.tvr_radix_create(cache.h, isolation.encode("utf-8"))
+        if not self.h:
+            raise InvalidArgument(self.lib.tvr_last_error().decode())
+
+    def __del__(self):
+        self.close()
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.tvr_radix_destroy(self.h)
+            self.h = None
+
+    def _check(self, rc):
+        if rc:
+            raise _ERRORS.get(rc, OracleError)(self.lib.tvr_last_error().decode())
+
+    @staticmethod
+    def _tokens(tokens):
+        t = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+        return t, t.ctypes.data_as(C.POINTER(C.c_int32))
+
+    def size(self):
+        n = _sz()
+        self._check(self.lib.tvr_radix_size(self.h, C.byref(n)))
+        return n.value
+
+    def lookup(self, tokens):
+        t, p = self._tokens(tokens)
+        node, matched = _u64(), _sz()
+        self._check(self.lib.tvr_radix_lookup(self.h, p, t.size, C.byref(node), C.byref(matched)))
+        return node.value, matched.value
+
+    def insert(self, tokens):
+        t, p = self._tokens(tokens)
+        node = _u64()
+        self._check(self.lib.tvr_radix_insert(self.h, p, t.size, C.byref(node)))
+        return node.value
+
+    def attach(self, node, sequence):
+        self._check(self.lib.tvr_radix_attach(self.h, node, sequence))
+
+    def reuse(self, tokens, partial=False):
+        t, p = self._tokens(tokens)
+        seq, length = _u64(), _sz()
+        self._check(self.lib.tvr_radix_reuse(self.h, p, t.size, int(partial), C.byref(seq), C.byref(length)))
+        self.cache._seqs.add(seq.value)
+        return seq.value, length.value
+
+    def pin(self, node):
+        self._check(self.lib.tvr_radix_pin(self.h, node))
+
+    def unpin(self, node):
+        self._check(self.lib.tvr_radix_unpin(self.h, node))
+
+    def touch(self, node):
+        self._check(self.lib.tvr_radix_touch(self.h, node))
+
+    def eviction_candidate(self):
+        node = _u64()
+        self._check(self.lib.tvr_radix_eviction_candidate(self.h, C.byref(node)))
+        return node.value or None
+
+    def evict_one(self):
+        e = C.c_int()
+        self._check(self.lib.tvr_radix_evict_one(self.h, C.byref(e)))
+        return bool(e.value)
+
+    def reset(self):
+        self._check(self.lib.tvr_radix_reset(self.h))
+
+    def node(self, node_id):
+        parent, elen, pins, acc, kvlen, kvb, ch = _u64(), _sz(), _sz(), _u64(), _sz(), _sz(), _sz()
+        self._check(self.lib.tvr_radix_node(self.h, node_id, C.byref(parent), None, 0, C.byref(elen), C.byref(pins),
+                                            C.byref(acc), C.byref(kvlen), C.byref(kvb), C.byref(ch)))
+        edge = np.zeros(max(1, elen.value), np.int32)
+        self._check(self.lib.tvr_radix_node(self.h, node_id, C.byref(parent), edge.ctypes.data_as(C.POINTER(C.c_int32)),
+                                            elen.value, C.byref(elen), C.byref(pins), C.byref(acc), C.byref(kvlen),
+                                            C.byref(kvb), C.byref(ch)))
+        has_kv = kvb.value != (1 << 64) - 1
+        return {"id": node_id, "parent": parent.value, "edge": [int(x) for x in edge[: elen.value]],
+                "pins": pins.value, "accessed": acc.value, "kv_length": kvlen.value if has_kv else None,
+                "kv_blocks": kvb.value if has_kv else None, "children": ch.value}
+
+    def external_references(self):
+        counts = np.zeros(self.cache.max_blocks, np.uint64)
+        self._check(self.lib.tvr_radix_external_references(self.h, counts.ctypes.data_as(C.POINTER(_sz)),
+                                                           counts.size))
+        return [int(x) for x in counts]

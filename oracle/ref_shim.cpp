@@ -10,8 +10,11 @@
 #include "tvara/attention.hpp"
 #include "tvara/kv.hpp"
 #include "tvara/quant.hpp"
+#include "tvara/radix.hpp"
 
+#include <algorithm>
 #include <cstring>
+#include <span>
 #include <new>
 #include <string>
 
@@ -269,6 +272,74 @@ int tvr_grouped_attention(const float* q, const float* keys, const float* values
         auto o = tvara::grouped_attention(std::span<const float>(q, cfg.hidden), std::span<const float>(keys, n),
                                           std::span<const float>(values, n), positions, cfg);
         std::memcpy(out, o.data(), o.size() * sizeof(float));
+    });
+}
+
+// ---- RadixCache (radix.hpp) over a reference cache
+struct tvr_radix {
+    tvara::RadixCache tree;
+    tvr_radix(tvara::PagedCache& c, const char* iso) : tree(c, iso) {}
+};
+
+tvr_radix* tvr_radix_create(tvr_cache* c, const char* isolation) {
+    tvr_radix* out = nullptr;
+    guard([&] { out = new tvr_radix(c->cache, isolation ? isolation : ""); });
+    return out;
+}
+void tvr_radix_destroy(tvr_radix* r) { delete r; }
+int tvr_radix_insert(tvr_radix* r, const std::int32_t* t, std::size_t n, std::uint64_t* node) {
+    return guard([&] { *node = r->tree.insert(std::span<const std::int32_t>(t, n)); });
+}
+int tvr_radix_lookup(tvr_radix* r, const std::int32_t* t, std::size_t n, std::uint64_t* node, std::size_t* matched) {
+    return guard([&] {
+        auto m = r->tree.lookup(std::span<const std::int32_t>(t, n));
+        *node = m.node;
+        *matched = m.tokens;
+    });
+}
+int tvr_radix_attach(tvr_radix* r, std::uint64_t node, std::uint64_t seq) {
+    return guard([&] { r->tree.attach(node, seq); });
+}
+int tvr_radix_reuse(tvr_radix* r, const std::int32_t* t, std::size_t n, int partial, std::uint64_t* seq,
+                    std::size_t* length) {
+    return guard([&] {
+        auto x = r->tree.reuse(std::span<const std::int32_t>(t, n), partial != 0);
+        *seq = x.first;
+        *length = x.second;
+    });
+}
+int tvr_radix_pin(tvr_radix* r, std::uint64_t node) { return guard([&] { r->tree.pin(node); }); }
+int tvr_radix_unpin(tvr_radix* r, std::uint64_t node) { return guard([&] { r->tree.unpin(node); }); }
+int tvr_radix_touch(tvr_radix* r, std::uint64_t node) { return guard([&] { r->tree.touch(node); }); }
+int tvr_radix_eviction_candidate(tvr_radix* r, std::uint64_t* node) {
+    return guard([&] {
+        auto c = r->tree.eviction_candidate();
+        *node = c ? *c : 0;
+    });
+}
+int tvr_radix_evict_one(tvr_radix* r, int* evicted) { return guard([&] { *evicted = r->tree.evict_one() ? 1 : 0; }); }
+int tvr_radix_reset(tvr_radix* r) { return guard([&] { r->tree.reset(); }); }
+int tvr_radix_size(tvr_radix* r, std::size_t* n) { return guard([&] { *n = r->tree.size(); }); }
+int tvr_radix_node(tvr_radix* r, std::uint64_t id, std::uint64_t* parent, std::int32_t* edge, std::size_t cap,
+                   std::size_t* edge_len, std::size_t* pins, std::uint64_t* accessed, std::size_t* kv_length,
+                   std::size_t* kv_blocks, std::size_t* children) {
+    return guard([&] {
+        const auto& n = r->tree.node(id);
+        *parent = n.parent;
+        *edge_len = n.edge.size();
+        std::copy(n.edge.begin(), n.edge.begin() + std::min(cap, n.edge.size()), edge);
+        *pins = n.pins;
+        *accessed = n.accessed;
+        *kv_length = n.kv ? n.kv->length : 0;
+        *kv_blocks = n.kv ? n.kv->blocks.size() : static_cast<std::size_t>(-1);
+        *children = n.children.size();
+    });
+}
+int tvr_radix_external_references(tvr_radix* r, std::size_t* counts, std::size_t cap) {
+    return guard([&] {
+        auto c = r->tree.external_references();
+        if (cap < c.size()) throw std::invalid_argument("reference count buffer too small");
+        std::copy(c.begin(), c.end(), counts);
     });
 }
 

@@ -5,6 +5,7 @@ import numpy as np
 import pytest
 
 import kv_cases
+import radix_cases
 from tvara_amd import synth
 
 
@@ -52,3 +53,27 @@ def test_q8_0_dequantize_matches_reference(ref):
     for h in range(0, 65536, 7):
         a, b = ref.half_to_float(h), ref.ref_half_to_float(h)
         assert (np.isnan(a) and np.isnan(b)) or np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)
+
+
+def _oracle_tree(ref):
+    from oracle.radix import Radix
+
+    return lambda cache, iso: Radix(cache, iso, (ref.InvalidArgument, ref.LogicError, ref.OracleError))
+
+
+def test_radix_known_answers_hold_for_reference(ref):
+    # the restated test_radix.cpp checks hold for the reference's RadixCache
+    radix_cases.known_answers(ref.RefCache(1, 1, 1, 4, 64), ref.RefRadix)
+
+
+def test_radix_oracle_known_answers(ref):
+    radix_cases.known_answers(ref.Cache(1, 1, 1, 4, 64), _oracle_tree(ref))
+
+
+@pytest.mark.parametrize("geometry,seed,alphabet", [((1, 1, 2, 4, 24), 1, 3), ((2, 1, 2, 3, 40), 2, 4),
+                                                    ((1, 2, 2, 2, 16), 3, 2), ((1, 1, 1, 5, 64), 4, 6)])
+def test_radix_oracle_matches_reference(ref, geometry, seed, alphabet):
+    layers, kv_heads, dim, _, _ = geometry
+    rc, oc = ref.RefCache(*geometry), ref.Cache(*geometry)
+    pairs = [(rc, ref.RefRadix(rc, "model/tokenizer/tenant")), (oc, _oracle_tree(ref)(oc, "model/tokenizer/tenant"))]
+    assert radix_cases.random_ops(pairs, 400, seed, layers * kv_heads * dim, alphabet) > 10

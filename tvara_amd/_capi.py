@@ -40,6 +40,23 @@ SIGNATURES = {
     "tvara_sequence_decode_batch": (C.c_int, [_vp, _u64, C.POINTER(C.c_uint32), _sz, _fp, _sz]),
     "tvara_sequence_truncate": (C.c_int, [_vp, _u64, _sz]),
     "tvara_sequences_decode": (C.c_int, [_vp, C.POINTER(_u64), C.POINTER(C.c_uint32), _sz, _fp, _sz]),
+    "tvara_model_cache": (_vp, [_vp]),
+    "tvara_radix_create": (_vp, [_vp, C.c_char_p]),
+    "tvara_radix_destroy": (None, [_vp]),
+    "tvara_radix_insert": (C.c_int, [_vp, C.POINTER(C.c_int32), _sz, C.POINTER(_u64)]),
+    "tvara_radix_lookup": (C.c_int, [_vp, C.POINTER(C.c_int32), _sz, C.POINTER(_u64), C.POINTER(_sz)]),
+    "tvara_radix_attach": (C.c_int, [_vp, _u64, _u64]),
+    "tvara_radix_reuse": (C.c_int, [_vp, C.POINTER(C.c_int32), _sz, C.c_int, C.POINTER(_u64), C.POINTER(_sz)]),
+    "tvara_radix_pin": (C.c_int, [_vp, _u64]),
+    "tvara_radix_unpin": (C.c_int, [_vp, _u64]),
+    "tvara_radix_touch": (C.c_int, [_vp, _u64]),
+    "tvara_radix_eviction_candidate": (C.c_int, [_vp, C.POINTER(_u64)]),
+    "tvara_radix_evict_one": (C.c_int, [_vp, C.POINTER(C.c_int)]),
+    "tvara_radix_reset": (C.c_int, [_vp]),
+    "tvara_radix_size": (C.c_int, [_vp, C.POINTER(_sz)]),
+    "tvara_radix_node": (C.c_int, [_vp, _u64, C.POINTER(_u64), C.POINTER(C.c_int32), _sz, C.POINTER(_sz),
+                                   C.POINTER(_sz), C.POINTER(_u64), C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),
+    "tvara_radix_external_references": (C.c_int, [_vp, C.POINTER(_sz), _sz]),
     "tvara_last_error": (C.c_char_p, []),
     "tvara_last_status": (C.c_int, []),
     "tvara_kv_cache_create": (_vp, [_sz, _sz, _sz, _sz, _sz, C.c_int]),

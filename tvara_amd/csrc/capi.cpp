@@ -15,15 +15,25 @@
 
 #include "kv_cache.hpp"
 #include "model.hpp"
+#include "radix.hpp"
 
 using tvara_amd::AttnPlan;
 using tvara_amd::DeviceCache;
 using tvara_amd::Geometry;
 using tvara_amd::Handle;
 
+// a cache handle either owns its DeviceCache (tvara_kv_cache_create) or lends
+// a model's (tvara_model_cache; destroying that handle does nothing)
 struct tvara_kv_cache {
-    DeviceCache cache;
-    tvara_kv_cache(const Geometry& g, int format) : cache(g, format) {}
+    std::unique_ptr<DeviceCache> owned;
+    DeviceCache* cache = nullptr;
+    tvara_kv_cache(const Geometry& g, int format)
+        : owned(std::make_unique<DeviceCache>(g, format)), cache(owned.get()) {}
+    explicit tvara_kv_cache(DeviceCache* lent) : cache(lent) {}
+};
+
+struct tvara_radix {
+    std::unique_ptr<tvara_amd::RadixCache> tree;
 };
 
 struct tvara_attn_plan {
@@ -35,6 +45,7 @@ struct tvara_attn_plan {
 // mutex held for every call that touches sequences
 struct tvara_model {
     std::unique_ptr<tvara_amd::DeviceModel> model;
+    std::unique_ptr<tvara_kv_cache> kv;  // the model's cache, lent as a KV handle
     std::mutex mutex;
 };
 
@@ -80,7 +91,7 @@ int guard(F&& f) {
 
 DeviceCache& live(tvara_kv_cache* c) {
     if (!c) throw std::invalid_argument("closed KV cache");
-    return c->cache;
+    return *c->cache;
 }
 
 Handle handle(tvara_kv_handle h) { return Handle{static_cast<size_t>(h.id), h.generation}; }
@@ -153,7 +164,9 @@ tvara_kv_cache* tvara_kv_cache_create(size_t layers, size_t kv_heads, size_t hea
     return out;
 }
 
-void tvara_kv_cache_destroy(tvara_kv_cache* cache) { delete cache; }
+void tvara_kv_cache_destroy(tvara_kv_cache* cache) {
+    if (cache && cache->owned) delete cache;  // a lent handle belongs to its model
+}
 
 size_t tvara_kv_block_bytes(tvara_kv_cache* cache) {
     size_t n = 0;
@@ -479,6 +492,7 @@ tvara_model* tvara_model_open(const char* path, size_t blocks, size_t tokens) {
         if (!path || !*path) throw std::invalid_argument("empty model path");
         auto m = std::make_unique<tvara_model>();
         m->model = std::make_unique<tvara_amd::DeviceModel>(path, blocks, tokens);
+        m->kv = std::make_unique<tvara_kv_cache>(&m->model->cache());
         return m.release();
     } catch (const std::exception& e) {
         failed(TVARA_ERROR, e.what());
@@ -636,6 +650,118 @@ int tvara_sequences_decode(tvara_model* model, const uint64_t* sequences, const 
         failed(TVARA_ERROR, "unknown batch error");
         return -1;
     }
+}
+
+tvara_kv_cache* tvara_model_cache(tvara_model* model) {
+    if (!model) {
+        failed(TVARA_INVALID, "closed model");
+        return nullptr;
+    }
+    return model->kv.get();
+}
+
+// ------------------------------------------------------------- prefix cache
+// RadixCache (radix.hpp:17-131) over a cache handle
+
+tvara_radix* tvara_radix_create(tvara_kv_cache* cache, const char* isolation) {
+    tvara_radix* out = nullptr;
+    guard([&] {
+        auto r = std::make_unique<tvara_radix>();
+        r->tree = std::make_unique<tvara_amd::RadixCache>(live(cache), isolation ? isolation : "");
+        out = r.release();
+    });
+    return out;
+}
+
+void tvara_radix_destroy(tvara_radix* radix) { delete radix; }
+
+namespace {
+tvara_amd::RadixCache& tree(tvara_radix* r) {
+    if (!r) throw std::invalid_argument("closed prefix cache");
+    return *r->tree;
+}
+}  // namespace
+
+int tvara_radix_insert(tvara_radix* radix, const int32_t* tokens, size_t count, uint64_t* node) {
+    return guard([&] {
+        if (!tokens && count) throw std::invalid_argument("invalid prefix tokens");
+        const uint64_t id = tree(radix).insert(tokens, count);
+        if (node) *node = id;
+    });
+}
+
+int tvara_radix_lookup(tvara_radix* radix, const int32_t* tokens, size_t count, uint64_t* node, size_t* matched) {
+    return guard([&] {
+        if (!tokens && count) throw std::invalid_argument("invalid prefix tokens");
+        const auto m = tree(radix).lookup(tokens, count);
+        if (node) *node = m.first;
+        if (matched) *matched = m.second;
+    });
+}
+
+int tvara_radix_attach(tvara_radix* radix, uint64_t node, uint64_t sequence) {
+    return guard([&] { tree(radix).attach(node, sequence); });
+}
+
+int tvara_radix_reuse(tvara_radix* radix, const int32_t* tokens, size_t count, int partial, uint64_t* sequence,
+                      size_t* length) {
+    return guard([&] {
+        if (!tokens && count) throw std::invalid_argument("invalid prefix tokens");
+        const auto r = tree(radix).reuse(tokens, count, partial != 0);
+        if (sequence) *sequence = r.first;
+        if (length) *length = r.second;
+    });
+}
+
+int tvara_radix_pin(tvara_radix* radix, uint64_t node) { return guard([&] { tree(radix).pin(node); }); }
+int tvara_radix_unpin(tvara_radix* radix, uint64_t node) { return guard([&] { tree(radix).unpin(node); }); }
+int tvara_radix_touch(tvara_radix* radix, uint64_t node) { return guard([&] { tree(radix).touch(node); }); }
+
+int tvara_radix_eviction_candidate(tvara_radix* radix, uint64_t* node) {
+    return guard([&] {
+        const auto c = tree(radix).eviction_candidate();
+        if (node) *node = c ? *c : 0;
+    });
+}
+
+int tvara_radix_evict_one(tvara_radix* radix, int* evicted) {
+    return guard([&] {
+        const bool e = tree(radix).evict_one();
+        if (evicted) *evicted = e ? 1 : 0;
+    });
+}
+
+int tvara_radix_reset(tvara_radix* radix) { return guard([&] { tree(radix).reset(); }); }
+
+int tvara_radix_size(tvara_radix* radix, size_t* size) {
+    return guard([&] {
+        const size_t n = tree(radix).size();
+        if (size) *size = n;
+    });
+}
+
+int tvara_radix_node(tvara_radix* radix, uint64_t id, uint64_t* parent, int32_t* edge, size_t edge_capacity,
+                     size_t* edge_length, size_t* pins, uint64_t* accessed, size_t* kv_length, size_t* kv_blocks,
+                     size_t* children) {
+    return guard([&] {
+        const tvara_amd::RadixNode& n = tree(radix).node(id);
+        if (parent) *parent = n.parent;
+        if (edge_length) *edge_length = n.edge.size();
+        if (edge) std::copy(n.edge.begin(), n.edge.begin() + std::min(edge_capacity, n.edge.size()), edge);
+        if (pins) *pins = n.pins;
+        if (accessed) *accessed = n.accessed;
+        if (kv_length) *kv_length = n.kv ? n.kv->length : 0;
+        if (kv_blocks) *kv_blocks = n.kv ? n.kv->blocks.size() : static_cast<size_t>(-1);
+        if (children) *children = n.children.size();
+    });
+}
+
+int tvara_radix_external_references(tvara_radix* radix, size_t* counts, size_t capacity) {
+    return guard([&] {
+        const auto c = tree(radix).external_references();
+        if (!counts || capacity < c.size()) throw std::invalid_argument("reference count buffer too small");
+        std::copy(c.begin(), c.end(), counts);
+    });
 }
 
 int tvara_profile_enable(int enabled) {

@@ -48,10 +48,27 @@ class PagedCache:
             _capi.raise_last()
         self.block_bytes = self.lib.tvara_kv_block_bytes(self.h)
 
+    @classmethod
+    def lent(cls, handle, layers, kv_heads, head_dim, tokens_per_block, max_blocks, owner=None, fmt=F32):
+        """Wrap a cache handle another object owns (tvara_model_cache); closing
+        it does not destroy the cache.  `owner` is kept alive with it."""
+        self = cls.__new__(cls)
+        self.lib = _capi.lib()
+        self.geometry = (layers, kv_heads, head_dim, tokens_per_block, max_blocks)
+        self.layers, self.kv_heads, self.head_dim, self.tokens_per_block, self.max_blocks = self.geometry
+        self.format = fmt
+        self.kv_width = kv_heads * head_dim
+        self.h = handle
+        self._owner = owner
+        self.block_bytes = self.lib.tvara_kv_block_bytes(self.h)
+        return self
+
     def close(self):
         if getattr(self, "h", None):
-            self.lib.tvara_kv_cache_destroy(self.h)
+            if getattr(self, "_owner", None) is None:
+                self.lib.tvara_kv_cache_destroy(self.h)
             self.h = None
+            self._owner = None
 
     def __del__(self):
         self.close()

@@ -32,6 +32,7 @@ class NativeModel:
         if not self._handle:
             self._raise_error()
         self._finalizer = weakref.finalize(self, lib.tvara_model_close, self._handle)
+        self._max_blocks, self._block_tokens = max_blocks, block_tokens
         self.vocab_size = int(lib.tvara_model_vocab_size(self._handle))
         self.context_size = int(lib.tvara_model_context_size(self._handle))
 
@@ -137,6 +138,23 @@ class NativeModel:
                                                     output.size):
                 self._raise_error()
         return output
+
+    def cache(self):
+        """The model's KV cache as a tvara_amd.kv.PagedCache (tvara_model_cache):
+        fork, snapshots, retain / release, import and the prefix cache
+        (tvara_amd.radix.RadixCache) work on the model's sequences."""
+        from . import kv
+
+        with self._lock:
+            self._check_open()
+            h = self._library.tvara_model_cache(self._handle)
+            if not h:
+                self._raise_error()
+            md = self.metadata
+            heads, kvh = md["llama.attention.head_count"], md["llama.attention.head_count_kv"]
+            dim = md["llama.embedding_length"] // heads
+            return kv.PagedCache.lent(h, md["llama.block_count"], kvh, dim, self._block_tokens, self._max_blocks,
+                                      owner=self)
 
     def truncate(self, sequence, length):
         with self._lock:
