@@ -53,6 +53,11 @@ SPECS = {
     "q8_0-gqa4": dict(matrix_type=gf.T_Q8_0, heads=8, kv_heads=2, hidden=128, intermediate=256),
     "q4_0-mha": dict(matrix_type=gf.T_Q4_0, heads=4, kv_heads=4, rope_layout="interleaved"),
     "q4_k-256": dict(matrix_type=gf.T_Q4_K, hidden=256, intermediate=512, heads=4, kv_heads=1, layers=3),
+    # Q8_0 kept quantised in HBM, the tied embedding too: a vocabulary and
+    # widths that leave partial 16-row tiles and group counts not divisible
+    # by four
+    "q8_0-tied-ragged": dict(matrix_type=gf.T_Q8_0, embed_type=gf.T_Q8_0, output=False, vocab=100, hidden=96,
+                             intermediate=160, heads=3, kv_heads=1),
 }
 
 
@@ -173,14 +178,34 @@ def test_nonfinite_weight_rejected(tmp_path, ref_capi):
     assert a == b == "nonfinite model weight"
 
 
-@pytest.mark.parametrize("nseq", [3, 20])
-def test_sequences_decode_matches_serial_reference(tmp_path, ref_capi, nseq):
+@pytest.mark.parametrize("scale", [0x7C00, 0x7E00])  # fp16 inf, NaN
+def test_nonfinite_q8_0_scale_rejected(tmp_path, ref_capi, scale):
+    # a Q8_0 matrix kept quantised: a non-finite group scale makes its values
+    # non-finite, which the reference rejects at load (model.hpp:138)
+    spec = gf.LlamaSpec(matrix_type=gf.T_Q8_0)
+    tensors = spec.tensors()
+    i = next(k for k, t in enumerate(tensors) if t[0] == "blk.1.ffn_up.weight")
+    name, dims, ttype, payload = tensors[i]
+    raw = bytearray(payload() if isinstance(payload, gf.Lazy) else payload)
+    raw[34 * 5:34 * 5 + 2] = scale.to_bytes(2, "little")
+    tensors[i] = (name, dims, ttype, bytes(raw))
+    path = tmp_path / "bad.gguf"
+    gf.write_gguf(path, spec.metadata(), tensors)
+    a = errors(None, native.NativeModel, path)
+    b = errors(None, native.NativeModel, path, ref_capi)
+    assert a == b == "nonfinite model weight"
+
+
+@pytest.mark.parametrize("nseq,embed", [(3, gf.T_F32), (20, gf.T_F32), (41, gf.T_Q8_0), (70, gf.T_Q8_0)])
+def test_sequences_decode_matches_serial_reference(tmp_path, ref_capi, nseq, embed):
     # one pass for many sequences (tvara_sequences_decode) against the
-    # reference decoding each sequence on its own
-    spec = gf.LlamaSpec(matrix_type=gf.T_Q8_0, hidden=128, intermediate=256, heads=8, kv_heads=2)
+    # reference decoding each sequence on its own; 41 and 70 sequences take
+    # partial and multiple 64-vector passes of the batched Q8_0 products
+    spec = gf.LlamaSpec(matrix_type=gf.T_Q8_0, embed_type=embed, output=embed == gf.T_F32, hidden=128,
+                        intermediate=256, heads=8, kv_heads=2)
     path = spec.write(tmp_path / "m.gguf")
-    mine = native.NativeModel(path, max_blocks=256, block_tokens=4)
-    ref = native.NativeModel(path, library=ref_capi, max_blocks=256, block_tokens=4)
+    mine = native.NativeModel(path, max_blocks=512, block_tokens=4)
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=512, block_tokens=4)
     rng = np.random.default_rng(nseq)
     sm = [mine.new_sequence() for _ in range(nseq)]
     sr = [ref.new_sequence() for _ in range(nseq)]

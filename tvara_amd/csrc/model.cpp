@@ -54,34 +54,74 @@ DeviceModel::DeviceModel(const std::string& path, size_t max_blocks, size_t bloc
     const ModelConfig& c = cfg_;
     const size_t H = c.hidden, I = c.intermediate, KV = c.kv_width();
 
-    // weights: every tensor dequantised to f32 in HBM, as load_weights does
-    // on the host (model.hpp:119-134,156-169); fused row blocks Wq|Wk|Wv and
-    // Wgate|Wup feed one matvec launch each
+    // weights: norms and every matrix not in Q8_0 dequantised to f32 in HBM,
+    // as load_weights does on the host (model.hpp:119-134,156-169); Q8_0
+    // matrices stay quantised (tiled, see Weight) and dequantise inside the
+    // products to the same floats.  Fused row blocks Wq|Wk|Wv and
+    // Wgate|Wup feed one product each; a block is Q8_0 only when all its
+    // parts are.
     DeviceBuffer staging;
     bad_.ensure(sizeof(int));
     TVARA_HIP(hipMemset(bad_.ptr, 0, sizeof(int)));
+    int* bad_flag = static_cast<int*>(bad_.ptr);
     auto load = [&](const std::string& name, float* dst) {
         const gguf::TensorInfo& t = file.tensor(name);
         const size_t n = elements(t), bytes = gguf::tensor_bytes(t);
         const uint8_t* src = file.payload(t);
         if (t.type == gguf::kF32) {
             TVARA_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
-            launch_dequant(t.type, nullptr, n, dst, static_cast<int*>(bad_.ptr), nullptr);
+            launch_dequant(t.type, nullptr, n, dst, bad_flag, nullptr);
         } else {
             void* raw = staging.ensure(bytes);
             TVARA_HIP(hipMemcpy(raw, src, bytes, hipMemcpyHostToDevice));
-            launch_dequant(t.type, static_cast<const uint8_t*>(raw), n, dst, static_cast<int*>(bad_.ptr), nullptr);
+            launch_dequant(t.type, static_cast<const uint8_t*>(raw), n, dst, bad_flag, nullptr);
         }
         TVARA_HIP(hipDeviceSynchronize());
     };
-    embedding_.ensure(c.vocab * H * sizeof(float));
-    load("token_embd.weight", at(embedding_, 0));
+    // parts: (tensor name, rows); every part has `cols` columns
+    auto load_weight = [&](const std::vector<std::pair<std::string, size_t>>& parts, size_t cols, Weight& w) {
+        size_t rows = 0;
+        bool q8 = true;
+        for (const auto& [name, r] : parts) {
+            rows += r;
+            q8 = q8 && file.tensor(name).type == gguf::kQ8_0;
+        }
+        if (rows > static_cast<size_t>(std::numeric_limits<int>::max()) || cols > (1u << 30))
+            throw std::invalid_argument("invalid native model configuration");
+        w.rows = static_cast<int>(rows);
+        w.cols = static_cast<int>(cols);
+        w.q8 = q8;
+        if (!q8) {
+            w.f32.ensure(rows * cols * sizeof(float));
+            size_t offset = 0;
+            for (const auto& [name, r] : parts) {
+                load(name, at(w.f32, offset));
+                offset += r * cols;
+            }
+            return;
+        }
+        const size_t tiles = static_cast<size_t>(w.tiles()), groups = cols / 32;
+        w.q.ensure(tiles * 16 * cols);
+        w.d.ensure(tiles * groups * 16 * sizeof(uint16_t));
+        TVARA_HIP(hipMemset(w.q.ptr, 0, tiles * 16 * cols));
+        TVARA_HIP(hipMemset(w.d.ptr, 0, tiles * groups * 16 * sizeof(uint16_t)));
+        int row0 = 0;
+        for (const auto& [name, r] : parts) {
+            const gguf::TensorInfo& t = file.tensor(name);
+            const size_t bytes = gguf::tensor_bytes(t);
+            void* raw = staging.ensure(bytes);
+            TVARA_HIP(hipMemcpy(raw, file.payload(t), bytes, hipMemcpyHostToDevice));
+            launch_q8_repack(static_cast<const uint8_t*>(raw), static_cast<int>(r), w.cols, row0, w, bad_flag, nullptr);
+            TVARA_HIP(hipDeviceSynchronize());
+            row0 += static_cast<int>(r);
+        }
+    };
+    load_weight({{"token_embd.weight", c.vocab}}, H, embedding_);
     final_norm_.ensure(H * sizeof(float));
     load("output_norm.weight", at(final_norm_, 0));
     if (doc.tensors.count("output.weight")) {
         has_output_ = true;
-        output_.ensure(c.vocab * H * sizeof(float));
-        load("output.weight", at(output_, 0));
+        load_weight({{"output.weight", c.vocab}}, H, output_);
     }
     layers_.resize(c.layers);
     for (size_t i = 0; i < c.layers; ++i) {
@@ -91,17 +131,10 @@ DeviceModel::DeviceModel(const std::string& path, size_t max_blocks, size_t bloc
         load(p + "attn_norm.weight", at(L.attn_norm, 0));
         L.ffn_norm.ensure(H * sizeof(float));
         load(p + "ffn_norm.weight", at(L.ffn_norm, 0));
-        L.qkv.ensure((H + 2 * KV) * H * sizeof(float));
-        load(p + "attn_q.weight", at(L.qkv, 0));
-        load(p + "attn_k.weight", at(L.qkv, H * H));
-        load(p + "attn_v.weight", at(L.qkv, (H + KV) * H));
-        L.out.ensure(H * H * sizeof(float));
-        load(p + "attn_output.weight", at(L.out, 0));
-        L.gate_up.ensure(2 * I * H * sizeof(float));
-        load(p + "ffn_gate.weight", at(L.gate_up, 0));
-        load(p + "ffn_up.weight", at(L.gate_up, I * H));
-        L.down.ensure(H * I * sizeof(float));
-        load(p + "ffn_down.weight", at(L.down, 0));
+        load_weight({{p + "attn_q.weight", H}, {p + "attn_k.weight", KV}, {p + "attn_v.weight", KV}}, H, L.qkv);
+        load_weight({{p + "attn_output.weight", H}}, H, L.out);
+        load_weight({{p + "ffn_gate.weight", I}, {p + "ffn_up.weight", I}}, H, L.gate_up);
+        load_weight({{p + "ffn_down.weight", H}}, I, L.down);
     }
     int bad = 0;
     TVARA_HIP(hipMemcpy(&bad, bad_.ptr, sizeof(int), hipMemcpyDeviceToHost));
@@ -144,7 +177,11 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
     float* gate = at(gate_, 0);
     float* up = at(up_, 0);
 
-    TVARA_HIP(hipMemcpyAsync(x, at(embedding_, token * c.hidden), c.hidden * sizeof(float), hipMemcpyDeviceToDevice, s));
+    if (embedding_.q8)
+        launch_gather_embedding_q8(embedding_, nullptr, static_cast<uint32_t>(token), 1, x, s);
+    else
+        TVARA_HIP(hipMemcpyAsync(x, at(embedding_.f32, token * c.hidden), c.hidden * sizeof(float),
+                                 hipMemcpyDeviceToDevice, s));
     // (cos, sin) of this position, computed as rotary() does (model.hpp:66-68)
     auto* cs = static_cast<float*>(rope_host_.acquire(c.head_dim() * sizeof(float)));
     for (int i = 0; i < D / 2; ++i) {
@@ -167,27 +204,42 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
         float* vl = at(vall_, l * c.kv_width());
         launch_rmsnorm(x, at(L.attn_norm, 0), norm, H, c.rms_epsilon, s);
         const MatvecSegment qkv[3] = {{q, H, nullptr}, {kl, KV, nullptr}, {vl, KV, nullptr}};
-        launch_matvec(at(L.qkv, 0), H + 2 * KV, H, norm, qkv, 3, s);
+        matvec(L.qkv, norm, qkv, 3, s);
         launch_rope(q, static_cast<int>(c.heads), kl, static_cast<int>(c.kv_heads), D, at(rope_, 0), c.interleaved_rope,
                     s);
         plan.launch(static_cast<int>(l), q, kl, vl, attn, s);
         const MatvecSegment o[1] = {{x, H, x}};
-        launch_matvec(at(L.out, 0), H, H, attn, o, 1, s);
+        matvec(L.out, attn, o, 1, s);
         launch_rmsnorm(x, at(L.ffn_norm, 0), norm, H, c.rms_epsilon, s);
         const MatvecSegment gu[2] = {{gate, I, nullptr}, {up, I, nullptr}};
-        launch_matvec(at(L.gate_up, 0), 2 * I, H, norm, gu, 2, s);
+        matvec(L.gate_up, norm, gu, 2, s);
         launch_swiglu(gate, up, I, s);
         const MatvecSegment d[1] = {{x, H, x}};
-        launch_matvec(at(L.down, 0), H, I, gate, d, 1, s);
+        matvec(L.down, gate, d, 1, s);
     }
     launch_rmsnorm(x, at(final_norm_, 0), norm, H, c.rms_epsilon, s);
     const MatvecSegment lg[1] = {{at(logits_, 0), static_cast<int>(c.vocab), nullptr}};
-    launch_matvec(has_output_ ? at(output_, 0) : at(embedding_, 0), static_cast<int>(c.vocab), H, norm, lg, 1, s);
+    matvec(has_output_ ? output_ : embedding_, norm, lg, 1, s);
     plan.check();  // a non-finite score fails the token before anything is appended
     // the token's K/V for every layer, appended after all layers succeeded
     // (paged_model.hpp:27)
     cache_->append_batch(&sequence, 1, at(kall_, 0), at(vall_, 0), true);
     TVARA_HIP(hipMemcpy(logits_host, logits_.ptr, c.vocab * sizeof(float), hipMemcpyDeviceToHost));
+}
+
+void DeviceModel::matvec(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s) {
+    if (w.q8)
+        launch_matvec_q8(w, v, seg, nseg, s);
+    else
+        launch_matvec(static_cast<const float*>(w.f32.ptr), w.rows, w.cols, v, seg, nseg, s);
+}
+
+void DeviceModel::batch_matvec(const Weight& w, const float* x, int n, const MatvecSegment* seg, int nseg,
+                               hipStream_t s) {
+    if (w.q8)
+        launch_batch_matvec_q8(w, x, n, seg, nseg, bhalves_, bwork_, s);
+    else
+        launch_batch_matvec(static_cast<const float*>(w.f32.ptr), w.rows, w.cols, x, n, seg, nseg, bwork_, s);
 }
 
 void DeviceModel::ensure_batch(size_t n) {
@@ -266,7 +318,10 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     TVARA_HIP(hipMemcpyAsync(btok_.ptr, host, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     TVARA_HIP(hipMemcpyAsync(brope_.ptr, cs, n * c.head_dim() * sizeof(float), hipMemcpyHostToDevice, s));
     bhost_.release(s);
-    launch_gather_embedding(at(embedding_, 0), static_cast<const uint32_t*>(btok_.ptr), N, H, x, s);
+    if (embedding_.q8)
+        launch_gather_embedding_q8(embedding_, static_cast<const uint32_t*>(btok_.ptr), 0, N, x, s);
+    else
+        launch_gather_embedding(at(embedding_.f32, 0), static_cast<const uint32_t*>(btok_.ptr), N, H, x, s);
 
     AttnPlan plan;
     plan.build(cache_.get(), seqs, positions, std::vector<uint8_t>(n, 1), static_cast<int>(c.heads), 0);
@@ -276,23 +331,22 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
         float* vl = at(bv_, l * n * c.kv_width());
         launch_rmsnorm(x, at(L.attn_norm, 0), norm, H, c.rms_epsilon, s, N);
         const MatvecSegment qkv[3] = {{q, H, nullptr}, {kl, KV, nullptr}, {vl, KV, nullptr}};
-        launch_batch_matvec(at(L.qkv, 0), H + 2 * KV, H, norm, N, qkv, 3, bwork_, s);
+        batch_matvec(L.qkv, norm, N, qkv, 3, s);
         launch_rope(q, static_cast<int>(c.heads), kl, static_cast<int>(c.kv_heads), D, at(brope_, 0),
                     c.interleaved_rope, s, N);
         plan.launch(static_cast<int>(l), q, kl, vl, attn, s);
         const MatvecSegment o[1] = {{x, H, x}};
-        launch_batch_matvec(at(L.out, 0), H, H, attn, N, o, 1, bwork_, s);
+        batch_matvec(L.out, attn, N, o, 1, s);
         launch_rmsnorm(x, at(L.ffn_norm, 0), norm, H, c.rms_epsilon, s, N);
         const MatvecSegment gu[2] = {{gate, I, nullptr}, {up, I, nullptr}};
-        launch_batch_matvec(at(L.gate_up, 0), 2 * I, H, norm, N, gu, 2, bwork_, s);
+        batch_matvec(L.gate_up, norm, N, gu, 2, s);
         launch_swiglu(gate, up, N * I, s);
         const MatvecSegment d[1] = {{x, H, x}};
-        launch_batch_matvec(at(L.down, 0), H, I, gate, N, d, 1, bwork_, s);
+        batch_matvec(L.down, gate, N, d, 1, s);
     }
     launch_rmsnorm(x, at(final_norm_, 0), norm, H, c.rms_epsilon, s, N);
     const MatvecSegment lg[1] = {{at(blogits_, 0), static_cast<int>(c.vocab), nullptr}};
-    launch_batch_matvec(has_output_ ? at(output_, 0) : at(embedding_, 0), static_cast<int>(c.vocab), H, norm, N, lg, 1,
-                        bwork_, s);
+    batch_matvec(has_output_ ? output_ : embedding_, norm, N, lg, 1, s);
     plan.check();
     launch_interleave_layers(at(bk_, 0), at(bkapp_, 0), static_cast<int>(c.layers), N, KV, s);
     launch_interleave_layers(at(bv_, 0), at(bvapp_, 0), static_cast<int>(c.layers), N, KV, s);

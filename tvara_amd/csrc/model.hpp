@@ -21,7 +21,35 @@ struct MatvecSegment {
     const float* residual;
 };
 
+// A weight matrix in HBM: f32 rows, or Q8_0 kept quantised.  The Q8_0 form
+// is tiled for the kernels that read it: rows are cut into tiles of 16
+// (zero-padded) and, per (tile, group of 32 columns), the 512 int8 sit in
+// the operand order of a 16x16x32 MFMA -- lane l holds row l%16, columns
+// 8(l/16) .. 8(l/16)+7 of the group -- followed in a separate plane by the
+// 16 rows' fp16 group scales.  Value = float(d) * q, as dequantize_q8_0
+// computes it (quant.hpp:39-49).
+struct Weight {
+    bool q8 = false;
+    int rows = 0, cols = 0;
+    DeviceBuffer f32;  // [rows][cols] floats
+    DeviceBuffer q;    // int8 [tiles][cols/32][64][8]
+    DeviceBuffer d;    // fp16 bits [tiles][cols/32][16]
+    int tiles() const { return (rows + 15) / 16; }
+    int groups() const { return cols / 32; }
+};
+
 void launch_dequant(uint32_t type, const uint8_t* raw, size_t n, float* out, int* bad, hipStream_t s);
+// GGUF Q8_0 rows [rows][cols/32][34 B] into rows row0.. of a tiled Weight;
+// flags `bad` when a group scale is not finite (then so is a value)
+void launch_q8_repack(const uint8_t* raw, int rows, int cols, int row0, Weight& w, int* bad, hipStream_t s);
+void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s);
+// the batched product over Q8_0 tiles on the MFMA units; `halves` and `work`
+// are scratch grown as needed
+void launch_batch_matvec_q8(const Weight& w, const float* x, int n, const MatvecSegment* seg, int nseg,
+                            DeviceBuffer& halves, DeviceBuffer& work, hipStream_t s);
+// out[j] = row idx[j] (or `row` when idx is null) of a Q8_0 table, dequantised
+void launch_gather_embedding_q8(const Weight& w, const uint32_t* idx, uint32_t row, int n, float* out,
+                                hipStream_t s);
 // `rows` rows of a batch, each normalised on its own
 void launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t s, int rows = 1);
 void launch_matvec(const float* w, int rows, int cols, const float* v, const MatvecSegment* seg, int nseg,
@@ -63,20 +91,25 @@ public:
 
 private:
     struct Layer {
-        DeviceBuffer attn_norm, ffn_norm, qkv, out, gate_up, down;
+        DeviceBuffer attn_norm, ffn_norm;
+        Weight qkv, out, gate_up, down;
     };
+    void matvec(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s);
+    void batch_matvec(const Weight& w, const float* x, int n, const MatvecSegment* seg, int nseg, hipStream_t s);
 
     ModelConfig cfg_;
     std::string metadata_;
     std::unique_ptr<DeviceCache> cache_;
-    DeviceBuffer embedding_, output_, final_norm_;
+    Weight embedding_, output_;
+    DeviceBuffer final_norm_;
     bool has_output_ = false;
     std::vector<Layer> layers_;
     // per-token work buffers
     DeviceBuffer x_, norm_, q_, kall_, vall_, attn_, gate_, up_, logits_, rope_, bad_;
     PinnedBuffer rope_host_;
     // batch work buffers, grown to the largest batch seen
-    DeviceBuffer bx_, bnorm_, bq_, bk_, bv_, bkapp_, bvapp_, battn_, bgate_, bup_, blogits_, brope_, btok_, bwork_;
+    DeviceBuffer bx_, bnorm_, bq_, bk_, bv_, bkapp_, bvapp_, battn_, bgate_, bup_, blogits_, brope_, btok_, bwork_,
+        bhalves_;
     PinnedBuffer bhost_;
     size_t batch_cap_ = 0;
     void ensure_batch(size_t n);

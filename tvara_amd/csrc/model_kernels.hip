@@ -9,6 +9,7 @@
 // accumulate in double and round once, as quant::dot_f32 and rms_norm do.
 #include "model.hpp"
 #include "q8.hpp"
+#include "device_util.hpp"
 
 namespace tvara_amd {
 namespace {
@@ -324,6 +325,295 @@ __global__ void swiglu_kernel(float* gate, const float* up, int n) {
     gate[i] = __fmul_rn(g, __fmul_rn(sig, up[i]));
 }
 
+// ------------------------------------------------------------- Q8_0 weights
+
+// one thread per (row, group): the 34-byte GGUF group to its tile slots
+__global__ void q8_repack_kernel(const uint8_t* raw, int rows, int groups, int row0, uint8_t* q, uint16_t* d,
+                                 int* bad) {
+    const size_t total = static_cast<size_t>(rows) * groups;
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const int r = static_cast<int>(i / groups), g = static_cast<int>(i % groups);
+        const uint8_t* src = raw + i * 34;
+        const int row = row0 + r, rr = row % 16;
+        const size_t block = static_cast<size_t>(row / 16) * groups + g;
+        const uint16_t h = static_cast<uint16_t>(src[0] | (src[1] << 8));
+        d[block * 16 + rr] = h;
+        if (!__builtin_isfinite(half_bits_to_float(h))) atomicOr(bad, 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint8_t* dst = q + (block * 64 + rr + 16 * j) * 8;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) dst[b] = src[2 + 8 * j + b];
+        }
+    }
+}
+
+struct Q8MatvecArgs {
+    const uint2* q;
+    const uint16_t* d;
+    const float* v;
+    int rows, groups;
+    MatvecSegment seg[3];
+    int nseg;
+};
+
+// sum of 8 int8 (two dwords) times 8 floats, in f32
+__device__ __forceinline__ float dot8(uint2 q, float4 a, float4 b) {
+    float s = sbyte_to_float<0>(q.x) * a.x;
+    s = fmaf(sbyte_to_float<1>(q.x), a.y, s);
+    s = fmaf(sbyte_to_float<2>(q.x), a.z, s);
+    s = fmaf(sbyte_to_float<3>(q.x), a.w, s);
+    s = fmaf(sbyte_to_float<0>(q.y), b.x, s);
+    s = fmaf(sbyte_to_float<1>(q.y), b.y, s);
+    s = fmaf(sbyte_to_float<2>(q.y), b.z, s);
+    return fmaf(sbyte_to_float<3>(q.y), b.w, s);
+}
+
+__device__ __forceinline__ void write_segment(const MatvecSegment* seg, int nseg, int row, size_t col_offset_rows,
+                                              float y) {
+    int r = row, s = 0;
+    while (s + 1 < nseg && r >= seg[s].rows) r -= seg[s++].rows;
+    const size_t at = col_offset_rows * seg[s].rows + r;
+    seg[s].out[at] = seg[s].residual ? __fadd_rn(seg[s].residual[at], y) : y;
+}
+
+// y = W v over Q8_0 tiles: a workgroup per 16-row tile, its W waves taking
+// contiguous shares of the groups.  Lane l accumulates row l%16 over its
+// eight columns of each group: the eight products in f32, scaled by the
+// group's d and added in double; lanes and waves are then summed in double
+// and the row rounds to float once.
+template <int W>
+__global__ __launch_bounds__(W * 64) void matvec_q8_kernel(const Q8MatvecArgs a) {
+    __shared__ double red[W][16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tile = blockIdx.x;
+    const int per = (a.groups + W - 1) / W;
+    const int g0 = min(a.groups, wave * per), g1 = min(a.groups, g0 + per);
+    const uint2* qp = a.q + static_cast<size_t>(tile) * a.groups * 64 + lane;
+    const uint16_t* dp = a.d + static_cast<size_t>(tile) * a.groups * 16 + (lane & 15);
+    const float* vp = a.v + 8 * (lane >> 4);
+    double acc = 0;
+    int g = g0;
+    for (; g + 4 <= g1; g += 4) {
+        uint2 qq[4];
+        uint16_t dd[4];
+        float4 va[4], vb[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            qq[u] = qp[static_cast<size_t>(g + u) * 64];
+            dd[u] = dp[static_cast<size_t>(g + u) * 16];
+            va[u] = *reinterpret_cast<const float4*>(vp + 32 * (g + u));
+            vb[u] = *reinterpret_cast<const float4*>(vp + 32 * (g + u) + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            acc = fma(static_cast<double>(half_bits_to_float(dd[u])), static_cast<double>(dot8(qq[u], va[u], vb[u])),
+                      acc);
+    }
+    for (; g < g1; ++g) {
+        const uint2 qq = qp[static_cast<size_t>(g) * 64];
+        const float4 va = *reinterpret_cast<const float4*>(vp + 32 * g);
+        const float4 vb = *reinterpret_cast<const float4*>(vp + 32 * g + 4);
+        acc = fma(static_cast<double>(half_bits_to_float(dp[static_cast<size_t>(g) * 16])),
+                  static_cast<double>(dot8(qq, va, vb)), acc);
+    }
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    if (lane < 16) red[wave][lane] = acc;
+    __syncthreads();
+    if (wave || lane >= 16) return;
+    double t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < W; ++w) t += red[w][lane];
+    const int row = tile * 16 + lane;
+    if (row < a.rows) write_segment(a.seg, a.nseg, row, 0, static_cast<float>(t));
+}
+
+// The batched product runs on fp16 MFMAs.  int8 weights are exact in fp16;
+// each activation x is scaled by a power of two per vector (max |x| into
+// [2^13, 2^14), exact) and split as x = hi + lo with hi = fp16(x) and
+// lo = fp16(x - hi), which keeps 22 of its 24 bits.  One 16x16x32 MFMA then
+// covers exactly one Q8_0 group: C = A*Bhi + A*Blo in f32, and the
+// accumulator takes d * C.  The halves of vector j, column k sit where lane
+// (j%16) + 16((k%32)/8) of vector tile j/16 reads them as a B operand:
+// halves[((vt*groups + g)*2 + part)*64 + lane][k%8].
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void split_halves_kernel(const float* x, int cols, int groups, _Float16* halves,
+                                                            float* unscale) {
+    __shared__ float part[4];
+    const int j = blockIdx.x;
+    const float* xr = x + static_cast<size_t>(j) * cols;
+    float m = 0.f;
+    for (int k = threadIdx.x; k < cols; k += 256) m = fmaxf(m, fabsf(xr[k]));
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    int e = 0;
+    if (m > 0.f && __builtin_isfinite(m)) frexpf(m, &e);
+    const int shift = m > 0.f && __builtin_isfinite(m) ? 14 - e : 0;
+    const float up = ldexpf(1.f, shift);
+    if (threadIdx.x == 0) unscale[j] = ldexpf(1.f, -shift);
+    const int vt = j / 16, jl = j % 16;
+    for (int k = threadIdx.x; k < cols; k += 256) {
+        const float v = xr[k] * up;
+        const _Float16 hi = static_cast<_Float16>(v);
+        const _Float16 lo = static_cast<_Float16>(v - static_cast<float>(hi));
+        const int g = k / 32, lane = jl + 16 * ((k % 32) / 8);
+        const size_t at = ((static_cast<size_t>(vt) * groups + g) * 2 * 64 + lane) * 8 + k % 8;
+        halves[at] = hi;
+        halves[at + 64 * 8] = lo;
+    }
+}
+
+// eight int8 (two dwords) to eight fp16: each byte b, offset by 128, becomes
+// the fp16 1024 + (b ^ 0x80) (0x64 above the byte), from which 1152 is
+// subtracted exactly
+__device__ __forceinline__ half8 i8x8_to_half8(uint2 q) {
+    const uint32_t x = q.x ^ 0x80808080u, y = q.y ^ 0x80808080u;
+    const uint32_t w[4] = {__builtin_amdgcn_perm(0x64646464u, x, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, y, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, y, 0x04030402u)};
+    const half2v bias = {static_cast<_Float16>(1152.f), static_cast<_Float16>(1152.f)};
+    half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v h = __builtin_bit_cast(half2v, w[i]) - bias;
+        r[2 * i] = h[0];
+        r[2 * i + 1] = h[1];
+    }
+    return r;
+}
+
+struct Q8BatchArgs {
+    const uint2* q;
+    const uint16_t* d;
+    const uint4* halves;  // 8 fp16 per lane, see split_halves_kernel
+    const float* unscale;
+    int rows, tiles, groups, n;
+    MatvecSegment seg[3];
+    int nseg;
+    int groups_per_split;
+    float* partial;  // split-K: [gridDim.y][n][rows], else null
+};
+
+// A workgroup of four waves covers 4*RT row tiles and up to NT vector tiles
+// of 16 over a share of the groups; each wave owns RT row tiles.  The
+// halves of CH groups at a time are staged in LDS (double buffered) and read
+// by all four waves; the int8 tiles come straight from HBM into registers.
+template <int RT, int NT>
+__global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
+    constexpr int CH = 2;
+    __shared__ uint4 bs[2][CH][NT][2][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gbeg = blockIdx.y * a.groups_per_split;
+    const int gend = min(a.groups, gbeg + a.groups_per_split);
+    const int nchunks = (gend - gbeg + CH - 1) / CH;
+    int tile[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) tile[r] = min((blockIdx.x * 4 + wave) * RT + r, a.tiles - 1);
+
+    auto stage = [&](int buf, int chunk) {
+        constexpr int per_stage = CH * NT * 2 * 64;
+#pragma unroll
+        for (int i = 0; i < (per_stage + 255) / 256; ++i) {
+            const int e = threadIdx.x + 256 * i;
+            if (e < per_stage) {
+                const int l = e % 64, part = (e / 64) % 2, vt = (e / 128) % NT, c = e / (128 * NT);
+                const int g = min(gbeg + chunk * CH + c, gend - 1);
+                bs[buf][c][vt][part][l] = a.halves[((static_cast<size_t>(vt) * a.groups + g) * 2 + part) * 64 + l];
+            }
+        }
+    };
+
+    float4v acc[RT][NT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int v = 0; v < NT; ++v) acc[r][v] = float4v{0.f, 0.f, 0.f, 0.f};
+
+    stage(0, 0);
+    __syncthreads();
+    for (int chunk = 0; chunk < nchunks; ++chunk) {
+        const int buf = chunk & 1;
+        if (chunk + 1 < nchunks) stage(buf ^ 1, chunk + 1);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int g = gbeg + chunk * CH + c;
+            if (g < gend) {  // uniform across the workgroup
+                half8 am[RT];
+                float dv[RT][4];
+#pragma unroll
+                for (int r = 0; r < RT; ++r) {
+                    const size_t blk = static_cast<size_t>(tile[r]) * a.groups + g;
+                    am[r] = i8x8_to_half8(a.q[blk * 64 + lane]);
+                    const uint2 dd = *reinterpret_cast<const uint2*>(a.d + blk * 16 + 4 * (lane >> 4));
+                    dv[r][0] = half_bits_to_float(static_cast<uint16_t>(dd.x & 0xffff));
+                    dv[r][1] = half_bits_to_float(static_cast<uint16_t>(dd.x >> 16));
+                    dv[r][2] = half_bits_to_float(static_cast<uint16_t>(dd.y & 0xffff));
+                    dv[r][3] = half_bits_to_float(static_cast<uint16_t>(dd.y >> 16));
+                }
+#pragma unroll
+                for (int v = 0; v < NT; ++v) {
+                    const half8 bh = __builtin_bit_cast(half8, bs[buf][c][v][0][lane]);
+                    const half8 bl = __builtin_bit_cast(half8, bs[buf][c][v][1][lane]);
+#pragma unroll
+                    for (int r = 0; r < RT; ++r) {
+                        float4v cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[r], bh, float4v{0.f, 0.f, 0.f, 0.f}, 0,
+                                                                            0, 0);
+                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[r], bl, cc, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[r][v][i] = fmaf(dv[r][i], cc[i], acc[r][v][i]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    // lane l holds rows 4(l/16)+i of each tile, vector l%16 of each vector tile
+#pragma unroll
+    for (int v = 0; v < NT; ++v) {
+        const int j = v * 16 + (lane & 15);
+        if (j >= a.n) continue;
+        const float us = a.unscale[j];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const int t = (blockIdx.x * 4 + wave) * RT + r;
+            if (t >= a.tiles) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = t * 16 + 4 * (lane >> 4) + i;
+                if (row >= a.rows) continue;
+                const float y = acc[r][v][i] * us;
+                if (a.partial)
+                    a.partial[(static_cast<size_t>(blockIdx.y) * a.n + j) * a.rows + row] = y;
+                else
+                    write_segment(a.seg, a.nseg, row, static_cast<size_t>(j), y);
+            }
+        }
+    }
+}
+
+// element (j, c) of row idx[j] (or `row`) of a Q8_0 table
+__global__ void gather_embedding_q8_kernel(const uint8_t* q, const uint16_t* d, int groups, const uint32_t* idx,
+                                           uint32_t row, int n, int h, float* out) {
+    const size_t total = static_cast<size_t>(n) * h;
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const int j = static_cast<int>(i / h), c = static_cast<int>(i % h);
+        const uint32_t r = idx ? idx[j] : row;
+        const size_t blk = static_cast<size_t>(r / 16) * groups + c / 32;
+        const int lane = static_cast<int>(r % 16) + 16 * ((c % 32) / 8);
+        const float dv = half_bits_to_float(d[blk * 16 + r % 16]);
+        out[i] = __fmul_rn(dv, static_cast<float>(static_cast<int8_t>(q[(blk * 64 + lane) * 8 + c % 8])));
+    }
+}
+
 unsigned grid_for(size_t n) {
     return static_cast<unsigned>(std::min<size_t>((n + kThreads - 1) / kThreads, 8192));
 }
@@ -421,6 +711,113 @@ void launch_rope(float* q, int qheads, float* k, int kheads, int dim, const floa
 
 void launch_swiglu(float* gate, const float* up, int n, hipStream_t s) {
     launch("model_swiglu", swiglu_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, s, gate, up, n);
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_q8_repack(const uint8_t* raw, int rows, int cols, int row0, Weight& w, int* bad, hipStream_t s) {
+    const size_t total = static_cast<size_t>(rows) * (cols / 32);
+    if (!total) return;
+    launch("model_q8_repack", q8_repack_kernel, dim3(grid_for(total)), dim3(kThreads), 0, s, raw, rows, cols / 32, row0,
+           static_cast<uint8_t*>(w.q.ptr), static_cast<uint16_t*>(w.d.ptr), bad);
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s) {
+    Q8MatvecArgs a{};
+    a.q = static_cast<const uint2*>(w.q.ptr);
+    a.d = static_cast<const uint16_t*>(w.d.ptr);
+    a.v = v;
+    a.rows = w.rows;
+    a.groups = w.groups();
+    a.nseg = nseg;
+    for (int i = 0; i < nseg; ++i) a.seg[i] = seg[i];
+    // waves per tile: enough workgroups x waves to fill the chip (about
+    // 2,048 waves), no more waves than groups
+    const int tiles = w.tiles();
+    const int want = std::max(1, std::min(a.groups, 2048 / std::max(tiles, 1)));
+    if (want >= 8)
+        launch("model_matvec_q8", matvec_q8_kernel<8>, dim3(tiles), dim3(512), 0, s, a);
+    else if (want >= 4)
+        launch("model_matvec_q8", matvec_q8_kernel<4>, dim3(tiles), dim3(256), 0, s, a);
+    else if (want >= 2)
+        launch("model_matvec_q8", matvec_q8_kernel<2>, dim3(tiles), dim3(128), 0, s, a);
+    else
+        launch("model_matvec_q8", matvec_q8_kernel<1>, dim3(tiles), dim3(64), 0, s, a);
+    TVARA_HIP(hipGetLastError());
+}
+
+namespace {
+template <int RT>
+void launch_batch_q8_rt(int nt, dim3 grid, hipStream_t s, const Q8BatchArgs& a) {
+    switch (nt) {
+        case 1: launch("model_matvec_q8", batch_q8_kernel<RT, 1>, grid, dim3(256), 0, s, a); break;
+        case 2: launch("model_matvec_q8", batch_q8_kernel<RT, 2>, grid, dim3(256), 0, s, a); break;
+        case 3: launch("model_matvec_q8", batch_q8_kernel<RT, 3>, grid, dim3(256), 0, s, a); break;
+        default: launch("model_matvec_q8", batch_q8_kernel<RT, 4>, grid, dim3(256), 0, s, a); break;
+    }
+}
+}  // namespace
+
+void launch_batch_matvec_q8(const Weight& w, const float* x, int n, const MatvecSegment* seg, int nseg,
+                            DeviceBuffer& halves, DeviceBuffer& work, hipStream_t s) {
+    const int groups = w.groups(), tiles = w.tiles(), cols = w.cols;
+    for (int j0 = 0; j0 < n; j0 += 64) {
+        const int nj = std::min(64, n - j0), nt = (nj + 15) / 16;
+        // halves of up to 64 vectors, then one float of unscale per vector
+        const size_t half_bytes = static_cast<size_t>(nt) * groups * 2 * 64 * 8 * sizeof(_Float16);
+        auto* base = static_cast<char*>(halves.ensure(half_bytes + 64 * sizeof(float)));
+        auto* hv = reinterpret_cast<_Float16*>(base);
+        auto* unscale = reinterpret_cast<float*>(base + half_bytes);
+        launch("model_split_halves", split_halves_kernel, dim3(nj), dim3(256), 0, s, x + static_cast<size_t>(j0) * cols,
+               cols, groups, hv, unscale);
+        Q8BatchArgs a{};
+        a.q = static_cast<const uint2*>(w.q.ptr);
+        a.d = static_cast<const uint16_t*>(w.d.ptr);
+        a.halves = reinterpret_cast<const uint4*>(hv);
+        a.unscale = unscale;
+        a.rows = w.rows;
+        a.tiles = tiles;
+        a.groups = groups;
+        a.n = nj;
+        a.nseg = nseg;
+        for (int i = 0; i < nseg; ++i) {
+            a.seg[i] = seg[i];
+            a.seg[i].out = seg[i].out + static_cast<size_t>(j0) * seg[i].rows;
+            if (seg[i].residual) a.seg[i].residual = seg[i].residual + static_cast<size_t>(j0) * seg[i].rows;
+        }
+        // two row tiles per wave when that still gives 128 workgroups; then
+        // split the groups until the launch has about 512
+        const int rt = (tiles + 7) / 8 >= 128 ? 2 : 1;
+        const int gx = (tiles + 4 * rt - 1) / (4 * rt);
+        const int want = std::max(1, std::min((groups + 1) / 2, (512 + gx - 1) / gx));
+        const int per = (groups + want - 1) / want, splits = (groups + per - 1) / per;
+        a.groups_per_split = per;
+        if (splits > 1) a.partial = static_cast<float*>(work.ensure(static_cast<size_t>(splits) * nj * w.rows * sizeof(float)));
+        const dim3 grid(gx, splits);
+        if (rt == 2)
+            launch_batch_q8_rt<2>(nt, grid, s, a);
+        else
+            launch_batch_q8_rt<1>(nt, grid, s, a);
+        if (splits > 1) {
+            BatchMatvecArgs b{};
+            b.rows = w.rows;
+            b.n = nj;
+            b.nseg = nseg;
+            for (int i = 0; i < nseg; ++i) b.seg[i] = a.seg[i];
+            b.partial = a.partial;
+            launch("model_matvec_sum", split_sum_kernel, dim3(grid_for(static_cast<size_t>(nj) * w.rows)),
+                   dim3(kThreads), 0, s, b, splits);
+        }
+    }
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_gather_embedding_q8(const Weight& w, const uint32_t* idx, uint32_t row, int n, float* out,
+                                hipStream_t s) {
+    const size_t total = static_cast<size_t>(n) * w.cols;
+    launch("model_embedding", gather_embedding_q8_kernel, dim3(grid_for(total)), dim3(kThreads), 0, s,
+           static_cast<const uint8_t*>(w.q.ptr), static_cast<const uint16_t*>(w.d.ptr), w.groups(), idx, row, n,
+           w.cols, out);
     TVARA_HIP(hipGetLastError());
 }
 
