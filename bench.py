@@ -155,6 +155,23 @@ def bench_prefill(args):
     assert np.isfinite(out.numpy()).all()
     tfs = w.flops() / (kernel_ms * 1e-3) / 1e12
     log(f"prefill kernel {kernel_ms * 1e3:.1f} us, call {ms_per_step * 1e3:.1f} us, {tfs:.1f} TFLOP/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import pyoracle
+
+        if pyoracle.ref_available():
+            # the reference's fused_prompt_attention (its FP64 loop, one
+            # thread) over the whole workload, sequence by sequence
+            ref = pyoracle.RefCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks())
+            rseqs = workloads.fill_prefill(ref, w)
+            t0 = time.perf_counter()
+            for i, rs in enumerate(rseqs):
+                ref.fused_prompt_attention(w.chunk_queries(i), rs, 0, w.prefix, w.chunk, w.heads, w.context)
+            cpu_s = time.perf_counter() - t0
+            cpu = {"value": round(w.flops() / cpu_s / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "reference",
+                   "sample": f"the whole workload ({w.sequences} chunks of {w.chunk} rows, {w.heads} heads) through "
+                             f"the reference's fused_prompt_attention, 1 thread: {cpu_s:.2f} s",
+                   "seconds": round(cpu_s, 3)}
     print(json.dumps({
         "metric": "paged chunked prefill attn: achieved TFLOP/s (MFMA utilisation), 1 MI355X",
         "value": round(w.flops() / (ms_per_step * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
@@ -166,7 +183,7 @@ def bench_prefill(args):
                      "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
                      "traffic": hbm_traffic(w.name, "paged_prefill_bf16"), "kernel": "paged_prefill_bf16",
                      "kernel_avg_us": round(kernel_ms * 1e3, 3), "algorithmic_flops": w.flops()},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }), flush=True)
 
 

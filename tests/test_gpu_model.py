@@ -266,3 +266,78 @@ def test_sequences_decode_odd_width_falls_back(tmp_path, ref_capi):
         got = mine.decode_sequences(sm, toks)
         ok, err = close(got, np.stack([ref.logits(r, t) for r, t in zip(sr, toks)]))
         assert ok, err
+
+
+class _SerialBackend:
+    """The reference's NativeSchedulerBackend loop (scheduler.py:201-210),
+    over any NativeModel (here the reference's own library)."""
+
+    def __init__(self, model):
+        self.model, self.sequences, self.pending = model, {}, {}
+
+    def create(self, key):
+        self.sequences[key] = self.model._new_sequence()
+
+    def prefill(self, key, tokens):
+        for token in tokens:
+            self.pending[key] = self.model.logits(self.sequences[key], token)
+
+    def decode_batch(self, keys):
+        result = []
+        for key in keys:
+            logits = self.pending[key]
+            if not np.isfinite(logits).all():
+                raise ValueError("Nonfinite model logits")
+            token = int(logits.argmax())
+            result.append(token)
+            self.pending[key] = self.model.logits(self.sequences[key], token)
+        return result
+
+
+def test_scheduler_backend_batches_like_serial_reference(tmp_path, ref_capi):
+    # the batched backend against the reference's serial loop: the same
+    # greedy tokens and pending logits within the bar, including a key listed
+    # twice in one iteration and a key dropped midway
+    from tvara_amd.scheduler import NativeSchedulerBackend
+
+    spec = gf.LlamaSpec(matrix_type=gf.T_Q8_0, hidden=128, intermediate=256, heads=8, kv_heads=2, vocab=64)
+    path = spec.write(tmp_path / "m.gguf")
+    mine = NativeSchedulerBackend(native.NativeModel(path, max_blocks=256, block_tokens=4))
+    ref = _SerialBackend(native.NativeModel(path, library=ref_capi, max_blocks=256, block_tokens=4))
+    keys = [f"r{i}" for i in range(9)]
+    rng = np.random.default_rng(5)
+    for k in keys:
+        prompt = [int(t) for t in rng.integers(0, spec.vocab, int(rng.integers(1, 6)))]
+        for b in (mine, ref):
+            b.create(k)
+            b.prefill(k, prompt)
+    for step in range(5):
+        batch = keys + ([keys[2]] if step == 1 else [])
+        # greedy choices can only differ where two logits tie within the bar
+        margins = [np.sort(ref.pending[k])[-2:] for k in batch]
+        got, want = mine.decode_batch(batch), ref.decode_batch(batch)
+        for k, g, w, m in zip(batch, got, want, margins):
+            assert g == w or abs(m[1] - m[0]) < 1e-3, (step, k, g, w)
+        if got != want:
+            pytest.skip("a greedy choice tied within the bar; the sequences diverge from here")
+        for k in keys:
+            ok, err = close(mine.pending[k], ref.pending[k])
+            assert ok, (step, k, err)
+        if step == 2:
+            mine.drop(keys[0])
+            ref.model._drop_sequence(ref.sequences.pop(keys[0]))
+            keys = keys[1:]
+    bad = keys[3]
+    for b in (mine, ref):
+        b.pending[bad] = np.full(spec.vocab, np.nan, np.float32)
+    cache = mine.model.cache()
+    before = {k: cache.length(mine.sequences[k]) for k in keys}
+    for b in (mine, ref):
+        with pytest.raises(ValueError, match="Nonfinite model logits"):
+            b.decode_batch(keys)
+    # the keys before the bad one were decoded, the rest were not
+    after = {k: cache.length(mine.sequences[k]) for k in keys}
+    assert [after[k] - before[k] for k in keys] == [1, 1, 1] + [0] * (len(keys) - 3)
+    for k in keys[:3]:
+        ok, err = close(mine.pending[k], ref.pending[k])
+        assert ok, (k, err)
