@@ -687,10 +687,92 @@ __global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
     }
 }
 
+// The same merge with one wave per (row, head) and four heads per
+// workgroup, for head_dim = 4 * LPR with LPR a power of two up to 64: lane
+// (r, u) holds float4 u of splits r, r + R, ... (R = 64 / LPR), U of them
+// per memory round trip, and the R slots combine by shuffles.
+template <int LPR, int U>
+__global__ __launch_bounds__(256) void merge_wave_kernel(const DecodeArgs a) {
+    constexpr int R = 64 / LPR, D = 4 * LPR;
+    const int lane = threadIdx.x & 63, h = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const int row = blockIdx.x;
+    if (h >= a.heads) return;
+    const int4 en = a.entries[row];
+    const int nsplit = en.z >> 1;
+    if (nsplit <= 1) return;
+    const int u = lane % LPR, r = lane / LPR;
+    const size_t step = static_cast<size_t>(a.heads);
+    const float* ml = a.part_ml + (static_cast<size_t>(en.w) * step + h) * 2;
+    const float* pa = a.part_acc + (static_cast<size_t>(en.w) * step + h) * D;
+    float M = -INFINITY, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < nsplit; s0 += R * U) {
+        float m[U], l[U];
+        float4 x[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const int sp = s0 + k * R + r;
+            const bool ok = sp < nsplit;
+            m[k] = ok ? ml[sp * step * 2] : -INFINITY;
+            l[k] = ok ? ml[sp * step * 2 + 1] : 0.f;
+            x[k] = ok ? *reinterpret_cast<const float4*>(pa + sp * step * D + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float mc = M;
+#pragma unroll
+        for (int k = 0; k < U; ++k) mc = fmaxf(mc, m[k]);
+        if (mc != -INFINITY) {
+            const float sc = fast_exp2(M - mc);  // 0 while M is still -inf
+            L *= sc;
+            acc.x *= sc;
+            acc.y *= sc;
+            acc.z *= sc;
+            acc.w *= sc;
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                const float w = fast_exp2(m[k] - mc);  // 0 for an empty slot
+                L = fmaf(w, l[k], L);
+                acc.x = fmaf(w, x[k].x, acc.x);
+                acc.y = fmaf(w, x[k].y, acc.y);
+                acc.z = fmaf(w, x[k].z, acc.z);
+                acc.w = fmaf(w, x[k].w, acc.w);
+            }
+            M = mc;
+        }
+    }
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) {
+        const float Mo = __shfl_xor(M, off), Lo = __shfl_xor(L, off);
+        const float4 ao = make_float4(__shfl_xor(acc.x, off), __shfl_xor(acc.y, off), __shfl_xor(acc.z, off),
+                                      __shfl_xor(acc.w, off));
+        const float Mt = fmaxf(M, Mo);
+        const float w1 = M == -INFINITY ? 0.f : fast_exp2(M - Mt);
+        const float w2 = Mo == -INFINITY ? 0.f : fast_exp2(Mo - Mt);
+        L = fmaf(w1, L, w2 * Lo);
+        acc.x = fmaf(w1, acc.x, w2 * ao.x);
+        acc.y = fmaf(w1, acc.y, w2 * ao.y);
+        acc.z = fmaf(w1, acc.z, w2 * ao.z);
+        acc.w = fmaf(w1, acc.w, w2 * ao.w);
+        M = Mt;
+    }
+    if (r) return;
+    const float inv = 1.f / L;
+    *reinterpret_cast<float4*>(a.out + (static_cast<size_t>(row) * a.heads + h) * D + 4 * u) =
+        make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+}
+
 void launch_merge(const DecodeArgs& a, int nrows, hipStream_t s) {
     const int D = a.lay.head_dim;
     const dim3 grid(nrows, a.heads), block(256);
-    if (D % 4 == 0 && D <= 256)
+    const dim3 wgrid(nrows, (a.heads + 3) / 4);
+    if (D == 64)
+        launch("paged_decode_merge", merge_wave_kernel<16, 4>, wgrid, block, 0, s, a);
+    else if (D == 128)
+        launch("paged_decode_merge", merge_wave_kernel<32, 8>, wgrid, block, 0, s, a);
+    else if (D == 256)
+        launch("paged_decode_merge", merge_wave_kernel<64, 8>, wgrid, block, 0, s, a);
+    else if (D == 32)
+        launch("paged_decode_merge", merge_wave_kernel<8, 4>, wgrid, block, 0, s, a);
+    else if (D % 4 == 0 && D <= 256)
         launch("paged_decode_merge", merge_kernel<4, 1, 8>, grid, block, 0, s, a);
     else if (D % 4 == 0)
         launch("paged_decode_merge", merge_kernel<4, 2, 8>, grid, block, 0, s, a);
