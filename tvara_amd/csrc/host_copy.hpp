@@ -1,0 +1,48 @@
+// Device-to-pageable-host copies at pinned-memory speed: the data moves in
+// chunks through two pinned staging buffers (DMA of chunk i+1 in flight while
+// chunk i is copied out) and a small pool of host threads copies each chunk
+// into the caller's buffer.  A single hipMemcpy into pageable memory stages
+// through the driver's own buffers on one thread.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <condition_variable>
+#include <cstddef>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+namespace tvara_amd {
+
+class HostCopier {
+public:
+    HostCopier();
+    ~HostCopier();
+    HostCopier(const HostCopier&) = delete;
+    HostCopier& operator=(const HostCopier&) = delete;
+    // synchronous: returns when `bytes` from device `src` (after the work
+    // already queued on `s`) are in host `dst`
+    void from_device(void* dst, const void* src, size_t bytes, hipStream_t s);
+
+private:
+    void parallel_copy(char* dst, const char* src, size_t bytes);
+    void worker(int index);
+
+    static constexpr size_t kChunk = size_t(4) << 20;
+    void* pinned_[2] = {nullptr, nullptr};
+    hipEvent_t done_[2] = {nullptr, nullptr};
+    std::vector<std::thread> threads_;
+    std::mutex mu_;
+    std::condition_variable work_cv_, done_cv_;
+    // the current job: part k of parts goes to worker k - 1 (part 0 stays on
+    // the calling thread)
+    char* job_dst_ = nullptr;
+    const char* job_src_ = nullptr;
+    size_t job_bytes_ = 0;
+    int parts_ = 0, pending_ = 0;
+    unsigned long generation_ = 0;
+    bool stop_ = false;
+};
+
+}  // namespace tvara_amd

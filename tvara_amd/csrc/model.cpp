@@ -224,7 +224,7 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
     // the token's K/V for every layer, appended after all layers succeeded
     // (paged_model.hpp:27)
     cache_->append_batch(&sequence, 1, at(kall_, 0), at(vall_, 0), true);
-    TVARA_HIP(hipMemcpy(logits_host, logits_.ptr, c.vocab * sizeof(float), hipMemcpyDeviceToHost));
+    copier_.from_device(logits_host, logits_.ptr, c.vocab * sizeof(float), s);
 }
 
 void DeviceModel::matvec(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s) {
@@ -234,18 +234,20 @@ void DeviceModel::matvec(const Weight& w, const float* v, const MatvecSegment* s
         launch_matvec(static_cast<const float*>(w.f32.ptr), w.rows, w.cols, v, seg, nseg, s);
 }
 
-void DeviceModel::batch_matvec(const Weight& w, const float* x, int n, const MatvecSegment* seg, int nseg,
-                               hipStream_t s) {
-    if (w.q8)
-        launch_batch_matvec_q8(w, x, n, seg, nseg, bhalves_, bwork_, s);
-    else
-        launch_batch_matvec(static_cast<const float*>(w.f32.ptr), w.rows, w.cols, x, n, seg, nseg, bwork_, s);
-}
-
 void DeviceModel::ensure_batch(size_t n) {
     if (n <= batch_cap_) return;
     const ModelConfig& c = cfg_;
     const size_t H = c.hidden, I = c.intermediate, KV = c.kv_width(), L = c.layers, F = sizeof(float);
+    if (!part_rows_) {
+        auto note = [&](const Weight& w) { part_rows_ = std::max(part_rows_, static_cast<size_t>(batch_splits(w)) * w.rows); };
+        for (const Layer& l : layers_) {
+            note(l.qkv);
+            note(l.out);
+            note(l.gate_up);
+            note(l.down);
+        }
+        note(has_output_ ? output_ : embedding_);
+    }
     bx_.ensure(n * H * F);
     bnorm_.ensure(n * H * F);
     bq_.ensure(n * H * F);
@@ -255,10 +257,12 @@ void DeviceModel::ensure_batch(size_t n) {
     bvapp_.ensure(n * L * KV * F);
     battn_.ensure(n * H * F);
     bgate_.ensure(n * I * F);
-    bup_.ensure(n * I * F);
     blogits_.ensure(n * c.vocab * F);
     brope_.ensure(n * c.head_dim() * F);
     btok_.ensure(n * sizeof(uint32_t));
+    bpart_.ensure(n * part_rows_ * F);
+    bhalves_.ensure((n + 15) / 16 * 16 * std::max(H, I) * 2 * sizeof(_Float16));
+    bunscale_.ensure(n * F);
     batch_cap_ = n;
 }
 
@@ -280,8 +284,9 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     }
     if (n > static_cast<size_t>(std::numeric_limits<int>::max() / std::max<size_t>(c.vocab, c.hidden)))
         throw std::invalid_argument("decode batch too large");
-    if (c.hidden % 32 || c.intermediate % 32) {
-        // the batched matvec tiles K by 32: decode the sequences one by one
+    if (c.hidden % 32 || c.intermediate % 32 || c.hidden > 16384 || c.intermediate > 16384) {
+        // the batched products tile K by 32 and the epilogues hold a row of
+        // up to 16,384 in registers: decode the sequences one by one
         size_t done = 0;
         try {
             for (; done < n; ++done) decode(seqs[done], tokens[done], logits_host + done * c.vocab);
@@ -301,7 +306,11 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     float* q = at(bq_, 0);
     float* attn = at(battn_, 0);
     float* gate = at(bgate_, 0);
-    float* up = at(bup_, 0);
+    float* part = at(bpart_, 0);
+    auto* halves = static_cast<_Float16*>(bhalves_.ptr);
+    float* unscale = at(bunscale_, 0);
+    auto halves_for = [&](const Weight& w) { return w.q8 ? halves : nullptr; };
+    const Weight& logits_w = has_output_ ? output_ : embedding_;
 
     // tokens and each row's (cos, sin) go up through one pinned staging area
     const size_t tok_bytes = (n * sizeof(uint32_t) + 15) / 16 * 16;
@@ -323,30 +332,39 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     else
         launch_gather_embedding(at(embedding_.f32, 0), static_cast<const uint32_t*>(btok_.ptr), N, H, x, s);
 
+    // Per layer: the products write split sums, and each epilogue finishes
+    // what follows its product (RoPE; the residual add with the next
+    // RMSNorm; SwiGLU) and writes the next product's input.
     AttnPlan plan;
     plan.build(cache_.get(), seqs, positions, std::vector<uint8_t>(n, 1), static_cast<int>(c.heads), 0);
+    launch_resid_norm(nullptr, 0, x, at(layers_[0].attn_norm, 0), N, H, c.rms_epsilon, norm,
+                      halves_for(layers_[0].qkv), unscale, s);
     for (size_t l = 0; l < c.layers; ++l) {
         Layer& L = layers_[l];
         float* kl = at(bk_, l * n * c.kv_width());
         float* vl = at(bv_, l * n * c.kv_width());
-        launch_rmsnorm(x, at(L.attn_norm, 0), norm, H, c.rms_epsilon, s, N);
-        const MatvecSegment qkv[3] = {{q, H, nullptr}, {kl, KV, nullptr}, {vl, KV, nullptr}};
-        batch_matvec(L.qkv, norm, N, qkv, 3, s);
-        launch_rope(q, static_cast<int>(c.heads), kl, static_cast<int>(c.kv_heads), D, at(brope_, 0),
-                    c.interleaved_rope, s, N);
+        launch_batch_product(L.qkv, norm, halves, unscale, N, part, s);
+        launch_qkv_epilogue(part, batch_splits(L.qkv), N, static_cast<int>(c.heads), static_cast<int>(c.kv_heads), D,
+                            c.interleaved_rope, at(brope_, 0), q, kl, vl, s);
         plan.launch(static_cast<int>(l), q, kl, vl, attn, s);
-        const MatvecSegment o[1] = {{x, H, x}};
-        batch_matvec(L.out, attn, N, o, 1, s);
-        launch_rmsnorm(x, at(L.ffn_norm, 0), norm, H, c.rms_epsilon, s, N);
-        const MatvecSegment gu[2] = {{gate, I, nullptr}, {up, I, nullptr}};
-        batch_matvec(L.gate_up, norm, N, gu, 2, s);
-        launch_swiglu(gate, up, N * I, s);
-        const MatvecSegment d[1] = {{x, H, x}};
-        batch_matvec(L.down, gate, N, d, 1, s);
+        if (L.out.q8) launch_split_halves(attn, N, H, halves, unscale, s);
+        launch_batch_product(L.out, attn, halves, unscale, N, part, s);
+        launch_resid_norm(part, batch_splits(L.out), x, at(L.ffn_norm, 0), N, H, c.rms_epsilon, norm,
+                          halves_for(L.gate_up), unscale, s);
+        launch_batch_product(L.gate_up, norm, halves, unscale, N, part, s);
+        launch_swiglu_epilogue(part, batch_splits(L.gate_up), N, I, gate, halves_for(L.down), unscale, s);
+        launch_batch_product(L.down, gate, halves, unscale, N, part, s);
+        const bool last = l + 1 == c.layers;
+        launch_resid_norm(part, batch_splits(L.down), x, last ? at(final_norm_, 0) : at(layers_[l + 1].attn_norm, 0), N,
+                          H, c.rms_epsilon, norm, halves_for(last ? logits_w : layers_[l + 1].qkv), unscale, s);
     }
-    launch_rmsnorm(x, at(final_norm_, 0), norm, H, c.rms_epsilon, s, N);
-    const MatvecSegment lg[1] = {{at(blogits_, 0), static_cast<int>(c.vocab), nullptr}};
-    batch_matvec(has_output_ ? output_ : embedding_, norm, N, lg, 1, s);
+    const int vocab = static_cast<int>(c.vocab);
+    if (batch_splits(logits_w) == 1) {
+        launch_batch_product(logits_w, norm, halves, unscale, N, at(blogits_, 0), s);
+    } else {
+        launch_batch_product(logits_w, norm, halves, unscale, N, part, s);
+        launch_split_sum(part, batch_splits(logits_w), N, vocab, at(blogits_, 0), s);
+    }
     plan.check();
     launch_interleave_layers(at(bk_, 0), at(bkapp_, 0), static_cast<int>(c.layers), N, KV, s);
     launch_interleave_layers(at(bv_, 0), at(bvapp_, 0), static_cast<int>(c.layers), N, KV, s);
@@ -357,7 +375,7 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
         for (size_t i = 0; i < applied; ++i) cache_->truncate(seqs[i], positions[i]);  // all or nothing
         throw;
     }
-    TVARA_HIP(hipMemcpy(logits_host, blogits_.ptr, n * c.vocab * sizeof(float), hipMemcpyDeviceToHost));
+    copier_.from_device(logits_host, blogits_.ptr, n * c.vocab * sizeof(float), s);
 }
 
 }  // namespace tvara_amd

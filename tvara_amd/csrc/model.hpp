@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "host_copy.hpp"
 #include "kv_cache.hpp"
 
 namespace tvara_amd {
@@ -43,10 +44,27 @@ void launch_dequant(uint32_t type, const uint8_t* raw, size_t n, float* out, int
 // flags `bad` when a group scale is not finite (then so is a value)
 void launch_q8_repack(const uint8_t* raw, int rows, int cols, int row0, Weight& w, int* bad, hipStream_t s);
 void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s);
-// the batched product over Q8_0 tiles on the MFMA units; `halves` and `work`
-// are scratch grown as needed
-void launch_batch_matvec_q8(const Weight& w, const float* x, int n, const MatvecSegment* seg, int nseg,
-                            DeviceBuffer& halves, DeviceBuffer& work, hipStream_t s);
+// Batched products for n vectors (one per sequence) write f32 sums per K
+// split, out[split][n][rows]; batch_splits gives the split count.  Q8_0
+// weights read the vectors as fp16 halves (launch_split_halves or an
+// epilogue below writes them, with a power-of-two unscale per vector), f32
+// weights read x [n][cols].
+int batch_splits(const Weight& w);
+void launch_batch_product(const Weight& w, const float* x, const _Float16* halves, const float* unscale, int n,
+                          float* out, hipStream_t s);
+void launch_split_halves(const float* x, int n, int cols, _Float16* halves, float* unscale, hipStream_t s);
+void launch_split_sum(const float* p, int splits, int n, int rows, float* out, hipStream_t s);
+// the split sums of the fused QKV product into q, k (rotated by row j's
+// (cos, sin) at cs + j*dim) and v
+void launch_qkv_epilogue(const float* p, int splits, int n, int qheads, int kheads, int dim, bool interleaved,
+                         const float* cs, float* q, float* k, float* v, hipStream_t s);
+// x += the split sums (p may be null), then RMSNorm into norm and, when
+// halves is given, into the next product's halves
+void launch_resid_norm(const float* p, int splits, float* x, const float* w, int n, int h, float eps, float* norm,
+                       _Float16* halves, float* unscale, hipStream_t s);
+// SwiGLU of the fused gate|up sums into out and, when given, halves
+void launch_swiglu_epilogue(const float* p, int splits, int n, int inter, float* out, _Float16* halves,
+                            float* unscale, hipStream_t s);
 // out[j] = row idx[j] (or `row` when idx is null) of a Q8_0 table, dequantised
 void launch_gather_embedding_q8(const Weight& w, const uint32_t* idx, uint32_t row, int n, float* out,
                                 hipStream_t s);
@@ -54,10 +72,6 @@ void launch_gather_embedding_q8(const Weight& w, const uint32_t* idx, uint32_t r
 void launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps, hipStream_t s, int rows = 1);
 void launch_matvec(const float* w, int rows, int cols, const float* v, const MatvecSegment* seg, int nseg,
                    hipStream_t s);
-// W applied to n vectors x[j] (row-major [n][cols]); segment s of output j at
-// seg[s].out + j * seg[s].rows
-void launch_batch_matvec(const float* w, int rows, int cols, const float* x, int n, const MatvecSegment* seg, int nseg,
-                         DeviceBuffer& work, hipStream_t s);
 void launch_interleave_layers(const float* src, float* dst, int layers, int n, int kv, hipStream_t s);
 void launch_gather_embedding(const float* table, const uint32_t* idx, int n, int h, float* out, hipStream_t s);
 // row j of a batch rotates q + j*qheads*dim and k + j*kheads*dim by cs + j*dim
@@ -95,7 +109,6 @@ private:
         Weight qkv, out, gate_up, down;
     };
     void matvec(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s);
-    void batch_matvec(const Weight& w, const float* x, int n, const MatvecSegment* seg, int nseg, hipStream_t s);
 
     ModelConfig cfg_;
     std::string metadata_;
@@ -108,9 +121,11 @@ private:
     DeviceBuffer x_, norm_, q_, kall_, vall_, attn_, gate_, up_, logits_, rope_, bad_;
     PinnedBuffer rope_host_;
     // batch work buffers, grown to the largest batch seen
-    DeviceBuffer bx_, bnorm_, bq_, bk_, bv_, bkapp_, bvapp_, battn_, bgate_, bup_, blogits_, brope_, btok_, bwork_,
-        bhalves_;
+    DeviceBuffer bx_, bnorm_, bq_, bk_, bv_, bkapp_, bvapp_, battn_, bgate_, blogits_, brope_, btok_, bpart_, bhalves_,
+        bunscale_;
+    size_t part_rows_ = 0;  // largest splits x rows of a batched product
     PinnedBuffer bhost_;
+    HostCopier copier_;
     size_t batch_cap_ = 0;
     void ensure_batch(size_t n);
 };

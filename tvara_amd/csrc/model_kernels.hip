@@ -176,7 +176,8 @@ struct BatchMatvecArgs {
     MatvecSegment seg[3];  // output j of segment s: seg.out[j * seg.rows + r]
     int nseg;
     int chunks_per_split;  // K chunks of kTileK per blockIdx.y
-    float* partial;        // split-K: [gridDim.y][n][rows] partial sums, else null
+    float* partial;        // split-K: [gridDim.y][n_total][rows] partial sums, else null
+    int n_total, j0;       // partial layout: vector stride and this launch's first vector
 };
 
 __global__ __launch_bounds__(256) void batch_matvec_kernel(const BatchMatvecArgs a) {
@@ -230,14 +231,14 @@ __global__ __launch_bounds__(256) void batch_matvec_kernel(const BatchMatvecArgs
         }
         __syncthreads();
     }
-    if (a.partial) {  // split-K: the fixed-order sum happens in split_sum_kernel
-        float* p = a.partial + static_cast<size_t>(blockIdx.y) * a.n * a.rows;
+    if (a.partial) {  // split-K: the fixed-order sum happens afterwards
+        float* p = a.partial + static_cast<size_t>(blockIdx.y) * a.n_total * a.rows;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 if (row0 + mr + i < a.rows && mv + j < a.n)
-                    p[static_cast<size_t>(mv + j) * a.rows + row0 + mr + i] = acc[i][j];
+                    p[static_cast<size_t>(a.j0 + mv + j) * a.rows + row0 + mr + i] = acc[i][j];
         return;
     }
 #pragma unroll
@@ -431,17 +432,51 @@ __global__ __launch_bounds__(W * 64) void matvec_q8_kernel(const Q8MatvecArgs a)
 }
 
 // The batched product runs on fp16 MFMAs.  int8 weights are exact in fp16;
-// each activation x is scaled by a power of two per vector (max |x| into
+// each activation vector is scaled by a power of two (max |x| into
 // [2^13, 2^14), exact) and split as x = hi + lo with hi = fp16(x) and
 // lo = fp16(x - hi), which keeps 22 of its 24 bits.  One 16x16x32 MFMA then
 // covers exactly one Q8_0 group: C = A*Bhi + A*Blo in f32, and the
-// accumulator takes d * C.  The halves of vector j, column k sit where lane
-// (j%16) + 16((k%32)/8) of vector tile j/16 reads them as a B operand:
-// halves[((vt*groups + g)*2 + part)*64 + lane][k%8].
+// accumulator takes d * C.  Element k of vector j sits where lane
+// (j%16) + 16((k%32)/8) of vector tile j/16 reads it as a B operand:
+// halves[((vt*groups + k/32)*2 + part)*64 + lane][k%8], part 0 = hi, 1 = lo.
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Write element k of vector j (already scaled by the vector's power of two)
+__device__ __forceinline__ void put_halves(_Float16* halves, int groups, int j, int k, float v) {
+    const _Float16 hi = static_cast<_Float16>(v);
+    const _Float16 lo = static_cast<_Float16>(v - static_cast<float>(hi));
+    const int lane = (j % 16) + 16 * ((k % 32) / 8);
+    const size_t at = ((static_cast<size_t>(j / 16) * groups + k / 32) * 2 * 64 + lane) * 8 + k % 8;
+    halves[at] = hi;
+    halves[at + 64 * 8] = lo;
+}
+
+// the power of two that brings max |x| into [2^13, 2^14) (1 for 0 or a
+// non-finite maximum, which then propagates)
+__device__ __forceinline__ int halves_shift(float m) {
+    int e = 0;
+    if (m > 0.f && __builtin_isfinite(m)) {
+        frexpf(m, &e);
+        return 14 - e;
+    }
+    return 0;
+}
+
+// max over the workgroup (every thread gets it); scratch holds a float per wave
+__device__ __forceinline__ float block_max(float m, float* scratch) {
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = m;
+    __syncthreads();
+    float r = scratch[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) r = fmaxf(r, scratch[w]);
+    return r;
+}
+
+// halves of vector j = blockIdx.x (a row of cols floats)
 __global__ __launch_bounds__(256) void split_halves_kernel(const float* x, int cols, int groups, _Float16* halves,
                                                             float* unscale) {
     __shared__ float part[4];
@@ -449,25 +484,10 @@ __global__ __launch_bounds__(256) void split_halves_kernel(const float* x, int c
     const float* xr = x + static_cast<size_t>(j) * cols;
     float m = 0.f;
     for (int k = threadIdx.x; k < cols; k += 256) m = fmaxf(m, fabsf(xr[k]));
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
-    int e = 0;
-    if (m > 0.f && __builtin_isfinite(m)) frexpf(m, &e);
-    const int shift = m > 0.f && __builtin_isfinite(m) ? 14 - e : 0;
+    const int shift = halves_shift(block_max(m, part));
     const float up = ldexpf(1.f, shift);
     if (threadIdx.x == 0) unscale[j] = ldexpf(1.f, -shift);
-    const int vt = j / 16, jl = j % 16;
-    for (int k = threadIdx.x; k < cols; k += 256) {
-        const float v = xr[k] * up;
-        const _Float16 hi = static_cast<_Float16>(v);
-        const _Float16 lo = static_cast<_Float16>(v - static_cast<float>(hi));
-        const int g = k / 32, lane = jl + 16 * ((k % 32) / 8);
-        const size_t at = ((static_cast<size_t>(vt) * groups + g) * 2 * 64 + lane) * 8 + k % 8;
-        halves[at] = hi;
-        halves[at + 64 * 8] = lo;
-    }
+    for (int k = threadIdx.x; k < cols; k += 256) put_halves(halves, groups, j, k, xr[k] * up);
 }
 
 // eight int8 (two dwords) to eight fp16: each byte b, offset by 128, becomes
@@ -493,43 +513,68 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint2 q) {
 struct Q8BatchArgs {
     const uint2* q;
     const uint16_t* d;
-    const uint4* halves;  // 8 fp16 per lane, see split_halves_kernel
+    const uint4* halves;  // 8 fp16 per lane, see put_halves
     const float* unscale;
-    int rows, tiles, groups, n;
-    MatvecSegment seg[3];
-    int nseg;
+    int rows, tiles, groups;
+    int n, vt0;  // vectors in this launch, first vector tile
+    int n_total;
     int groups_per_split;
-    float* partial;  // split-K: [gridDim.y][n][rows], else null
+    float* out;  // [gridDim.y][n_total][rows]
 };
 
+template <int RT, int CH>
+struct TilesChunk {
+    uint2 q[RT][CH], d[RT][CH];
+};
+
+template <int RT, int CH>
+__device__ __forceinline__ TilesChunk<RT, CH> q8_load_tiles(const Q8BatchArgs& a, int gbeg, int gend, int chunk,
+                                                            const int (&tile)[RT], int lane) {
+    TilesChunk<RT, CH> t;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int g = min(gbeg + chunk * CH + c, gend - 1);
+            const size_t blk = static_cast<size_t>(tile[r]) * a.groups + g;
+            t.q[r][c] = a.q[blk * 64 + lane];
+            t.d[r][c] = *reinterpret_cast<const uint2*>(a.d + blk * 16 + 4 * (lane >> 4));
+        }
+    return t;
+}
+
+// the halves of chunk `chunk` (clamped) into hb[BPT]: element e of a chunk is
+// ((c*NT + vt)*2 + part)*64 + l, thread t takes e = t, t + 256, ...
+#define Q8_LOAD_HALVES(chunk)                                                                                       \
+    _Pragma("unroll") for (int i = 0; i < BPT; ++i) {                                                               \
+        const int e = threadIdx.x + 256 * i;                                                                        \
+        const int l = e & 63, part = (e >> 6) & 1, vt = (e >> 7) % NT, c = (e >> 7) / NT;                          \
+        const int g = min(gbeg + (chunk) * CH + c, gend - 1);                                                      \
+        hb[i] = reinterpret_cast<const u32x4*>(a.halves)[((static_cast<size_t>(a.vt0 + vt) * a.groups + g) * 2 + part) * \
+                                                         64 + l];                                                   \
+    }
+
 // A workgroup of four waves covers 4*RT row tiles and up to NT vector tiles
-// of 16 over a share of the groups; each wave owns RT row tiles.  The
-// halves of CH groups at a time are staged in LDS (double buffered) and read
-// by all four waves; the int8 tiles come straight from HBM into registers.
+// of 16 over a share of the groups; each wave owns RT row tiles.  K advances
+// in chunks of CH groups.  While chunk c is multiplied, the loads of chunk
+// c+1 are in flight: its halves into registers (written to the other LDS
+// buffer afterwards, one barrier per chunk) and its int8 tiles and scales
+// straight from HBM into registers.  The prefetch is unconditional (the last
+// chunk re-reads itself) so the compiler keeps it ahead of the arithmetic.
 template <int RT, int NT>
 __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
-    constexpr int CH = 2;
-    __shared__ uint4 bs[2][CH][NT][2][64];
+    constexpr int CH = 4;
+    constexpr int BU = CH * NT * 2 * 64;  // uint4 of halves per chunk
+    constexpr int BPT = BU / 256;
+    __shared__ u32x4 bs[2][BU];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int G = a.groups;
     const int gbeg = blockIdx.y * a.groups_per_split;
-    const int gend = min(a.groups, gbeg + a.groups_per_split);
+    const int gend = min(G, gbeg + a.groups_per_split);
     const int nchunks = (gend - gbeg + CH - 1) / CH;
     int tile[RT];
 #pragma unroll
-    for (int r = 0; r < RT; ++r) tile[r] = min((blockIdx.x * 4 + wave) * RT + r, a.tiles - 1);
-
-    auto stage = [&](int buf, int chunk) {
-        constexpr int per_stage = CH * NT * 2 * 64;
-#pragma unroll
-        for (int i = 0; i < (per_stage + 255) / 256; ++i) {
-            const int e = threadIdx.x + 256 * i;
-            if (e < per_stage) {
-                const int l = e % 64, part = (e / 64) % 2, vt = (e / 128) % NT, c = e / (128 * NT);
-                const int g = min(gbeg + chunk * CH + c, gend - 1);
-                bs[buf][c][vt][part][l] = a.halves[((static_cast<size_t>(vt) * a.groups + g) * 2 + part) * 64 + l];
-            }
-        }
-    };
+    for (int r = 0; r < RT; ++r) tile[r] = min((static_cast<int>(blockIdx.x) * 4 + wave) * RT + r, a.tiles - 1);
 
     float4v acc[RT][NT];
 #pragma unroll
@@ -537,65 +582,202 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
 #pragma unroll
         for (int v = 0; v < NT; ++v) acc[r][v] = float4v{0.f, 0.f, 0.f, 0.f};
 
-    stage(0, 0);
+    // The halves of chunk c+1 sit in registers during chunk c: they go to LDS
+    // at the top of the next iteration, before the loads of chunk c+2 are
+    // issued, so a load is never consumed in the iteration that issued it.
+    // The int8 tiles and scales of chunk c+1 load into the register set that
+    // chunk c does not use: the loop is unrolled by two over sets ta / tb.
+    u32x4 hb[BPT];
+    Q8_LOAD_HALVES(0)
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) bs[0][threadIdx.x + 256 * i] = hb[i];
+    Q8_LOAD_HALVES(min(1, nchunks - 1))
+    TilesChunk<RT, CH> ta = q8_load_tiles<RT, CH>(a, gbeg, gend, 0, tile, lane), tb;
     __syncthreads();
-    for (int chunk = 0; chunk < nchunks; ++chunk) {
-        const int buf = chunk & 1;
-        if (chunk + 1 < nchunks) stage(buf ^ 1, chunk + 1);
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int g = gbeg + chunk * CH + c;
-            if (g < gend) {  // uniform across the workgroup
-                half8 am[RT];
-                float dv[RT][4];
-#pragma unroll
-                for (int r = 0; r < RT; ++r) {
-                    const size_t blk = static_cast<size_t>(tile[r]) * a.groups + g;
-                    am[r] = i8x8_to_half8(a.q[blk * 64 + lane]);
-                    const uint2 dd = *reinterpret_cast<const uint2*>(a.d + blk * 16 + 4 * (lane >> 4));
-                    dv[r][0] = half_bits_to_float(static_cast<uint16_t>(dd.x & 0xffff));
-                    dv[r][1] = half_bits_to_float(static_cast<uint16_t>(dd.x >> 16));
-                    dv[r][2] = half_bits_to_float(static_cast<uint16_t>(dd.y & 0xffff));
-                    dv[r][3] = half_bits_to_float(static_cast<uint16_t>(dd.y >> 16));
-                }
-#pragma unroll
-                for (int v = 0; v < NT; ++v) {
-                    const half8 bh = __builtin_bit_cast(half8, bs[buf][c][v][0][lane]);
-                    const half8 bl = __builtin_bit_cast(half8, bs[buf][c][v][1][lane]);
-#pragma unroll
-                    for (int r = 0; r < RT; ++r) {
-                        float4v cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[r], bh, float4v{0.f, 0.f, 0.f, 0.f}, 0,
-                                                                            0, 0);
-                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[r], bl, cc, 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[r][v][i] = fmaf(dv[r][i], cc[i], acc[r][v][i]);
-                    }
-                }
-            }
-        }
-        __syncthreads();
+
+#define Q8_CHUNK(chunk, CUR, NXT)                                                                                   \
+    {                                                                                                               \
+        const int buf = (chunk) & 1;                                                                                \
+        _Pragma("unroll") for (int i = 0; i < BPT; ++i) bs[buf ^ 1][threadIdx.x + 256 * i] = hb[i];                 \
+        Q8_LOAD_HALVES(min((chunk) + 2, nchunks - 1))                                                              \
+        NXT = q8_load_tiles<RT, CH>(a, gbeg, gend, min((chunk) + 1, nchunks - 1), tile, lane);                     \
+        _Pragma("unroll") for (int c = 0; c < CH; ++c) {                                                            \
+            if (gbeg + (chunk) * CH + c < gend) { /* uniform across the workgroup */                                \
+                half8 am[RT];                                                                                       \
+                float dv[RT][4];                                                                                    \
+                _Pragma("unroll") for (int r = 0; r < RT; ++r) {                                                    \
+                    am[r] = i8x8_to_half8(CUR.q[r][c]);                                                             \
+                    dv[r][0] = half_bits_to_float(static_cast<uint16_t>(CUR.d[r][c].x & 0xffff));                   \
+                    dv[r][1] = half_bits_to_float(static_cast<uint16_t>(CUR.d[r][c].x >> 16));                      \
+                    dv[r][2] = half_bits_to_float(static_cast<uint16_t>(CUR.d[r][c].y & 0xffff));                   \
+                    dv[r][3] = half_bits_to_float(static_cast<uint16_t>(CUR.d[r][c].y >> 16));                      \
+                }                                                                                                   \
+                _Pragma("unroll") for (int v = 0; v < NT; ++v) {                                                    \
+                    const half8 bh = __builtin_bit_cast(half8, bs[buf][((c * NT + v) * 2) * 64 + lane]);            \
+                    const half8 bl = __builtin_bit_cast(half8, bs[buf][((c * NT + v) * 2 + 1) * 64 + lane]);        \
+                    _Pragma("unroll") for (int r = 0; r < RT; ++r) {                                                \
+                        float4v cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[r], bh, float4v{0.f, 0.f, 0.f, 0.f}, \
+                                                                            0, 0, 0);                               \
+                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[r], bl, cc, 0, 0, 0);                        \
+                        _Pragma("unroll") for (int i = 0; i < 4; ++i) acc[r][v][i] =                                \
+                            fmaf(dv[r][i], cc[i], acc[r][v][i]);                                                    \
+                    }                                                                                               \
+                }                                                                                                   \
+            }                                                                                                       \
+        }                                                                                                           \
+        __syncthreads();                                                                                            \
     }
+
+    for (int chunk = 0;; chunk += 2) {
+        Q8_CHUNK(chunk, ta, tb)
+        if (chunk + 1 >= nchunks) break;
+        Q8_CHUNK(chunk + 1, tb, ta)
+        if (chunk + 2 >= nchunks) break;
+    }
+#undef Q8_CHUNK
     // lane l holds rows 4(l/16)+i of each tile, vector l%16 of each vector tile
+    float* out = a.out + static_cast<size_t>(blockIdx.y) * a.n_total * a.rows;
 #pragma unroll
     for (int v = 0; v < NT; ++v) {
-        const int j = v * 16 + (lane & 15);
-        if (j >= a.n) continue;
+        const int jl = v * 16 + (lane & 15);
+        if (jl >= a.n) continue;
+        const int j = a.vt0 * 16 + jl;
         const float us = a.unscale[j];
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
-            const int t = (blockIdx.x * 4 + wave) * RT + r;
+            const int t = (static_cast<int>(blockIdx.x) * 4 + wave) * RT + r;
             if (t >= a.tiles) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = t * 16 + 4 * (lane >> 4) + i;
-                if (row >= a.rows) continue;
-                const float y = acc[r][v][i] * us;
-                if (a.partial)
-                    a.partial[(static_cast<size_t>(blockIdx.y) * a.n + j) * a.rows + row] = y;
-                else
-                    write_segment(a.seg, a.nseg, row, static_cast<size_t>(j), y);
+                if (row < a.rows) out[static_cast<size_t>(j) * a.rows + row] = acc[r][v][i] * us;
             }
         }
+    }
+}
+
+// ---------------------------------------------------------- batch epilogues
+//
+// The batched products write f32 sums per K split, [splits][n][rows]; these
+// kernels add the splits in order (from 0.f, as one split's value is itself)
+// and apply what follows the product in the layer.
+
+__device__ __forceinline__ float split_total(const float* p, int splits, size_t stride, size_t at) {
+    float s = 0.f;
+    for (int k = 0; k < splits; ++k) s += p[k * stride + at];
+    return s;
+}
+
+// Q|K|V rows of vector j: q and k rotated by row j's (cos, sin)
+// (model.hpp:63-72), v copied; one thread per rotation pair or v element
+__global__ void qkv_epilogue_kernel(const float* p, int splits, int n, int qheads, int kheads, int dim, int interleaved,
+                                    const float* cs, float* q, float* k, float* v) {
+    const int half = dim / 2, rows = (qheads + 2 * kheads) * dim, kw = kheads * dim;
+    const int pairs = (qheads + kheads) * half, per = pairs + kw;
+    const size_t stride = static_cast<size_t>(n) * rows;
+    const size_t total = static_cast<size_t>(n) * per;
+    for (size_t t = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; t < total;
+         t += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const int j = static_cast<int>(t / per), e = static_cast<int>(t % per);
+        const size_t base = static_cast<size_t>(j) * rows;
+        if (e >= pairs) {
+            const int c = e - pairs;
+            v[static_cast<size_t>(j) * kw + c] = split_total(p, splits, stride, base + qheads * dim + kw + c);
+            continue;
+        }
+        const int h = e / half, i = e % half;
+        const int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : i + half;
+        const float left = split_total(p, splits, stride, base + h * dim + ia);
+        const float right = split_total(p, splits, stride, base + h * dim + ib);
+        const float c = cs[static_cast<size_t>(j) * dim + 2 * i], s = cs[static_cast<size_t>(j) * dim + 2 * i + 1];
+        float* x = h < qheads ? q + (static_cast<size_t>(j) * qheads + h) * dim
+                              : k + (static_cast<size_t>(j) * kheads + (h - qheads)) * dim;
+        x[ia] = __fsub_rn(__fmul_rn(left, c), __fmul_rn(right, s));
+        x[ib] = __fadd_rn(__fmul_rn(right, c), __fmul_rn(left, s));
+    }
+}
+
+// one workgroup per vector; rows up to kEpiThreads * kEpiPerThread = 16,384
+// are held in registers
+constexpr int kEpiThreads = 1024, kEpiPerThread = 16;
+
+// Vector j = blockIdx.x: x += the product's sum (the residual add, when p is
+// given), then RMSNorm with w (model.hpp:54-61: sum of squares in double,
+// scale rounded to float, (x * s) * w) into `norm` and, when `halves` is
+// given, into the next product's fp16 halves.  The row is kept in LDS
+// (dynamic, h floats).
+__global__ __launch_bounds__(kEpiThreads) void resid_norm_kernel(const float* p, int splits, float* x, const float* w, int n,
+                                                         int h, float eps, float* norm, _Float16* halves, int groups,
+                                                         float* unscale) {
+    extern __shared__ float row[];
+    __shared__ double part[kEpiThreads / 64];
+    __shared__ float mpart[kEpiThreads / 64];
+    const int j = blockIdx.x;
+    float* xr = x + static_cast<size_t>(j) * h;
+    const size_t stride = static_cast<size_t>(n) * h;
+    double sq = 0;
+    for (int e = threadIdx.x; e < h; e += kEpiThreads) {
+        float y = xr[e];
+        if (p) {
+            y = __fadd_rn(y, split_total(p, splits, stride, static_cast<size_t>(j) * h + e));
+            xr[e] = y;
+        }
+        row[e] = y;
+        sq += static_cast<double>(y) * y;
+    }
+    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = sq;
+    __syncthreads();
+    double t = 0;
+    for (int wv = 0; wv < kEpiThreads / 64; ++wv) t += part[wv];
+    const float inv = static_cast<float>(1.0 / sqrt(t / static_cast<double>(h) + static_cast<double>(eps)));
+    float mx = 0.f;
+    for (int e = threadIdx.x; e < h; e += kEpiThreads) {
+        const float v = __fmul_rn(__fmul_rn(row[e], inv), w[e]);
+        norm[static_cast<size_t>(j) * h + e] = v;
+        row[e] = v;
+        mx = fmaxf(mx, fabsf(v));
+    }
+    if (!halves) return;
+    const int shift = halves_shift(block_max(mx, mpart));
+    const float up = ldexpf(1.f, shift);
+    if (threadIdx.x == 0) unscale[j] = ldexpf(1.f, -shift);
+    for (int e = threadIdx.x; e < h; e += kEpiThreads) put_halves(halves, groups, j, e, row[e] * up);
+}
+
+// Vector j = blockIdx.x of the fused gate|up product: gate * (sigmoid(gate)
+// * up) (model.hpp:111-116) into `out` and, when given, the next product's
+// halves
+__global__ __launch_bounds__(kEpiThreads) void swiglu_epilogue_kernel(const float* p, int splits, int n, int inter, float* out,
+                                                              _Float16* halves, int groups, float* unscale) {
+    __shared__ float mpart[kEpiThreads / 64];
+    const int j = blockIdx.x;
+    const size_t stride = static_cast<size_t>(n) * 2 * inter, base = static_cast<size_t>(j) * 2 * inter;
+    float val[kEpiPerThread];
+    float mx = 0.f;
+#pragma unroll
+    for (int m = 0; m < kEpiPerThread; ++m) {
+        const int e = threadIdx.x + kEpiThreads * m;
+        val[m] = 0.f;
+        if (e < inter) {
+            const float g = split_total(p, splits, stride, base + e);
+            const float u = split_total(p, splits, stride, base + inter + e);
+            const float small = expf(-fabsf(g));
+            const float one = __fadd_rn(1.f, small);
+            const float sig = g >= 0 ? __fdiv_rn(1.f, one) : __fdiv_rn(small, one);
+            val[m] = __fmul_rn(g, __fmul_rn(sig, u));
+            out[static_cast<size_t>(j) * inter + e] = val[m];
+            mx = fmaxf(mx, fabsf(val[m]));
+        }
+    }
+    if (!halves) return;
+    const int shift = halves_shift(block_max(mx, mpart));
+    const float up = ldexpf(1.f, shift);
+    if (threadIdx.x == 0) unscale[j] = ldexpf(1.f, -shift);
+#pragma unroll
+    for (int m = 0; m < kEpiPerThread; ++m) {
+        const int e = threadIdx.x + kEpiThreads * m;
+        if (e < inter) put_halves(halves, groups, j, e, val[m] * up);
     }
 }
 
@@ -641,33 +823,15 @@ void launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps
     TVARA_HIP(hipGetLastError());
 }
 
-void launch_batch_matvec(const float* w, int rows, int cols, const float* x, int n, const MatvecSegment* seg, int nseg,
-                         DeviceBuffer& work, hipStream_t s) {
-    if (cols % kTileK) throw std::invalid_argument("batched matvec needs a row width divisible by 32");
-    const int tiles = (rows + kTileRows - 1) / kTileRows, chunks = cols / kTileK;
-    // split K until the launch has about 512 workgroups (two per CU)
-    const int want = std::max(1, std::min(chunks, (512 + tiles - 1) / tiles));
-    const int per = (chunks + want - 1) / want, splits = (chunks + per - 1) / per;
-    for (int j0 = 0; j0 < n; j0 += kTileVecs) {
-        BatchMatvecArgs a{};
-        a.w = w;
-        a.x = x + static_cast<size_t>(j0) * cols;
-        a.rows = rows;
-        a.cols = cols;
-        a.n = std::min(kTileVecs, n - j0);
-        a.nseg = nseg;
-        a.chunks_per_split = per;
-        for (int i = 0; i < nseg; ++i) {
-            a.seg[i] = seg[i];
-            a.seg[i].out = seg[i].out + static_cast<size_t>(j0) * seg[i].rows;
-            if (seg[i].residual) a.seg[i].residual = seg[i].residual + static_cast<size_t>(j0) * seg[i].rows;
-        }
-        if (splits > 1) a.partial = static_cast<float*>(work.ensure(static_cast<size_t>(splits) * a.n * rows * sizeof(float)));
-        launch("model_matvec", batch_matvec_kernel, dim3(tiles, splits), dim3(256), 0, s, a);
-        if (splits > 1)
-            launch("model_matvec_sum", split_sum_kernel, dim3(grid_for(static_cast<size_t>(a.n) * rows)), dim3(kThreads),
-                   0, s, a, splits);
-    }
+void launch_split_sum(const float* p, int splits, int n, int rows, float* out, hipStream_t s) {
+    BatchMatvecArgs b{};
+    b.rows = rows;
+    b.n = n;
+    b.nseg = 1;
+    b.seg[0] = MatvecSegment{out, rows, nullptr};
+    b.partial = const_cast<float*>(p);
+    launch("model_matvec_sum", split_sum_kernel, dim3(grid_for(static_cast<size_t>(n) * rows)), dim3(kThreads), 0, s, b,
+           splits);
     TVARA_HIP(hipGetLastError());
 }
 
@@ -756,59 +920,111 @@ void launch_batch_q8_rt(int nt, dim3 grid, hipStream_t s, const Q8BatchArgs& a) 
         default: launch("model_matvec_q8", batch_q8_kernel<RT, 4>, grid, dim3(256), 0, s, a); break;
     }
 }
+
+// row tiles per wave and groups per K split of the batched Q8_0 product: two
+// tiles per wave for the largest matrices; the groups are split only while
+// the launch has fewer than one workgroup per CU, and never below 16 a split
+struct Q8Plan {
+    int rt, gx, per, splits;
+};
+Q8Plan q8_plan(const Weight& w) {
+    Q8Plan p{};
+    const int tiles = w.tiles(), groups = w.groups();
+    p.rt = tiles >= 2048 ? 2 : 1;
+    p.gx = (tiles + 4 * p.rt - 1) / (4 * p.rt);
+    const int want = p.gx >= 256 ? 1 : std::min((256 + p.gx - 1) / p.gx, std::max(1, groups / 16));
+    p.per = (groups + want - 1) / want;
+    p.splits = (groups + p.per - 1) / p.per;
+    return p;
+}
+
+struct F32Plan {
+    int tiles, per, splits;
+};
+F32Plan f32_plan(int rows, int cols) {
+    F32Plan p{};
+    p.tiles = (rows + kTileRows - 1) / kTileRows;
+    const int chunks = cols / kTileK;
+    const int want = std::max(1, std::min(chunks, (512 + p.tiles - 1) / p.tiles));
+    p.per = (chunks + want - 1) / want;
+    p.splits = (chunks + p.per - 1) / p.per;
+    return p;
+}
 }  // namespace
 
-void launch_batch_matvec_q8(const Weight& w, const float* x, int n, const MatvecSegment* seg, int nseg,
-                            DeviceBuffer& halves, DeviceBuffer& work, hipStream_t s) {
-    const int groups = w.groups(), tiles = w.tiles(), cols = w.cols;
-    for (int j0 = 0; j0 < n; j0 += 64) {
-        const int nj = std::min(64, n - j0), nt = (nj + 15) / 16;
-        // halves of up to 64 vectors, then one float of unscale per vector
-        const size_t half_bytes = static_cast<size_t>(nt) * groups * 2 * 64 * 8 * sizeof(_Float16);
-        auto* base = static_cast<char*>(halves.ensure(half_bytes + 64 * sizeof(float)));
-        auto* hv = reinterpret_cast<_Float16*>(base);
-        auto* unscale = reinterpret_cast<float*>(base + half_bytes);
-        launch("model_split_halves", split_halves_kernel, dim3(nj), dim3(256), 0, s, x + static_cast<size_t>(j0) * cols,
-               cols, groups, hv, unscale);
-        Q8BatchArgs a{};
-        a.q = static_cast<const uint2*>(w.q.ptr);
-        a.d = static_cast<const uint16_t*>(w.d.ptr);
-        a.halves = reinterpret_cast<const uint4*>(hv);
-        a.unscale = unscale;
-        a.rows = w.rows;
-        a.tiles = tiles;
-        a.groups = groups;
-        a.n = nj;
-        a.nseg = nseg;
-        for (int i = 0; i < nseg; ++i) {
-            a.seg[i] = seg[i];
-            a.seg[i].out = seg[i].out + static_cast<size_t>(j0) * seg[i].rows;
-            if (seg[i].residual) a.seg[i].residual = seg[i].residual + static_cast<size_t>(j0) * seg[i].rows;
+int batch_splits(const Weight& w) { return w.q8 ? q8_plan(w).splits : f32_plan(w.rows, w.cols).splits; }
+
+void launch_batch_product(const Weight& w, const float* x, const _Float16* halves, const float* unscale, int n,
+                          float* out, hipStream_t s) {
+    if (w.q8) {
+        const Q8Plan p = q8_plan(w);
+        for (int j0 = 0; j0 < n; j0 += 64) {
+            const int nj = std::min(64, n - j0);
+            Q8BatchArgs a{};
+            a.q = static_cast<const uint2*>(w.q.ptr);
+            a.d = static_cast<const uint16_t*>(w.d.ptr);
+            a.halves = reinterpret_cast<const uint4*>(halves);
+            a.unscale = unscale;
+            a.rows = w.rows;
+            a.tiles = w.tiles();
+            a.groups = w.groups();
+            a.n = nj;
+            a.vt0 = j0 / 16;
+            a.n_total = n;
+            a.groups_per_split = p.per;
+            a.out = out;
+            const dim3 grid(p.gx, p.splits);
+            if (p.rt == 2)
+                launch_batch_q8_rt<2>((nj + 15) / 16, grid, s, a);
+            else
+                launch_batch_q8_rt<1>((nj + 15) / 16, grid, s, a);
         }
-        // two row tiles per wave when that still gives 128 workgroups; then
-        // split the groups until the launch has about 512
-        const int rt = (tiles + 7) / 8 >= 128 ? 2 : 1;
-        const int gx = (tiles + 4 * rt - 1) / (4 * rt);
-        const int want = std::max(1, std::min((groups + 1) / 2, (512 + gx - 1) / gx));
-        const int per = (groups + want - 1) / want, splits = (groups + per - 1) / per;
-        a.groups_per_split = per;
-        if (splits > 1) a.partial = static_cast<float*>(work.ensure(static_cast<size_t>(splits) * nj * w.rows * sizeof(float)));
-        const dim3 grid(gx, splits);
-        if (rt == 2)
-            launch_batch_q8_rt<2>(nt, grid, s, a);
-        else
-            launch_batch_q8_rt<1>(nt, grid, s, a);
-        if (splits > 1) {
-            BatchMatvecArgs b{};
-            b.rows = w.rows;
-            b.n = nj;
-            b.nseg = nseg;
-            for (int i = 0; i < nseg; ++i) b.seg[i] = a.seg[i];
-            b.partial = a.partial;
-            launch("model_matvec_sum", split_sum_kernel, dim3(grid_for(static_cast<size_t>(nj) * w.rows)),
-                   dim3(kThreads), 0, s, b, splits);
+    } else {
+        if (w.cols % kTileK) throw std::invalid_argument("batched matvec needs a row width divisible by 32");
+        const F32Plan p = f32_plan(w.rows, w.cols);
+        for (int j0 = 0; j0 < n; j0 += kTileVecs) {
+            BatchMatvecArgs a{};
+            a.w = static_cast<const float*>(w.f32.ptr);
+            a.x = x + static_cast<size_t>(j0) * w.cols;
+            a.rows = w.rows;
+            a.cols = w.cols;
+            a.n = std::min(kTileVecs, n - j0);
+            a.chunks_per_split = p.per;
+            a.partial = out;
+            a.n_total = n;
+            a.j0 = j0;
+            launch("model_matvec", batch_matvec_kernel, dim3(p.tiles, p.splits), dim3(256), 0, s, a);
         }
     }
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_split_halves(const float* x, int n, int cols, _Float16* halves, float* unscale, hipStream_t s) {
+    launch("model_split_halves", split_halves_kernel, dim3(n), dim3(256), 0, s, x, cols, cols / 32, halves, unscale);
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_qkv_epilogue(const float* p, int splits, int n, int qheads, int kheads, int dim, bool interleaved,
+                         const float* cs, float* q, float* k, float* v, hipStream_t s) {
+    const size_t total = static_cast<size_t>(n) * ((qheads + kheads) * (dim / 2) + kheads * dim);
+    launch("model_qkv_epilogue", qkv_epilogue_kernel, dim3(grid_for(total)), dim3(kThreads), 0, s, p, splits, n, qheads,
+           kheads, dim, interleaved ? 1 : 0, cs, q, k, v);
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_resid_norm(const float* p, int splits, float* x, const float* w, int n, int h, float eps, float* norm,
+                       _Float16* halves, float* unscale, hipStream_t s) {
+    if (h > kEpiThreads * kEpiPerThread) throw std::invalid_argument("batched decode width above 16384");
+    launch("model_resid_norm", resid_norm_kernel, dim3(n), dim3(kEpiThreads), static_cast<size_t>(h) * sizeof(float), s,
+           p, splits, x, w, n, h, eps, norm, halves, h / 32, unscale);
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_swiglu_epilogue(const float* p, int splits, int n, int inter, float* out, _Float16* halves,
+                            float* unscale, hipStream_t s) {
+    if (inter > kEpiThreads * kEpiPerThread) throw std::invalid_argument("batched decode width above 16384");
+    launch("model_swiglu_epilogue", swiglu_epilogue_kernel, dim3(n), dim3(kEpiThreads), 0, s, p, splits, n, inter, out,
+           halves, inter / 32, unscale);
     TVARA_HIP(hipGetLastError());
 }
 
