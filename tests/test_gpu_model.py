@@ -58,6 +58,9 @@ SPECS = {
     # by four
     "q8_0-tied-ragged": dict(matrix_type=gf.T_Q8_0, embed_type=gf.T_Q8_0, output=False, vocab=100, hidden=96,
                              intermediate=160, heads=3, kv_heads=1),
+    # Q8_0 with the split RoPE layout (rotation outside the product epilogue)
+    "q8_0-split-rope": dict(matrix_type=gf.T_Q8_0, rope_layout="split", hidden=128, intermediate=256, heads=4,
+                            kv_heads=2),
 }
 
 

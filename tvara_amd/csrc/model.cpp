@@ -78,8 +78,11 @@ DeviceModel::DeviceModel(const std::string& path, size_t max_blocks, size_t bloc
         }
         TVARA_HIP(hipDeviceSynchronize());
     };
-    // parts: (tensor name, rows); every part has `cols` columns
-    auto load_weight = [&](const std::vector<std::pair<std::string, size_t>>& parts, size_t cols, Weight& w) {
+    // parts: (tensor name, rows); every part has `cols` columns.  With
+    // `interleave` (two parts of equal rows, kept as Q8_0), row i of part k
+    // becomes row 2i + k.
+    auto load_weight = [&](const std::vector<std::pair<std::string, size_t>>& parts, size_t cols, Weight& w,
+                           bool interleave = false) {
         size_t rows = 0;
         bool q8 = true;
         for (const auto& [name, r] : parts) {
@@ -100,20 +103,23 @@ DeviceModel::DeviceModel(const std::string& path, size_t max_blocks, size_t bloc
             }
             return;
         }
-        const size_t tiles = static_cast<size_t>(w.tiles()), groups = cols / 32;
-        w.q.ensure(tiles * 16 * cols);
-        w.d.ensure(tiles * groups * 16 * sizeof(uint16_t));
-        TVARA_HIP(hipMemset(w.q.ptr, 0, tiles * 16 * cols));
-        TVARA_HIP(hipMemset(w.d.ptr, 0, tiles * groups * 16 * sizeof(uint16_t)));
+        const size_t tiles = static_cast<size_t>(w.tiles()), pairs = static_cast<size_t>(w.pairs());
+        const size_t qbytes = tiles * pairs * 64 * 16, dbytes = tiles * pairs * 16 * 2 * sizeof(uint16_t);
+        w.q.ensure(qbytes);
+        w.d.ensure(dbytes);
+        TVARA_HIP(hipMemset(w.q.ptr, 0, qbytes));
+        TVARA_HIP(hipMemset(w.d.ptr, 0, dbytes));
+        w.interleaved = interleave;
         int row0 = 0;
         for (const auto& [name, r] : parts) {
             const gguf::TensorInfo& t = file.tensor(name);
             const size_t bytes = gguf::tensor_bytes(t);
             void* raw = staging.ensure(bytes);
             TVARA_HIP(hipMemcpy(raw, file.payload(t), bytes, hipMemcpyHostToDevice));
-            launch_q8_repack(static_cast<const uint8_t*>(raw), static_cast<int>(r), w.cols, row0, w, bad_flag, nullptr);
+            launch_q8_repack(static_cast<const uint8_t*>(raw), static_cast<int>(r), w.cols, row0, interleave ? 2 : 1, w,
+                             bad_flag, nullptr);
             TVARA_HIP(hipDeviceSynchronize());
-            row0 += static_cast<int>(r);
+            row0 += interleave ? 1 : static_cast<int>(r);
         }
     };
     load_weight({{"token_embd.weight", c.vocab}}, H, embedding_);
@@ -133,7 +139,7 @@ DeviceModel::DeviceModel(const std::string& path, size_t max_blocks, size_t bloc
         load(p + "ffn_norm.weight", at(L.ffn_norm, 0));
         load_weight({{p + "attn_q.weight", H}, {p + "attn_k.weight", KV}, {p + "attn_v.weight", KV}}, H, L.qkv);
         load_weight({{p + "attn_output.weight", H}}, H, L.out);
-        load_weight({{p + "ffn_gate.weight", I}, {p + "ffn_up.weight", I}}, H, L.gate_up);
+        load_weight({{p + "ffn_gate.weight", I}, {p + "ffn_up.weight", I}}, H, L.gate_up, true);
         load_weight({{p + "ffn_down.weight", H}}, I, L.down);
     }
     int bad = 0;
@@ -171,7 +177,6 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
     const int H = static_cast<int>(c.hidden), I = static_cast<int>(c.intermediate);
     const int KV = static_cast<int>(c.kv_width()), D = static_cast<int>(c.head_dim());
     float* x = at(x_, 0);
-    float* norm = at(norm_, 0);
     float* q = at(q_, 0);
     float* attn = at(attn_, 0);
     float* gate = at(gate_, 0);
@@ -202,24 +207,30 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
         Layer& L = layers_[l];
         float* kl = at(kall_, l * c.kv_width());
         float* vl = at(vall_, l * c.kv_width());
-        launch_rmsnorm(x, at(L.attn_norm, 0), norm, H, c.rms_epsilon, s);
         const MatvecSegment qkv[3] = {{q, H, nullptr}, {kl, KV, nullptr}, {vl, KV, nullptr}};
-        matvec(L.qkv, norm, qkv, 3, s);
-        launch_rope(q, static_cast<int>(c.heads), kl, static_cast<int>(c.kv_heads), D, at(rope_, 0), c.interleaved_rope,
-                    s);
+        if (L.qkv.q8 && c.interleaved_rope) {  // RoPE in the product's epilogue
+            launch_matvec_q8(L.qkv, x, qkv, 3, s, at(L.attn_norm, 0), c.rms_epsilon, at(rope_, 0), D, H + KV);
+        } else {
+            matvec(L.qkv, x, qkv, 3, s, at(L.attn_norm, 0));
+            launch_rope(q, static_cast<int>(c.heads), kl, static_cast<int>(c.kv_heads), D, at(rope_, 0),
+                        c.interleaved_rope, s);
+        }
         plan.launch(static_cast<int>(l), q, kl, vl, attn, s);
         const MatvecSegment o[1] = {{x, H, x}};
         matvec(L.out, attn, o, 1, s);
-        launch_rmsnorm(x, at(L.ffn_norm, 0), norm, H, c.rms_epsilon, s);
-        const MatvecSegment gu[2] = {{gate, I, nullptr}, {up, I, nullptr}};
-        matvec(L.gate_up, norm, gu, 2, s);
-        launch_swiglu(gate, up, I, s);
+        if (L.gate_up.interleaved) {  // SwiGLU in the product's epilogue, into gate
+            const MatvecSegment gu[1] = {{gate, 2 * I, nullptr}};
+            matvec(L.gate_up, x, gu, 1, s, at(L.ffn_norm, 0));
+        } else {
+            const MatvecSegment gu[2] = {{gate, I, nullptr}, {up, I, nullptr}};
+            matvec(L.gate_up, x, gu, 2, s, at(L.ffn_norm, 0));
+            launch_swiglu(gate, up, I, s);
+        }
         const MatvecSegment d[1] = {{x, H, x}};
         matvec(L.down, gate, d, 1, s);
     }
-    launch_rmsnorm(x, at(final_norm_, 0), norm, H, c.rms_epsilon, s);
     const MatvecSegment lg[1] = {{at(logits_, 0), static_cast<int>(c.vocab), nullptr}};
-    matvec(has_output_ ? output_ : embedding_, norm, lg, 1, s);
+    matvec(has_output_ ? output_ : embedding_, x, lg, 1, s, at(final_norm_, 0));
     plan.check();  // a non-finite score fails the token before anything is appended
     // the token's K/V for every layer, appended after all layers succeeded
     // (paged_model.hpp:27)
@@ -227,11 +238,17 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
     copier_.from_device(logits_host, logits_.ptr, c.vocab * sizeof(float), s);
 }
 
-void DeviceModel::matvec(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s) {
-    if (w.q8)
-        launch_matvec_q8(w, v, seg, nseg, s);
-    else
-        launch_matvec(static_cast<const float*>(w.f32.ptr), w.rows, w.cols, v, seg, nseg, s);
+void DeviceModel::matvec(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s,
+                         const float* norm_w) {
+    if (w.q8) {
+        launch_matvec_q8(w, v, seg, nseg, s, norm_w, cfg_.rms_epsilon);
+        return;
+    }
+    if (norm_w) {  // the f32 product reads a normalised copy
+        launch_rmsnorm(v, norm_w, at(norm_, 0), w.cols, cfg_.rms_epsilon, s);
+        v = at(norm_, 0);
+    }
+    launch_matvec(static_cast<const float*>(w.f32.ptr), w.rows, w.cols, v, seg, nseg, s);
 }
 
 void DeviceModel::ensure_batch(size_t n) {
@@ -352,7 +369,8 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
         launch_resid_norm(part, batch_splits(L.out), x, at(L.ffn_norm, 0), N, H, c.rms_epsilon, norm,
                           halves_for(L.gate_up), unscale, s);
         launch_batch_product(L.gate_up, norm, halves, unscale, N, part, s);
-        launch_swiglu_epilogue(part, batch_splits(L.gate_up), N, I, gate, halves_for(L.down), unscale, s);
+        launch_swiglu_epilogue(part, batch_splits(L.gate_up), N, I, gate, halves_for(L.down), unscale, s,
+                               L.gate_up.interleaved);
         launch_batch_product(L.down, gate, halves, unscale, N, part, s);
         const bool last = l + 1 == c.layers;
         launch_resid_norm(part, batch_splits(L.down), x, last ? at(final_norm_, 0) : at(layers_[l + 1].attn_norm, 0), N,

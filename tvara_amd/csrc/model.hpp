@@ -24,26 +24,40 @@ struct MatvecSegment {
 
 // A weight matrix in HBM: f32 rows, or Q8_0 kept quantised.  The Q8_0 form
 // is tiled for the kernels that read it: rows are cut into tiles of 16
-// (zero-padded) and, per (tile, group of 32 columns), the 512 int8 sit in
-// the operand order of a 16x16x32 MFMA -- lane l holds row l%16, columns
-// 8(l/16) .. 8(l/16)+7 of the group -- followed in a separate plane by the
-// 16 rows' fp16 group scales.  Value = float(d) * q, as dequantize_q8_0
-// computes it (quant.hpp:39-49).
+// (zero-padded) and the groups of 32 columns into pairs (an odd last group
+// is paired with a zero group).  Per (tile, pair), lane l of a wave holds 16
+// bytes: row l%16, columns 8(l/16) .. 8(l/16)+7 of the pair's first group
+// then of its second -- each half is the operand a 16x16x32 MFMA lane reads
+// for one group.  A separate plane holds, per (tile, pair), the 16 rows'
+// fp16 scales of both groups ([row][2]).  Value = float(d) * q, as
+// dequantize_q8_0 computes it (quant.hpp:39-49).
 struct Weight {
     bool q8 = false;
     int rows = 0, cols = 0;
     DeviceBuffer f32;  // [rows][cols] floats
-    DeviceBuffer q;    // int8 [tiles][cols/32][64][8]
-    DeviceBuffer d;    // fp16 bits [tiles][cols/32][16]
+    DeviceBuffer q;    // int8 [tiles][pairs][64][16]
+    DeviceBuffer d;    // fp16 bits [tiles][pairs][16][2]
+    // a fused gate|up block stored with its rows interleaved (row 2i is gate
+    // row i, 2i + 1 is up row i), so that the SwiGLU pairs meet in a tile
+    bool interleaved = false;
     int tiles() const { return (rows + 15) / 16; }
     int groups() const { return cols / 32; }
+    int pairs() const { return (groups() + 1) / 2; }
 };
 
 void launch_dequant(uint32_t type, const uint8_t* raw, size_t n, float* out, int* bad, hipStream_t s);
 // GGUF Q8_0 rows [rows][cols/32][34 B] into rows row0.. of a tiled Weight;
 // flags `bad` when a group scale is not finite (then so is a value)
-void launch_q8_repack(const uint8_t* raw, int rows, int cols, int row0, Weight& w, int* bad, hipStream_t s);
-void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s);
+// (rows row0, row0 + stride, ...); stride 2 interleaves two parts
+void launch_q8_repack(const uint8_t* raw, int rows, int cols, int row0, int stride, Weight& w, int* bad,
+                      hipStream_t s);
+// y = W v; with norm_w set, v is rms_norm(x = the v argument) * norm_w,
+// computed inside the launch; rope_cs (interleaved RoPE of the first
+// rope_rows rows) and an interleaved gate|up weight (SwiGLU into seg[0])
+// apply in the epilogue
+void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s,
+                      const float* norm_w = nullptr, float eps = 0.f, const float* rope_cs = nullptr,
+                      int rope_dim = 0, int rope_rows = 0);
 // Batched products for n vectors (one per sequence) write f32 sums per K
 // split, out[split][n][rows]; batch_splits gives the split count.  Q8_0
 // weights read the vectors as fp16 halves (launch_split_halves or an
@@ -64,7 +78,7 @@ void launch_resid_norm(const float* p, int splits, float* x, const float* w, int
                        _Float16* halves, float* unscale, hipStream_t s);
 // SwiGLU of the fused gate|up sums into out and, when given, halves
 void launch_swiglu_epilogue(const float* p, int splits, int n, int inter, float* out, _Float16* halves,
-                            float* unscale, hipStream_t s);
+                            float* unscale, hipStream_t s, bool interleaved);
 // out[j] = row idx[j] (or `row` when idx is null) of a Q8_0 table, dequantised
 void launch_gather_embedding_q8(const Weight& w, const uint32_t* idx, uint32_t row, int n, float* out,
                                 hipStream_t s);
@@ -108,7 +122,9 @@ private:
         DeviceBuffer attn_norm, ffn_norm;
         Weight qkv, out, gate_up, down;
     };
-    void matvec(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s);
+    // y = W v, or W rms_norm(x) * norm_w when norm_w is given (v is then x)
+    void matvec(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s,
+                const float* norm_w = nullptr);
 
     ModelConfig cfg_;
     std::string metadata_;

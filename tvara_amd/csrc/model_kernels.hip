@@ -329,21 +329,22 @@ __global__ void swiglu_kernel(float* gate, const float* up, int n) {
 // ------------------------------------------------------------- Q8_0 weights
 
 // one thread per (row, group): the 34-byte GGUF group to its tile slots
-__global__ void q8_repack_kernel(const uint8_t* raw, int rows, int groups, int row0, uint8_t* q, uint16_t* d,
-                                 int* bad) {
+__global__ void q8_repack_kernel(const uint8_t* raw, int rows, int groups, int row0, int stride, uint8_t* q,
+                                 uint16_t* d, int* bad) {
+    const int pairs = (groups + 1) / 2;
     const size_t total = static_cast<size_t>(rows) * groups;
     for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
          i += static_cast<size_t>(gridDim.x) * blockDim.x) {
         const int r = static_cast<int>(i / groups), g = static_cast<int>(i % groups);
         const uint8_t* src = raw + i * 34;
-        const int row = row0 + r, rr = row % 16;
-        const size_t block = static_cast<size_t>(row / 16) * groups + g;
+        const int row = row0 + r * stride, rr = row % 16;
+        const size_t block = static_cast<size_t>(row / 16) * pairs + g / 2;
         const uint16_t h = static_cast<uint16_t>(src[0] | (src[1] << 8));
-        d[block * 16 + rr] = h;
+        d[(block * 16 + rr) * 2 + g % 2] = h;
         if (!__builtin_isfinite(half_bits_to_float(h))) atomicOr(bad, 1);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            uint8_t* dst = q + (block * 64 + rr + 16 * j) * 8;
+            uint8_t* dst = q + (block * 64 + rr + 16 * j) * 16 + (g % 2) * 8;
 #pragma unroll
             for (int b = 0; b < 8; ++b) dst[b] = src[2 + 8 * j + b];
         }
@@ -351,24 +352,33 @@ __global__ void q8_repack_kernel(const uint8_t* raw, int rows, int groups, int r
 }
 
 struct Q8MatvecArgs {
-    const uint2* q;
-    const uint16_t* d;
-    const float* v;
-    int rows, groups;
+    const uint4* q;
+    const uint32_t* d;  // the two groups' fp16 scales of a row, per (tile, pair)
+    const float* v;     // the input, or x when norm_w is set
+    const float* norm_w;  // RMSNorm weight: the input is rms_norm(x) * norm_w
+    float eps;
+    int rows, tiles, groups, pairs, cols;
     MatvecSegment seg[3];
     int nseg;
+    // epilogue on adjacent row pairs (2i, 2i+1): rotate the first rope_rows
+    // rows by rope_cs (interleaved RoPE over rope_dim-wide heads), or, with
+    // swiglu, write gate * (sigmoid(gate) * up) of rows (gate i, up i) to
+    // seg[0].out[i]
+    const float* rope_cs;
+    int rope_dim, rope_rows;
+    int swiglu;
 };
 
 // sum of 8 int8 (two dwords) times 8 floats, in f32
-__device__ __forceinline__ float dot8(uint2 q, float4 a, float4 b) {
-    float s = sbyte_to_float<0>(q.x) * a.x;
-    s = fmaf(sbyte_to_float<1>(q.x), a.y, s);
-    s = fmaf(sbyte_to_float<2>(q.x), a.z, s);
-    s = fmaf(sbyte_to_float<3>(q.x), a.w, s);
-    s = fmaf(sbyte_to_float<0>(q.y), b.x, s);
-    s = fmaf(sbyte_to_float<1>(q.y), b.y, s);
-    s = fmaf(sbyte_to_float<2>(q.y), b.z, s);
-    return fmaf(sbyte_to_float<3>(q.y), b.w, s);
+__device__ __forceinline__ float dot8(uint32_t lo, uint32_t hi, float4 a, float4 b) {
+    float s = sbyte_to_float<0>(lo) * a.x;
+    s = fmaf(sbyte_to_float<1>(lo), a.y, s);
+    s = fmaf(sbyte_to_float<2>(lo), a.z, s);
+    s = fmaf(sbyte_to_float<3>(lo), a.w, s);
+    s = fmaf(sbyte_to_float<0>(hi), b.x, s);
+    s = fmaf(sbyte_to_float<1>(hi), b.y, s);
+    s = fmaf(sbyte_to_float<2>(hi), b.z, s);
+    return fmaf(sbyte_to_float<3>(hi), b.w, s);
 }
 
 __device__ __forceinline__ void write_segment(const MatvecSegment* seg, int nseg, int row, size_t col_offset_rows,
@@ -379,56 +389,117 @@ __device__ __forceinline__ void write_segment(const MatvecSegment* seg, int nseg
     seg[s].out[at] = seg[s].residual ? __fadd_rn(seg[s].residual[at], y) : y;
 }
 
-// y = W v over Q8_0 tiles: a workgroup per 16-row tile, its W waves taking
-// contiguous shares of the groups.  Lane l accumulates row l%16 over its
-// eight columns of each group: the eight products in f32, scaled by the
-// group's d and added in double; lanes and waves are then summed in double
-// and the row rounds to float once.
-template <int W>
+// y = W v over Q8_0 tiles: a workgroup per RT 16-row tiles, its W waves
+// taking contiguous shares of the group pairs, U pairs a step with every
+// load issued first (16 bytes of weights per lane per tile and pair).  The
+// input vector is staged in LDS first -- normalised there when the product
+// follows an RMSNorm (model.hpp:54-61: sum of squares in double, the scale
+// rounded to float, (x * s) * w), which each workgroup computes for itself.
+// Lane l accumulates row l%16 of each tile over its eight columns of each
+// group: the eight products in f32, times the group's d, added in double;
+// lanes and waves are then summed in double and each row rounds to float
+// once.  Pairs past the share, and the zero group that completes an odd
+// count, are selected away rather than multiplied (their loads stay in
+// bounds).
+template <int W, int RT>
 __global__ __launch_bounds__(W * 64) void matvec_q8_kernel(const Q8MatvecArgs a) {
-    __shared__ double red[W][16];
+    constexpr int U = 4;
+    extern __shared__ float vs[];  // cols floats
+    __shared__ double red[W][RT][16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int tile = blockIdx.x;
-    const int per = (a.groups + W - 1) / W;
-    const int g0 = min(a.groups, wave * per), g1 = min(a.groups, g0 + per);
-    const uint2* qp = a.q + static_cast<size_t>(tile) * a.groups * 64 + lane;
-    const uint16_t* dp = a.d + static_cast<size_t>(tile) * a.groups * 16 + (lane & 15);
-    const float* vp = a.v + 8 * (lane >> 4);
-    double acc = 0;
-    int g = g0;
-    for (; g + 4 <= g1; g += 4) {
-        uint2 qq[4];
-        uint16_t dd[4];
-        float4 va[4], vb[4];
+    const int P = a.pairs, G = a.groups, C = a.cols;
+    if (a.norm_w) {
+        double sq = 0;
+        for (int k = threadIdx.x; k < C; k += W * 64) sq += static_cast<double>(a.v[k]) * a.v[k];
+        for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+        if (lane == 0) red[wave][0][0] = sq;
+        __syncthreads();
+        double t = 0;
+        for (int w = 0; w < W; ++w) t += red[w][0][0];
+        const float inv = static_cast<float>(1.0 / sqrt(t / static_cast<double>(C) + static_cast<double>(a.eps)));
+        for (int k = threadIdx.x; k < C; k += W * 64) vs[k] = __fmul_rn(__fmul_rn(a.v[k], inv), a.norm_w[k]);
+        __syncthreads();  // red is reused below
+    } else {
+        for (int k = 4 * threadIdx.x; k < C; k += 4 * W * 64)
+            *reinterpret_cast<float4*>(vs + k) = *reinterpret_cast<const float4*>(a.v + k);
+    }
+    __syncthreads();
+    const int per = (P + W - 1) / W;
+    const int p0 = min(P, wave * per), p1 = min(P, p0 + per);
+    int tl[RT];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            qq[u] = qp[static_cast<size_t>(g + u) * 64];
-            dd[u] = dp[static_cast<size_t>(g + u) * 16];
-            va[u] = *reinterpret_cast<const float4*>(vp + 32 * (g + u));
-            vb[u] = *reinterpret_cast<const float4*>(vp + 32 * (g + u) + 4);
+    for (int r = 0; r < RT; ++r) tl[r] = min(static_cast<int>(blockIdx.x) * RT + r, a.tiles - 1);
+    const float* vp = vs + 8 * (lane >> 4);
+    double acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) acc[r] = 0;
+    for (int p = p0; p < p1; p += U) {
+        uint4 qq[RT][U];
+        uint32_t dd[RT][U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int pc = min(p + u, p1 - 1);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const size_t blk = static_cast<size_t>(tl[r]) * P + pc;
+                qq[r][u] = a.q[blk * 64 + lane];
+                dd[r][u] = a.d[blk * 16 + (lane & 15)];
+            }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            acc = fma(static_cast<double>(half_bits_to_float(dd[u])), static_cast<double>(dot8(qq[u], va[u], vb[u])),
-                      acc);
+        for (int u = 0; u < U; ++u) {
+            const int pc = min(p + u, p1 - 1);
+            const bool live = p + u < p1, second = 2 * pc + 1 < G;
+            const int c0 = 64 * pc, c1 = second ? c0 + 32 : c0;
+            const float4 v0 = *reinterpret_cast<const float4*>(vp + c0);
+            const float4 v1 = *reinterpret_cast<const float4*>(vp + c0 + 4);
+            const float4 v2 = *reinterpret_cast<const float4*>(vp + c1);
+            const float4 v3 = *reinterpret_cast<const float4*>(vp + c1 + 4);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const double s0 = static_cast<double>(half_bits_to_float(static_cast<uint16_t>(dd[r][u] & 0xffff))) *
+                                  dot8(qq[r][u].x, qq[r][u].y, v0, v1);
+                const double s1 = static_cast<double>(half_bits_to_float(static_cast<uint16_t>(dd[r][u] >> 16))) *
+                                  dot8(qq[r][u].z, qq[r][u].w, v2, v3);
+                const double t = second ? s0 + s1 : s0;
+                acc[r] += live ? t : 0.0;
+            }
+        }
     }
-    for (; g < g1; ++g) {
-        const uint2 qq = qp[static_cast<size_t>(g) * 64];
-        const float4 va = *reinterpret_cast<const float4*>(vp + 32 * g);
-        const float4 vb = *reinterpret_cast<const float4*>(vp + 32 * g + 4);
-        acc = fma(static_cast<double>(half_bits_to_float(dp[static_cast<size_t>(g) * 16])),
-                  static_cast<double>(dot8(qq, va, vb)), acc);
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        acc[r] += __shfl_xor(acc[r], 16);
+        acc[r] += __shfl_xor(acc[r], 32);
+        if (lane < 16) red[wave][r][lane] = acc[r];
     }
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
-    if (lane < 16) red[wave][lane] = acc;
     __syncthreads();
     if (wave || lane >= 16) return;
-    double t = red[0][lane];
 #pragma unroll
-    for (int w = 1; w < W; ++w) t += red[w][lane];
-    const int row = tile * 16 + lane;
-    if (row < a.rows) write_segment(a.seg, a.nseg, row, 0, static_cast<float>(t));
+    for (int r = 0; r < RT; ++r) {
+        double t = red[0][r][lane];
+#pragma unroll
+        for (int w = 1; w < W; ++w) t += red[w][r][lane];
+        const int tile = static_cast<int>(blockIdx.x) * RT + r, row = tile * 16 + lane;
+        float y = static_cast<float>(t);
+        const float other = __shfl_xor(y, 1);  // the row-pair partner (lanes 0..15 all take part)
+        if (a.swiglu) {
+            // model.hpp:111-116, with the overflow-free sigmoid
+            if (!(lane & 1) && tile < a.tiles && row + 1 < a.rows) {
+                const float small = expf(-fabsf(y));
+                const float one = __fadd_rn(1.f, small);
+                const float sig = y >= 0 ? __fdiv_rn(1.f, one) : __fdiv_rn(small, one);
+                a.seg[0].out[row / 2] = __fmul_rn(y, __fmul_rn(sig, other));
+            }
+            continue;
+        }
+        if (a.rope_cs && row < a.rope_rows) {  // model.hpp:63-72
+            const int i = (row % a.rope_dim) / 2;
+            const float c = a.rope_cs[2 * i], sn = a.rope_cs[2 * i + 1];
+            y = lane & 1 ? __fadd_rn(__fmul_rn(y, c), __fmul_rn(other, sn))
+                         : __fsub_rn(__fmul_rn(y, c), __fmul_rn(other, sn));
+        }
+        if (tile < a.tiles && row < a.rows) write_segment(a.seg, a.nseg, row, 0, y);
+    }
 }
 
 // The batched product runs on fp16 MFMAs.  int8 weights are exact in fp16;
@@ -511,11 +582,11 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint2 q) {
 }
 
 struct Q8BatchArgs {
-    const uint2* q;
+    const uint4* q;
     const uint16_t* d;
     const uint4* halves;  // 8 fp16 per lane, see put_halves
     const float* unscale;
-    int rows, tiles, groups;
+    int rows, tiles, groups, pairs;
     int n, vt0;  // vectors in this launch, first vector tile
     int n_total;
     int groups_per_split;
@@ -524,21 +595,22 @@ struct Q8BatchArgs {
 
 template <int RT, int CH>
 struct TilesChunk {
-    uint2 q[RT][CH], d[RT][CH];
+    uint4 q[RT][CH / 2], d[RT][CH / 2];  // per group pair
 };
 
 template <int RT, int CH>
 __device__ __forceinline__ TilesChunk<RT, CH> q8_load_tiles(const Q8BatchArgs& a, int gbeg, int gend, int chunk,
                                                             const int (&tile)[RT], int lane) {
     TilesChunk<RT, CH> t;
+    const int plast = (gend - 1) / 2;
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int g = min(gbeg + chunk * CH + c, gend - 1);
-            const size_t blk = static_cast<size_t>(tile[r]) * a.groups + g;
+        for (int c = 0; c < CH / 2; ++c) {
+            const int p = min((gbeg + chunk * CH) / 2 + c, plast);
+            const size_t blk = static_cast<size_t>(tile[r]) * a.pairs + p;
             t.q[r][c] = a.q[blk * 64 + lane];
-            t.d[r][c] = *reinterpret_cast<const uint2*>(a.d + blk * 16 + 4 * (lane >> 4));
+            t.d[r][c] = *reinterpret_cast<const uint4*>(a.d + (blk * 16 + 4 * (lane >> 4)) * 2);
         }
     return t;
 }
@@ -606,11 +678,13 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
                 half8 am[RT];                                                                                       \
                 float dv[RT][4];                                                                                    \
                 _Pragma("unroll") for (int r = 0; r < RT; ++r) {                                                    \
-                    am[r] = i8x8_to_half8(CUR.q[r][c]);                                                             \
-                    dv[r][0] = half_bits_to_float(static_cast<uint16_t>(CUR.d[r][c].x & 0xffff));                   \
-                    dv[r][1] = half_bits_to_float(static_cast<uint16_t>(CUR.d[r][c].x >> 16));                      \
-                    dv[r][2] = half_bits_to_float(static_cast<uint16_t>(CUR.d[r][c].y & 0xffff));                   \
-                    dv[r][3] = half_bits_to_float(static_cast<uint16_t>(CUR.d[r][c].y >> 16));                      \
+                    const uint4 qp = CUR.q[r][c / 2], dp = CUR.d[r][c / 2];                                         \
+                    am[r] = i8x8_to_half8(c % 2 ? make_uint2(qp.z, qp.w) : make_uint2(qp.x, qp.y));                 \
+                    const int sh = c % 2 ? 16 : 0;                                                                  \
+                    dv[r][0] = half_bits_to_float(static_cast<uint16_t>(dp.x >> sh));                               \
+                    dv[r][1] = half_bits_to_float(static_cast<uint16_t>(dp.y >> sh));                               \
+                    dv[r][2] = half_bits_to_float(static_cast<uint16_t>(dp.z >> sh));                               \
+                    dv[r][3] = half_bits_to_float(static_cast<uint16_t>(dp.w >> sh));                               \
                 }                                                                                                   \
                 _Pragma("unroll") for (int v = 0; v < NT; ++v) {                                                    \
                     const half8 bh = __builtin_bit_cast(half8, bs[buf][((c * NT + v) * 2) * 64 + lane]);            \
@@ -749,7 +823,8 @@ __global__ __launch_bounds__(kEpiThreads) void resid_norm_kernel(const float* p,
 // * up) (model.hpp:111-116) into `out` and, when given, the next product's
 // halves
 __global__ __launch_bounds__(kEpiThreads) void swiglu_epilogue_kernel(const float* p, int splits, int n, int inter, float* out,
-                                                              _Float16* halves, int groups, float* unscale) {
+                                                              _Float16* halves, int groups, float* unscale,
+                                                              int interleaved) {
     __shared__ float mpart[kEpiThreads / 64];
     const int j = blockIdx.x;
     const size_t stride = static_cast<size_t>(n) * 2 * inter, base = static_cast<size_t>(j) * 2 * inter;
@@ -760,8 +835,9 @@ __global__ __launch_bounds__(kEpiThreads) void swiglu_epilogue_kernel(const floa
         const int e = threadIdx.x + kEpiThreads * m;
         val[m] = 0.f;
         if (e < inter) {
-            const float g = split_total(p, splits, stride, base + e);
-            const float u = split_total(p, splits, stride, base + inter + e);
+            const size_t ge = interleaved ? base + 2 * e : base + e, ue = interleaved ? ge + 1 : base + inter + e;
+            const float g = split_total(p, splits, stride, ge);
+            const float u = split_total(p, splits, stride, ue);
             const float small = expf(-fabsf(g));
             const float one = __fadd_rn(1.f, small);
             const float sig = g >= 0 ? __fdiv_rn(1.f, one) : __fdiv_rn(small, one);
@@ -782,17 +858,18 @@ __global__ __launch_bounds__(kEpiThreads) void swiglu_epilogue_kernel(const floa
 }
 
 // element (j, c) of row idx[j] (or `row`) of a Q8_0 table
-__global__ void gather_embedding_q8_kernel(const uint8_t* q, const uint16_t* d, int groups, const uint32_t* idx,
+__global__ void gather_embedding_q8_kernel(const uint8_t* q, const uint16_t* d, int pairs, const uint32_t* idx,
                                            uint32_t row, int n, int h, float* out) {
     const size_t total = static_cast<size_t>(n) * h;
     for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
          i += static_cast<size_t>(gridDim.x) * blockDim.x) {
         const int j = static_cast<int>(i / h), c = static_cast<int>(i % h);
         const uint32_t r = idx ? idx[j] : row;
-        const size_t blk = static_cast<size_t>(r / 16) * groups + c / 32;
+        const int g = c / 32;
+        const size_t blk = static_cast<size_t>(r / 16) * pairs + g / 2;
         const int lane = static_cast<int>(r % 16) + 16 * ((c % 32) / 8);
-        const float dv = half_bits_to_float(d[blk * 16 + r % 16]);
-        out[i] = __fmul_rn(dv, static_cast<float>(static_cast<int8_t>(q[(blk * 64 + lane) * 8 + c % 8])));
+        const float dv = half_bits_to_float(d[(blk * 16 + r % 16) * 2 + g % 2]);
+        out[i] = __fmul_rn(dv, static_cast<float>(static_cast<int8_t>(q[(blk * 64 + lane) * 16 + (g % 2) * 8 + c % 8])));
     }
 }
 
@@ -878,35 +955,56 @@ void launch_swiglu(float* gate, const float* up, int n, hipStream_t s) {
     TVARA_HIP(hipGetLastError());
 }
 
-void launch_q8_repack(const uint8_t* raw, int rows, int cols, int row0, Weight& w, int* bad, hipStream_t s) {
+void launch_q8_repack(const uint8_t* raw, int rows, int cols, int row0, int stride, Weight& w, int* bad,
+                      hipStream_t s) {
     const size_t total = static_cast<size_t>(rows) * (cols / 32);
     if (!total) return;
     launch("model_q8_repack", q8_repack_kernel, dim3(grid_for(total)), dim3(kThreads), 0, s, raw, rows, cols / 32, row0,
-           static_cast<uint8_t*>(w.q.ptr), static_cast<uint16_t*>(w.d.ptr), bad);
+           stride, static_cast<uint8_t*>(w.q.ptr), static_cast<uint16_t*>(w.d.ptr), bad);
     TVARA_HIP(hipGetLastError());
 }
 
-void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s) {
+void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg, int nseg, hipStream_t s,
+                      const float* norm_w, float eps, const float* rope_cs, int rope_dim, int rope_rows) {
+    if (w.cols > 15360) throw std::invalid_argument("Q8_0 matrix wider than 15,360 columns");
     Q8MatvecArgs a{};
-    a.q = static_cast<const uint2*>(w.q.ptr);
-    a.d = static_cast<const uint16_t*>(w.d.ptr);
+    a.q = static_cast<const uint4*>(w.q.ptr);
+    a.d = static_cast<const uint32_t*>(w.d.ptr);
     a.v = v;
+    a.norm_w = norm_w;
+    a.eps = eps;
     a.rows = w.rows;
+    a.tiles = w.tiles();
     a.groups = w.groups();
+    a.pairs = w.pairs();
+    a.cols = w.cols;
     a.nseg = nseg;
     for (int i = 0; i < nseg; ++i) a.seg[i] = seg[i];
-    // waves per tile: enough workgroups x waves to fill the chip (about
-    // 2,048 waves), no more waves than groups
-    const int tiles = w.tiles();
-    const int want = std::max(1, std::min(a.groups, 2048 / std::max(tiles, 1)));
-    if (want >= 8)
-        launch("model_matvec_q8", matvec_q8_kernel<8>, dim3(tiles), dim3(512), 0, s, a);
-    else if (want >= 4)
-        launch("model_matvec_q8", matvec_q8_kernel<4>, dim3(tiles), dim3(256), 0, s, a);
-    else if (want >= 2)
-        launch("model_matvec_q8", matvec_q8_kernel<2>, dim3(tiles), dim3(128), 0, s, a);
-    else
-        launch("model_matvec_q8", matvec_q8_kernel<1>, dim3(tiles), dim3(64), 0, s, a);
+    a.rope_cs = rope_cs;
+    a.rope_dim = rope_dim;
+    a.rope_rows = rope_rows;
+    a.swiglu = w.interleaved ? 1 : 0;
+    // two tiles per workgroup (sharing the staged input) when there are
+    // many; waves per workgroup so that about 4,096 waves share the pairs,
+    // at most sixteen and no more than there are pairs
+    const int rt = a.tiles >= 1024 ? 2 : 1;
+    const int wgs = (a.tiles + rt - 1) / rt;
+    const int want = std::max(1, std::min(a.pairs, 4096 / std::max(wgs, 1)));
+    const dim3 grid(wgs);
+    const size_t lds = static_cast<size_t>(w.cols) * sizeof(float);
+    auto go = [&](auto kernel, int waves) { launch("model_matvec_q8", kernel, grid, dim3(64 * waves), lds, s, a); };
+    if (rt == 2) {
+        if (want >= 8) go(matvec_q8_kernel<8, 2>, 8);
+        else if (want >= 4) go(matvec_q8_kernel<4, 2>, 4);
+        else if (want >= 2) go(matvec_q8_kernel<2, 2>, 2);
+        else go(matvec_q8_kernel<1, 2>, 1);
+    } else {
+        if (want >= 16) go(matvec_q8_kernel<16, 1>, 16);
+        else if (want >= 8) go(matvec_q8_kernel<8, 1>, 8);
+        else if (want >= 4) go(matvec_q8_kernel<4, 1>, 4);
+        else if (want >= 2) go(matvec_q8_kernel<2, 1>, 2);
+        else go(matvec_q8_kernel<1, 1>, 1);
+    }
     TVARA_HIP(hipGetLastError());
 }
 
@@ -934,6 +1032,7 @@ Q8Plan q8_plan(const Weight& w) {
     p.gx = (tiles + 4 * p.rt - 1) / (4 * p.rt);
     const int want = p.gx >= 256 ? 1 : std::min((256 + p.gx - 1) / p.gx, std::max(1, groups / 16));
     p.per = (groups + want - 1) / want;
+    p.per += p.per % 2;  // splits start on a group pair
     p.splits = (groups + p.per - 1) / p.per;
     return p;
 }
@@ -961,13 +1060,14 @@ void launch_batch_product(const Weight& w, const float* x, const _Float16* halve
         for (int j0 = 0; j0 < n; j0 += 64) {
             const int nj = std::min(64, n - j0);
             Q8BatchArgs a{};
-            a.q = static_cast<const uint2*>(w.q.ptr);
+            a.q = static_cast<const uint4*>(w.q.ptr);
             a.d = static_cast<const uint16_t*>(w.d.ptr);
             a.halves = reinterpret_cast<const uint4*>(halves);
             a.unscale = unscale;
             a.rows = w.rows;
             a.tiles = w.tiles();
             a.groups = w.groups();
+            a.pairs = w.pairs();
             a.n = nj;
             a.vt0 = j0 / 16;
             a.n_total = n;
@@ -1021,10 +1121,10 @@ void launch_resid_norm(const float* p, int splits, float* x, const float* w, int
 }
 
 void launch_swiglu_epilogue(const float* p, int splits, int n, int inter, float* out, _Float16* halves,
-                            float* unscale, hipStream_t s) {
+                            float* unscale, hipStream_t s, bool interleaved) {
     if (inter > kEpiThreads * kEpiPerThread) throw std::invalid_argument("batched decode width above 16384");
     launch("model_swiglu_epilogue", swiglu_epilogue_kernel, dim3(n), dim3(kEpiThreads), 0, s, p, splits, n, inter, out,
-           halves, inter / 32, unscale);
+           halves, inter / 32, unscale, interleaved ? 1 : 0);
     TVARA_HIP(hipGetLastError());
 }
 
@@ -1032,7 +1132,7 @@ void launch_gather_embedding_q8(const Weight& w, const uint32_t* idx, uint32_t r
                                 hipStream_t s) {
     const size_t total = static_cast<size_t>(n) * w.cols;
     launch("model_embedding", gather_embedding_q8_kernel, dim3(grid_for(total)), dim3(kThreads), 0, s,
-           static_cast<const uint8_t*>(w.q.ptr), static_cast<const uint16_t*>(w.d.ptr), w.groups(), idx, row, n,
+           static_cast<const uint8_t*>(w.q.ptr), static_cast<const uint16_t*>(w.d.ptr), w.pairs(), idx, row, n,
            w.cols, out);
     TVARA_HIP(hipGetLastError());
 }
