@@ -1,14 +1,17 @@
-"""Build libtvara_capi.so for gfx950 with hipcc, in-tree.
+"""Build libtvara_capi.so for gfx950, in-tree.
 
 The library goes to build/release/libtvara_capi.so, the path the reference's
-ctypes loader searches (python/tvara/native.py:17-23).  Every source compiles
-for gfx950 only, with packed-FP32 instruction selection disabled.
+ctypes loader searches (python/tvara/native.py:17-23).  The build is the
+repository's CMakeLists.txt (HIP language, ROCm clang, gfx950 only, packed-FP32
+instruction selection disabled), configured into build/release with Ninja.
+Where cmake is absent the same flags drive hipcc directly.
 """
 
 from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import shutil
 import subprocess
 import sys
 from pathlib import Path
@@ -39,19 +42,37 @@ def sources():
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
-def _compile(src: Path, obj: Path, verbose: bool):
-    lang = ["-x", "hip"] if src.suffix == ".hip" else []
-    cmd = [HIPCC, *FLAGS, *lang, "-c", str(src), "-o", str(obj)]
+def _run(cmd, verbose):
     if verbose:
-        print(" ".join(cmd), flush=True)
+        print(" ".join(map(str, cmd)), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr[-8000:]}")
-    return res.stderr
+        raise RuntimeError(f"{cmd[0]} failed:\n{res.stdout[-4000:]}\n{res.stderr[-8000:]}")
+    return res
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every source for gfx950 and link the shared library."""
+def build_cmake(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Configure (once) and build every source with CMake; always recompiles."""
+    jobs = jobs or min(os.cpu_count() or 4, 8)
+    generator = ["-G", "Ninja"] if shutil.which("ninja") else []
+    cache = OUT_DIR / "CMakeCache.txt"
+    if cache.exists() and "Ninja" not in cache.read_text(errors="ignore") and generator:
+        shutil.rmtree(OUT_DIR)  # a tree configured by another generator
+    OUT_DIR.mkdir(parents=True, exist_ok=True)
+    _run(["cmake", "-S", str(ROOT), "-B", str(OUT_DIR), *generator, "-DCMAKE_BUILD_TYPE=Release"], verbose)
+    _run(["cmake", "--build", str(OUT_DIR), "--clean-first", "-j", str(jobs)], verbose)
+    if not LIBRARY.exists():
+        raise RuntimeError(f"cmake built no {LIBRARY}")
+    return LIBRARY
+
+
+def _compile(src: Path, obj: Path, verbose: bool):
+    lang = ["-x", "hip"] if src.suffix == ".hip" else []
+    return _run([HIPCC, *FLAGS, *lang, "-c", str(src), "-o", str(obj)], verbose).stderr
+
+
+def build_hipcc(verbose: bool = False, jobs: int | None = None) -> Path:
+    """The same build with hipcc alone (hosts without cmake)."""
     obj_dir = OUT_DIR / "obj"
     obj_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
@@ -64,14 +85,16 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
             if verbose and warnings.strip():
                 print(warnings, file=sys.stderr)
     tmp = LIBRARY.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stderr[-8000:]}")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIBRARY)
     return LIBRARY
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every source for gfx950 and link the shared library."""
+    if shutil.which("cmake"):
+        return build_cmake(verbose, jobs)
+    return build_hipcc(verbose, jobs)
 
 
 if __name__ == "__main__":
