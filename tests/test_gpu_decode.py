@@ -250,6 +250,95 @@ def test_huge_scores_stay_finite(device, oracle):
     assert np.isfinite(got).all() and refmath.close(got, want, TOL)
 
 
+def _q8_sequence(device, oracle, kv_heads, dim, length, k, v, pool=8):
+    """A Q8_0 cache holding one sequence of k/v (already dequantised Q8_0 values)."""
+    dev = device.PagedCache(1, kv_heads, dim, 16, pool, fmt=device.Q8_0)
+    s = dev.create_sequence()
+    dev.append_many(s, k, v)
+    return dev, s
+
+
+def _q8_values(oracle, x):
+    return oracle.dequantize_q8_0(oracle.quantize_q8_0(x)).reshape(x.shape)
+
+
+@pytest.mark.parametrize("dim,group", [(64, 4), (128, 4), (128, 2), (128, 8)])
+def test_q8_tail_and_visible(device, oracle, dim, group):
+    for length, visible in [(53, None), (53, 54), (53, 20), (300, 1), (300, 299), (64, 33)]:
+        say("q8 tail", dim, group, length, visible)
+        got, want = _single(device, oracle, 2 * group, 2, dim, 16, length, seed=7, tail=True, visible=visible,
+                            fmt=device.Q8_0)
+        assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+    # an empty Q8_0 cache with a tail attends to the (f32) tail alone
+    dev = device.PagedCache(1, 2, dim, 16, 4, fmt=device.Q8_0)
+    s = dev.create_sequence()
+    tv = synth.normal(4, "tv", 2 * dim)
+    out = attention.fused_paged_attention(synth.normal(4, "q", 2 * group * dim), dev, s, 0, 2 * group, 64,
+                                          synth.normal(4, "tk", 2 * dim), tv)
+    assert np.array_equal(out.reshape(2 * group, dim), np.repeat(tv.reshape(2, dim), group, axis=0))
+
+
+def test_q8_zero_query_is_mean_of_values(device, oracle):
+    # q = 0 gives every position the same score, so each query head returns the
+    # mean of its KV head's values (tests/core/test_model.cpp:46-51)
+    for dim, kv_heads, group, length in [(64, 2, 4, 77), (128, 8, 4, 300), (128, 4, 2, 33), (64, 3, 3, 16)]:
+        say("q8 zero query", dim, kv_heads, group, length)
+        w = kv_heads * dim
+        k = _q8_values(oracle, synth.normal(11, "k", length * w).reshape(length, w))
+        v = _q8_values(oracle, synth.normal(11, "v", length * w).reshape(length, w))
+        dev, s = _q8_sequence(device, oracle, kv_heads, dim, length, k, v, pool=length // 16 + 2)
+        heads = kv_heads * group
+        got = attention.fused_paged_attention(np.zeros(heads * dim, np.float32), dev, s, 0, heads, 4096)
+        want = np.repeat(v.astype(np.float64).reshape(length, kv_heads, dim).mean(axis=0), group, axis=0).reshape(-1)
+        assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+def test_q8_unused_slots_and_junk_never_leak(device, oracle):
+    # Q8_0 form of prefill_t174.cpp: NaN group scales and junk int8 in the
+    # unused slots of the last block, for the int8-MFMA score path (group <= 4)
+    # and the vector path (group 8)
+    nan_group = np.concatenate([np.frombuffer(np.float16(np.nan).tobytes(), np.uint8), np.full(32, 0x81, np.uint8)])
+    for dim, kv_heads, group in [(64, 2, 4), (128, 2, 4), (128, 2, 3), (128, 1, 8)]:
+        for length in (1, 15, 16, 17, 31, 32, 33, 47):
+            say("q8 poison", dim, kv_heads, group, length)
+            w = kv_heads * dim
+            k = _q8_values(oracle, synth.signal(length * w).reshape(length, w))
+            v = _q8_values(oracle, synth.signal(length * w, 2).reshape(length, w))
+            dev, s = _q8_sequence(device, oracle, kv_heads, dim, length, k, v)
+            h = dev.physical_block(s, length - 1)
+            gpr = w // 32
+            for slot in range(length % 16 or 16, 16):
+                for kind in (0, 1):
+                    dev.block_write(h, ((kind * 16 + slot) * gpr) * 34, np.tile(nan_group, gpr))
+            heads = kv_heads * group
+            q = synth.signal(heads * dim, 3)
+            got = attention.fused_paged_attention(q, dev, s, 0, heads, 128)
+            assert refmath.close(got, refmath.attention(q, k, v, heads, kv_heads, dim), TOL)
+            dev.audit()
+
+
+def test_q8_wide_ranges(device, oracle):
+    # per-token magnitudes from 1e-4 to 1e1 (group scales from ~1e-6, fp16
+    # subnormals, to ~0.3; scores up to ~1e2, so the running maximum moves),
+    # queries with one large head and one near-zero head; against float64
+    # attention on the dequantised values
+    for dim, kv_heads, group in [(128, 2, 4), (64, 2, 4), (128, 4, 1)]:
+        length = 200
+        say("q8 ranges", dim, kv_heads, group)
+        w = kv_heads * dim
+        mag = np.float32(10.0) ** np.linspace(-4, 1, length, dtype=np.float32)[synth.permutation(5, "m", length)]
+        k = _q8_values(oracle, synth.normal(5, "k", length * w).reshape(length, w) * mag[:, None])
+        v = _q8_values(oracle, synth.normal(5, "v", length * w).reshape(length, w) * mag[:, None])
+        dev, s = _q8_sequence(device, oracle, kv_heads, dim, length, k, v, pool=length // 16 + 2)
+        heads = kv_heads * group
+        q = synth.normal(5, "q", heads * dim).reshape(heads, dim)
+        q[0] *= np.float32(4.0)
+        q[-1] *= np.float32(1e-5)
+        got = attention.fused_paged_attention(q.reshape(-1), dev, s, 0, heads, 4096)
+        want = refmath.attention(q.reshape(-1), k, v, heads, kv_heads, dim)
+        assert np.isfinite(got).all() and refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
 def test_prompt_chunk_f32(device, oracle):
     # fused_prompt_attention (prefill_t173.cpp): rows see their own prefix only
     g = (1, 1, 8, 7, 20)

@@ -26,16 +26,34 @@ enum Format : int { kF32 = 0, kQ8 = 1 };
 // Where a (layer, kind, slot, column) element of a block lives in HBM.
 //  f32: the reference layout, ((layer*2+kind)*tpb+slot)*kv_width+column floats
 //       (kv.hpp:30-33), so block bytes are the reference's bytes.
-//  Q8_0: one section per (layer, kind) of `section` bytes: an int8 plane
-//       [tpb][kv_width] followed by an fp16 scale plane [tpb][kv_width/32];
-//       the canonical image is the reference element order cut into 34-byte
-//       groups (little-endian fp16 d, then 32 int8).
+//  Q8_0: one section per (layer, kind) of `section` bytes holding each KV head
+//       in turn: the head's int8 plane [tpb][head_dim] followed by its fp16
+//       scale plane [tpb][head_dim/32], `head_bytes` per head (16-byte
+//       aligned).  A head's tokens in a block are then one contiguous run
+//       (2,176 B for 16 tokens at head_dim 128), which is what one decode wave
+//       reads.  The canonical image is the reference element order cut into
+//       34-byte groups (little-endian fp16 d, then 32 int8).
 struct BlockLayout {
     int format;
     int layers, kv_heads, head_dim, tpb, kv_width;
-    size_t stride;   // bytes between consecutive blocks in the pool (256-aligned)
-    size_t section;  // Q8_0: bytes per (layer, kind) section
+    size_t stride;      // bytes between consecutive blocks in the pool (256-aligned)
+    size_t section;     // Q8_0: bytes per (layer, kind) section
+    size_t head_bytes;  // Q8_0: bytes per KV head within a section
 };
+
+// Q8_0: offset within a section of the int8 of (slot, column) and of the
+// fp16 scale of (slot, group of 32 columns), columns and groups counted
+// across the whole kv_width row
+__host__ __device__ inline size_t q8_byte_offset(const BlockLayout& lay, int slot, int column) {
+    const int h = column / lay.head_dim;
+    return static_cast<size_t>(h) * lay.head_bytes + static_cast<size_t>(slot) * lay.head_dim + (column - h * lay.head_dim);
+}
+
+__host__ __device__ inline size_t q8_scale_offset(const BlockLayout& lay, int slot, int group) {
+    const int ng = lay.head_dim / 32, h = group / ng;
+    return static_cast<size_t>(h) * lay.head_bytes + static_cast<size_t>(lay.tpb) * lay.head_dim +
+           (static_cast<size_t>(slot) * ng + (group - h * ng)) * 2;
+}
 
 // Block initialisation: zero-fill (src < 0, BlockPool::allocate, kv.hpp:48)
 // or whole-block copy (copy-on-write, kv.hpp:99).
@@ -104,6 +122,7 @@ void launch_canonical_to_q8(char* pool, const BlockLayout& lay, int64_t id, cons
 // decode.hip
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, hipStream_t s);
 int decode_waves(int kv_heads, int group, int format, int head_dim);
+int decode_budget_per_cu(int group, int format, int head_dim);
 // prefill.hip
 bool prefill_bf16_supported(const BlockLayout& lay, int group);
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s);

@@ -21,6 +21,7 @@
 // *err, matching OnlineAttention::update's rejection (attention.hpp:11).
 #include <algorithm>
 #include <cstdlib>
+#include <string>
 #include <type_traits>
 
 #include "common.hpp"
@@ -391,11 +392,11 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
     const int nblk = (t1 - t0 + 15) >> 4;
     const int bids = lane < nblk ? tab[(t0 >> 4) + lane] : 0;
     const size_t sec = a.lay.section;
-    const size_t qcol = static_cast<size_t>(kh) * D + 16 * c;
-    const size_t scol = (static_cast<size_t>(kh) * D + 16 * c) / 32;
-    const size_t plane = static_cast<size_t>(16) * kvw;  // int8 plane bytes of a section
+    const size_t qcol = static_cast<size_t>(kh) * D + 16 * c;  // column in the f32 tail row
+    // this head's run of the section: int8 [16][D], then fp16 scales [16][D/32]
+    const size_t qoff = static_cast<size_t>(kh) * a.lay.head_bytes + 16 * c;
+    const size_t soff = static_cast<size_t>(kh) * a.lay.head_bytes + 16 * D + (16 * c / 32) * 2;
     const size_t ksec = static_cast<size_t>(a.layer) * 2 * sec, vsec = ksec + sec;
-    const int gpr = kvw / 32;
 
     struct Tile {
         uint4 kq, vq;
@@ -408,10 +409,10 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
         const int slot = (tb & 15) + tg;
         const char* base = a.pool + static_cast<size_t>(bid) * a.lay.stride;
         if (ok) {
-            x.kq = *reinterpret_cast<const uint4*>(base + ksec + static_cast<size_t>(slot) * kvw + qcol);
-            x.vq = *reinterpret_cast<const uint4*>(base + vsec + static_cast<size_t>(slot) * kvw + qcol);
-            x.ks = *reinterpret_cast<const uint16_t*>(base + ksec + plane + (static_cast<size_t>(slot) * gpr + scol) * 2);
-            x.vs = *reinterpret_cast<const uint16_t*>(base + vsec + plane + (static_cast<size_t>(slot) * gpr + scol) * 2);
+            x.kq = *reinterpret_cast<const uint4*>(base + ksec + qoff + static_cast<size_t>(slot) * D);
+            x.vq = *reinterpret_cast<const uint4*>(base + vsec + qoff + static_cast<size_t>(slot) * D);
+            x.ks = *reinterpret_cast<const uint16_t*>(base + ksec + soff + static_cast<size_t>(slot) * (D / 16));
+            x.vs = *reinterpret_cast<const uint16_t*>(base + vsec + soff + static_cast<size_t>(slot) * (D / 16));
         } else {
             x.kq = x.vq = make_uint4(0, 0, 0, 0);
             x.ks = x.vs = 0;
@@ -486,6 +487,350 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
                                [](int cc, int e4) { return 16 * cc + 4 * e4; });
 }
 
+// ------------------------------------------- Q8_0 blocks, scores on int8 MFMA
+//
+// The score side runs on the int8 matrix cores.  v_mfma_i32_16x16x32_i8
+// multiplies a 16 x 32 int8 A by a 32 x 16 int8 B into exact int32 sums; lane
+// l supplies row (A) or column (B) l%16 at k-slots 8(l/16)..+7 and receives
+// rows 4(l/16)..+3 of column l%16.  One Q8_0 group (32 columns) is one k
+// range, so each group's sums can take that group's scale d[t][g].
+//   B: the raw int8 K bytes of 16 tokens (column = token).  A wave loads its
+//      head's K run contiguously (16 bytes per lane) and restages it in LDS,
+//      because the operand layout puts consecutive lanes on different tokens.
+//   A: the query, split exactly into four base-128 int8 pieces,
+//      x = q * 127 / max|q| = a0 + a1/128 + a2/128^2 + a3/128^3 (|a0| <= 127,
+//      |aj| <= 64, remainder below 2^-22 of max|q|), one row per
+//      (head h, piece j) = 4h + j.
+// Lane (u, t) then holds the four pieces of head u for token t; the score is
+// qscale * max|q_u|/127 * sum_g d[t][g] * sum_j 128^-j C_g[j], one score per
+// lane (16 tokens x 4 heads per MFMA group).
+//
+// The value side stays on the vector ALUs in f32, as decode_q8_kernel: a
+// 16-bit operand cannot carry p * d for every fp16 group scale d.  The
+// weights w[t][g][h] = p[t][h] * dV[t][g] go from the score layout to the
+// value layout (lane = token group x 16 columns) through LDS.  Against
+// decode_q8_kernel this removes the K conversions and the G x head_dim f32
+// products per token, about half of the vector instructions.
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// max / sum over the 16 lanes of a DPP row (every lane receives the result)
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp<0x124>(v));  // row_ror:4
+    return fmaxf(v, dpp<0x128>(v));  // row_ror:8
+}
+
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x124>(v);
+    return v + dpp<0x128>(v);
+}
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// LDS bytes per wave: the K rows of a 32-token tile ([32][D + 16] int8) and
+// the weights w[32 tokens][groups][4 heads]
+template <int D>
+constexpr size_t q8_mma_wave_lds() {
+    return 32 * (D + 16) + 32 * (D / 32) * 4 * sizeof(float);
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) {
+    constexpr int NG = D / 32;                      // Q8_0 groups per head row
+    constexpr int LPT = D / 16, TT = 64 / LPT, E = 16;
+    constexpr int VP = 32 / TT;                     // value passes per 32-token tile
+    constexpr int KP = D / 64;                      // 16-byte K chunks per lane and block
+    constexpr int KRS = D + 16;                     // LDS row of one token's K (padded against bank conflicts)
+    static_assert(G >= 1 && G <= 4, "four query heads per KV head at most");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int groups = a.lay.kv_heads / nwaves;
+    const int item = static_cast<int>(blockIdx.x) / groups;
+    const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
+    const int2 it = a.items[item];
+    const int4 en = a.entries[it.x];
+    const int nsplit = en.z >> 1;
+    const bool tail = (en.z & 1) && it.y == nsplit - 1;
+    const int t0 = it.y * a.split_tokens;
+    const int t1 = min(t0 + a.split_tokens, en.y);
+    const int n = max(t1 - t0, 0);
+    const int kvw = a.lay.kv_width;
+    const int u = lane >> 4, t16 = lane & 15;         // score layout: head u, token t16
+    const int c = lane & (LPT - 1), tg = lane / LPT;  // value layout: token group, 16 columns
+
+    extern __shared__ float lds[];
+    char* kl = reinterpret_cast<char*>(lds) + static_cast<size_t>(wave) * q8_mma_wave_lds<D>();  // [32][D + 16] int8
+    float* wl = reinterpret_cast<float*>(kl + 32 * KRS);  // [32 tokens][NG][4 heads]
+
+    // query pieces: lane (u, r) holds piece r%4 of head r/4 at columns 32g + 8u .. +7
+    long qa[NG];
+    float wsc;  // qscale * max|q| / 127 of head u
+    {
+        const int hq = t16 >> 2, jp = t16 & 3;
+        const bool hv = hq < G;
+        const float* qr = a.q + (static_cast<size_t>(it.x) * a.heads + static_cast<size_t>(kh) * G + (hv ? hq : 0)) * D;
+        float qv[NG][8];
+        float mx = 0.f;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const float4 x0 = hv ? *reinterpret_cast<const float4*>(qr + 32 * g + 8 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 x1 = hv ? *reinterpret_cast<const float4*>(qr + 32 * g + 8 * u + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            qv[g][0] = x0.x; qv[g][1] = x0.y; qv[g][2] = x0.z; qv[g][3] = x0.w;
+            qv[g][4] = x1.x; qv[g][5] = x1.y; qv[g][6] = x1.z; qv[g][7] = x1.w;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(qv[g][e]));
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float inv = mx > 0.f ? 127.f / mx : 0.f;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            uint32_t w[2] = {0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = qv[g][e] * inv;
+                const float a0 = __builtin_rintf(x);
+                float r = (x - a0) * 128.f;  // exact: |x - a0| <= 1/2, power-of-two scaling
+                const float a1 = __builtin_rintf(r);
+                r = (r - a1) * 128.f;
+                const float a2 = __builtin_rintf(r);
+                r = (r - a2) * 128.f;
+                const float a3 = __builtin_rintf(r);
+                const float pc = jp == 0 ? a0 : (jp == 1 ? a1 : (jp == 2 ? a2 : a3));
+                w[e >> 2] |= (static_cast<uint32_t>(static_cast<int>(pc)) & 0xffu) << (8 * (e & 3));
+            }
+            qa[g] = static_cast<long>((static_cast<uint64_t>(w[1]) << 32) | w[0]);
+        }
+        // the max of head h sits in every lane whose row is 4h + j: take lane 4h
+        const float m0 = readlane_f(mx, 0), m1 = readlane_f(mx, 4), m2 = readlane_f(mx, 8), m3 = readlane_f(mx, 12);
+        const float mh = u == 0 ? m0 : (u == 1 ? m1 : (u == 2 ? m2 : m3));
+        wsc = a.qscale * (mh / 127.f);
+    }
+
+    float acc[G][E];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
+    float mv = -INFINITY, lv = 0.f;  // head u's running max (row-uniform); this lane's share of the normaliser
+    bool bad = false;
+
+    const int32_t* tab = a.tables + en.x;
+    const int nblk = (n + 15) >> 4;
+    const int bids = lane < nblk ? tab[(t0 >> 4) + lane] : 0;
+    const size_t sec = a.lay.section;
+    // this head's run of a section: int8 [16][D] then fp16 scales [16][NG]
+    const size_t ksec = static_cast<size_t>(a.layer) * 2 * sec + static_cast<size_t>(kh) * a.lay.head_bytes;
+    const size_t vsec = ksec + sec;
+    const size_t kcol = static_cast<size_t>(kh) * D;  // column of the f32 tail row
+
+    // Loads are contiguous: lane i takes bytes 16i (+1024m) of a head's int8
+    // plane, and the 16 tokens' scales are one 16 * NG * 2 byte run.
+    struct Tile {
+        u32x4_t kq[2][KP];   // K int8 of each half, natural order (staged in LDS for the MFMA operand)
+        uint2 ks[2], vs[2];  // the NG group scales of token t16 (K and V)
+        uint4 vq[VP];        // value layout: token k * TT + tg, columns 16c .. +15
+    };
+    auto block_base = [&](int i, int b) {
+        const int bid = __builtin_amdgcn_readlane(bids, min(2 * i + b, nblk - 1));
+        return a.pool + static_cast<size_t>(bid) * a.lay.stride;
+    };
+    auto load = [&](Tile& x, int i) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const char* kb = block_base(i, b) + ksec;
+            const char* vb = kb + sec;
+#pragma unroll
+            for (int m = 0; m < KP; ++m) x.kq[b][m] = *reinterpret_cast<const u32x4_t*>(kb + 1024 * m + 16 * lane);
+            const size_t so = 16 * D + static_cast<size_t>(t16) * NG * 2;
+            if constexpr (NG >= 4) {
+                x.ks[b] = *reinterpret_cast<const uint2*>(kb + so);
+                x.vs[b] = *reinterpret_cast<const uint2*>(vb + so);
+            } else {
+                x.ks[b] = make_uint2(*reinterpret_cast<const uint32_t*>(kb + so), 0u);
+                x.vs[b] = make_uint2(*reinterpret_cast<const uint32_t*>(vb + so), 0u);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < VP; ++k) {
+            const int b = (k * TT) >> 4;
+            x.vq[k] = *reinterpret_cast<const uint4*>(block_base(i, b) + vsec + static_cast<size_t>((k * TT) & 15) * D +
+                                                      16 * lane);
+        }
+    };
+    auto scale_of = [](uint2 s, int g) {
+        const uint32_t w = g < 2 ? s.x : s.y;
+        return half_bits_to_float(static_cast<uint16_t>((g & 1) ? (w >> 16) : (w & 0xffffu)));
+    };
+    // online-softmax step for one row-uniform tile maximum tm of head u
+    auto rescale = [&](float tm) {
+        if (__any(tm > mv + kThreshold)) {
+            const float mnew = fmaxf(mv, tm);
+            const float alpha = (mnew == -INFINITY) ? 1.f : fast_exp2(mv - mnew);
+            mv = mnew;
+            lv *= alpha;
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float ah = readlane_f(alpha, 16 * h);
+#pragma unroll
+                for (int e = 0; e < E; ++e) acc[h][e] *= ah;
+            }
+        }
+    };
+    auto process = [&](const Tile& x, int i) {
+        // K rows of both halves into LDS; lane (u, t) then reads its 8-byte k-slots of token t
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int m = 0; m < KP; ++m) {
+                const int byte = 1024 * m + 16 * lane;
+                *reinterpret_cast<u32x4_t*>(kl + (16 * b + byte / D) * KRS + byte % D) = x.kq[b][m];
+            }
+        float s[2];
+        bool ok[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            float sc = 0.f;
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                const uint2 kv = *reinterpret_cast<const uint2*>(kl + (16 * b + t16) * KRS + 32 * g + 8 * u);
+                i32x4_t r = {0, 0, 0, 0};
+                r = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[g], __builtin_bit_cast(long, kv), r, 0, 0, 0);
+                const float xg = fmaf(static_cast<float>(r[3]), 0x1p-21f,
+                                      fmaf(static_cast<float>(r[2]), 0x1p-14f,
+                                           fmaf(static_cast<float>(r[1]), 0x1p-7f, static_cast<float>(r[0]))));
+                sc = fmaf(scale_of(x.ks[b], g), xg, sc);
+            }
+            sc *= wsc;
+            ok[b] = (32 * i + 16 * b + t16 < n) && u < G;
+            bad |= ok[b] && !__builtin_isfinite(sc);
+            s[b] = ok[b] ? sc : -INFINITY;
+        }
+        rescale(row_max16(fmaxf(s[0], s[1])));
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const float p = ok[b] ? fast_exp2(s[b] - mv) : 0.f;
+            lv += p;
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+                wl[((16 * b + t16) * NG + g) * 4 + u] = ok[b] ? p * scale_of(x.vs[b], g) : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < VP; ++k) {
+            const float4 w4 = *reinterpret_cast<const float4*>(wl + ((k * TT + tg) * NG + (c >> 1)) * 4);
+            const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+            float vf[16];
+            unpack_i8(x.vq[k], vf);
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int e = 0; e < E; ++e) acc[h][e] = fmaf(wv[h], vf[e], acc[h][e]);
+        }
+    };
+
+    // Two tiles of 32 tokens (two blocks) in flight; prefetches past the last
+    // tile re-read it, and a tile past the end is fully masked.
+    const int ntiles = (n + 31) >> 5;
+    if (ntiles > 0) {
+        const int last = ntiles - 1;
+        Tile ta, tb;
+        load(ta, 0);
+        asm volatile("" ::: "memory");
+        load(tb, min(1, last));
+        asm volatile("" ::: "memory");
+        for (int i = 0; i < ntiles; i += 2) {
+            process(ta, i);
+            load(ta, min(i + 2, last));
+            asm volatile("" ::: "memory");
+            process(tb, i + 1);
+            load(tb, min(i + 3, last));
+            asm volatile("" ::: "memory");
+        }
+    }
+    if (tail) {  // the uncommitted token arrives as f32 and is the last position (attention.hpp:80)
+        constexpr int CPL = D / 16;
+        float part = 0.f;
+        if (u < G) {
+            const float* qh = a.q + (static_cast<size_t>(it.x) * a.heads + static_cast<size_t>(kh) * G + u) * D + t16 * CPL;
+            const float* tk = a.tail_k + static_cast<size_t>(it.x) * kvw + kcol + t16 * CPL;
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) part = fmaf(qh[e], tk[e], part);
+        }
+        float st = row_sum16(part) * a.qscale;
+        const bool okt = u < G;
+        bad |= okt && !__builtin_isfinite(st);
+        st = okt ? st : -INFINITY;
+        rescale(st);
+        const float p = okt ? fast_exp2(st - mv) : 0.f;
+        lv += t16 == 0 ? p : 0.f;
+        float ph[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) ph[h] = readlane_f(p, 16 * h);
+        if (tg == 0) {
+            const float* tv = a.tail_v + static_cast<size_t>(it.x) * kvw + kcol + 16 * c;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float v = tv[e];
+#pragma unroll
+                for (int h = 0; h < G; ++h) acc[h][e] = fmaf(ph[h], v, acc[h][e]);
+            }
+        }
+    }
+    // Sum the token groups in registers (DPP within a 16-lane row, shuffles
+    // across the four rows): lane c < LPT then holds columns 16c .. 16c+15 of
+    // every head, so the split needs neither LDS nor a workgroup barrier.
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            float v = acc[h][e];
+            v += dpp<0x128>(v);                          // row_ror:8
+            if constexpr (LPT == 4) v += dpp<0x124>(v);  // row_ror:4
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            acc[h][e] = v;
+        }
+    const float lsum = row_sum16(lv);
+    float mh[G], lh[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        mh[h] = readlane_f(mv, 16 * h);
+        lh[h] = readlane_f(lsum, 16 * h);
+    }
+    const size_t head0 = static_cast<size_t>(kh) * G;
+    if (lane < LPT) {
+        float* dst = nsplit == 1 ? a.out + (static_cast<size_t>(it.x) * a.heads + head0) * D
+                                 : a.part_acc + (static_cast<size_t>(item) * a.heads + head0) * D;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float sc = nsplit == 1 ? 1.f / lh[h] : 1.f;
+#pragma unroll
+            for (int e4 = 0; e4 < E / 4; ++e4)
+                *reinterpret_cast<float4*>(dst + h * D + 16 * c + 4 * e4) =
+                    make_float4(acc[h][4 * e4] * sc, acc[h][4 * e4 + 1] * sc, acc[h][4 * e4 + 2] * sc,
+                                acc[h][4 * e4 + 3] * sc);
+        }
+    }
+    if (nsplit > 1 && lane < G) {
+        float m = mh[0], l = lh[0];
+#pragma unroll
+        for (int h = 1; h < G; ++h) {
+            m = lane == h ? mh[h] : m;
+            l = lane == h ? lh[h] : l;
+        }
+        float* o = a.part_ml + (static_cast<size_t>(item) * a.heads + head0 + lane) * 2;
+        o[0] = m;
+        o[1] = l;
+    }
+    if (__any(bad) && lane == 0) *a.err = 1;
+}
+
 // --------------------------------------------------- any shape (one wave per head)
 
 __device__ __forceinline__ float element(const DecodeArgs& a, int block, int kind, int slot, int column) {
@@ -495,9 +840,8 @@ __device__ __forceinline__ float element(const DecodeArgs& a, int block, int kin
         return reinterpret_cast<const float*>(base)[(static_cast<size_t>(a.layer * 2 + kind) * a.lay.tpb + slot) * kvw +
                                                     column];
     const char* sec = base + static_cast<size_t>(a.layer * 2 + kind) * a.lay.section;
-    const int8_t qv = reinterpret_cast<const int8_t*>(sec)[static_cast<size_t>(slot) * kvw + column];
-    const uint16_t d = reinterpret_cast<const uint16_t*>(sec + static_cast<size_t>(a.lay.tpb) * kvw)
-        [static_cast<size_t>(slot) * (kvw / 32) + column / 32];
+    const int8_t qv = reinterpret_cast<const int8_t*>(sec)[q8_byte_offset(a.lay, slot, column)];
+    const uint16_t d = *reinterpret_cast<const uint16_t*>(sec + q8_scale_offset(a.lay, slot, column / 32));
     return half_bits_to_float(d) * static_cast<float>(qv);
 }
 
@@ -796,11 +1140,41 @@ void launch_q8(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
            a);
 }
 
+template <int D, int G>
+void launch_q8_mma(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
+    const size_t lds = static_cast<size_t>(waves) * q8_mma_wave_lds<D>();
+    launch("paged_decode", decode_q8_mma_kernel<D, G>, dim3(nitems * (a.lay.kv_heads / waves)), dim3(64 * waves), lds,
+           s, a);
+}
+
+// Q8_0 scores on the int8 matrix cores for up to four query heads per KV
+// head; TVARA_Q8_DECODE=valu selects the all-VALU kernel.
+bool q8_mma_enabled(int group) {
+    static const bool valu = [] {
+        const char* env = std::getenv("TVARA_Q8_DECODE");
+        return env && std::string(env) == "valu";
+    }();
+    return group <= 4 && !valu;
+}
+
+bool q8_mma_shape(int group, int format, int head_dim) {
+    return format != kF32 && (head_dim == 64 || head_dim == 128) && q8_mma_enabled(group);
+}
+
 template <int D>
 bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
     constexpr int LPT = D == 64 ? 4 : 8;
     const int G = a.group;
     if (G > LPT) return false;
+    if (a.lay.format != kF32 && q8_mma_enabled(G)) {
+        switch (G) {
+            case 1: launch_q8_mma<D, 1>(a, nitems, waves, s); return true;
+            case 2: launch_q8_mma<D, 2>(a, nitems, waves, s); return true;
+            case 3: launch_q8_mma<D, 3>(a, nitems, waves, s); return true;
+            case 4: launch_q8_mma<D, 4>(a, nitems, waves, s); return true;
+            default: break;
+        }
+    }
     if (a.lay.format == kF32) {
         switch (G) {
             case 1: launch_f32<D, 1, LPT>(a, nitems, waves, s); return true;
@@ -843,18 +1217,33 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
 
 // Waves per workgroup (one per KV head), measured on MI355X: eight for f32
 // blocks (a workgroup streams whole 2 KiB slot rows; about one workgroup per
-// CU is best), four for Q8_0 (more, shorter workgroups hide its longer
-// per-tile arithmetic), at most two for groups above four query heads; a
-// divisor of kv_heads whose reduction buffers fit 64 KiB of LDS.
+// CU is best), four for Q8_0 (the int8-MFMA kernel: 207 us against 210 us
+// with eight on the Llama-3-8B batch; the vector kernel: more, shorter
+// workgroups hide its longer per-tile arithmetic), at most two for groups
+// above four query heads; a divisor of kv_heads whose LDS fits 64 KiB.
 // TVARA_DECODE_WAVES overrides it for tuning.
 int decode_waves(int kv_heads, int group, int format, int head_dim) {
+    const bool mma = q8_mma_shape(group, format, head_dim);
     int w = format == kF32 ? 8 : 4;
     if (const char* env = std::getenv("TVARA_DECODE_WAVES")) w = std::atoi(env);
     if (group > 4) w = std::min(w, 2);
     w = std::max(1, std::min(w, 8));
-    auto lds = [&](int n) { return static_cast<size_t>(n) * (4 * group * head_dim + 2 * group) * sizeof(float); };
+    auto lds = [&](int n) {
+        return mma ? static_cast<size_t>(n) * (32 * (head_dim + 16) + 32 * (head_dim / 32) * 4 * sizeof(float))
+                   : static_cast<size_t>(n) * (4 * group * head_dim + 2 * group) * sizeof(float);
+    };
     while (w > 1 && (kv_heads % w || lds(w) > 65536)) --w;
     return w;
+}
+
+// Workgroups per CU a decode launch is sized for (the split length is the
+// shortest whose launch fits CUs x this): one for f32 blocks, two for the
+// int8-MFMA Q8_0 kernel (two 8-wave workgroups' worth of registers per CU),
+// four for the vector Q8_0 kernel.  TVARA_DECODE_BUDGET overrides it.
+int decode_budget_per_cu(int group, int format, int head_dim) {
+    if (const char* env = std::getenv("TVARA_DECODE_BUDGET")) return std::max(1, std::atoi(env));
+    if (format == kF32) return 1;
+    return q8_mma_shape(group, format, head_dim) ? 2 : 4;
 }
 
 static int waves_for(const DecodeArgs& a) {

@@ -130,7 +130,8 @@ DeviceCache::DeviceCache(const Geometry& g, int format) : g_(g), format_(format)
         lay_.section = g_.tokens_per_block * kvw * sizeof(float);
         lay_.stride = round_up(g_.elements_per_block() * sizeof(float), 256);
     } else {
-        lay_.section = round_up(g_.tokens_per_block * kvw + g_.tokens_per_block * (kvw / 32) * 2, 16);
+        lay_.head_bytes = round_up(g_.tokens_per_block * g_.head_dim + g_.tokens_per_block * (g_.head_dim / 32) * 2, 16);
+        lay_.section = g_.kv_heads * lay_.head_bytes;
         lay_.stride = round_up(2 * g_.layers * lay_.section, 256);
     }
     if (lay_.stride > kMax / g_.max_blocks) throw std::invalid_argument("KV capacity overflow");
@@ -532,8 +533,8 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     if (tab.size() > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
         throw std::invalid_argument("attention batch too large");
     // Split length: the shortest (a multiple of 16 from 64 to 1,024 tokens)
-    // whose launch fits the workgroup budget -- one workgroup per CU for f32
-    // blocks, four for Q8_0 (measured best on MI355X: the 64-sequence
+    // whose launch fits the workgroup budget of the decode kernel that will
+    // run (decode_budget_per_cu, measured on MI355X: the 64-sequence
     // Llama-3.2-1B batch and the 16 x 32,768 Llama-3-8B Q8_0 batch).
     size_t split = split_override;
     if (!split) {
@@ -542,7 +543,8 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     if (!split) {
         const size_t groups = g.kv_heads / static_cast<size_t>(decode_waves(static_cast<int>(g.kv_heads), group,
                                                                              c->format(), static_cast<int>(g.head_dim)));
-        const size_t budget = static_cast<size_t>(c->compute_units()) * (c->format() == kF32 ? 1 : 4);
+        const size_t budget = static_cast<size_t>(c->compute_units()) *
+                              decode_budget_per_cu(group, c->format(), static_cast<int>(g.head_dim));
         auto workgroups = [&](size_t sp) {
             size_t n = 0;
             for (size_t len : cached) n += std::max<size_t>(1, (len + sp - 1) / sp);

@@ -63,9 +63,6 @@ __global__ __launch_bounds__(kThreads) void append_rows_q8_kernel(char* pool, Bl
     const int layer = blockIdx.x >> 1, kind = blockIdx.x & 1;
     const float* src = (kind ? values : keys) + (static_cast<size_t>(op.src_row) * lay.layers + layer) * lay.kv_width;
     char* sec = pool + static_cast<size_t>(op.block) * lay.stride + static_cast<size_t>(layer * 2 + kind) * lay.section;
-    int8_t* qrow = reinterpret_cast<int8_t*>(sec) + static_cast<size_t>(op.slot) * lay.kv_width;
-    uint16_t* drow = reinterpret_cast<uint16_t*>(sec + static_cast<size_t>(lay.tpb) * lay.kv_width) +
-                     static_cast<size_t>(op.slot) * (lay.kv_width / 32);
     const int groups = lay.kv_width / 32;
     const int l32 = threadIdx.x & 31;
     for (int g = threadIdx.x >> 5; g < groups; g += blockDim.x >> 5) {
@@ -75,8 +72,8 @@ __global__ __launch_bounds__(kThreads) void append_rows_q8_kernel(char* pool, Bl
         uint16_t d;
         int8_t qv;
         q8_encode_element(x, amax, &d, &qv);
-        qrow[g * 32 + l32] = qv;
-        if (l32 == 0) drow[g] = d;
+        reinterpret_cast<int8_t*>(sec)[q8_byte_offset(lay, op.slot, g * 32 + l32)] = qv;
+        if (l32 == 0) *reinterpret_cast<uint16_t*>(sec + q8_scale_offset(lay, op.slot, g)) = d;
     }
 }
 
@@ -88,9 +85,8 @@ __device__ __forceinline__ float load_element(const char* pool, const BlockLayou
                                                         lay.kv_width +
                                                     column];
     const char* sec = base + static_cast<size_t>(layer * 2 + kind) * lay.section;
-    const int8_t q = reinterpret_cast<const int8_t*>(sec)[static_cast<size_t>(slot) * lay.kv_width + column];
-    const uint16_t d = reinterpret_cast<const uint16_t*>(sec + static_cast<size_t>(lay.tpb) * lay.kv_width)
-        [static_cast<size_t>(slot) * (lay.kv_width / 32) + column / 32];
+    const int8_t q = reinterpret_cast<const int8_t*>(sec)[q8_byte_offset(lay, slot, column)];
+    const uint16_t d = *reinterpret_cast<const uint16_t*>(sec + q8_scale_offset(lay, slot, column / 32));
     return half_bits_to_float(d) * static_cast<float>(q);  // dequantize_q8_0 (quant.hpp:43-47)
 }
 
@@ -120,8 +116,8 @@ __device__ __forceinline__ uint32_t canonical_q8_byte(const char* base, const Bl
     const int gcol = static_cast<int>(group % gpr);
     const int sec = static_cast<int>(row / lay.tpb), slot = static_cast<int>(row % lay.tpb);
     const unsigned char* s = reinterpret_cast<const unsigned char*>(base + static_cast<size_t>(sec) * lay.section);
-    if (off < 2) return s[static_cast<size_t>(lay.tpb) * lay.kv_width + (static_cast<size_t>(slot) * gpr + gcol) * 2 + off];
-    return s[static_cast<size_t>(slot) * lay.kv_width + gcol * 32 + (off - 2)];
+    if (off < 2) return s[q8_scale_offset(lay, slot, gcol) + off];
+    return s[q8_byte_offset(lay, slot, gcol * 32) + (off - 2)];
 }
 
 __device__ __forceinline__ size_t canonical_words(const BlockLayout& lay) {
@@ -172,8 +168,8 @@ __global__ __launch_bounds__(kThreads) void q8_to_canonical_kernel(const char* p
         const int gcol = static_cast<int>(g % gpr);
         const int sec = static_cast<int>(row / lay.tpb), slot = static_cast<int>(row % lay.tpb);
         const unsigned char* s = reinterpret_cast<const unsigned char*>(base + static_cast<size_t>(sec) * lay.section);
-        const unsigned char* d = s + static_cast<size_t>(lay.tpb) * lay.kv_width + (static_cast<size_t>(slot) * gpr + gcol) * 2;
-        const unsigned char* q = s + static_cast<size_t>(slot) * lay.kv_width + gcol * 32;
+        const unsigned char* d = s + q8_scale_offset(lay, slot, gcol);
+        const unsigned char* q = s + q8_byte_offset(lay, slot, gcol * 32);
         uint8_t* o = out + g * 34;
         o[0] = d[0];
         o[1] = d[1];
@@ -192,8 +188,8 @@ __global__ __launch_bounds__(kThreads) void canonical_to_q8_kernel(char* pool, B
         const int gcol = static_cast<int>(g % gpr);
         const int sec = static_cast<int>(row / lay.tpb), slot = static_cast<int>(row % lay.tpb);
         unsigned char* s = reinterpret_cast<unsigned char*>(base + static_cast<size_t>(sec) * lay.section);
-        unsigned char* d = s + static_cast<size_t>(lay.tpb) * lay.kv_width + (static_cast<size_t>(slot) * gpr + gcol) * 2;
-        unsigned char* q = s + static_cast<size_t>(slot) * lay.kv_width + gcol * 32;
+        unsigned char* d = s + q8_scale_offset(lay, slot, gcol);
+        unsigned char* q = s + q8_byte_offset(lay, slot, gcol * 32);
         const uint8_t* i8 = in + g * 34;
         d[0] = i8[0];
         d[1] = i8[1];
