@@ -147,6 +147,34 @@ def test_prefill_plan_matches_call(device, oracle, precision):
         plan.launch(0, dq.ptr, out.ptr)
 
 
+@pytest.mark.parametrize("group", [1, 4])
+def test_bf16_nan_poisoned_unused_slots(device, oracle, group):
+    # prefill_t174.cpp for the MFMA path: NaN in the unused slots of the last
+    # block (past the cached length, inside the last 64-key tile) never reaches
+    # a row; chunks that end at the cache end, 16-key boundaries and mid-block
+    heads, kv_heads, dim = 2 * group, 2, 64
+    w = kv_heads * dim
+    for n, rows in [(137, 37), (33, 33), (80, 16), (1, 1)]:
+        say("prefill bf16 poison", group, n, rows)
+        dev = device.PagedCache(1, kv_heads, dim, 16, n // 16 + 3)
+        ref = oracle.Cache(1, kv_heads, dim, 16, n // 16 + 3)
+        k = synth.normal(21, "k", n * w).reshape(n, w)
+        v = synth.normal(21, "v", n * w).reshape(n, w)
+        sd, sr = dev.create_sequence(), ref.create_sequence()
+        dev.append_many(sd, k, v)
+        ref.append_many(sr, k, v)
+        h = dev.physical_block(sd, n - 1)
+        for slot in range(n % 16 or 16, 16):
+            for kind in (0, 1):
+                dev.block_write(h, dev.kv_offset(0, kind, slot), np.full(w, np.nan, np.float32))
+        q = synth.normal(21, "q", rows * heads * dim).reshape(rows, heads * dim)
+        got = attention.prefill_batch(dev, q, [sd], [n - rows], [rows], 0, heads, 4096, precision="bf16")
+        want = ref.fused_prompt_attention(q, sr, 0, n - rows, rows, heads, 4096).reshape(rows, -1)
+        assert np.isfinite(got).all()
+        ok, err = bf16_ok(got.reshape(rows, -1), want, SHORT_ROWS)
+        assert ok, err
+
+
 def test_bf16_rejections(device):
     dev = device.PagedCache(1, 2, 128, 16, 8)
     s = dev.create_sequence()

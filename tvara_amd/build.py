@@ -47,7 +47,9 @@ def _run(cmd, verbose):
         print(" ".join(map(str, cmd)), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"{cmd[0]} failed:\n{res.stdout[-4000:]}\n{res.stderr[-8000:]}")
+        out = res.stdout + res.stderr
+        errors = "\n".join(line for line in out.splitlines() if "error" in line or "FAILED" in line)
+        raise RuntimeError(f"{cmd[0]} failed:\n{errors[-8000:]}\n--- tail ---\n{out[-3000:]}")
     return res
 
 
@@ -60,9 +62,19 @@ def build_cmake(verbose: bool = False, jobs: int | None = None) -> Path:
         shutil.rmtree(OUT_DIR)  # a tree configured by another generator
     OUT_DIR.mkdir(parents=True, exist_ok=True)
     _run(["cmake", "-S", str(ROOT), "-B", str(OUT_DIR), *generator, "-DCMAKE_BUILD_TYPE=Release"], verbose)
-    _run(["cmake", "--build", str(OUT_DIR), "--clean-first", "-j", str(jobs)], verbose)
+    # a failed build raises and leaves the previous library in place
+    keep = LIBRARY.with_suffix(".so.prev")
+    if LIBRARY.exists():
+        os.replace(LIBRARY, keep)
+    try:
+        _run(["cmake", "--build", str(OUT_DIR), "--clean-first", "-j", str(jobs)], verbose)
+    except RuntimeError:
+        if keep.exists() and not LIBRARY.exists():
+            os.replace(keep, LIBRARY)
+        raise
     if not LIBRARY.exists():
         raise RuntimeError(f"cmake built no {LIBRARY}")
+    keep.unlink(missing_ok=True)
     return LIBRARY
 
 

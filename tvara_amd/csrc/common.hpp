@@ -107,6 +107,8 @@ struct PrefillArgs {
     float* out;
     float qscale;
     int* err;
+    int chunk_tiles;  // query tiles per (sequence, KV head) pair (set by the launcher)
+    int pairs;        // sequences x KV heads
 };
 
 // launchers (kernels.hip)

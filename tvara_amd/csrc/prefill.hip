@@ -20,6 +20,8 @@
 // score - m ready for exp2, and the normaliser is one more MFMA tile whose A
 // operand is a row of ones.  The causal mask is applied on tiles that reach
 // past a row's own position.
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace tvara_amd {
@@ -34,6 +36,15 @@ constexpr int kRows = 32, kKeys = 64;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 on an LDS address
+__device__ __forceinline__ bf16x4 tr16_read(const __bf16* p) {
+    typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+    return __builtin_bit_cast(bf16x4, v);
+}
+
 __device__ __forceinline__ bf16x4 to_bf16(float4 v) {
     const f32x4 f = {v.x, v.y, v.z, v.w};
     return __builtin_convertvector(f, bf16x4);
@@ -45,19 +56,27 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     constexpr int QT = kWaves * PW;      // chunk positions per workgroup
     constexpr int KC = D / 32;           // K-dimension chunks of S^T
     constexpr int DT = D / 16;           // output column tiles
-    constexpr int KSTR = D + 8;          // LDS row pitch of K (bf16), padded
-    constexpr int VSTR = kKeys + 8;      // LDS row pitch of V^T (bf16), padded
+    constexpr int KSTR = D + 8;          // LDS row pitch of K (bf16): 144 B, conflict-free b128 operand reads
+    constexpr int VSTR = D + 16;         // LDS row pitch of V (bf16): 160 B, conflict-free transposing reads
     static_assert(D == 64, "the staging map covers 64 columns");
+    constexpr int SP = kKeys * 16 / (64 * kWaves);  // staging passes per tile (16 lanes per key row)
+    static_assert(SP >= 1 && SP * 64 * kWaves == kKeys * 16, "the staging map covers whole key rows");
     __shared__ __attribute__((aligned(16))) __bf16 klds[2][kKeys * KSTR];
-    __shared__ __attribute__((aligned(16))) __bf16 vlds[2][D * VSTR];
+    __shared__ __attribute__((aligned(16))) __bf16 vlds[2][kKeys * VSTR];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r16 = lane & 15;
-    const int kh = blockIdx.y;
-    const int4 sd = a.seqs[blockIdx.z];  // table offset, start, rows, first query row
+    // XCD-aware order: workgroups are dispatched to the 8 XCDs round-robin by
+    // id, so the chunk tiles of one (sequence, KV head) pair get ids of one
+    // residue mod 8 and share that XCD's L2 for their common K/V tiles.
+    const int id = static_cast<int>(blockIdx.x), xcd = id & 7, k = id >> 3;
+    const int pair = (k / a.chunk_tiles) * 8 + xcd, ct = k % a.chunk_tiles;
+    if (pair >= a.pairs) return;
+    const int kh = pair % a.lay.kv_heads;
+    const int4 sd = a.seqs[pair / a.lay.kv_heads];  // table offset, start, rows, first query row
     const int start = sd.y, nrows = sd.z;
-    const int q0 = blockIdx.x * QT;
-    if (q0 >= nrows) return;  // the whole workgroup: grid.x covers the longest chunk
+    const int q0 = ct * QT;
+    if (q0 >= nrows) return;  // the whole workgroup: chunk_tiles covers the longest chunk
     const int kmax = start + min(q0 + QT, nrows);  // keys this workgroup reads: [0, kmax)
     const int ntiles = (kmax + kKeys - 1) / kKeys;
     const int pw0 = q0 + wave * PW;
@@ -89,29 +108,44 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
         }
     }
 
-    // staging map: thread -> 4 consecutive keys (one block) x 4 columns
-    const int key4 = tid & 15, col = 4 * (tid >> 4);
-    float4 kreg[4], vreg[4];
-    auto gload = [&](int kt) {
-        const int kb = kt * kKeys + 4 * key4;
-        const int bid = kb < kmax ? tab[kb >> 4] : 0;
-        const float* base = pool + static_cast<size_t>(bid) * bstride + static_cast<size_t>(kb & 15) * kvw + col;
+    // staging map: 16 lanes per key row (4 columns each), 4 * kWaves keys per
+    // pass, SP passes per 64-key tile; a wave's four rows lie in one paged block
+    // (the block ids are loaded one tile ahead of the K/V rows, so no wave
+    // waits on a table lookup before issuing its loads)
+    constexpr int KPP = 4 * kWaves;  // keys per staging pass
+    const int skey = tid >> 4, col = 4 * (tid & 15);
+    float4 kA[SP], vA[SP], kB[SP], vB[SP];  // two register stages (even / odd tiles)
+    int bA[SP], bB[SP];
+    // Every load is unconditional (a key past the chunk's reach reads the last
+    // reachable key): a load under a branch makes the compiler wait for all
+    // outstanding loads where the branches join.  Such keys lie past every
+    // row's causal limit, so their scores are masked; their V rows are zeroed
+    // when staged, so a non-finite value there cannot reach a row as 0 * NaN.
+    auto tabload = [&](int kt, int (&b)[SP]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const bool ok = kb + j < kmax;  // keys past the chunk's reach are never read
-            kreg[j] = ok ? *reinterpret_cast<const float4*>(base + j * kvw + koff) : make_float4(0.f, 0.f, 0.f, 0.f);
-            vreg[j] = ok ? *reinterpret_cast<const float4*>(base + j * kvw + voff) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int p = 0; p < SP; ++p) {
+            const int key = min(kt * kKeys + KPP * p + skey, kmax - 1);
+            b[p] = tab[key >> 4];
         }
     };
-    auto lstore = [&](int buf) {
+    auto gload = [&](int kt, const int (&b)[SP], float4 (&kreg)[SP], float4 (&vreg)[SP]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<bf16x4*>(&klds[buf][(4 * key4 + j) * KSTR + col]) = to_bf16(kreg[j]);
-        const float4 v0 = vreg[0], v1 = vreg[1], v2 = vreg[2], v3 = vreg[3];
-        *reinterpret_cast<bf16x4*>(&vlds[buf][(col + 0) * VSTR + 4 * key4]) = to_bf16(make_float4(v0.x, v1.x, v2.x, v3.x));
-        *reinterpret_cast<bf16x4*>(&vlds[buf][(col + 1) * VSTR + 4 * key4]) = to_bf16(make_float4(v0.y, v1.y, v2.y, v3.y));
-        *reinterpret_cast<bf16x4*>(&vlds[buf][(col + 2) * VSTR + 4 * key4]) = to_bf16(make_float4(v0.z, v1.z, v2.z, v3.z));
-        *reinterpret_cast<bf16x4*>(&vlds[buf][(col + 3) * VSTR + 4 * key4]) = to_bf16(make_float4(v0.w, v1.w, v2.w, v3.w));
+        for (int p = 0; p < SP; ++p) {
+            const int key = kt * kKeys + KPP * p + skey;
+            const float* base = pool + static_cast<size_t>(b[p]) * bstride +
+                                static_cast<size_t>(min(key, kmax - 1) & 15) * kvw + col;
+            kreg[p] = *reinterpret_cast<const float4*>(base + koff);
+            vreg[p] = *reinterpret_cast<const float4*>(base + voff);
+        }
+    };
+    auto lstore = [&](int kt, int buf, const float4 (&kreg)[SP], const float4 (&vreg)[SP]) {
+#pragma unroll
+        for (int p = 0; p < SP; ++p) {
+            const bool ok = kt * kKeys + KPP * p + skey < kmax;
+            *reinterpret_cast<bf16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = to_bf16(kreg[p]);
+            *reinterpret_cast<bf16x4*>(&vlds[buf][(KPP * p + skey) * VSTR + col]) =
+                to_bf16(ok ? vreg[p] : make_float4(0.f, 0.f, 0.f, 0.f));
+        }
     };
 
     // acc[DT] is the normaliser: A = a row of ones (A row l%16 comes from lane
@@ -127,15 +161,11 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) lim[nt] = start + pw0 + (16 * nt + r16) / G;  // last visible key of the row
 
-    const bool stager = tid < 256;  // the staging map covers 256 threads
-    if (stager) {
-        gload(0);
-        lstore(0);
-    }
-    __syncthreads();
-    for (int kt = 0; kt < ntiles; ++kt) {
-        const int buf = kt & 1;
-        if (stager && kt + 1 < ntiles) gload(kt + 1);
+    // Tile t's K/V rows are requested two iterations before they are written
+    // to LDS (register stages A for even tiles, B for odd), its block ids four
+    // iterations before; every load is unconditional (past the last tile they
+    // re-read it), so no branch makes the compiler wait for them early.
+    auto compute = [&](int kt, int buf) {
         const int kbase = kt * kKeys;
         if (kbase < wave_kmax) {
             // scores arrive as score - m: the accumulators start at -m (the
@@ -157,7 +187,16 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                     s[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[0][kc], s[mt][0], 0, 0, 0);
                     s[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[1][kc], s[mt][1], 0, 0, 0);
                 }
-            const bool diag = kbase + kKeys - 1 > start + pw0;
+            // the causal mask only on tiles that reach past a row's own position
+            if (kbase + kKeys - 1 > start + pw0) {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (kbase + 16 * mt + 4 * g + i > lim[nt]) s[mt][nt][i] = -INFINITY;
+            }
             float rmax[2];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
@@ -165,12 +204,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        float v = s[mt][nt][i];
-                        if (diag && kbase + 16 * mt + 4 * g + i > lim[nt]) v = -INFINITY;
-                        s[mt][nt][i] = v;
-                        mx = fmaxf(mx, v);
-                    }
+                    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nt][i]);
                 mx = fmaxf(mx, __shfl_xor(mx, 16));
                 mx = fmaxf(mx, __shfl_xor(mx, 32));
                 rmax[nt] = mx;
@@ -214,13 +248,18 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                     pop[nt][kc] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 }
             }
+            // V^T operand by transposing LDS reads (ds_read_b64_tr_b16): within
+            // each 16-lane group, lane i receives element i%4 of the chunk that
+            // lane 4j + i/4 addresses, as its element j; lane 16g + 4j + q
+            // addresses key row 4g + j (+16 for the second half), columns
+            // 16dt + 4q, so lane (g, i) gets column 16dt + i of keys 4g + j
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
-                    const __bf16* vrow = &vlds[buf][(16 * dt + r16) * VSTR + 32 * kc + 4 * g];
-                    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
-                    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 16);
+                    const __bf16* vrow = &vlds[buf][(32 * kc + 4 * g + (r16 >> 2)) * VSTR + 16 * dt + 4 * (r16 & 3)];
+                    const bf16x4 lo = tr16_read(vrow);
+                    const bf16x4 hi = tr16_read(vrow + 16 * VSTR);
                     const bf16x8 vop = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                     acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[0][kc], acc[dt][0], 0, 0, 0);
                     acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[1][kc], acc[dt][1], 0, 0, 0);
@@ -231,7 +270,27 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                 acc[DT][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[1][kc], acc[DT][1], 0, 0, 0);
             }
         }
-        if (stager && kt + 1 < ntiles) lstore(buf ^ 1);
+    };
+    auto tile = [&](int t) { return min(t, ntiles - 1); };
+    tabload(0, bA);
+    gload(0, bA, kA, vA);
+    tabload(tile(1), bB);
+    gload(tile(1), bB, kB, vB);
+    tabload(tile(2), bA);
+    tabload(tile(3), bB);
+    lstore(0, 0, kA, vA);
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; kt += 2) {
+        gload(tile(kt + 2), bA, kA, vA);
+        tabload(tile(kt + 4), bA);
+        compute(kt, 0);
+        lstore(tile(kt + 1), 1, kB, vB);
+        __syncthreads();
+        if (kt + 1 >= ntiles) break;
+        gload(tile(kt + 3), bB, kB, vB);
+        tabload(tile(kt + 5), bB);
+        compute(kt + 1, 1);
+        lstore(tile(kt + 2), 0, kA, vA);
         __syncthreads();
     }
 
@@ -257,11 +316,28 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 // eight waves per workgroup (measured on MI355X against four: 158 against 225
 // us on the 8 x (2,048 + 512) chunk; K/V tiles are re-read by half as many
 // workgroups) and 64-key tiles (128-key tiles measured 177 us)
+template <int G, int W>
+void launch_gw(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
+    constexpr int QT = W * (kRows / G);
+    PrefillArgs b = a;
+    b.chunk_tiles = (max_rows + QT - 1) / QT;
+    b.pairs = nseqs * a.lay.kv_heads;
+    const int groups8 = (b.pairs + 7) / 8;  // ids = 8 XCDs x pair groups x chunk tiles
+    launch("paged_prefill_bf16", prefill_bf16_kernel<64, G, W>, dim3(8 * groups8 * b.chunk_tiles), dim3(64 * W), 0, s,
+           b);
+}
+
+// waves per workgroup (TVARA_PREFILL_WAVES: 4 or 8)
 template <int G>
 void launch_g(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
-    constexpr int QT = 8 * (kRows / G);
-    const dim3 grid((max_rows + QT - 1) / QT, a.lay.kv_heads, nseqs);
-    launch("paged_prefill_bf16", prefill_bf16_kernel<64, G, 8>, grid, dim3(64 * 8), 0, s, a);
+    static const int waves = [] {
+        const char* env = std::getenv("TVARA_PREFILL_WAVES");
+        return env && std::atoi(env) == 4 ? 4 : 8;
+    }();
+    if (waves == 4)
+        launch_gw<G, 4>(a, nseqs, max_rows, s);
+    else
+        launch_gw<G, 8>(a, nseqs, max_rows, s);
 }
 
 }  // namespace
