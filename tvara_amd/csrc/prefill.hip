@@ -45,6 +45,18 @@ __device__ __forceinline__ bf16x4 tr16_read(const __bf16* p) {
     return __builtin_bit_cast(bf16x4, v);
 }
 
+// max over lanes l%16 + 16r (the four 16-lane rows) in registers:
+// permlane32_swap(v, v) yields (low half, high half) of v in every lane,
+// permlane16_swap(v, v) yields (even row, odd row) of its pair
+__device__ __forceinline__ float cross_row_max(float v) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    v = fmaxf(__builtin_bit_cast(float, h[0]), __builtin_bit_cast(float, h[1]));
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+
 __device__ __forceinline__ bf16x4 to_bf16(float4 v) {
     const f32x4 f = {v.x, v.y, v.z, v.w};
     return __builtin_convertvector(f, bf16x4);
@@ -205,9 +217,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nt][i]);
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
-                rmax[nt] = mx;
+                rmax[nt] = cross_row_max(mx);
             }
             if (first) {
                 // every row sees key 0 here, so its maximum is finite
@@ -230,44 +240,48 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                     for (int dt = 0; dt <= DT; ++dt) acc[dt][nt] *= alpha;
                 }
             }
-            // P^T as the B operand of O^T = V^T P^T: keys {4g+i, 16+4g+i} of each 32-key half
-            bf16x8 pop[2][2];
+            // P^T as the B operand of O^T = V^T P^T: keys {4g+i, 16+4g+i} of each
+            // 32-key half kc (s already holds score - m; a masked score gives
+            // exp2(-inf) = 0).  Row half 1's probabilities for a key half are
+            // computed between the two halves' products, so the vector ALU
+            // works while the matrix core runs half 0's MFMAs.
+            auto probs = [&](int nt, int kc) {
+                float p[2][4];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                float p[4][4];
-                // s already holds score - m; a masked score gives exp2(-inf) = 0
+                for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) p[mt][i] = fast_exp2(s[mt][nt][i]);
-#pragma unroll
-                for (int kc = 0; kc < 2; ++kc) {
-                    const bf16x4 lo = to_bf16(make_float4(p[2 * kc][0], p[2 * kc][1], p[2 * kc][2], p[2 * kc][3]));
-                    const bf16x4 hi =
-                        to_bf16(make_float4(p[2 * kc + 1][0], p[2 * kc + 1][1], p[2 * kc + 1][2], p[2 * kc + 1][3]));
-                    pop[nt][kc] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                }
-            }
+                    for (int i = 0; i < 4; ++i) p[h][i] = fast_exp2(s[2 * kc + h][nt][i]);
+                const bf16x4 lo = to_bf16(make_float4(p[0][0], p[0][1], p[0][2], p[0][3]));
+                const bf16x4 hi = to_bf16(make_float4(p[1][0], p[1][1], p[1][2], p[1][3]));
+                return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            };
+            bf16x8 pop0[2];
+            pop0[0] = probs(0, 0);
+            pop0[1] = probs(0, 1);
             // V^T operand by transposing LDS reads (ds_read_b64_tr_b16): within
             // each 16-lane group, lane i receives element i%4 of the chunk that
             // lane 4j + i/4 addresses, as its element j; lane 16g + 4j + q
             // addresses key row 4g + j (+16 for the second half), columns
             // 16dt + 4q, so lane (g, i) gets column 16dt + i of keys 4g + j
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc)
+            for (int kc = 0; kc < 2; ++kc) {
+                bf16x8 vop[DT];
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
                     const __bf16* vrow = &vlds[buf][(32 * kc + 4 * g + (r16 >> 2)) * VSTR + 16 * dt + 4 * (r16 & 3)];
                     const bf16x4 lo = tr16_read(vrow);
                     const bf16x4 hi = tr16_read(vrow + 16 * VSTR);
-                    const bf16x8 vop = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[0][kc], acc[dt][0], 0, 0, 0);
-                    acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[1][kc], acc[dt][1], 0, 0, 0);
+                    vop[dt] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 }
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-                acc[DT][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[0][kc], acc[DT][0], 0, 0, 0);
-                acc[DT][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[1][kc], acc[DT][1], 0, 0, 0);
+                for (int dt = 0; dt < DT; ++dt)
+                    acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[dt], pop0[kc], acc[dt][0], 0, 0, 0);
+                acc[DT][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop0[kc], acc[DT][0], 0, 0, 0);
+                const bf16x8 pop1 = probs(1, kc);
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+                    acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[dt], pop1, acc[dt][1], 0, 0, 0);
+                acc[DT][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop1, acc[DT][1], 0, 0, 0);
             }
         }
     };
