@@ -76,6 +76,14 @@ struct RowOp {
 // longest split a decode work item covers: 64 blocks of 16 tokens (the
 // kernels hold a split's block ids one per lane of a wave)
 constexpr size_t kMaxSplitTokens = 1024;
+constexpr int kMaxSplitBlocks = 64;  // block ids per work item (16-token blocks)
+
+// Per attention row: (first work item, number of splits), passed in the
+// merge kernel's arguments when a plan has at most kInlineRows rows.
+constexpr int kInlineRows = 128;
+struct RowSplits {
+    int2 r[kInlineRows];
+};
 
 struct DecodeArgs {
     const char* pool;
@@ -86,6 +94,11 @@ struct DecodeArgs {
     const int4* entries;  // x: table offset, y: cached tokens, z: tail | nsplit<<1, w: first item
     const int2* items;    // x: row, y: split index
     int split_tokens;
+    // 16-token blocks: per work item x: row, y: first token, z: end token,
+    // w: tail (the row's uncommitted token is this item's last) | several splits << 1;
+    // and the item's block ids, kMaxSplitBlocks per item
+    const int4* work;
+    const int32_t* work_blocks;
     const float* q;
     const float* tail_k;  // [rows][kv_width] or null
     const float* tail_v;
@@ -122,7 +135,8 @@ void launch_checksums(const char* pool, const BlockLayout& lay, const int64_t* i
 void launch_q8_to_canonical(const char* pool, const BlockLayout& lay, int64_t id, uint8_t* out, hipStream_t s);
 void launch_canonical_to_q8(char* pool, const BlockLayout& lay, int64_t id, const uint8_t* in, hipStream_t s);
 // decode.hip
-void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, hipStream_t s);
+void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
+                   hipStream_t s);
 int decode_waves(int kv_heads, int group, int format, int head_dim);
 int decode_budget_per_cu(int group, int format, int head_dim);
 // prefill.hip

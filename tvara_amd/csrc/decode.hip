@@ -130,6 +130,14 @@ __device__ __forceinline__ float softmax_step(float s, bool own, int lane, RowSt
     return p;
 }
 
+// sum over the token groups of a wave that share head slot / column lane c
+template <int LPT>
+__device__ __forceinline__ float token_group_sum(float v) {
+    v += dpp<0x128>(v);                          // row_ror:8
+    if constexpr (LPT == 4) v += dpp<0x124>(v);  // row_ror:4
+    return cross_row_sum(v);
+}
+
 // Reduce the token groups of a wave and write the split's result: the
 // normalised output when the row has one split, otherwise the partial
 // (acc, m, l) that merge_kernel combines.  (Merging in the last workgroup to
@@ -139,7 +147,7 @@ __device__ __forceinline__ float softmax_step(float s, bool own, int lane, RowSt
 // e4-th float4.
 template <int D, int G, int LPT, int E, class Col>
 __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G][E], RowState& st, int lane, int wave,
-                                             int nwaves, int kh, int item, int row, int first, int nsplit, Col col) {
+                                             int nwaves, int kh, int item, int row, int nsplit, Col col) {
     extern __shared__ float lds[];
     const int c = lane & (LPT - 1);
     st.l = wave_sum_across(st.l, LPT);
@@ -206,12 +214,12 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
     const int groups = a.lay.kv_heads / nwaves;
     const int item = static_cast<int>(blockIdx.x) / groups;
     const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
-    const int2 it = a.items[item];
-    const int4 en = a.entries[it.x];
-    const int nsplit = en.z >> 1;
-    const bool tail = (en.z & 1) && it.y == nsplit - 1;
-    const int t0 = it.y * a.split_tokens;
-    const int t1 = min(t0 + a.split_tokens, en.y);
+    // the item's descriptor and block ids come in two independent loads
+    const int4 it = a.work[item];  // row, first token, end token, tail | several splits << 1
+    const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
+    const int nsplit = (it.w & 2) ? 2 : 1;  // the finish only tells one split from several
+    const bool tail = (it.w & 1) != 0;
+    const int t0 = it.y, t1 = it.z;
     const int c = lane & (LPT - 1), tg = lane / LPT;
     const int kvw = a.lay.kv_width;
 
@@ -240,11 +248,10 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
 
     const float* pool = reinterpret_cast<const float*>(a.pool);
     const size_t bstride = a.lay.stride / sizeof(float);
-    // the split's block ids, one per lane (a split spans at most 64 blocks);
-    // a tile's id is read from the owning lane, so the loop issues no table loads
-    const int32_t* tab = a.tables + en.x;
-    const int nblk = (t1 - t0 + 15) >> 4;
-    const int bids = lane < nblk ? tab[(t0 >> 4) + lane] : 0;
+    // bids holds the split's block ids, one per lane (a split spans at most 64
+    // blocks); a tile's id is read from the owning lane, so the loop issues no
+    // table loads
+
     const size_t koff = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D + 4 * c;
     const size_t voff = koff + 16 * static_cast<size_t>(kvw);
 
@@ -330,7 +337,7 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
         }
         process(ka, va, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, item - it.y, nsplit,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
                                [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
 }
 
@@ -356,12 +363,12 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
     const int groups = a.lay.kv_heads / nwaves;
     const int item = static_cast<int>(blockIdx.x) / groups;
     const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
-    const int2 it = a.items[item];
-    const int4 en = a.entries[it.x];
-    const int nsplit = en.z >> 1;
-    const bool tail = (en.z & 1) && it.y == nsplit - 1;
-    const int t0 = it.y * a.split_tokens;
-    const int t1 = min(t0 + a.split_tokens, en.y);
+    // the item's descriptor and block ids come in two independent loads
+    const int4 it = a.work[item];  // row, first token, end token, tail | several splits << 1
+    const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
+    const int nsplit = (it.w & 2) ? 2 : 1;  // the finish only tells one split from several
+    const bool tail = (it.w & 1) != 0;
+    const int t0 = it.y, t1 = it.z;
     const int c = lane & (LPT - 1), tg = lane / LPT;
     const int kvw = a.lay.kv_width;
 
@@ -386,11 +393,10 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
         for (int e = 0; e < E; ++e) acc[h][e] = 0.f;
     RowState st;
 
-    // the split's block ids, one per lane (a split spans at most 64 blocks);
-    // a tile's id is read from the owning lane, so the loop issues no table loads
-    const int32_t* tab = a.tables + en.x;
-    const int nblk = (t1 - t0 + 15) >> 4;
-    const int bids = lane < nblk ? tab[(t0 >> 4) + lane] : 0;
+    // bids holds the split's block ids, one per lane (a split spans at most 64
+    // blocks); a tile's id is read from the owning lane, so the loop issues no
+    // table loads
+
     const size_t sec = a.lay.section;
     const size_t qcol = static_cast<size_t>(kh) * D + 16 * c;  // column in the f32 tail row
     // this head's run of the section: int8 [16][D], then fp16 scales [16][D/32]
@@ -483,7 +489,7 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
         }
         process_f(kf, 1.f, vf, 1.f, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, item - it.y, nsplit,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
                                [](int cc, int e4) { return 16 * cc + 4 * e4; });
 }
 
@@ -553,12 +559,12 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
     const int groups = a.lay.kv_heads / nwaves;
     const int item = static_cast<int>(blockIdx.x) / groups;
     const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
-    const int2 it = a.items[item];
-    const int4 en = a.entries[it.x];
-    const int nsplit = en.z >> 1;
-    const bool tail = (en.z & 1) && it.y == nsplit - 1;
-    const int t0 = it.y * a.split_tokens;
-    const int t1 = min(t0 + a.split_tokens, en.y);
+    // the item's descriptor and block ids come in two independent loads
+    const int4 it = a.work[item];  // row, first token, end token, tail | several splits << 1
+    const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
+    const int nsplit = (it.w & 2) ? 2 : 1;  // the finish only tells one split from several
+    const bool tail = (it.w & 1) != 0;
+    const int t0 = it.y, t1 = it.z;
     const int n = max(t1 - t0, 0);
     const int kvw = a.lay.kv_width;
     const int u = lane >> 4, t16 = lane & 15;         // score layout: head u, token t16
@@ -621,9 +627,7 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
     float mv = -INFINITY, lv = 0.f;  // head u's running max (row-uniform); this lane's share of the normaliser
     bool bad = false;
 
-    const int32_t* tab = a.tables + en.x;
     const int nblk = (n + 15) >> 4;
-    const int bids = lane < nblk ? tab[(t0 >> 4) + lane] : 0;
     const size_t sec = a.lay.section;
     // this head's run of a section: int8 [16][D] then fp16 scales [16][NG]
     const size_t ksec = static_cast<size_t>(a.layer) * 2 * sec + static_cast<size_t>(kh) * a.lay.head_bytes;
@@ -782,19 +786,14 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
             }
         }
     }
-    // Sum the token groups in registers (DPP within a 16-lane row, shuffles
-    // across the four rows): lane c < LPT then holds columns 16c .. 16c+15 of
+    // Sum the token groups in registers (DPP within a 16-lane row, permlane
+    // swaps across the four rows): lane c < LPT then holds columns 16c .. 16c+15 of
     // every head, so the split needs neither LDS nor a workgroup barrier.
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            float v = acc[h][e];
-            v += dpp<0x128>(v);                          // row_ror:8
-            if constexpr (LPT == 4) v += dpp<0x124>(v);  // row_ror:4
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            acc[h][e] = v;
+            acc[h][e] = token_group_sum<LPT>(acc[h][e]);
         }
     const float lsum = row_sum16(lv);
     float mh[G], lh[G];
@@ -929,21 +928,21 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(const DecodeArgs a) 
 // before the first is used, so a row of up to R * U splits costs one memory
 // round trip.  Each lane keeps an online maximum over its splits; the R lanes
 // of a unit are combined through LDS.
-template <int V, int UPL, int U>
-__global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
+template <int V, int UPL, int U, bool kInline>
+__global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a, const RowSplits rs) {
     using T = typename std::conditional<V == 4, float4, float>::type;
     __shared__ float sm[256], sl[256];
     __shared__ T sa[256][UPL];
     const int row = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-    const int4 en = a.entries[row];
-    const int nsplit = en.z >> 1;
+    const int2 en = kInline ? rs.r[row] : make_int2(a.entries[row].w, a.entries[row].z >> 1);  // first item, splits
+    const int nsplit = en.y;
     if (nsplit <= 1) return;
     const int D = a.lay.head_dim, nu = D / V;
     const int lpr = min(64, nu), R = 256 / lpr;
     const int u0 = lane % lpr, r = lane / lpr;
     const size_t step = static_cast<size_t>(a.heads);
-    const float* ml = a.part_ml + (static_cast<size_t>(en.w) * step + h) * 2;
-    const float* pa = a.part_acc + (static_cast<size_t>(en.w) * step + h) * D;
+    const float* ml = a.part_ml + (static_cast<size_t>(en.x) * step + h) * 2;
+    const float* pa = a.part_acc + (static_cast<size_t>(en.x) * step + h) * D;
 
     auto zero = [] {
         if constexpr (V == 4) return make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1035,19 +1034,21 @@ __global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
 // workgroup, for head_dim = 4 * LPR with LPR a power of two up to 64: lane
 // (r, u) holds float4 u of splits r, r + R, ... (R = 64 / LPR), U of them
 // per memory round trip, and the R slots combine by shuffles.
-template <int LPR, int U>
-__global__ __launch_bounds__(256) void merge_wave_kernel(const DecodeArgs a) {
+template <int LPR, int U, bool kInline>
+__global__ __launch_bounds__(256) void merge_wave_kernel(const DecodeArgs a, const RowSplits rs) {
     constexpr int R = 64 / LPR, D = 4 * LPR;
     const int lane = threadIdx.x & 63, h = blockIdx.y * 4 + (threadIdx.x >> 6);
     const int row = blockIdx.x;
     if (h >= a.heads) return;
-    const int4 en = a.entries[row];
-    const int nsplit = en.z >> 1;
+    // (first item, splits) of the row: from the kernel arguments when the
+    // plan has few rows (no dependent load before the partials), else from HBM
+    const int2 en = kInline ? rs.r[row] : make_int2(a.entries[row].w, a.entries[row].z >> 1);
+    const int nsplit = en.y;
     if (nsplit <= 1) return;
     const int u = lane % LPR, r = lane / LPR;
     const size_t step = static_cast<size_t>(a.heads);
-    const float* ml = a.part_ml + (static_cast<size_t>(en.w) * step + h) * 2;
-    const float* pa = a.part_acc + (static_cast<size_t>(en.w) * step + h) * D;
+    const float* ml = a.part_ml + (static_cast<size_t>(en.x) * step + h) * 2;
+    const float* pa = a.part_acc + (static_cast<size_t>(en.x) * step + h) * D;
     float M = -INFINITY, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s0 = 0; s0 < nsplit; s0 += R * U) {
@@ -1104,24 +1105,34 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(const DecodeArgs a) {
         make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
-void launch_merge(const DecodeArgs& a, int nrows, hipStream_t s) {
+template <bool kInline>
+void launch_merge_t(const DecodeArgs& a, const RowSplits& rs, int nrows, hipStream_t s) {
     const int D = a.lay.head_dim;
     const dim3 grid(nrows, a.heads), block(256);
-    const dim3 wgrid(nrows, (a.heads + 3) / 4);
+    // one wave per (row, head), four heads per workgroup (sixteen measured
+    // no faster on the Llama-3.2-1B batch and slower on the Llama-3-8B one)
+    const dim3 wgrid(nrows, (a.heads + 3) / 4), wblock(256);
     if (D == 64)
-        launch("paged_decode_merge", merge_wave_kernel<16, 4>, wgrid, block, 0, s, a);
+        launch("paged_decode_merge", merge_wave_kernel<16, 4, kInline>, wgrid, wblock, 0, s, a, rs);
     else if (D == 128)
-        launch("paged_decode_merge", merge_wave_kernel<32, 8>, wgrid, block, 0, s, a);
+        launch("paged_decode_merge", merge_wave_kernel<32, 8, kInline>, wgrid, wblock, 0, s, a, rs);
     else if (D == 256)
-        launch("paged_decode_merge", merge_wave_kernel<64, 8>, wgrid, block, 0, s, a);
+        launch("paged_decode_merge", merge_wave_kernel<64, 8, kInline>, wgrid, wblock, 0, s, a, rs);
     else if (D == 32)
-        launch("paged_decode_merge", merge_wave_kernel<8, 4>, wgrid, block, 0, s, a);
+        launch("paged_decode_merge", merge_wave_kernel<8, 4, kInline>, wgrid, wblock, 0, s, a, rs);
     else if (D % 4 == 0 && D <= 256)
-        launch("paged_decode_merge", merge_kernel<4, 1, 8>, grid, block, 0, s, a);
+        launch("paged_decode_merge", merge_kernel<4, 1, 8, kInline>, grid, block, 0, s, a, rs);
     else if (D % 4 == 0)
-        launch("paged_decode_merge", merge_kernel<4, 2, 8>, grid, block, 0, s, a);
+        launch("paged_decode_merge", merge_kernel<4, 2, 8, kInline>, grid, block, 0, s, a, rs);
     else
-        launch("paged_decode_merge", merge_kernel<1, 8, 4>, grid, block, 0, s, a);
+        launch("paged_decode_merge", merge_kernel<1, 8, 4, kInline>, grid, block, 0, s, a, rs);
+}
+
+void launch_merge(const DecodeArgs& a, const RowSplits* inline_rows, int nrows, hipStream_t s) {
+    if (inline_rows && nrows <= kInlineRows)
+        launch_merge_t<true>(a, *inline_rows, nrows, s);
+    else
+        launch_merge_t<false>(a, RowSplits{}, nrows, s);
 }
 
 template <int D, int G, int LPT>
@@ -1255,7 +1266,8 @@ bool decode_fast_path(const DecodeArgs& a) {
            a.group <= (a.lay.head_dim == 64 ? 4 : 8);
 }
 
-void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, hipStream_t s) {
+void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
+                   hipStream_t s) {
     if (nitems <= 0) return;
     {
         bool done = false;
@@ -1271,7 +1283,7 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
         TVARA_HIP(hipGetLastError());
     }
     if (need_merge) {
-        launch_merge(a, nrows, s);
+        launch_merge(a, inline_rows, nrows, s);
         TVARA_HIP(hipGetLastError());
     }
 }

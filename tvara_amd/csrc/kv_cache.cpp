@@ -561,8 +561,11 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     // the decode kernels keep a split's block ids in one register per lane
     split = std::min(round_up(std::max<size_t>(split, 16), 16), kMaxSplitTokens);
     split_tokens = static_cast<int>(split);
-    std::vector<int4> ent(rows);
+    std::vector<int4> ent(rows), work;
     std::vector<int2> its;
+    std::vector<int32_t> work_ids;
+    const bool blocks16 = g.tokens_per_block == 16;
+    inline_ok = rows <= kInlineRows;
     need_merge = false;
     kv_bytes = 0;
     const double bytes_per_element = c->format() == kF32 ? 4.0 : 34.0 / 32.0;
@@ -570,9 +573,17 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
         const size_t n = cached[r];
         const int tail = tail_rows.empty() ? 0 : (tail_rows[r] ? 1 : 0);
         const int nsplit = static_cast<int>(std::max<size_t>(1, (n + split - 1) / split));
-        ent[r] = make_int4(offset[seq_of_row[r]], static_cast<int>(n), tail | (nsplit << 1),
-                           static_cast<int>(its.size()));
-        for (int s = 0; s < nsplit; ++s) its.push_back(make_int2(r, s));
+        const int first = static_cast<int>(its.size());
+        const int32_t base = offset[seq_of_row[r]];
+        ent[r] = make_int4(base, static_cast<int>(n), tail | (nsplit << 1), first);
+        if (inline_ok) inline_rows.r[r] = make_int2(first, nsplit);
+        for (int s = 0; s < nsplit; ++s) {
+            its.push_back(make_int2(r, s));
+            const int t0 = static_cast<int>(s * split), t1 = static_cast<int>(std::min(n, (s + 1) * split));
+            work.push_back(make_int4(r, t0, t1, ((tail && s == nsplit - 1) ? 1 : 0) | (nsplit > 1 ? 2 : 0)));
+            const int nb = blocks16 ? (t1 - t0 + 15) / 16 : 0;
+            for (int j = 0; j < kMaxSplitBlocks; ++j) work_ids.push_back(j < nb ? tab[base + t0 / 16 + j] : 0);
+        }
         need_merge |= nsplit > 1;
         kv_bytes += static_cast<size_t>(static_cast<double>(n + tail) * g.kv_width() * 2 * bytes_per_element);
     }
@@ -584,6 +595,8 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     put(tables, tab.data(), tab.size() * sizeof(int32_t));
     put(entries, ent.data(), ent.size() * sizeof(int4));
     put(items_buf, its.data(), its.size() * sizeof(int2));
+    put(work_buf, work.data(), work.size() * sizeof(int4));
+    put(work_blocks, work_ids.data(), work_ids.size() * sizeof(int32_t));
     if (need_merge) {
         part_acc.ensure(static_cast<size_t>(items) * heads * g.head_dim * sizeof(float));
         part_ml.ensure(static_cast<size_t>(items) * heads * 2 * sizeof(float));
@@ -608,6 +621,8 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.entries = static_cast<const int4*>(entries.ptr);
     a.items = static_cast<const int2*>(items_buf.ptr);
     a.split_tokens = split_tokens;
+    a.work = static_cast<const int4*>(work_buf.ptr);
+    a.work_blocks = static_cast<const int32_t*>(work_blocks.ptr);
     a.q = q;
     a.tail_k = tail_k;
     a.tail_v = tail_v;
@@ -616,7 +631,7 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.part_ml = static_cast<float*>(part_ml.ptr);
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
     a.err = static_cast<int*>(err.ptr);
-    launch_decode(a, items, rows, need_merge, s);
+    launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, s);
 }
 
 void AttnPlan::check() {

@@ -23,6 +23,7 @@
 #include <cstdlib>
 
 #include "common.hpp"
+#include "device_util.hpp"
 
 namespace tvara_amd {
 namespace {
@@ -43,18 +44,6 @@ __device__ __forceinline__ bf16x4 tr16_read(const __bf16* p) {
     typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
     const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
     return __builtin_bit_cast(bf16x4, v);
-}
-
-// max over lanes l%16 + 16r (the four 16-lane rows) in registers:
-// permlane32_swap(v, v) yields (low half, high half) of v in every lane,
-// permlane16_swap(v, v) yields (even row, odd row) of its pair
-__device__ __forceinline__ float cross_row_max(float v) {
-    const auto h = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
-                                                    false, false);
-    v = fmaxf(__builtin_bit_cast(float, h[0]), __builtin_bit_cast(float, h[1]));
-    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
-                                                    false, false);
-    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
 }
 
 __device__ __forceinline__ bf16x4 to_bf16(float4 v) {
