@@ -56,6 +56,30 @@ def test_batch_append_matches_sequential(device, oracle):
             assert np.array_equal(a.block_data(h), b.block_data(h))
 
 
+def test_batch_append_op_count_limits(device, oracle):
+    # batches of 400 appends pass their block ops in the kernel arguments, 401
+    # upload them; with one token per block every append also starts a block
+    g = (2, 2, 8, 1, 1700)
+    a, b = oracle.Cache(*g), device.PagedCache(*g)
+    w = 2 * 16
+    rng = np.random.default_rng(7)
+    for c in (a, b):
+        for _ in range(3):
+            c.create_sequence()
+    for n in (400, 401, 399, 401):
+        say("batch of", n)
+        seqs = [1 + i % 3 for i in range(n)]
+        k = rng.standard_normal((n, w)).astype(np.float32)
+        v = rng.standard_normal((n, w)).astype(np.float32)
+        a.append_batch(seqs, k, v)
+        b.append_batch(seqs, k, v)
+        assert a.state() == b.state()
+    for s in a.sequence_ids():
+        for layer in (0, 1):
+            assert np.array_equal(a.read_all(s, layer), b.read_all(s, layer))
+            assert np.array_equal(a.read_all(s, layer, True), b.read_all(s, layer, True))
+
+
 def test_batch_exhaustion_applies_prefix(device, oracle):
     # a batch that runs out of blocks keeps the appends before the failure, as
     # a loop over PagedCache::append would, and the failed one changes nothing

@@ -62,6 +62,17 @@ struct BlockInitOp {
     int64_t src;
 };
 
+// Block work passed in the kernel arguments (no upload) when a call has at
+// most kInlineOps of it: init ops as (dst, src or -1) int32 pairs, row ops as
+// (block, slot << 16 | input row) with slot and row below 65,536.
+constexpr int kInlineOps = 400;
+struct InlineInitOps {
+    int2 op[kInlineOps];
+};
+struct InlineRowOps {
+    int2 op[kInlineOps];
+};
+
 // One appended token: destination block, slot and the row of the input.
 struct RowOp {
     int32_t block;
@@ -126,6 +137,9 @@ struct PrefillArgs {
 
 // launchers (kernels.hip)
 void launch_block_init(char* pool, size_t stride, const BlockInitOp* ops, int n, hipStream_t s);
+void launch_block_init_inline(char* pool, size_t stride, const InlineInitOps& ops, int n, hipStream_t s);
+void launch_append_rows_inline(char* pool, const BlockLayout& lay, const InlineRowOps& ops, int n, const float* keys,
+                               const float* values, hipStream_t s);
 void launch_append_rows(char* pool, const BlockLayout& lay, const RowOp* ops, int n, const float* keys,
                         const float* values, hipStream_t s);
 void launch_gather_rows(const char* pool, const BlockLayout& lay, const int2* rows, int n, int layer, int kind,

@@ -375,7 +375,14 @@ size_t DeviceCache::append_batch(const uint64_t* seqs, size_t n, const float* ke
     }
     if (applied) {
         flush();
-        if (!init.empty()) {
+        // small batches pass their ops in the kernel arguments (no upload copy)
+        if (!init.empty() && init.size() <= static_cast<size_t>(kInlineOps) &&
+            g_.max_blocks <= static_cast<size_t>(std::numeric_limits<int32_t>::max())) {
+            InlineInitOps ops;
+            for (size_t i = 0; i < init.size(); ++i)
+                ops.op[i] = make_int2(static_cast<int>(init[i].dst), static_cast<int>(init[i].src));
+            launch_block_init_inline(pool_, lay_.stride, ops, static_cast<int>(init.size()), stream_);
+        } else if (!init.empty()) {
             auto* d = upload(*this, kInitOps, init.data(), init.size());
             launch_block_init(pool_, lay_.stride, d, static_cast<int>(init.size()), stream_);
         }
@@ -386,8 +393,17 @@ size_t DeviceCache::append_batch(const uint64_t* seqs, size_t n, const float* ke
             k = upload(*this, kKeys, keys, applied * w);
             v = upload(*this, kValues, values, applied * w);
         }
-        auto* d = upload(*this, kRowOps, rows.data(), rows.size());
-        launch_append_rows(pool_, lay_, d, static_cast<int>(rows.size()), k, v, stream_);
+        if (format_ == kF32 && rows.size() <= static_cast<size_t>(kInlineOps) && g_.tokens_per_block <= 32768 &&
+            applied <= 65536 && g_.kv_width() % 4 == 0 &&
+            lay_.stride / 16 <= static_cast<size_t>(std::numeric_limits<int32_t>::max())) {
+            InlineRowOps ops;
+            for (size_t i = 0; i < rows.size(); ++i)
+                ops.op[i] = make_int2(rows[i].block, (rows[i].slot << 16) | rows[i].src_row);
+            launch_append_rows_inline(pool_, lay_, ops, static_cast<int>(rows.size()), k, v, stream_);
+        } else {
+            auto* d = upload(*this, kRowOps, rows.data(), rows.size());
+            launch_append_rows(pool_, lay_, d, static_cast<int>(rows.size()), k, v, stream_);
+        }
     }
     if (applied_out) *applied_out = applied;
     if (failure) std::rethrow_exception(failure);

@@ -32,6 +32,57 @@ __global__ __launch_bounds__(kThreads) void block_init_kernel(char* pool, size_t
     }
 }
 
+// The same zero-fill / copy with the ops in the kernel arguments.
+__global__ __launch_bounds__(kThreads) void block_init_inline_kernel(char* pool, size_t stride, const InlineInitOps ops) {
+    const int2 op = ops.op[blockIdx.y];
+    uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<size_t>(op.x) * stride);
+    const size_t units = stride / 16;
+    const size_t step = static_cast<size_t>(gridDim.x) * blockDim.x;
+    if (op.y >= 0) {
+        const uint4* src = reinterpret_cast<const uint4*>(pool + static_cast<size_t>(op.y) * stride);
+        for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < units; i += step)
+            dst[i] = src[i];
+    } else {
+        const uint4 zero = make_uint4(0, 0, 0, 0);
+        for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < units; i += step)
+            dst[i] = zero;
+    }
+}
+
+// PagedCache::append row copies (kv.hpp:103-106) for f32 blocks with the ops
+// in the kernel arguments.  grid.x = op, grid.y = chunk of kAppendUnroll *
+// kThreads 16-byte units of the token's rows over every (layer, kind); each
+// thread requests all its units before storing the first.  Requires
+// kv_width % 4 == 0.
+constexpr int kAppendUnroll = 8;
+
+__global__ __launch_bounds__(kThreads) void append_rows_f32_inline_kernel(char* pool, BlockLayout lay,
+                                                                          const InlineRowOps ops,
+                                                                          const float* __restrict__ keys,
+                                                                          const float* __restrict__ values) {
+    const int2 op = ops.op[blockIdx.x];
+    const int slot = op.y >> 16, src_row = op.y & 0xffff;
+    const int row4 = lay.kv_width / 4;  // 16-byte units per (layer, kind) row
+    const int units = lay.layers * 2 * row4;
+    const float4* krow = reinterpret_cast<const float4*>(keys + static_cast<size_t>(src_row) * lay.layers * lay.kv_width);
+    const float4* vrow = reinterpret_cast<const float4*>(values + static_cast<size_t>(src_row) * lay.layers * lay.kv_width);
+    float4* block = reinterpret_cast<float4*>(pool + static_cast<size_t>(op.x) * lay.stride);
+    const int u0 = blockIdx.y * (kAppendUnroll * kThreads) + threadIdx.x;
+    float4 x[kAppendUnroll];
+    int dst[kAppendUnroll];
+#pragma unroll
+    for (int j = 0; j < kAppendUnroll; ++j) {
+        const int u = min(u0 + j * kThreads, units - 1);  // clamped: every load is issued
+        const int r = u / row4, c4 = u - r * row4;        // r = layer * 2 + kind
+        const int src = (r >> 1) * row4 + c4;
+        x[j] = (r & 1) ? vrow[src] : krow[src];
+        dst[j] = (r * lay.tpb + slot) * row4 + c4;
+    }
+#pragma unroll
+    for (int j = 0; j < kAppendUnroll; ++j)
+        if (u0 + j * kThreads < units) block[dst[j]] = x[j];
+}
+
 // PagedCache::append row copies (kv.hpp:103-106): grid.x = layer*2+kind,
 // grid.y = op.  Source rows are [src_row][layers][kv_width].
 __global__ __launch_bounds__(kThreads) void append_rows_f32_kernel(char* pool, BlockLayout lay,
@@ -209,6 +260,24 @@ void launch_block_init(char* pool, size_t stride, const BlockInitOp* ops, int n,
         const int count = std::min(kMaxGridY, n - base);
         launch("kv_block_init", block_init_kernel, dim3(gx, count), dim3(kThreads), 0, s, pool, stride, ops + base);
     }
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_block_init_inline(char* pool, size_t stride, const InlineInitOps& ops, int n, hipStream_t s) {
+    if (n <= 0) return;
+    const size_t units = stride / 16;
+    const unsigned gx = static_cast<unsigned>(std::min<size_t>((units + kThreads - 1) / kThreads, 512));
+    launch("kv_block_init", block_init_inline_kernel, dim3(gx, n), dim3(kThreads), 0, s, pool, stride, ops);
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_append_rows_inline(char* pool, const BlockLayout& lay, const InlineRowOps& ops, int n, const float* keys,
+                               const float* values, hipStream_t s) {
+    if (n <= 0) return;
+    const int units = lay.layers * 2 * (lay.kv_width / 4);
+    const int chunks = (units + kAppendUnroll * kThreads - 1) / (kAppendUnroll * kThreads);
+    launch("kv_append_rows", append_rows_f32_inline_kernel, dim3(n, chunks), dim3(kThreads), 0, s, pool, lay, ops,
+           keys, values);
     TVARA_HIP(hipGetLastError());
 }
 
