@@ -65,11 +65,12 @@ def build(device, oracle, heads, kv_heads, dim, specs, seed, tpb=16):
     return dev, ref, ds, rs, qs
 
 
+@pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
-def test_bf16_small_shapes(device, oracle, group):
-    heads, kv_heads, dim = 2 * group, 2, 64
+def test_bf16_small_shapes(device, oracle, group, dim):
+    heads, kv_heads = 2 * group, 2
     specs = [(137, 100, 37), (64, 0, 64), (20, 3, 17)]
-    say("prefill bf16 group", group)
+    say("prefill bf16 group", group, "dim", dim)
     dev, ref, ds, rs, qs = build(device, oracle, heads, kv_heads, dim, specs, seed=group)
     starts = [s for _, s, _ in specs]
     counts = [r for _, _, r in specs]
@@ -82,8 +83,9 @@ def test_bf16_small_shapes(device, oracle, group):
     assert ok, err
 
 
-def test_bf16_c4_shape(device, oracle):
-    w = workloads.prefill_c4()
+@pytest.mark.parametrize("make", [workloads.prefill_c4, workloads.prefill_8b], ids=["d64", "d128"])
+def test_bf16_c4_shape(device, oracle, make):
+    w = make()
     say("prefill", w.name)
     g = (1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks())
     dev, ref = device.PagedCache(*g), oracle.Cache(*g)
@@ -147,15 +149,16 @@ def test_prefill_plan_matches_call(device, oracle, precision):
         plan.launch(0, dq.ptr, out.ptr)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("group", [1, 4])
-def test_bf16_nan_poisoned_unused_slots(device, oracle, group):
+def test_bf16_nan_poisoned_unused_slots(device, oracle, group, dim):
     # prefill_t174.cpp for the MFMA path: NaN in the unused slots of the last
     # block (past the cached length, inside the last 64-key tile) never reaches
     # a row; chunks that end at the cache end, 16-key boundaries and mid-block
-    heads, kv_heads, dim = 2 * group, 2, 64
+    heads, kv_heads = 2 * group, 2
     w = kv_heads * dim
     for n, rows in [(137, 37), (33, 33), (80, 16), (1, 1)]:
-        say("prefill bf16 poison", group, n, rows)
+        say("prefill bf16 poison", group, dim, n, rows)
         dev = device.PagedCache(1, kv_heads, dim, 16, n // 16 + 3)
         ref = oracle.Cache(1, kv_heads, dim, 16, n // 16 + 3)
         k = synth.normal(21, "k", n * w).reshape(n, w)
@@ -176,12 +179,12 @@ def test_bf16_nan_poisoned_unused_slots(device, oracle, group):
 
 
 def test_bf16_rejections(device):
-    dev = device.PagedCache(1, 2, 128, 16, 8)
+    dev = device.PagedCache(1, 2, 32, 16, 8)
     s = dev.create_sequence()
-    x = synth.normal(1, "x", 20 * 256).reshape(20, 256)
+    x = synth.normal(1, "x", 20 * 64).reshape(20, 64)
     dev.append_many(s, x, x)
-    q = synth.normal(1, "q", 4 * 4 * 128)
-    with pytest.raises(device.InvalidArgument):  # head_dim 128 has no bf16 tile kernel yet
+    q = synth.normal(1, "q", 4 * 4 * 32)
+    with pytest.raises(device.InvalidArgument):  # bf16 tile kernels cover head_dim 64 and 128
         attention.prefill_batch(dev, q, [s], [10], [4], 0, 4, 64, precision="bf16")
     dev = device.PagedCache(1, 2, 64, 16, 8)
     s = dev.create_sequence()

@@ -51,6 +51,11 @@ __device__ __forceinline__ bf16x4 to_bf16(float4 v) {
     return __builtin_convertvector(f, bf16x4);
 }
 
+__device__ __forceinline__ bf16x4 to_bf16(f32x4 v) { return __builtin_convertvector(v, bf16x4); }
+
+// word 3 of a raw buffer descriptor (32-bit data format, no swizzle)
+constexpr int kBufferWord3 = 0x00020000;
+
 template <int D, int G, int kWaves>
 __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const PrefillArgs a) {
     constexpr int PW = kRows / G;        // chunk positions per wave
@@ -59,9 +64,11 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     constexpr int DT = D / 16;           // output column tiles
     constexpr int KSTR = D + 8;          // LDS row pitch of K (bf16): 144 B, conflict-free b128 operand reads
     constexpr int VSTR = D + 16;         // LDS row pitch of V (bf16): 160 B, conflict-free transposing reads
-    static_assert(D == 64, "the staging map covers 64 columns");
-    constexpr int SP = kKeys * 16 / (64 * kWaves);  // staging passes per tile (16 lanes per key row)
-    static_assert(SP >= 1 && SP * 64 * kWaves == kKeys * 16, "the staging map covers whole key rows");
+    static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+    constexpr int LPR = D / 4;                // staging lanes per key row (4 columns each)
+    constexpr int KPP = 64 * kWaves / LPR;    // keys per staging pass
+    constexpr int SP = kKeys / KPP;           // staging passes per tile
+    static_assert(SP >= 1 && SP * KPP == kKeys, "the staging map covers whole key rows");
     __shared__ __attribute__((aligned(16))) __bf16 klds[2][kKeys * KSTR];
     __shared__ __attribute__((aligned(16))) __bf16 vlds[2][kKeys * VSTR];
 
@@ -84,8 +91,6 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     const int wave_kmax = pw0 < nrows ? start + min(pw0 + PW, nrows) : 0;
     const int kvw = a.lay.kv_width;
     const int32_t* tab = a.tables + sd.x;
-    const float* pool = reinterpret_cast<const float*>(a.pool);
-    const size_t bstride = a.lay.stride / sizeof(float);
     const size_t koff = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D;
     const size_t voff = koff + 16 * static_cast<size_t>(kvw);
 
@@ -109,43 +114,60 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
         }
     }
 
-    // staging map: 16 lanes per key row (4 columns each), 4 * kWaves keys per
-    // pass, SP passes per 64-key tile; a wave's four rows lie in one paged block
-    // (the block ids are loaded one tile ahead of the K/V rows, so no wave
-    // waits on a table lookup before issuing its loads)
-    constexpr int KPP = 4 * kWaves;  // keys per staging pass
-    const int skey = tid >> 4, col = 4 * (tid & 15);
-    float4 kA[SP], vA[SP], kB[SP], vB[SP];  // two register stages (even / odd tiles)
-    int bA[SP], bB[SP];
-    // Every load is unconditional (a key past the chunk's reach reads the last
-    // reachable key): a load under a branch makes the compiler wait for all
+    // staging map: D/4 lanes per key row (4 columns each), KPP keys per pass,
+    // SP passes per 64-key tile.  A wave's rows in a pass are 64/LPR aligned
+    // consecutive keys, so they lie in one paged block: the block id and base
+    // address are wave-uniform (scalar registers) and a lane's offset within
+    // the block depends only on its row and the pass.  The block ids are loaded
+    // two tiles ahead of the K/V rows, so no wave waits on a table lookup
+    // before issuing its loads.
+    const int skey = tid / LPR, col = 4 * (tid % LPR);
+    const int wkey = __builtin_amdgcn_readfirstlane(skey);  // the wave's first row in a pass
+    auto roff = [&](int p) {  // byte offset of the lane's K (or V) columns within the block's section
+        return static_cast<unsigned>((((KPP * p + skey) & 15) * kvw + col) * sizeof(float));
+    };
+    // K/V rows are read through a buffer descriptor per block (base = the
+    // block's K section of this layer and head, 32-bit lane offsets, reads
+    // bounded by the block's end)
+    const size_t kbytes = koff * sizeof(float);
+    const int vsec = static_cast<int>((voff - koff) * sizeof(float));
+    const int brange = static_cast<int>(a.lay.stride - kbytes);
+    // register stages of K/V rows in flight: two (even / odd tiles) at head_dim
+    // 64, one at 128, where two would not fit beside the accumulators
+    constexpr int kStages = D == 64 ? 2 : 1;
+    f32x4 kA[SP], vA[SP], kB[kStages == 2 ? SP : 1], vB[kStages == 2 ? SP : 1];
+    int bA[SP], bB[kStages == 2 ? SP : 1];
+    // Every load is unconditional: rows of a pass past the chunk's reach read
+    // the last reachable block (any slot of it: in bounds, possibly stale or
+    // never written).  A load under a branch makes the compiler wait for all
     // outstanding loads where the branches join.  Such keys lie past every
     // row's causal limit, so their scores are masked; their V rows are zeroed
     // when staged, so a non-finite value there cannot reach a row as 0 * NaN.
     auto tabload = [&](int kt, int (&b)[SP]) {
 #pragma unroll
-        for (int p = 0; p < SP; ++p) {
-            const int key = min(kt * kKeys + KPP * p + skey, kmax - 1);
-            b[p] = tab[key >> 4];
-        }
+        for (int p = 0; p < SP; ++p) b[p] = tab[min(kt * kKeys + KPP * p + wkey, kmax - 1) >> 4];
     };
-    auto gload = [&](int kt, const int (&b)[SP], float4 (&kreg)[SP], float4 (&vreg)[SP]) {
+    auto gload = [&](int kt, const int (&b)[SP], f32x4 (&kreg)[SP], f32x4 (&vreg)[SP]) {
 #pragma unroll
         for (int p = 0; p < SP; ++p) {
-            const int key = kt * kKeys + KPP * p + skey;
-            const float* base = pool + static_cast<size_t>(b[p]) * bstride +
-                                static_cast<size_t>(min(key, kmax - 1) & 15) * kvw + col;
-            kreg[p] = *reinterpret_cast<const float4*>(base + koff);
-            vreg[p] = *reinterpret_cast<const float4*>(base + voff);
+            const char* blk =
+                a.pool + static_cast<size_t>(__builtin_amdgcn_readfirstlane(b[p])) * a.lay.stride + kbytes;
+            const __amdgpu_buffer_rsrc_t r =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(blk), 0, brange, kBufferWord3);
+            kreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff(p), 0, 0);
+            vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff(p), vsec, 0);
         }
     };
-    auto lstore = [&](int kt, int buf, const float4 (&kreg)[SP], const float4 (&vreg)[SP]) {
+    auto lstore = [&](int kt, int buf, const f32x4 (&kreg)[SP], f32x4 (&vreg)[SP]) {
+        if (kt * kKeys + kKeys > kmax) {  // the chunk's last tile: zero V past its reach
+#pragma unroll
+            for (int p = 0; p < SP; ++p)
+                if (kt * kKeys + KPP * p + skey >= kmax) vreg[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
         for (int p = 0; p < SP; ++p) {
-            const bool ok = kt * kKeys + KPP * p + skey < kmax;
             *reinterpret_cast<bf16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = to_bf16(kreg[p]);
-            *reinterpret_cast<bf16x4*>(&vlds[buf][(KPP * p + skey) * VSTR + col]) =
-                to_bf16(ok ? vreg[p] : make_float4(0.f, 0.f, 0.f, 0.f));
+            *reinterpret_cast<bf16x4*>(&vlds[buf][(KPP * p + skey) * VSTR + col]) = to_bf16(vreg[p]);
         }
     };
 
@@ -275,26 +297,42 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
         }
     };
     auto tile = [&](int t) { return min(t, ntiles - 1); };
-    tabload(0, bA);
-    gload(0, bA, kA, vA);
-    tabload(tile(1), bB);
-    gload(tile(1), bB, kB, vB);
-    tabload(tile(2), bA);
-    tabload(tile(3), bB);
-    lstore(0, 0, kA, vA);
-    __syncthreads();
-    for (int kt = 0; kt < ntiles; kt += 2) {
-        gload(tile(kt + 2), bA, kA, vA);
-        tabload(tile(kt + 4), bA);
-        compute(kt, 0);
-        lstore(tile(kt + 1), 1, kB, vB);
+    if constexpr (kStages == 2) {
+        tabload(0, bA);
+        gload(0, bA, kA, vA);
+        tabload(tile(1), bB);
+        gload(tile(1), bB, kB, vB);
+        tabload(tile(2), bA);
+        tabload(tile(3), bB);
+        lstore(0, 0, kA, vA);
         __syncthreads();
-        if (kt + 1 >= ntiles) break;
-        gload(tile(kt + 3), bB, kB, vB);
-        tabload(tile(kt + 5), bB);
-        compute(kt + 1, 1);
-        lstore(tile(kt + 2), 0, kA, vA);
+        for (int kt = 0; kt < ntiles; kt += 2) {
+            gload(tile(kt + 2), bA, kA, vA);
+            tabload(tile(kt + 4), bA);
+            compute(kt, 0);
+            lstore(tile(kt + 1), 1, kB, vB);
+            __syncthreads();
+            if (kt + 1 >= ntiles) break;
+            gload(tile(kt + 3), bB, kB, vB);
+            tabload(tile(kt + 5), bB);
+            compute(kt + 1, 1);
+            lstore(tile(kt + 2), 0, kA, vA);
+            __syncthreads();
+        }
+    } else {
+        // one register stage: tile t + 1 is requested before tile t's products
+        tabload(0, bA);
+        gload(0, bA, kA, vA);
+        tabload(tile(1), bA);
+        lstore(0, 0, kA, vA);
         __syncthreads();
+        for (int kt = 0; kt < ntiles; ++kt) {
+            gload(tile(kt + 1), bA, kA, vA);
+            tabload(tile(kt + 2), bA);
+            compute(kt, kt & 1);
+            lstore(tile(kt + 1), (kt + 1) & 1, kA, vA);
+            __syncthreads();
+        }
     }
 
     bool bad = false;
@@ -319,14 +357,14 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 // eight waves per workgroup (measured on MI355X against four: 158 against 225
 // us on the 8 x (2,048 + 512) chunk; K/V tiles are re-read by half as many
 // workgroups) and 64-key tiles (128-key tiles measured 177 us)
-template <int G, int W>
+template <int D, int G, int W>
 void launch_gw(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     constexpr int QT = W * (kRows / G);
     PrefillArgs b = a;
     b.chunk_tiles = (max_rows + QT - 1) / QT;
     b.pairs = nseqs * a.lay.kv_heads;
     const int groups8 = (b.pairs + 7) / 8;  // ids = 8 XCDs x pair groups x chunk tiles
-    launch("paged_prefill_bf16", prefill_bf16_kernel<64, G, W>, dim3(8 * groups8 * b.chunk_tiles), dim3(64 * W), 0, s,
+    launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W>, dim3(8 * groups8 * b.chunk_tiles), dim3(64 * W), 0, s,
            b);
 }
 
@@ -337,22 +375,24 @@ void launch_g(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
         const char* env = std::getenv("TVARA_PREFILL_WAVES");
         return env && std::atoi(env) == 4 ? 4 : 8;
     }();
-    if (waves == 4)
-        launch_gw<G, 4>(a, nseqs, max_rows, s);
+    if (a.lay.head_dim == 128)
+        waves == 4 ? launch_gw<128, G, 4>(a, nseqs, max_rows, s) : launch_gw<128, G, 8>(a, nseqs, max_rows, s);
     else
-        launch_gw<G, 8>(a, nseqs, max_rows, s);
+        waves == 4 ? launch_gw<64, G, 4>(a, nseqs, max_rows, s) : launch_gw<64, G, 8>(a, nseqs, max_rows, s);
 }
 
 }  // namespace
 
 bool prefill_bf16_supported(const BlockLayout& lay, int group) {
-    return lay.format == kF32 && lay.tpb == 16 && lay.head_dim == 64 &&
-           (group == 1 || group == 2 || group == 4 || group == 8);
+    // the staging reads take 32-bit offsets within a block
+    return lay.format == kF32 && lay.tpb == 16 && (lay.head_dim == 64 || lay.head_dim == 128) &&
+           lay.stride < (size_t(1) << 31) && (group == 1 || group == 2 || group == 4 || group == 8);
 }
 
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     if (!prefill_bf16_supported(a.lay, a.group))
-        throw std::invalid_argument("bf16 prefill needs f32 blocks of 16 tokens, head_dim 64, GQA group 1/2/4/8");
+        throw std::invalid_argument(
+            "bf16 prefill needs f32 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, GQA group 1/2/4/8");
     if (nseqs <= 0 || max_rows <= 0) return;
     switch (a.group) {
         case 1: launch_g<1>(a, nseqs, max_rows, s); break;

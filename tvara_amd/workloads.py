@@ -172,6 +172,11 @@ def prefill_c4(**kw):
     return PrefillWorkload("llama-3.2-1b-chunked-prefill-8x(2048+512)", **kw)
 
 
+def prefill_8b(**kw):
+    """The same chunks at Llama-3-8B's attention shape (32/8 heads, d=128)."""
+    return PrefillWorkload("llama-3-8b-chunked-prefill-8x(2048+512)", head_dim=128, **kw)
+
+
 def fill_prefill(cache, w: PrefillWorkload):
     seqs = []
     for i in range(w.sequences):
