@@ -357,3 +357,54 @@ def test_prompt_chunk_f32(device, oracle):
     assert np.array_equal(attention.fused_prompt_attention(qs, dev, sd, 0, 11, 13, 4, 128), got)
     with pytest.raises(device.InvalidArgument):
         attention.fused_prompt_attention(qs, dev, sd, 0, 30, 13, 4, 128)
+
+
+@pytest.mark.parametrize("split", [0, 1024], ids=["merge-launch", "merge-in-kernel"])
+@pytest.mark.parametrize("fmt_name,dim,kv_heads,group", [("F32", 64, 8, 4), ("F32", 128, 4, 8), ("Q8_0", 128, 2, 8)])
+def test_plan_back_to_back_launches(device, oracle, monkeypatch, fmt_name, dim, kv_heads, group, split):
+    # rows of several splits: with the default split the launch fills the GPU
+    # and merge_kernel combines them; 1,024-token splits give a launch of a few
+    # dozen workgroups, where the last workgroup of each row merges (it counts
+    # the row's finished splits and resets the count).  48 launches queued
+    # without a wait, alternating two layers, all equal the first launch of
+    # their layer byte for byte and match the oracle
+    from tvara_amd import hip
+
+    if split:
+        monkeypatch.setenv("TVARA_SPLIT_TOKENS", str(split))
+
+    fmt = getattr(device, fmt_name)
+    heads, layers, tpb = kv_heads * group, 2, 16
+    lengths = [97, 3000, 640, 1, 2049, 1500, 4096, 33, 800, 2500, 16, 1234]
+    g = (layers, kv_heads, dim, tpb, sum((n + tpb - 1) // tpb for n in lengths) + 4)
+    dev, ref = device.PagedCache(*g, fmt=fmt), oracle.Cache(*g)
+    w = layers * kv_heads * dim
+    seqs = []
+    for i, n in enumerate(lengths):
+        k = synth.normal(31, f"k{i}", n * w).reshape(n, w)
+        v = synth.normal(31, f"v{i}", n * w).reshape(n, w)
+        if fmt_name == "Q8_0":
+            k = oracle.dequantize_q8_0(oracle.quantize_q8_0(k)).reshape(n, w)
+            v = oracle.dequantize_q8_0(oracle.quantize_q8_0(v)).reshape(n, w)
+        s, r = dev.create_sequence(), ref.create_sequence()
+        dev.append_many(s, k, v)
+        ref.append_many(r, k, v)
+        assert s == r
+        seqs.append(s)
+    q = synth.normal(31, "q", len(lengths) * heads * dim).reshape(len(lengths), heads * dim)
+    plan = attention.DecodePlan(dev, seqs, heads, 1 << 20)
+    assert plan.items > len(lengths)  # some rows have several splits
+    assert (plan.items < 64) == bool(split)
+    say("back-to-back", fmt_name, dim, kv_heads, group, "split", plan.split_tokens, "items", plan.items)
+    dq = hip.DeviceArray.from_numpy(q)
+    outs = [hip.DeviceArray(q.shape) for _ in range(48)]
+    for i, o in enumerate(outs):
+        plan.launch(i % 2, dq.ptr, o.ptr)
+    plan.check()
+    got = [o.numpy() for o in outs]
+    for i in range(2, len(got)):
+        assert np.array_equal(got[i], got[i % 2]), i
+    # Q8_0 blocks hold exactly the oracle's dequantised values, so both formats meet the f32 bar
+    for layer in (0, 1):
+        want = np.stack([ref.fused_paged_attention(q[i], s, layer, heads, 1 << 20) for i, s in enumerate(seqs)])
+        assert refmath.close(got[layer], want, TOL), refmath.max_rel(got[layer], want)

@@ -106,10 +106,14 @@ struct DecodeArgs {
     const int2* items;    // x: row, y: split index
     int split_tokens;
     // 16-token blocks: per work item x: row, y: first token, z: end token,
-    // w: tail (the row's uncommitted token is this item's last) | several splits << 1;
+    // w: tail (the row's uncommitted token is this item's last) | the row's splits << 1;
     // and the item's block ids, kMaxSplitBlocks per item
     const int4* work;
     const int32_t* work_blocks;
+    // per (row, KV-head group of a workgroup): splits finished in this launch,
+    // for kernels that merge a row's splits in its last workgroup (zero between
+    // launches; null: merge_kernel merges)
+    int* row_done;
     const float* q;
     const float* tail_k;  // [rows][kv_width] or null
     const float* tail_v;

@@ -145,9 +145,67 @@ __device__ __forceinline__ float token_group_sum(float v) {
 // writes back the XCD's L2 and they serialise, which costs far more than a
 // second launch.)  `col(c, e4)` is the head-local column of lane slot c's
 // e4-th float4.
+// The last workgroup of a row's splits merges them (a.row_done set).  Each
+// workgroup stores its partials with agent-scope relaxed atomic stores (they
+// reach the point of coherence shared by the XCDs' L2s), waits for them, and
+// counts its split with an agent-scope atomic; the workgroup that completes
+// the count reads every partial with agent-scope loads, combines them in
+// split order (the result does not depend on which workgroup finished last)
+// and resets the counter for the next launch.  No release fence is needed, so
+// no XCD's L2 is written back (a device-scope release per workgroup cost more
+// than a second launch).  Launches that share a plan must not overlap.
+template <int D, int G>
+__device__ __forceinline__ void merge_row_splits(const DecodeArgs& a, int lane, int kh, int first, int row,
+                                                 int nsplit) {
+    constexpr int U = 8;  // splits requested together
+    const size_t head0 = static_cast<size_t>(kh) * G;
+    float* out = a.out + (static_cast<size_t>(row) * a.heads + head0) * D;
+    auto ld = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    for (int o4 = lane; o4 < G * D / 4; o4 += 64) {
+        const int h = (4 * o4) / D;
+        float M = -INFINITY, L = 0.f;
+        float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s0 = 0; s0 < nsplit; s0 += U) {
+            float m[U], l[U];
+            float4 x[U];
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                const size_t it = static_cast<size_t>(first + min(s0 + k, nsplit - 1));
+                const float* ml = a.part_ml + (it * a.heads + head0 + h) * 2;
+                const float* pa = a.part_acc + (it * a.heads + head0) * D + 4 * o4;
+                m[k] = ld(ml);
+                l[k] = ld(ml + 1);
+                x[k] = make_float4(ld(pa), ld(pa + 1), ld(pa + 2), ld(pa + 3));
+            }
+            float mc = M;
+#pragma unroll
+            for (int k = 0; k < U; ++k)
+                if (s0 + k < nsplit) mc = fmaxf(mc, m[k]);
+            const float sc = M == -INFINITY ? 0.f : fast_exp2(M - mc);
+            L *= sc;
+            sum.x *= sc;
+            sum.y *= sc;
+            sum.z *= sc;
+            sum.w *= sc;
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                const float w = s0 + k < nsplit ? fast_exp2(m[k] - mc) : 0.f;
+                L = fmaf(w, l[k], L);
+                sum.x = fmaf(w, x[k].x, sum.x);
+                sum.y = fmaf(w, x[k].y, sum.y);
+                sum.z = fmaf(w, x[k].z, sum.z);
+                sum.w = fmaf(w, x[k].w, sum.w);
+            }
+            M = mc;
+        }
+        const float inv = 1.f / L;
+        *reinterpret_cast<float4*>(out + 4 * o4) = make_float4(sum.x * inv, sum.y * inv, sum.z * inv, sum.w * inv);
+    }
+}
+
 template <int D, int G, int LPT, int E, class Col>
 __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G][E], RowState& st, int lane, int wave,
-                                             int nwaves, int kh, int item, int row, int nsplit, Col col) {
+                                             int nwaves, int kh, int item, int first, int row, int nsplit, Col col) {
     extern __shared__ float lds[];
     const int c = lane & (LPT - 1);
     st.l = wave_sum_across(st.l, LPT);
@@ -193,16 +251,36 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
         if (nsplit == 1) {
             const float l = ml[G + (4 * o4) / D];
             *reinterpret_cast<float4*>(out + 4 * o4) = make_float4(sum.x / l, sum.y / l, sum.z / l, sum.w / l);
+        } else if (a.row_done) {
+            float* p = a.part_acc + (static_cast<size_t>(item) * a.heads + head0) * D + 4 * o4;
+            __hip_atomic_store(p, sum.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p + 1, sum.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p + 2, sum.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p + 3, sum.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
             *reinterpret_cast<float4*>(a.part_acc + (static_cast<size_t>(item) * a.heads + head0) * D + 4 * o4) = sum;
         }
     }
     if (nsplit > 1 && lane < G) {
         float* o = a.part_ml + (static_cast<size_t>(item) * a.heads + head0 + lane) * 2;
-        o[0] = ml[lane];
-        o[1] = ml[G + lane];
+        __hip_atomic_store(o, ml[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(o + 1, ml[G + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (__any(st.bad) && lane == 0) *a.err = 1;
+    if (nsplit > 1 && a.row_done) {
+        __shared__ int last;
+        // every wave's partial stores complete before the count moves
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int* done = a.row_done + static_cast<size_t>(row) * (a.lay.kv_heads / nwaves) + kh / nwaves;
+            const int prev = __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = prev == nsplit - 1;
+            if (last) __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (last) merge_row_splits<D, G>(a, lane, kh, first, row, nsplit);
+    }
 }
 
 // ------------------------------------------------------------- f32 blocks
@@ -215,9 +293,9 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
     const int item = static_cast<int>(blockIdx.x) / groups;
     const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
     // the item's descriptor and block ids come in two independent loads
-    const int4 it = a.work[item];  // row, first token, end token, tail | several splits << 1
+    const int4 it = a.work[item];  // row, first token, end token, tail | splits << 1
     const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
-    const int nsplit = (it.w & 2) ? 2 : 1;  // the finish only tells one split from several
+    const int nsplit = it.w >> 1;
     const bool tail = (it.w & 1) != 0;
     const int t0 = it.y, t1 = it.z;
     const int c = lane & (LPT - 1), tg = lane / LPT;
@@ -337,7 +415,7 @@ __global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
         }
         process(ka, va, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, item - t0 / a.split_tokens, it.x, nsplit,
                                [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
 }
 
@@ -364,9 +442,9 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
     const int item = static_cast<int>(blockIdx.x) / groups;
     const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
     // the item's descriptor and block ids come in two independent loads
-    const int4 it = a.work[item];  // row, first token, end token, tail | several splits << 1
+    const int4 it = a.work[item];  // row, first token, end token, tail | splits << 1
     const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
-    const int nsplit = (it.w & 2) ? 2 : 1;  // the finish only tells one split from several
+    const int nsplit = it.w >> 1;
     const bool tail = (it.w & 1) != 0;
     const int t0 = it.y, t1 = it.z;
     const int c = lane & (LPT - 1), tg = lane / LPT;
@@ -489,7 +567,7 @@ __global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
         }
         process_f(kf, 1.f, vf, 1.f, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, it.x, nsplit,
+    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, item - t0 / a.split_tokens, it.x, nsplit,
                                [](int cc, int e4) { return 16 * cc + 4 * e4; });
 }
 
@@ -560,9 +638,9 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
     const int item = static_cast<int>(blockIdx.x) / groups;
     const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
     // the item's descriptor and block ids come in two independent loads
-    const int4 it = a.work[item];  // row, first token, end token, tail | several splits << 1
+    const int4 it = a.work[item];  // row, first token, end token, tail | splits << 1
     const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
-    const int nsplit = (it.w & 2) ? 2 : 1;  // the finish only tells one split from several
+    const int nsplit = it.w >> 1;
     const bool tail = (it.w & 1) != 0;
     const int t0 = it.y, t1 = it.z;
     const int n = max(t1 - t0, 0);
@@ -1261,6 +1339,10 @@ static int waves_for(const DecodeArgs& a) {
     return decode_waves(a.lay.kv_heads, a.group, a.lay.format, a.lay.head_dim);
 }
 
+// the largest decode launch whose splits are merged in the kernel
+// (TVARA_INKERNEL_MERGE_MAX overrides it for tuning)
+constexpr int kInKernelMergeMaxWorkgroups = 128;
+
 bool decode_fast_path(const DecodeArgs& a) {
     return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128) &&
            a.group <= (a.lay.head_dim == 64 ? 4 : 8);
@@ -1269,21 +1351,41 @@ bool decode_fast_path(const DecodeArgs& a) {
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
                    hipStream_t s) {
     if (nitems <= 0) return;
+    // Small launches of the f32 and vector Q8_0 kernels merge a row's splits
+    // in its last workgroup: there the second launch is pure latency (the
+    // SmolLM2-135M row: 7.7 against 8.3 us per step).  A launch that fills
+    // the GPU keeps merge_kernel: every workgroup waiting for its partials to
+    // reach the point of coherence and for its count costs more than the
+    // launch (the Llama-3.2-1B batch of 253 workgroups: 105.5 against 102.8 us).
+    // The int8-MFMA Q8_0 and generic kernels always leave it to merge_kernel.
+    const bool fast = decode_fast_path(a);
+    const int wgs = fast ? nitems * (a.lay.kv_heads / waves_for(a)) : nitems * a.heads;
+    static const int max_wgs = [] {
+        const char* env = std::getenv("TVARA_INKERNEL_MERGE_MAX");
+        return env ? std::atoi(env) : kInKernelMergeMaxWorkgroups;
+    }();
+    const bool in_kernel =
+        fast && a.row_done && !(a.lay.format != kF32 && q8_mma_enabled(a.group)) && wgs <= max_wgs;
+    DecodeArgs b = a;
+    if (!in_kernel) b.row_done = nullptr;
+    bool merged = false;
     {
         bool done = false;
-        if (decode_fast_path(a)) {
-            const int waves = waves_for(a);
-            done = a.lay.head_dim == 64 ? dispatch_fast<64>(a, nitems, waves, s)
-                                        : dispatch_fast<128>(a, nitems, waves, s);
+        if (fast) {
+            const int waves = waves_for(b);
+            done = b.lay.head_dim == 64 ? dispatch_fast<64>(b, nitems, waves, s)
+                                        : dispatch_fast<128>(b, nitems, waves, s);
         }
         if (!done) {
-            if (a.lay.head_dim > kGenericMaxDim) throw std::invalid_argument("head_dim above 512 is not supported");
-            launch("paged_decode", decode_generic_kernel, dim3(nitems, a.heads), dim3(64), 0, s, a);
+            if (b.lay.head_dim > kGenericMaxDim) throw std::invalid_argument("head_dim above 512 is not supported");
+            b.row_done = nullptr;
+            launch("paged_decode", decode_generic_kernel, dim3(nitems, b.heads), dim3(64), 0, s, b);
         }
         TVARA_HIP(hipGetLastError());
+        merged = done && in_kernel;
     }
-    if (need_merge) {
-        launch_merge(a, inline_rows, nrows, s);
+    if (need_merge && !merged) {
+        launch_merge(b, inline_rows, nrows, s);
         TVARA_HIP(hipGetLastError());
     }
 }

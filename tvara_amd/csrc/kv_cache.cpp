@@ -596,7 +596,7 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
         for (int s = 0; s < nsplit; ++s) {
             its.push_back(make_int2(r, s));
             const int t0 = static_cast<int>(s * split), t1 = static_cast<int>(std::min(n, (s + 1) * split));
-            work.push_back(make_int4(r, t0, t1, ((tail && s == nsplit - 1) ? 1 : 0) | (nsplit > 1 ? 2 : 0)));
+            work.push_back(make_int4(r, t0, t1, ((tail && s == nsplit - 1) ? 1 : 0) | (nsplit << 1)));
             const int nb = blocks16 ? (t1 - t0 + 15) / 16 : 0;
             for (int j = 0; j < kMaxSplitBlocks; ++j) work_ids.push_back(j < nb ? tab[base + t0 / 16 + j] : 0);
         }
@@ -616,6 +616,10 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     if (need_merge) {
         part_acc.ensure(static_cast<size_t>(items) * heads * g.head_dim * sizeof(float));
         part_ml.ensure(static_cast<size_t>(items) * heads * 2 * sizeof(float));
+        // split counters of the in-kernel merge, one per (row, KV head) at most
+        const size_t bytes = static_cast<size_t>(rows) * g.kv_heads * sizeof(int);
+        row_done.ensure(bytes);
+        TVARA_HIP(hipMemset(row_done.ptr, 0, bytes));
     }
     err.ensure(sizeof(int));
     TVARA_HIP(hipMemset(err.ptr, 0, sizeof(int)));
@@ -645,6 +649,7 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.out = out;
     a.part_acc = static_cast<float*>(part_acc.ptr);
     a.part_ml = static_cast<float*>(part_ml.ptr);
+    a.row_done = need_merge ? static_cast<int*>(row_done.ptr) : nullptr;
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
     a.err = static_cast<int*>(err.ptr);
     launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, s);

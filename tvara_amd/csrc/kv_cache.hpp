@@ -140,7 +140,7 @@ struct AttnPlan {
     int rows = 0, heads = 0, group = 0, items = 0, split_tokens = 0;
     bool need_merge = false, with_tail = false, inline_ok = false;
     size_t kv_bytes = 0;  // algorithmic K/V bytes one launch reads
-    DeviceBuffer tables, entries, items_buf, work_buf, work_blocks, part_acc, part_ml, err;
+    DeviceBuffer tables, entries, items_buf, work_buf, work_blocks, part_acc, part_ml, row_done, err;
     RowSplits inline_rows{};  // (first item, splits) per row when rows <= kInlineRows
     // Builds the plan for rows reading `cached[r]` tokens of `seq_of_row[r]`,
     // followed by the row's uncommitted tail token when tail_rows[r] != 0.
