@@ -196,3 +196,25 @@ def test_bf16_rejections(device):
         attention.prefill_batch(dev, q, [s], [10], [4], 0, 4, 64, precision="bf16")
     with pytest.raises(device.InvalidArgument):  # chunk past the cached tokens
         attention.prefill_batch(dev, q, [s], [18], [4], 0, 4, 64, precision="bf16")
+
+
+@pytest.mark.parametrize("precision", ["bf16", "f32"])
+@pytest.mark.parametrize("dim", [64, 128])
+def test_chunk_invariant_under_future_tokens(device, precision, dim):
+    # prefill_t173.cpp:6: tokens appended after a chunk (here huge and NaN
+    # values, in the chunk's last block and in new blocks) leave the chunk's
+    # rows byte-identical
+    heads, kv_heads, tpb = 8, 2, 16
+    w = kv_heads * dim
+    dev = device.PagedCache(1, kv_heads, dim, tpb, 24)
+    s = dev.create_sequence()
+    n, start, rows = 150, 110, 40
+    dev.append_many(s, synth.normal(41, "k", n * w).reshape(n, w), synth.normal(41, "v", n * w).reshape(n, w))
+    q = synth.normal(41, "q", rows * heads * dim).reshape(rows, heads * dim)
+    before = attention.prefill_batch(dev, q, [s], [start], [rows], 0, heads, 4096, precision=precision)
+    junk = np.full((60, w), 3e4, np.float32)
+    junk[::3] = np.nan
+    dev.append_many(s, junk, junk)
+    after = attention.prefill_batch(dev, q, [s], [start], [rows], 0, heads, 4096, precision=precision)
+    assert np.isfinite(before).all()
+    assert np.array_equal(before, after)
