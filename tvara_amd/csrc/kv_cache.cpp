@@ -616,10 +616,14 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     if (need_merge) {
         part_acc.ensure(static_cast<size_t>(items) * heads * g.head_dim * sizeof(float));
         part_ml.ensure(static_cast<size_t>(items) * heads * 2 * sizeof(float));
-        // split counters of the in-kernel merge, one per (row, KV head) at most
+        // split counters of the in-kernel merge, one per (row, KV head) at
+        // most; every launch that counts leaves them at zero again, so only a
+        // new allocation is cleared
         const size_t bytes = static_cast<size_t>(rows) * g.kv_heads * sizeof(int);
-        row_done.ensure(bytes);
-        TVARA_HIP(hipMemset(row_done.ptr, 0, bytes));
+        if (!row_done.ptr || row_done.bytes < bytes) {
+            row_done.ensure(bytes);
+            TVARA_HIP(hipMemset(row_done.ptr, 0, row_done.bytes));
+        }
     }
     err.ensure(sizeof(int));
     TVARA_HIP(hipMemset(err.ptr, 0, sizeof(int)));
