@@ -285,8 +285,13 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
 
 // ------------------------------------------------------------- f32 blocks
 
+// Above four query heads per KV head a workgroup has at most two waves and
+// the query and accumulator registers alone (2 * G * D / LPT per lane) fill
+// 256 VGPRs: the 128-thread bound lets the compiler keep the rest in AGPRs
+// (one wave per SIMD) instead of scratch (Llama-3-70B shape, d=128: 120
+// against 469 us; Q8_0 73 against 510 us).
 template <int D, int G, int LPT, int NB>
-__global__ __launch_bounds__(512) void decode_f32_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(G > 4 ? 128 : 512) void decode_f32_kernel(const DecodeArgs a) {
     constexpr int E = D / LPT, NV = E / 4, TT = 64 / LPT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int groups = a.lay.kv_heads / nwaves;
@@ -434,8 +439,8 @@ __device__ __forceinline__ void unpack_i8(uint4 w, float (&f)[16]) {
 
 // Each lane owns 16 consecutive columns (one dwordx4 of int8) = half a Q8_0
 // group, so a token's row of head_dim columns is LPT = head_dim/16 lanes.
-template <int D, int G>
-__global__ __launch_bounds__(512) void decode_q8_kernel(const DecodeArgs a) {
+template <int D, int G>  // launch bounds: as decode_f32_kernel
+__global__ __launch_bounds__(G > 4 ? 128 : 512) void decode_q8_kernel(const DecodeArgs a) {
     constexpr int LPT = D / 16, TT = 64 / LPT, E = 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int groups = a.lay.kv_heads / nwaves;
@@ -1328,9 +1333,14 @@ int decode_waves(int kv_heads, int group, int format, int head_dim) {
 // Workgroups per CU a decode launch is sized for (the split length is the
 // shortest whose launch fits CUs x this): one for f32 blocks, two for the
 // int8-MFMA Q8_0 kernel (two 8-wave workgroups' worth of registers per CU),
-// four for the vector Q8_0 kernel.  TVARA_DECODE_BUDGET overrides it.
+// four for the vector Q8_0 kernel, two above four query heads per KV head.
+// TVARA_DECODE_BUDGET overrides it.
 int decode_budget_per_cu(int group, int format, int head_dim) {
     if (const char* env = std::getenv("TVARA_DECODE_BUDGET")) return std::max(1, std::atoi(env));
+    // above four query heads per KV head the vector kernels hold one wave per
+    // SIMD in two-wave workgroups: two per CU (the Llama-3-70B shape, d=128:
+    // f32 94 against 120 us with one, Q8_0 65 against 73 us with four)
+    if (group > 4 && !q8_mma_shape(group, format, head_dim)) return 2;
     if (format == kF32) return 1;
     return q8_mma_shape(group, format, head_dim) ? 2 : 4;
 }

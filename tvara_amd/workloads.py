@@ -95,6 +95,14 @@ def decode_c5(sequences=16, length=32768):
                           q8=True, context=1 << 17)
 
 
+def decode_gqa8(q8=False, sequences=16, length=4096):
+    """Llama-3-70B's attention shape (64 query heads over 8 KV heads, d=128):
+    eight query heads per KV head."""
+    blocks = sequences * length // 16
+    name = "llama-3-70b-attn-decode-16x4096" + ("-q8_0" if q8 else "")
+    return DecodeWorkload(name, 64, 8, 128, [length] * sequences, blocks + 64, seed=6, q8=q8, context=1 << 17)
+
+
 def place_blocks(cache, order):
     """Make the pool hand out block ids in `order`: allocate every block, then
     release them in reverse (the LIFO free list pops the last release first)."""
