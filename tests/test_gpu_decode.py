@@ -99,8 +99,8 @@ def test_shapes_and_gqa_ratios(device, oracle, dim, kv_heads, group, length):
 
 
 # Q8_0 groups of 32 columns never straddle a head: head_dim is a multiple of 32
-Q8_SHAPES = [(64, 8, 1), (64, 8, 2), (64, 3, 3), (64, 2, 4), (128, 8, 4), (128, 2, 8), (128, 4, 5), (32, 2, 2),
-             (32, 1, 8)]
+Q8_SHAPES = [(64, 8, 1), (64, 8, 2), (64, 3, 3), (64, 2, 4), (128, 8, 4), (128, 2, 8), (128, 4, 5), (128, 2, 6),
+             (128, 3, 7), (32, 2, 2), (32, 1, 8)]
 
 
 @pytest.mark.parametrize("dim,kv_heads,group", Q8_SHAPES)
@@ -262,7 +262,7 @@ def _q8_values(oracle, x):
     return oracle.dequantize_q8_0(oracle.quantize_q8_0(x)).reshape(x.shape)
 
 
-@pytest.mark.parametrize("dim,group", [(64, 4), (128, 4), (128, 2), (128, 8)])
+@pytest.mark.parametrize("dim,group", [(64, 4), (128, 4), (128, 2), (128, 6), (128, 8)])
 def test_q8_tail_and_visible(device, oracle, dim, group):
     for length, visible in [(53, None), (53, 54), (53, 20), (300, 1), (300, 299), (64, 33)]:
         say("q8 tail", dim, group, length, visible)

@@ -156,6 +156,7 @@ void launch_canonical_to_q8(char* pool, const BlockLayout& lay, int64_t id, cons
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
                    hipStream_t s);
 int decode_waves(int kv_heads, int group, int format, int head_dim);
+int decode_slots(int kv_heads, int group, int format, int head_dim);  // waves' worth of work per work item
 int decode_budget_per_cu(int group, int format, int head_dim);
 // prefill.hip
 bool prefill_bf16_supported(const BlockLayout& lay, int group);

@@ -639,9 +639,14 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
     constexpr int KRS = D + 16;                     // LDS row of one token's K (padded against bank conflicts)
     static_assert(G >= 1 && G <= 4, "four query heads per KV head at most");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-    const int groups = a.lay.kv_heads / nwaves;
+    // a wave takes G query heads of one KV head: the group's heads in one
+    // slice (G = group) or, at six or eight per KV head, in two (G = group / 2)
+    const int halves = a.group / G;
+    const int groups = a.lay.kv_heads * halves / nwaves;
     const int item = static_cast<int>(blockIdx.x) / groups;
-    const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
+    const int slot = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
+    const int kh = slot / halves;
+    const size_t qh0 = static_cast<size_t>(kh) * a.group + static_cast<size_t>(slot % halves) * G;  // first query head
     // the item's descriptor and block ids come in two independent loads
     const int4 it = a.work[item];  // row, first token, end token, tail | splits << 1
     const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
@@ -663,7 +668,7 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
     {
         const int hq = t16 >> 2, jp = t16 & 3;
         const bool hv = hq < G;
-        const float* qr = a.q + (static_cast<size_t>(it.x) * a.heads + static_cast<size_t>(kh) * G + (hv ? hq : 0)) * D;
+        const float* qr = a.q + (static_cast<size_t>(it.x) * a.heads + qh0 + (hv ? hq : 0)) * D;
         float qv[NG][8];
         float mx = 0.f;
 #pragma unroll
@@ -844,7 +849,7 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
         constexpr int CPL = D / 16;
         float part = 0.f;
         if (u < G) {
-            const float* qh = a.q + (static_cast<size_t>(it.x) * a.heads + static_cast<size_t>(kh) * G + u) * D + t16 * CPL;
+            const float* qh = a.q + (static_cast<size_t>(it.x) * a.heads + qh0 + u) * D + t16 * CPL;
             const float* tk = a.tail_k + static_cast<size_t>(it.x) * kvw + kcol + t16 * CPL;
 #pragma unroll
             for (int e = 0; e < CPL; ++e) part = fmaf(qh[e], tk[e], part);
@@ -885,7 +890,7 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
         mh[h] = readlane_f(mv, 16 * h);
         lh[h] = readlane_f(lsum, 16 * h);
     }
-    const size_t head0 = static_cast<size_t>(kh) * G;
+    const size_t head0 = qh0;
     if (lane < LPT) {
         float* dst = nsplit == 1 ? a.out + (static_cast<size_t>(it.x) * a.heads + head0) * D
                                  : a.part_acc + (static_cast<size_t>(item) * a.heads + head0) * D;
@@ -1237,22 +1242,25 @@ void launch_q8(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
 template <int D, int G>
 void launch_q8_mma(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
     const size_t lds = static_cast<size_t>(waves) * q8_mma_wave_lds<D>();
-    launch("paged_decode", decode_q8_mma_kernel<D, G>, dim3(nitems * (a.lay.kv_heads / waves)), dim3(64 * waves), lds,
-           s, a);
+    const int slots = a.lay.kv_heads * (a.group / G);
+    launch("paged_decode", decode_q8_mma_kernel<D, G>, dim3(nitems * (slots / waves)), dim3(64 * waves), lds, s, a);
 }
 
 // Q8_0 scores on the int8 matrix cores for up to four query heads per KV
-// head; TVARA_Q8_DECODE=valu selects the all-VALU kernel.
+// head in one wave, six or eight in two waves of three or four;
+// TVARA_Q8_DECODE=valu selects the all-VALU kernel.
 bool q8_mma_enabled(int group) {
     static const bool valu = [] {
         const char* env = std::getenv("TVARA_Q8_DECODE");
         return env && std::string(env) == "valu";
     }();
-    return group <= 4 && !valu;
+    return (group <= 4 || group == 6 || group == 8) && !valu;
 }
 
 bool q8_mma_shape(int group, int format, int head_dim) {
-    return format != kF32 && (head_dim == 64 || head_dim == 128) && q8_mma_enabled(group);
+    // six or eight query heads per KV head only at head_dim 128 (at 64 the
+    // fast kernels take four at most)
+    return format != kF32 && q8_mma_enabled(group) && (head_dim == 128 || (head_dim == 64 && group <= 4));
 }
 
 template <int D>
@@ -1266,6 +1274,8 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
             case 2: launch_q8_mma<D, 2>(a, nitems, waves, s); return true;
             case 3: launch_q8_mma<D, 3>(a, nitems, waves, s); return true;
             case 4: launch_q8_mma<D, 4>(a, nitems, waves, s); return true;
+            case 6: launch_q8_mma<D, 3>(a, nitems, waves, s); return true;  // two slices of three
+            case 8: launch_q8_mma<D, 4>(a, nitems, waves, s); return true;  // two slices of four
             default: break;
         }
     }
@@ -1316,17 +1326,22 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
 // workgroups hide its longer per-tile arithmetic), at most two for groups
 // above four query heads; a divisor of kv_heads whose LDS fits 64 KiB.
 // TVARA_DECODE_WAVES overrides it for tuning.
+int decode_slots(int kv_heads, int group, int format, int head_dim) {
+    return kv_heads * (q8_mma_shape(group, format, head_dim) && group > 4 ? 2 : 1);
+}
+
 int decode_waves(int kv_heads, int group, int format, int head_dim) {
     const bool mma = q8_mma_shape(group, format, head_dim);
+    const int slots = decode_slots(kv_heads, group, format, head_dim);
     int w = format == kF32 ? 8 : 4;
     if (const char* env = std::getenv("TVARA_DECODE_WAVES")) w = std::atoi(env);
-    if (group > 4) w = std::min(w, 2);
+    if (group > 4 && !mma) w = std::min(w, 2);
     w = std::max(1, std::min(w, 8));
     auto lds = [&](int n) {
         return mma ? static_cast<size_t>(n) * (32 * (head_dim + 16) + 32 * (head_dim / 32) * 4 * sizeof(float))
                    : static_cast<size_t>(n) * (4 * group * head_dim + 2 * group) * sizeof(float);
     };
-    while (w > 1 && (kv_heads % w || lds(w) > 65536)) --w;
+    while (w > 1 && (slots % w || lds(w) > 65536)) --w;
     return w;
 }
 
@@ -1369,7 +1384,8 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
     // launch (the Llama-3.2-1B batch of 253 workgroups: 105.5 against 102.8 us).
     // The int8-MFMA Q8_0 and generic kernels always leave it to merge_kernel.
     const bool fast = decode_fast_path(a);
-    const int wgs = fast ? nitems * (a.lay.kv_heads / waves_for(a)) : nitems * a.heads;
+    const int wgs = fast ? nitems * (decode_slots(a.lay.kv_heads, a.group, a.lay.format, a.lay.head_dim) / waves_for(a))
+                         : nitems * a.heads;
     static const int max_wgs = [] {
         const char* env = std::getenv("TVARA_INKERNEL_MERGE_MAX");
         return env ? std::atoi(env) : kInKernelMergeMaxWorkgroups;

@@ -557,8 +557,9 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
         if (const char* env = std::getenv("TVARA_SPLIT_TOKENS")) split = std::strtoull(env, nullptr, 10);
     }
     if (!split) {
-        const size_t groups = g.kv_heads / static_cast<size_t>(decode_waves(static_cast<int>(g.kv_heads), group,
-                                                                             c->format(), static_cast<int>(g.head_dim)));
+        const int gw = static_cast<int>(g.kv_heads), gd = static_cast<int>(g.head_dim);
+        const size_t groups = static_cast<size_t>(decode_slots(gw, group, c->format(), gd)) /
+                              static_cast<size_t>(decode_waves(gw, group, c->format(), gd));
         const size_t budget = static_cast<size_t>(c->compute_units()) *
                               decode_budget_per_cu(group, c->format(), static_cast<int>(g.head_dim));
         auto workgroups = [&](size_t sp) {
