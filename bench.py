@@ -411,7 +411,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c3cow", "c4", "c4d128", "c5", "gqa8", "gqa8q8", "llama1b"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c3cow", "c4", "c4d128", "c5", "gqa8", "gqa8q8", "tiny", "tinyq8",
+                             "llama1b"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -443,7 +444,8 @@ def main():
     if args.workload == "llama1b":
         return bench_model(args)
     w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5,
-         "gqa8": workloads.decode_gqa8, "gqa8q8": lambda: workloads.decode_gqa8(q8=True)}[args.workload]()
+         "gqa8": workloads.decode_gqa8, "gqa8q8": lambda: workloads.decode_gqa8(q8=True),
+         "tiny": workloads.decode_tinyllama, "tinyq8": lambda: workloads.decode_tinyllama(q8=True)}[args.workload]()
     log(f"workload {w.name}: {w.sequences} sequences, {w.total_tokens} tokens")
     g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)
     cache = kv.PagedCache(*g, fmt=kv.Q8_0 if w.q8 else kv.F32)

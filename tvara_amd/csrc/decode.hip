@@ -639,8 +639,8 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
     constexpr int KRS = D + 16;                     // LDS row of one token's K (padded against bank conflicts)
     static_assert(G >= 1 && G <= 4, "four query heads per KV head at most");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-    // a wave takes G query heads of one KV head: the group's heads in one
-    // slice (G = group) or, at six or eight per KV head, in two (G = group / 2)
+    // a wave takes G query heads of one KV head (q8_mma_heads): the group's
+    // heads come in group / G slices over as many waves
     const int halves = a.group / G;
     const int groups = a.lay.kv_heads * halves / nwaves;
     const int item = static_cast<int>(blockIdx.x) / groups;
@@ -1246,36 +1246,42 @@ void launch_q8_mma(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
     launch("paged_decode", decode_q8_mma_kernel<D, G>, dim3(nitems * (slots / waves)), dim3(64 * waves), lds, s, a);
 }
 
-// Q8_0 scores on the int8 matrix cores for up to four query heads per KV
-// head in one wave, six or eight in two waves of three or four;
-// TVARA_Q8_DECODE=valu selects the all-VALU kernel.
-bool q8_mma_enabled(int group) {
+// Q8_0 scores on the int8 matrix cores: a wave takes up to four query heads
+// of a KV head, the group's heads in one slice or, for six and eight, two of
+// three and four; five and seven run one head a wave at head_dim 64 (the
+// vector kernel gives a token D/16 lanes, one head slot each, so four at 64)
+// and stay on the vector kernel at 128.  Returns the heads per wave, 0 for
+// the vector kernel.  TVARA_Q8_DECODE=valu selects the vector kernel where it
+// applies.
+int q8_mma_heads(int group, int head_dim) {
     static const bool valu = [] {
         const char* env = std::getenv("TVARA_Q8_DECODE");
         return env && std::string(env) == "valu";
     }();
-    return (group <= 4 || group == 6 || group == 8) && !valu;
+    if (head_dim != 64 && head_dim != 128) return 0;
+    if (group == 6 || group == 8) return valu ? 0 : group / 2;
+    if (group == 5 || group == 7) return head_dim == 64 ? 1 : 0;
+    return group <= 4 && !valu ? group : 0;
 }
 
 bool q8_mma_shape(int group, int format, int head_dim) {
-    // six or eight query heads per KV head only at head_dim 128 (at 64 the
-    // fast kernels take four at most)
-    return format != kF32 && q8_mma_enabled(group) && (head_dim == 128 || (head_dim == 64 && group <= 4));
+    return format != kF32 && q8_mma_heads(group, head_dim) > 0;
 }
 
+// Up to four query heads per KV head the f32 kernel gives a token D/16 lanes
+// (four at head_dim 64); five to eight take eight lanes a token at either
+// head_dim, so the queries and accumulators of a lane stay at 2 * G * D / 8.
 template <int D>
 bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
     constexpr int LPT = D == 64 ? 4 : 8;
     const int G = a.group;
-    if (G > LPT) return false;
-    if (a.lay.format != kF32 && q8_mma_enabled(G)) {
-        switch (G) {
+    if (G > 8) return false;
+    if (a.lay.format != kF32) {
+        switch (q8_mma_heads(G, D)) {
             case 1: launch_q8_mma<D, 1>(a, nitems, waves, s); return true;
             case 2: launch_q8_mma<D, 2>(a, nitems, waves, s); return true;
             case 3: launch_q8_mma<D, 3>(a, nitems, waves, s); return true;
             case 4: launch_q8_mma<D, 4>(a, nitems, waves, s); return true;
-            case 6: launch_q8_mma<D, 3>(a, nitems, waves, s); return true;  // two slices of three
-            case 8: launch_q8_mma<D, 4>(a, nitems, waves, s); return true;  // two slices of four
             default: break;
         }
     }
@@ -1287,14 +1293,12 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
             case 4: launch_f32<D, 4, LPT>(a, nitems, waves, s); return true;
             default: break;
         }
-        if constexpr (LPT == 8) {
-            switch (G) {
-                case 5: launch_f32<D, 5, LPT>(a, nitems, waves, s); return true;
-                case 6: launch_f32<D, 6, LPT>(a, nitems, waves, s); return true;
-                case 7: launch_f32<D, 7, LPT>(a, nitems, waves, s); return true;
-                case 8: launch_f32<D, 8, LPT>(a, nitems, waves, s); return true;
-                default: break;
-            }
+        switch (G) {
+            case 5: launch_f32<D, 5, 8>(a, nitems, waves, s); return true;
+            case 6: launch_f32<D, 6, 8>(a, nitems, waves, s); return true;
+            case 7: launch_f32<D, 7, 8>(a, nitems, waves, s); return true;
+            case 8: launch_f32<D, 8, 8>(a, nitems, waves, s); return true;
+            default: break;
         }
         return false;
     }
@@ -1305,7 +1309,7 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
         case 4: launch_q8<D, 4>(a, nitems, waves, s); return true;
         default: break;
     }
-    if constexpr (LPT == 8) {
+    if constexpr (LPT == 8) {  // the vector kernel's head slots: D/16 lanes a token
         switch (G) {
             case 5: launch_q8<D, 5>(a, nitems, waves, s); return true;
             case 6: launch_q8<D, 6>(a, nitems, waves, s); return true;
@@ -1327,7 +1331,7 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
 // above four query heads; a divisor of kv_heads whose LDS fits 64 KiB.
 // TVARA_DECODE_WAVES overrides it for tuning.
 int decode_slots(int kv_heads, int group, int format, int head_dim) {
-    return kv_heads * (q8_mma_shape(group, format, head_dim) && group > 4 ? 2 : 1);
+    return kv_heads * (q8_mma_shape(group, format, head_dim) ? group / q8_mma_heads(group, head_dim) : 1);
 }
 
 int decode_waves(int kv_heads, int group, int format, int head_dim) {
@@ -1348,14 +1352,17 @@ int decode_waves(int kv_heads, int group, int format, int head_dim) {
 // Workgroups per CU a decode launch is sized for (the split length is the
 // shortest whose launch fits CUs x this): one for f32 blocks, two for the
 // int8-MFMA Q8_0 kernel (two 8-wave workgroups' worth of registers per CU),
-// four for the vector Q8_0 kernel, two above four query heads per KV head.
+// four for the vector Q8_0 kernel; above four query heads per KV head two
+// (head_dim 128) or four (64).
 // TVARA_DECODE_BUDGET overrides it.
 int decode_budget_per_cu(int group, int format, int head_dim) {
     if (const char* env = std::getenv("TVARA_DECODE_BUDGET")) return std::max(1, std::atoi(env));
-    // above four query heads per KV head the vector kernels hold one wave per
-    // SIMD in two-wave workgroups: two per CU (the Llama-3-70B shape, d=128:
-    // f32 94 against 120 us with one, Q8_0 65 against 73 us with four)
-    if (group > 4 && !q8_mma_shape(group, format, head_dim)) return 2;
+    // above four query heads per KV head the vector kernels run two-wave
+    // workgroups: at head_dim 128 one wave per SIMD, two workgroups per CU
+    // (the Llama-3-70B shape: f32 94 against 120 us with one); at 64 (eight
+    // lanes a token, two or three waves per SIMD) four (TinyLlama's shape,
+    // 64 x 2,048 tokens: 42.8 against 45.6 us with two)
+    if (group > 4 && !q8_mma_shape(group, format, head_dim)) return head_dim == 64 ? 4 : 2;
     if (format == kF32) return 1;
     return q8_mma_shape(group, format, head_dim) ? 2 : 4;
 }
@@ -1369,8 +1376,7 @@ static int waves_for(const DecodeArgs& a) {
 constexpr int kInKernelMergeMaxWorkgroups = 128;
 
 bool decode_fast_path(const DecodeArgs& a) {
-    return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128) &&
-           a.group <= (a.lay.head_dim == 64 ? 4 : 8);
+    return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128) && a.group <= 8;
 }
 
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
@@ -1391,7 +1397,7 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
         return env ? std::atoi(env) : kInKernelMergeMaxWorkgroups;
     }();
     const bool in_kernel =
-        fast && a.row_done && !(a.lay.format != kF32 && q8_mma_enabled(a.group)) && wgs <= max_wgs;
+        fast && a.row_done && !q8_mma_shape(a.group, a.lay.format, a.lay.head_dim) && wgs <= max_wgs;
     DecodeArgs b = a;
     if (!in_kernel) b.row_done = nullptr;
     bool merged = false;

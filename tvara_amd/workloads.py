@@ -103,6 +103,14 @@ def decode_gqa8(q8=False, sequences=16, length=4096):
     return DecodeWorkload(name, 64, 8, 128, [length] * sequences, blocks + 64, seed=6, q8=q8, context=1 << 17)
 
 
+def decode_tinyllama(q8=False, sequences=64, length=2048):
+    """TinyLlama-1.1B's attention shape (32 query heads over 4 KV heads, d=64):
+    eight query heads per KV head at head_dim 64."""
+    blocks = sequences * length // 16
+    name = "tinyllama-1.1b-attn-decode-64x2048" + ("-q8_0" if q8 else "")
+    return DecodeWorkload(name, 32, 4, 64, [length] * sequences, blocks + 64, seed=7, q8=q8, context=1 << 17)
+
+
 def place_blocks(cache, order):
     """Make the pool hand out block ids in `order`: allocate every block, then
     release them in reverse (the LIFO free list pops the last release first)."""
