@@ -17,8 +17,10 @@
 // kThreshold, so exp2(s - m) stays below 2^kThreshold and the rescale runs a
 // handful of times per split instead of once per tile.
 //
-// Splits are merged by log-sum-exp in merge_kernel.  A non-finite score sets
-// *err, matching OnlineAttention::update's rejection (attention.hpp:11).
+// Splits are merged by log-sum-exp: in merge_kernel / merge_wave_kernel, or
+// for launches of at most 128 workgroups in the last workgroup of each row
+// (merge_row_splits).  A non-finite score sets *err, matching
+// OnlineAttention::update's rejection (attention.hpp:11).
 #include <algorithm>
 #include <cstdlib>
 #include <string>
