@@ -136,7 +136,7 @@ def bench_prefill(args, w):
     import numpy as np
 
     from tvara_amd import attention, hip, kv, workloads
-    cache = kv.PagedCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks())
+    cache = kv.PagedCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks(), fmt=kv.Q8_0 if w.q8 else kv.F32)
     seqs = workloads.fill_prefill(cache, w)
     q = hip.DeviceArray.from_numpy(np.concatenate([w.chunk_queries(i) for i in range(w.sequences)]))
     out = hip.DeviceArray(q.shape)
@@ -411,8 +411,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c3cow", "c4", "c4d128", "c5", "gqa8", "gqa8q8", "tiny", "tinyq8",
-                             "llama1b"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c5", "gqa8", "gqa8q8", "tiny",
+                             "tinyq8", "llama1b"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -437,8 +437,9 @@ def main():
         hip.synchronize()
         log(f"copied {args.copy_mib} MiB x3")
         del a, b
-    if args.workload in ("c4", "c4d128"):
-        return bench_prefill(args, workloads.prefill_c4() if args.workload == "c4" else workloads.prefill_8b())
+    if args.workload in ("c4", "c4d128", "c4q8"):
+        make = {"c4": workloads.prefill_c4, "c4d128": workloads.prefill_8b, "c4q8": workloads.prefill_c4_q8}
+        return bench_prefill(args, make[args.workload]())
     if args.workload in ("c3", "c3cow"):
         return bench_kv(args, args.workload == "c3cow")
     if args.workload == "llama1b":

@@ -47,15 +47,20 @@ def bf16_ok(got, want, bars):
     return refmath.close(got, want, bars[0]) and rms <= bars[1], (refmath.max_rel(got, want), rms)
 
 
-def build(device, oracle, heads, kv_heads, dim, specs, seed, tpb=16):
-    """specs: (cached tokens, chunk start, chunk rows) per sequence."""
+def build(device, oracle, heads, kv_heads, dim, specs, seed, tpb=16, q8=False):
+    """specs: (cached tokens, chunk start, chunk rows) per sequence.  q8: Q8_0
+    blocks, with the oracle holding the dequantised values."""
     nb = sum((n + tpb - 1) // tpb for n, _, _ in specs) + 4
-    dev, ref = device.PagedCache(1, kv_heads, dim, tpb, nb), oracle.Cache(1, kv_heads, dim, tpb, nb)
+    dev = device.PagedCache(1, kv_heads, dim, tpb, nb, fmt=device.Q8_0 if q8 else device.F32)
+    ref = oracle.Cache(1, kv_heads, dim, tpb, nb)
     w = kv_heads * dim
     ds, rs, qs = [], [], []
     for i, (n, start, rows) in enumerate(specs):
         k = synth.normal(seed, f"k{i}", n * w).reshape(n, w)
         v = synth.normal(seed, f"v{i}", n * w).reshape(n, w)
+        if q8:
+            k = oracle.dequantize_q8_0(oracle.quantize_q8_0(k)).reshape(n, w)
+            v = oracle.dequantize_q8_0(oracle.quantize_q8_0(v)).reshape(n, w)
         sd, sr = dev.create_sequence(), ref.create_sequence()
         dev.append_many(sd, k, v)
         ref.append_many(sr, k, v)
@@ -65,13 +70,14 @@ def build(device, oracle, heads, kv_heads, dim, specs, seed, tpb=16):
     return dev, ref, ds, rs, qs
 
 
+@pytest.mark.parametrize("fmt", ["f32", "q8_0"])
 @pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
-def test_bf16_small_shapes(device, oracle, group, dim):
+def test_bf16_small_shapes(device, oracle, group, dim, fmt):
     heads, kv_heads = 2 * group, 2
     specs = [(137, 100, 37), (64, 0, 64), (20, 3, 17)]
-    say("prefill bf16 group", group, "dim", dim)
-    dev, ref, ds, rs, qs = build(device, oracle, heads, kv_heads, dim, specs, seed=group)
+    say("prefill bf16 group", group, "dim", dim, fmt)
+    dev, ref, ds, rs, qs = build(device, oracle, heads, kv_heads, dim, specs, seed=group, q8=fmt == "q8_0")
     starts = [s for _, s, _ in specs]
     counts = [r for _, _, r in specs]
     got = attention.prefill_batch(dev, np.concatenate(qs), ds, starts, counts, 0, heads, 4096, precision="bf16")
@@ -83,12 +89,14 @@ def test_bf16_small_shapes(device, oracle, group, dim):
     assert ok, err
 
 
-@pytest.mark.parametrize("make", [workloads.prefill_c4, workloads.prefill_8b], ids=["d64", "d128"])
-def test_bf16_c4_shape(device, oracle, make):
+@pytest.mark.parametrize("make,fmt", [(workloads.prefill_c4, "f32"), (workloads.prefill_8b, "f32"),
+                                      (workloads.prefill_c4, "q8_0")], ids=["d64", "d128", "d64-q8_0"])
+def test_bf16_c4_shape(device, oracle, make, fmt):
     w = make()
-    say("prefill", w.name)
+    say("prefill", w.name, fmt)
     g = (1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks())
-    dev, ref = device.PagedCache(*g), oracle.Cache(*g)
+    q8 = fmt == "q8_0"
+    dev, ref = device.PagedCache(*g, fmt=device.Q8_0 if q8 else device.F32), oracle.Cache(*g)
     ds = workloads.fill_prefill(dev, w)
     q = np.concatenate([w.chunk_queries(i) for i in range(w.sequences)])
     got = attention.prefill_batch(dev, q, ds, [w.prefix] * w.sequences, [w.chunk] * w.sequences, 0, w.heads,
@@ -99,7 +107,11 @@ def test_bf16_c4_shape(device, oracle, make):
     want, gsel, fsel = [], [], []
     for i in range(w.sequences):
         s = ref.create_sequence()
-        ref.append_many(s, w.keys(i), w.values(i))
+        k, v = w.keys(i), w.values(i)
+        if q8:  # the oracle holds the dequantised values the Q8_0 blocks store
+            k = oracle.dequantize_q8_0(oracle.quantize_q8_0(k)).reshape(k.shape)
+            v = oracle.dequantize_q8_0(oracle.quantize_q8_0(v)).reshape(v.shape)
+        ref.append_many(s, k, v)
         qi = w.chunk_queries(i)
         for r in rows:
             want.append(ref.fused_prompt_attention(qi[r], s, 0, w.prefix + r, 1, w.heads, w.context))

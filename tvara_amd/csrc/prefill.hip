@@ -24,6 +24,7 @@
 
 #include "common.hpp"
 #include "device_util.hpp"
+#include "q8.hpp"
 
 namespace tvara_amd {
 namespace {
@@ -56,7 +57,9 @@ __device__ __forceinline__ bf16x4 to_bf16(f32x4 v) { return __builtin_convertvec
 // word 3 of a raw buffer descriptor (32-bit data format, no swizzle)
 constexpr int kBufferWord3 = 0x00020000;
 
-template <int D, int G, int kWaves>
+// kQ8: Q8_0 blocks (the head's int8 plane and fp16 group scales), dequantised
+// to bf16 when staged; otherwise f32 blocks.
+template <int D, int G, int kWaves, bool kQ8>
 __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const PrefillArgs a) {
     constexpr int PW = kRows / G;        // chunk positions per wave
     constexpr int QT = kWaves * PW;      // chunk positions per workgroup
@@ -91,8 +94,6 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     const int wave_kmax = pw0 < nrows ? start + min(pw0 + PW, nrows) : 0;
     const int kvw = a.lay.kv_width;
     const int32_t* tab = a.tables + sd.x;
-    const size_t koff = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D;
-    const size_t voff = koff + 16 * static_cast<size_t>(kvw);
 
     // Q^T as the B operand: row n = 16*nt + r16, columns 32*kc + 8*g .. +7
     bf16x8 qop[2][KC];
@@ -123,14 +124,22 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     // before issuing its loads.
     const int skey = tid / LPR, col = 4 * (tid % LPR);
     const int wkey = __builtin_amdgcn_readfirstlane(skey);  // the wave's first row in a pass
-    auto roff = [&](int p) {  // byte offset of the lane's K (or V) columns within the block's section
-        return static_cast<unsigned>((((KPP * p + skey) & 15) * kvw + col) * sizeof(float));
+    // byte offset within the block's K (or V) run of this head of the lane's
+    // four columns (f32, or Q8_0 int8) and, for Q8_0, of their group's scale
+    auto roff = [&](int p) {
+        const int slot = (KPP * p + skey) & 15;
+        return static_cast<unsigned>(kQ8 ? slot * D + col : (slot * kvw + col) * static_cast<int>(sizeof(float)));
+    };
+    auto soff = [&](int p) {
+        const int slot = (KPP * p + skey) & 15;
+        return static_cast<unsigned>(16 * D + (slot * (D / 32) + col / 32) * 2);
     };
     // K/V rows are read through a buffer descriptor per block (base = the
-    // block's K section of this layer and head, 32-bit lane offsets, reads
-    // bounded by the block's end)
-    const size_t kbytes = koff * sizeof(float);
-    const int vsec = static_cast<int>((voff - koff) * sizeof(float));
+    // block's K run of this layer and head, V one section further, 32-bit lane
+    // offsets, reads bounded by the block's end)
+    const size_t kbytes = kQ8 ? static_cast<size_t>(a.layer) * 2 * a.lay.section + static_cast<size_t>(kh) * a.lay.head_bytes
+                              : (static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D) * sizeof(float);
+    const int vsec = static_cast<int>(kQ8 ? a.lay.section : 16 * static_cast<size_t>(kvw) * sizeof(float));
     const int brange = static_cast<int>(a.lay.stride - kbytes);
     // register stages of K/V rows in flight: two (even / odd tiles) at head_dim
     // 64, one at 128, where two would not fit beside the accumulators
@@ -154,8 +163,30 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                 a.pool + static_cast<size_t>(__builtin_amdgcn_readfirstlane(b[p])) * a.lay.stride + kbytes;
             const __amdgpu_buffer_rsrc_t r =
                 __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(blk), 0, brange, kBufferWord3);
-            kreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff(p), 0, 0);
-            vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff(p), vsec, 0);
+            if constexpr (kQ8) {  // four int8 and their scale's bits, dequantised when staged
+                const unsigned kq = __builtin_amdgcn_raw_buffer_load_b32(r, roff(p), 0, 0);
+                const unsigned ks = __builtin_amdgcn_raw_buffer_load_b16(r, soff(p), 0, 0);
+                const unsigned vq = __builtin_amdgcn_raw_buffer_load_b32(r, roff(p), vsec, 0);
+                const unsigned vs = __builtin_amdgcn_raw_buffer_load_b16(r, soff(p), vsec, 0);
+                kreg[p] = f32x4{__builtin_bit_cast(float, kq), __builtin_bit_cast(float, ks), 0.f, 0.f};
+                vreg[p] = f32x4{__builtin_bit_cast(float, vq), __builtin_bit_cast(float, vs), 0.f, 0.f};
+            } else {
+                kreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff(p), 0, 0);
+                vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff(p), vsec, 0);
+            }
+        }
+    };
+    auto values = [](f32x4 x) {  // the staged f32 values (Q8_0: d * q, as dequantize_q8_0)
+        if constexpr (kQ8) {
+            // elements copied to scalars first: a bit cast of a vector element
+            // directly reads element 0 under this compiler
+            const float x0 = x[0], x1 = x[1];
+            const uint32_t q = __builtin_bit_cast(uint32_t, x0);
+            const float d = half_bits_to_float(static_cast<uint16_t>(__builtin_bit_cast(uint32_t, x1)));
+            return f32x4{sbyte_to_float<0>(q) * d, sbyte_to_float<1>(q) * d, sbyte_to_float<2>(q) * d,
+                         sbyte_to_float<3>(q) * d};
+        } else {
+            return x;
         }
     };
     auto lstore = [&](int kt, int buf, const f32x4 (&kreg)[SP], f32x4 (&vreg)[SP]) {
@@ -166,8 +197,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
         }
 #pragma unroll
         for (int p = 0; p < SP; ++p) {
-            *reinterpret_cast<bf16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = to_bf16(kreg[p]);
-            *reinterpret_cast<bf16x4*>(&vlds[buf][(KPP * p + skey) * VSTR + col]) = to_bf16(vreg[p]);
+            *reinterpret_cast<bf16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = to_bf16(values(kreg[p]));
+            *reinterpret_cast<bf16x4*>(&vlds[buf][(KPP * p + skey) * VSTR + col]) = to_bf16(values(vreg[p]));
         }
     };
 
@@ -359,13 +390,17 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 // workgroups) and 64-key tiles (128-key tiles measured 177 us)
 template <int D, int G, int W>
 void launch_gw(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
+    const bool q8 = a.lay.format == kQ8;
     constexpr int QT = W * (kRows / G);
     PrefillArgs b = a;
     b.chunk_tiles = (max_rows + QT - 1) / QT;
     b.pairs = nseqs * a.lay.kv_heads;
     const int groups8 = (b.pairs + 7) / 8;  // ids = 8 XCDs x pair groups x chunk tiles
-    launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W>, dim3(8 * groups8 * b.chunk_tiles), dim3(64 * W), 0, s,
-           b);
+    const dim3 grid(8 * groups8 * b.chunk_tiles), block(64 * W);
+    if (q8)
+        launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W, true>, grid, block, 0, s, b);
+    else
+        launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W, false>, grid, block, 0, s, b);
 }
 
 // waves per workgroup (TVARA_PREFILL_WAVES: 4 or 8)
@@ -385,14 +420,14 @@ void launch_g(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
 
 bool prefill_bf16_supported(const BlockLayout& lay, int group) {
     // the staging reads take 32-bit offsets within a block
-    return lay.format == kF32 && lay.tpb == 16 && (lay.head_dim == 64 || lay.head_dim == 128) &&
+    return (lay.format == kF32 || lay.format == kQ8) && lay.tpb == 16 && (lay.head_dim == 64 || lay.head_dim == 128) &&
            lay.stride < (size_t(1) << 31) && (group == 1 || group == 2 || group == 4 || group == 8);
 }
 
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     if (!prefill_bf16_supported(a.lay, a.group))
         throw std::invalid_argument(
-            "bf16 prefill needs f32 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, GQA group 1/2/4/8");
+            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, GQA group 1/2/4/8");
     if (nseqs <= 0 || max_rows <= 0) return;
     switch (a.group) {
         case 1: launch_g<1>(a, nseqs, max_rows, s); break;

@@ -152,6 +152,7 @@ class PrefillWorkload:
     tokens_per_block: int = 16
     seed: int = 4
     context: int = 8192
+    q8: bool = False  # Q8_0 blocks
 
     @property
     def kv_width(self):
@@ -181,11 +182,16 @@ class PrefillWorkload:
 
     def bytes(self):
         qo = 2 * self.sequences * self.chunk * self.heads * self.head_dim * 4
-        return qo + self.sequences * self.total * self.kv_width * 2 * 4
+        return qo + int(self.sequences * self.total * self.kv_width * 2 * (34 / 32 if self.q8 else 4))
 
 
 def prefill_c4(**kw):
     return PrefillWorkload("llama-3.2-1b-chunked-prefill-8x(2048+512)", **kw)
+
+
+def prefill_c4_q8(**kw):
+    """The Llama-3.2-1B chunks over Q8_0 blocks."""
+    return PrefillWorkload("llama-3.2-1b-chunked-prefill-8x(2048+512)-q8_0", q8=True, **kw)
 
 
 def prefill_8b(**kw):
