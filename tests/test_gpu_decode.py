@@ -361,7 +361,8 @@ def test_prompt_chunk_f32(device, oracle):
 
 
 @pytest.mark.parametrize("split", [0, 1024], ids=["merge-launch", "merge-in-kernel"])
-@pytest.mark.parametrize("fmt_name,dim,kv_heads,group", [("F32", 64, 8, 4), ("F32", 128, 4, 8), ("Q8_0", 128, 2, 8)])
+@pytest.mark.parametrize("fmt_name,dim,kv_heads,group", [("F32", 64, 8, 4), ("F32", 128, 4, 8), ("Q8_0", 128, 2, 8),
+                                                         ("Q8_0", 128, 2, 5), ("F32", 64, 4, 8)])
 def test_plan_back_to_back_launches(device, oracle, monkeypatch, fmt_name, dim, kv_heads, group, split):
     # rows of several splits: with the default split the launch fills the GPU
     # and merge_kernel combines them; 1,024-token splits give a launch of a few
