@@ -72,7 +72,7 @@ def build(device, oracle, heads, kv_heads, dim, specs, seed, tpb=16, q8=False):
 
 @pytest.mark.parametrize("fmt", ["f32", "q8_0"])
 @pytest.mark.parametrize("dim", [64, 128])
-@pytest.mark.parametrize("group", [1, 2, 4, 8])
+@pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_bf16_small_shapes(device, oracle, group, dim, fmt):
     heads, kv_heads = 2 * group, 2
     specs = [(137, 100, 37), (64, 0, 64), (20, 3, 17)]

@@ -61,7 +61,7 @@ constexpr int kBufferWord3 = 0x00020000;
 // to bf16 when staged; otherwise f32 blocks.
 template <int D, int G, int kWaves, bool kQ8>
 __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const PrefillArgs a) {
-    constexpr int PW = kRows / G;        // chunk positions per wave
+    constexpr int PW = kRows / G;        // chunk positions per wave; rows PW*G .. 31 are padding (G = 3, 5, 6, 7)
     constexpr int QT = kWaves * PW;      // chunk positions per workgroup
     constexpr int KC = D / 32;           // K-dimension chunks of S^T
     constexpr int DT = D / 16;           // output column tiles
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
             float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-            if (pos < nrows) {
+            if (pos < nrows && r < PW * G) {
                 const float* qp = a.q + (static_cast<size_t>(sd.w + pos) * a.heads + head) * D + 32 * kc + 8 * g;
                 x0 = *reinterpret_cast<const float4*>(qp);
                 x1 = *reinterpret_cast<const float4*>(qp + 4);
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
         // row 0 of the normaliser tile: lane r16 (group 0), element 0
         const float l = __shfl(acc[DT][nt][0], r16);
         const int r = 16 * nt + r16, pos = pw0 + r / G, head = kh * G + r % G;
-        if (pos >= nrows) continue;
+        if (pos >= nrows || r >= PW * G) continue;
         float* o = a.out + (static_cast<size_t>(sd.w + pos) * a.heads + head) * D + 4 * g;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
@@ -421,18 +421,22 @@ void launch_g(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
 bool prefill_bf16_supported(const BlockLayout& lay, int group) {
     // the staging reads take 32-bit offsets within a block
     return (lay.format == kF32 || lay.format == kQ8) && lay.tpb == 16 && (lay.head_dim == 64 || lay.head_dim == 128) &&
-           lay.stride < (size_t(1) << 31) && (group == 1 || group == 2 || group == 4 || group == 8);
+           lay.stride < (size_t(1) << 31) && group >= 1 && group <= 8;
 }
 
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     if (!prefill_bf16_supported(a.lay, a.group))
         throw std::invalid_argument(
-            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, GQA group 1/2/4/8");
+            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, GQA group 1-8");
     if (nseqs <= 0 || max_rows <= 0) return;
     switch (a.group) {
         case 1: launch_g<1>(a, nseqs, max_rows, s); break;
         case 2: launch_g<2>(a, nseqs, max_rows, s); break;
+        case 3: launch_g<3>(a, nseqs, max_rows, s); break;
         case 4: launch_g<4>(a, nseqs, max_rows, s); break;
+        case 5: launch_g<5>(a, nseqs, max_rows, s); break;
+        case 6: launch_g<6>(a, nseqs, max_rows, s); break;
+        case 7: launch_g<7>(a, nseqs, max_rows, s); break;
         default: launch_g<8>(a, nseqs, max_rows, s); break;
     }
     TVARA_HIP(hipGetLastError());
