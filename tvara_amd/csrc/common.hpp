@@ -114,6 +114,7 @@ struct DecodeArgs {
     // for kernels that merge a row's splits in its last workgroup (zero between
     // launches; null: merge_kernel merges)
     int* row_done;
+    int wave_splits;  // > 0: each row's splits are the waves of one workgroup per (row, KV head)
     const float* q;
     const float* tail_k;  // [rows][kv_width] or null
     const float* tail_v;
@@ -157,6 +158,7 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
                    hipStream_t s);
 int decode_waves(int kv_heads, int group, int format, int head_dim);
 int decode_slots(int kv_heads, int group, int format, int head_dim);  // waves' worth of work per work item
+int wave_split_waves(int rows, int kv_heads, int group, int format, int head_dim, int tpb, size_t max_tokens);
 int decode_budget_per_cu(int group, int format, int head_dim);
 // prefill.hip
 bool prefill_bf16_supported(const BlockLayout& lay, int group);

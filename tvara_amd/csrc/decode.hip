@@ -205,7 +205,7 @@ __device__ __forceinline__ void merge_row_splits(const DecodeArgs& a, int lane, 
     }
 }
 
-template <int D, int G, int LPT, int E, class Col>
+template <int D, int G, int LPT, int E, bool kWS = false, class Col>
 __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G][E], RowState& st, int lane, int wave,
                                              int nwaves, int kh, int item, int first, int row, int nsplit, Col col) {
     extern __shared__ float lds[];
@@ -238,6 +238,28 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
         ml[G + c] = st.l;
     }
     __syncthreads();
+    if constexpr (kWS) {
+        // the waves hold consecutive splits of one (row, KV head): combine
+        // their partials by log-sum-exp in split order, in LDS
+        const float* ml0 = lds + static_cast<size_t>(nwaves) * 4 * G * D;
+        float* outw = a.out + (static_cast<size_t>(row) * a.heads + static_cast<size_t>(kh) * G) * D;
+        for (int o = static_cast<int>(threadIdx.x); o < G * D; o += static_cast<int>(blockDim.x)) {
+            const int h = o / D;
+            float M = -INFINITY;
+            for (int w = 0; w < nwaves; ++w) M = fmaxf(M, ml0[w * 2 * G + h]);
+            float L = 0.f, sum = 0.f;
+            for (int w = 0; w < nwaves; ++w) {
+                const float mw = ml0[w * 2 * G + h];
+                const float wt = mw == -INFINITY ? 0.f : fast_exp2(mw - M);
+                const float* r = lds + static_cast<size_t>(w) * 4 * G * D + o;
+                L = fmaf(wt, ml0[w * 2 * G + G + h], L);
+                sum = fmaf(wt, r[0] + r[G * D] + r[2 * G * D] + r[3 * G * D], sum);
+            }
+            outw[o] = sum / L;
+        }
+        if (__any(st.bad) && lane == 0) *a.err = 1;
+        return;
+    }
     const size_t head0 = static_cast<size_t>(kh) * G;
     float* out = a.out + (static_cast<size_t>(row) * a.heads + head0) * D;
     for (int o4 = lane; o4 < G * D / 4; o4 += 64) {
@@ -292,13 +314,20 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
 // 256 VGPRs: the 128-thread bound lets the compiler keep the rest in AGPRs
 // (one wave per SIMD) instead of scratch (Llama-3-70B shape, d=128: 120
 // against 469 us; Q8_0 73 against 510 us).
-template <int D, int G, int LPT, int NB>
-__global__ __launch_bounds__(G > 4 ? 128 : 512) void decode_f32_kernel(const DecodeArgs a) {
+//
+// kWS (wave splits): a workgroup takes one (row, KV head) and its waves take
+// the row's consecutive splits (the plan gives every row as many splits as
+// the workgroup has waves), merged in LDS: no second launch and no global
+// round trip, for launches too small to fill the GPU.
+template <int D, int G, int LPT, int NB, bool kWS>
+__global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(const DecodeArgs a) {
     constexpr int E = D / LPT, NV = E / 4, TT = 64 / LPT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-    const int groups = a.lay.kv_heads / nwaves;
-    const int item = static_cast<int>(blockIdx.x) / groups;
-    const int kh = (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
+    const int groups = kWS ? 1 : a.lay.kv_heads / nwaves;
+    const int item = kWS ? (static_cast<int>(blockIdx.x) / a.lay.kv_heads) * nwaves + wave
+                         : static_cast<int>(blockIdx.x) / groups;
+    const int kh = kWS ? static_cast<int>(blockIdx.x) % a.lay.kv_heads
+                       : (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
     // the item's descriptor and block ids come in two independent loads
     const int4 it = a.work[item];  // row, first token, end token, tail | splits << 1
     const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
@@ -422,8 +451,8 @@ __global__ __launch_bounds__(G > 4 ? 128 : 512) void decode_f32_kernel(const Dec
         }
         process(ka, va, ok);
     }
-    finish_split<D, G, LPT, E>(a, acc, st, lane, wave, nwaves, kh, item, item - t0 / a.split_tokens, it.x, nsplit,
-                               [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
+    finish_split<D, G, LPT, E, kWS>(a, acc, st, lane, wave, nwaves, kh, item, item - t0 / a.split_tokens, it.x,
+                                    nsplit, [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
 }
 
 // ------------------------------------------------------------- Q8_0 blocks
@@ -1231,7 +1260,37 @@ void launch_f32(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
     const dim3 grid(nitems * (a.lay.kv_heads / waves)), block(64 * waves);
     // two tiles in flight: a third needs more than the 256 VGPRs that keep two
     // waves per SIMD, and measured slower
-    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2>, grid, block, lds, s, a);
+    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, false>, grid, block, lds, s, a);
+}
+
+template <int D, int G, int LPT>
+void launch_f32_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
+    const int waves = a.wave_splits;
+    const size_t lds = (static_cast<size_t>(waves) * 4 * G * D + waves * 2 * G) * sizeof(float);
+    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, true>, dim3(nrows * a.lay.kv_heads), dim3(64 * waves), lds,
+           s, a);
+}
+
+template <int D>
+void dispatch_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
+    constexpr int LPT = D == 64 ? 4 : 8;
+    switch (a.group) {
+        case 1: launch_f32_ws<D, 1, LPT>(a, nrows, s); return;
+        case 2: launch_f32_ws<D, 2, LPT>(a, nrows, s); return;
+        case 3: launch_f32_ws<D, 3, LPT>(a, nrows, s); return;
+        case 4: launch_f32_ws<D, 4, LPT>(a, nrows, s); return;
+        default: break;
+    }
+    if constexpr (D == 64) {
+        switch (a.group) {
+            case 5: launch_f32_ws<D, 5, 8>(a, nrows, s); return;
+            case 6: launch_f32_ws<D, 6, 8>(a, nrows, s); return;
+            case 7: launch_f32_ws<D, 7, 8>(a, nrows, s); return;
+            case 8: launch_f32_ws<D, 8, 8>(a, nrows, s); return;
+            default: break;
+        }
+    }
+    throw std::logic_error("wave-split decode: unsupported shape");
 }
 
 template <int D, int G>
@@ -1373,6 +1432,22 @@ static int waves_for(const DecodeArgs& a) {
     return decode_waves(a.lay.kv_heads, a.group, a.lay.format, a.lay.head_dim);
 }
 
+// Wave splits (one workgroup per (row, KV head), its waves the row's splits):
+// f32 blocks, the fast shapes that fit 512-thread workgroups, and launches of
+// at most 32 (row, KV head) pairs.  Returns the waves (splits per row), 0 for
+// the usual decomposition.
+int wave_split_waves(int rows, int kv_heads, int group, int format, int head_dim, int tpb, size_t max_tokens) {
+    if (const char* env = std::getenv("TVARA_WAVE_SPLITS"); env && std::atoi(env) == 0) return 0;
+    if (format != kF32 || tpb != 16 || (head_dim != 64 && head_dim != 128)) return 0;
+    if (group > 8 || (head_dim == 128 && group > 4)) return 0;
+    if (static_cast<size_t>(rows) * kv_heads > 32 || max_tokens > 1024) return 0;
+    // one split of at least 64 tokens a wave, at most eight waves, the
+    // partials of every wave in 64 KiB of LDS
+    const size_t per_wave = (4 * static_cast<size_t>(group) * head_dim + 2 * group) * sizeof(float);
+    const int w = static_cast<int>(std::min<size_t>({8, (max_tokens + 63) / 64, 65536 / per_wave}));
+    return w >= 2 ? w : 0;
+}
+
 // the largest decode launch whose splits are merged in the kernel
 // (TVARA_INKERNEL_MERGE_MAX overrides it for tuning)
 constexpr int kInKernelMergeMaxWorkgroups = 128;
@@ -1384,6 +1459,11 @@ bool decode_fast_path(const DecodeArgs& a) {
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
                    hipStream_t s) {
     if (nitems <= 0) return;
+    if (a.wave_splits) {  // the plan chose wave splits (wave_split_shape): merged in LDS
+        a.lay.head_dim == 64 ? dispatch_ws<64>(a, nrows, s) : dispatch_ws<128>(a, nrows, s);
+        TVARA_HIP(hipGetLastError());
+        return;
+    }
     // Small launches of the f32 and vector Q8_0 kernels merge a row's splits
     // in its last workgroup: there the second launch is pure latency (the
     // SmolLM2-135M row: 7.7 against 8.3 us per step).  A launch that fills

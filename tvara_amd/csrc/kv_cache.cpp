@@ -556,6 +556,14 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     if (!split) {
         if (const char* env = std::getenv("TVARA_SPLIT_TOKENS")) split = std::strtoull(env, nullptr, 10);
     }
+    // A launch too small to fill the GPU gives every row one split per wave of
+    // a workgroup per (row, KV head), merged in LDS (wave_split_waves).
+    size_t max_n = 0;
+    for (size_t n : cached) max_n = std::max(max_n, n);
+    wave_splits = split ? 0
+                        : wave_split_waves(rows, static_cast<int>(g.kv_heads), group, c->format(),
+                                           static_cast<int>(g.head_dim), static_cast<int>(g.tokens_per_block), max_n);
+    if (wave_splits) split = round_up((max_n + wave_splits - 1) / wave_splits, 16);
     if (!split) {
         const int gw = static_cast<int>(g.kv_heads), gd = static_cast<int>(g.head_dim);
         const size_t groups = static_cast<size_t>(decode_slots(gw, group, c->format(), gd)) /
@@ -589,19 +597,19 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     for (int r = 0; r < rows; ++r) {
         const size_t n = cached[r];
         const int tail = tail_rows.empty() ? 0 : (tail_rows[r] ? 1 : 0);
-        const int nsplit = static_cast<int>(std::max<size_t>(1, (n + split - 1) / split));
+        const int nsplit = wave_splits ? wave_splits : static_cast<int>(std::max<size_t>(1, (n + split - 1) / split));
         const int first = static_cast<int>(its.size());
         const int32_t base = offset[seq_of_row[r]];
         ent[r] = make_int4(base, static_cast<int>(n), tail | (nsplit << 1), first);
         if (inline_ok) inline_rows.r[r] = make_int2(first, nsplit);
         for (int s = 0; s < nsplit; ++s) {
             its.push_back(make_int2(r, s));
-            const int t0 = static_cast<int>(s * split), t1 = static_cast<int>(std::min(n, (s + 1) * split));
+            const int t0 = static_cast<int>(std::min(n, s * split)), t1 = static_cast<int>(std::min(n, (s + 1) * split));
             work.push_back(make_int4(r, t0, t1, ((tail && s == nsplit - 1) ? 1 : 0) | (nsplit << 1)));
             const int nb = blocks16 ? (t1 - t0 + 15) / 16 : 0;
             for (int j = 0; j < kMaxSplitBlocks; ++j) work_ids.push_back(j < nb ? tab[base + t0 / 16 + j] : 0);
         }
-        need_merge |= nsplit > 1;
+        need_merge |= nsplit > 1 && !wave_splits;
         kv_bytes += static_cast<size_t>(static_cast<double>(n + tail) * g.kv_width() * 2 * bytes_per_element);
     }
     items = static_cast<int>(its.size());
@@ -655,6 +663,7 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.part_acc = static_cast<float*>(part_acc.ptr);
     a.part_ml = static_cast<float*>(part_ml.ptr);
     a.row_done = need_merge ? static_cast<int*>(row_done.ptr) : nullptr;
+    a.wave_splits = wave_splits;
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
     a.err = static_cast<int*>(err.ptr);
     launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, s);

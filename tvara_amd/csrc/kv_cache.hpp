@@ -138,6 +138,7 @@ struct AttnPlan {
     DeviceCache* cache = nullptr;
     uint64_t epoch = 0;
     int rows = 0, heads = 0, group = 0, items = 0, split_tokens = 0;
+    int wave_splits = 0;  // > 0: splits per row = waves of one workgroup per (row, KV head)
     bool need_merge = false, with_tail = false, inline_ok = false;
     size_t kv_bytes = 0;  // algorithmic K/V bytes one launch reads
     DeviceBuffer tables, entries, items_buf, work_buf, work_blocks, part_acc, part_ml, row_done, err;
