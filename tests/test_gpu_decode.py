@@ -410,3 +410,40 @@ def test_plan_back_to_back_launches(device, oracle, monkeypatch, fmt_name, dim, 
     for layer in (0, 1):
         want = np.stack([ref.fused_paged_attention(q[i], s, layer, heads, 1 << 20) for i, s in enumerate(seqs)])
         assert refmath.close(got[layer], want, TOL), refmath.max_rel(got[layer], want)
+
+
+@pytest.mark.parametrize("scale", ["fill", "small"], ids=["merge-launch", "merge-in-kernel"])
+def test_ragged_rows_with_tail_only_rows(device, oracle, scale):
+    # rows with no cached token (the tail is their only position), one-token
+    # rows and rows ending on and off block edges, in a launch that fills the
+    # GPU (merge_kernel combines the splits) and in a small one (the last
+    # workgroup of each row merges them)
+    if scale == "fill":
+        lengths = [0, 1, 16, 17, 4096, 0, 300, 2047, 64, 65, 1000, 3001, 5, 0, 777, 2500] * 4
+    else:
+        lengths = [0, 1, 16, 17, 100, 0, 300, 47, 64, 65, 200, 31, 5, 0, 77, 250] * 3
+    kv_heads, dim, group, tpb = 8, 64, 4, 16
+    heads = kv_heads * group
+    g = (1, kv_heads, dim, tpb, sum((n + tpb - 1) // tpb for n in lengths) + 4)
+    dev, ref = device.PagedCache(*g), oracle.Cache(*g)
+    w = kv_heads * dim
+    seqs = []
+    for i, n in enumerate(lengths):
+        s, r = dev.create_sequence(), ref.create_sequence()
+        if n:
+            k = synth.normal(41, f"k{i}", n * w).reshape(n, w)
+            v = synth.normal(41, f"v{i}", n * w).reshape(n, w)
+            dev.append_many(s, k, v)
+            ref.append_many(r, k, v)
+        seqs.append(s)
+    rows = len(lengths)
+    q = synth.normal(41, "q", rows * heads * dim).reshape(rows, heads * dim)
+    tk = synth.normal(41, "tk", rows * w).reshape(rows, w)
+    tv = synth.normal(41, "tv", rows * w).reshape(rows, w)
+    plan = attention.DecodePlan(dev, seqs, heads, 1 << 20, with_tail=True)
+    assert (plan.items <= 128) == (scale == "small")
+    say("ragged rows", scale, "rows", rows, "tokens", sum(lengths), "items", plan.items)
+    got = attention.decode_batch(dev, q, seqs, 0, heads, 1 << 20, tail_keys=tk, tail_values=tv)
+    want = np.stack([ref.fused_paged_attention(q[i], s, 0, heads, 1 << 20, tail_key=tk[i], tail_value=tv[i])
+                     for i, s in enumerate(seqs)])
+    assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
