@@ -1229,12 +1229,15 @@ void launch_merge_t(const DecodeArgs& a, const RowSplits& rs, int nrows, hipStre
     const int D = a.lay.head_dim;
     const dim3 grid(nrows, a.heads), block(256);
     // one wave per (row, head), four heads per workgroup (sixteen measured
-    // no faster on the Llama-3.2-1B batch and slower on the Llama-3-8B one)
+    // no faster on the Llama-3.2-1B batch and slower on the Llama-3-8B one);
+    // a wave requests 16 splits at d=64 and 32 at d=128 before using any, so
+    // rows of up to that many splits cost one memory round trip (Llama-3-8B
+    // batch, 32 splits a row: 4.5 against 4.8-4.9 us with 16 at d=128)
     const dim3 wgrid(nrows, (a.heads + 3) / 4), wblock(256);
     if (D == 64)
         launch("paged_decode_merge", merge_wave_kernel<16, 4, kInline>, wgrid, wblock, 0, s, a, rs);
     else if (D == 128)
-        launch("paged_decode_merge", merge_wave_kernel<32, 8, kInline>, wgrid, wblock, 0, s, a, rs);
+        launch("paged_decode_merge", merge_wave_kernel<32, 16, kInline>, wgrid, wblock, 0, s, a, rs);
     else if (D == 256)
         launch("paged_decode_merge", merge_wave_kernel<64, 8, kInline>, wgrid, wblock, 0, s, a, rs);
     else if (D == 32)
