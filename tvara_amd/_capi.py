@@ -177,16 +177,29 @@ def model_lib(explicit=None):
     return handle
 
 
-def last_error() -> str:
-    msg = lib().tvara_last_error()
+def bind_subset(path):
+    """Any build that exports part of this ABI (the CPU test harness of the
+    ledger and prefix-cache exports): binds the names it has."""
+    handle = C.CDLL(str(Path(path).resolve()))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(handle, name, None)
+        if fn is not None:
+            fn.restype = restype
+            fn.argtypes = argtypes
+    return handle
+
+
+def last_error(library=None) -> str:
+    msg = (library or lib()).tvara_last_error()
     return msg.decode("utf-8", errors="replace") if msg else "native operation failed"
 
 
-def check(rc: int) -> None:
+def check(rc: int, library=None) -> None:
     if rc != OK:
-        raise _ERRORS.get(rc, NativeError)(last_error())
+        raise _ERRORS.get(rc, NativeError)(last_error(library))
 
 
-def raise_last():
+def raise_last(library=None):
     """Raise for a failed NULL- or 0-returning call."""
-    raise _ERRORS.get(lib().tvara_last_status(), NativeError)(last_error())
+    library = library or lib()
+    raise _ERRORS.get(library.tvara_last_status(), NativeError)(last_error(library))

@@ -13,9 +13,9 @@
 #include <string>
 #include <vector>
 
+#include "abi.hpp"
 #include "kv_cache.hpp"
 #include "model.hpp"
-#include "radix.hpp"
 
 using tvara_amd::AttnPlan;
 using tvara_amd::DeviceCache;
@@ -30,10 +30,6 @@ struct tvara_kv_cache {
     tvara_kv_cache(const Geometry& g, int format)
         : owned(std::make_unique<DeviceCache>(g, format)), cache(owned.get()) {}
     explicit tvara_kv_cache(DeviceCache* lent) : cache(lent) {}
-};
-
-struct tvara_radix {
-    std::unique_ptr<tvara_amd::RadixCache> tree;
 };
 
 struct tvara_attn_plan {
@@ -59,43 +55,16 @@ void profile_read(const char* prefix, double* ms, size_t* launches);
 void profile_reset();
 }  // namespace tvara_amd
 
+using tvara_amd::abi::exported;
+using tvara_amd::abi::failed;
+using tvara_amd::abi::guard;
+using tvara_amd::abi::handle;
+
 namespace {
-thread_local std::string error_message;
-thread_local int error_status = TVARA_OK;
-
-int failed(int status, const char* what) {
-    error_message = what;
-    error_status = status;
-    return status;
-}
-
-template <class F>
-int guard(F&& f) {
-    error_message.clear();
-    error_status = TVARA_OK;
-    try {
-        f();
-        return TVARA_OK;
-    } catch (const tvara_amd::CacheExhausted& e) {
-        return failed(TVARA_EXHAUSTED, e.what());
-    } catch (const std::invalid_argument& e) {
-        return failed(TVARA_INVALID, e.what());
-    } catch (const std::logic_error& e) {
-        return failed(TVARA_LOGIC, e.what());
-    } catch (const std::exception& e) {
-        return failed(TVARA_ERROR, e.what());
-    } catch (...) {
-        return failed(TVARA_ERROR, "unknown native error");
-    }
-}
-
 DeviceCache& live(tvara_kv_cache* c) {
     if (!c) throw std::invalid_argument("closed KV cache");
     return *c->cache;
 }
-
-Handle handle(tvara_kv_handle h) { return Handle{static_cast<size_t>(h.id), h.generation}; }
-tvara_kv_handle exported(Handle h) { return tvara_kv_handle{h.id, h.generation}; }
 
 // ModelConfig::validate (model.hpp:13-19), the part attention depends on
 void check_config(const DeviceCache& c, size_t heads, size_t context) {
@@ -148,11 +117,9 @@ struct Staged {
 };
 }  // namespace
 
+tvara_amd::KvLedger& tvara_amd::abi::ledger_of(tvara_kv_cache* cache) { return live(cache).ledger(); }
+
 extern "C" {
-
-const char* tvara_last_error(void) { return error_message.c_str(); }
-
-int tvara_last_status(void) { return error_status; }
 
 tvara_kv_cache* tvara_kv_cache_create(size_t layers, size_t kv_heads, size_t head_dim, size_t tokens_per_block,
                                       size_t max_blocks, int format) {
@@ -185,44 +152,6 @@ int tvara_kv_synchronize(tvara_kv_cache* cache) {
     });
 }
 
-int tvara_kv_pool_allocate(tvara_kv_cache* cache, tvara_kv_handle* out) {
-    return guard([&] {
-        if (!out) throw std::invalid_argument("null handle output");
-        *out = exported(live(cache).allocate());
-    });
-}
-
-int tvara_kv_pool_retain(tvara_kv_cache* cache, tvara_kv_handle h) {
-    return guard([&] { live(cache).retain(handle(h)); });
-}
-
-int tvara_kv_pool_release(tvara_kv_cache* cache, tvara_kv_handle h) {
-    return guard([&] { live(cache).release(handle(h)); });
-}
-
-int tvara_kv_pool_references(tvara_kv_cache* cache, tvara_kv_handle h, size_t* out) {
-    return guard([&] { *out = live(cache).references(handle(h)); });
-}
-
-int tvara_kv_pool_references_by_id(tvara_kv_cache* cache, size_t id, size_t* out) {
-    return guard([&] { *out = live(cache).references_by_id(id); });
-}
-
-size_t tvara_kv_pool_available(tvara_kv_cache* cache) {
-    size_t n = 0;
-    guard([&] { n = live(cache).available(); });
-    return n;
-}
-
-int tvara_kv_pool_audit(tvara_kv_cache* cache) {
-    return guard([&] { live(cache).pool_audit(); });
-}
-
-int tvara_kv_pool_state(tvara_kv_cache* cache, size_t* refs, uint64_t* generations, size_t* free_pop_order,
-                        size_t* free_count) {
-    return guard([&] { live(cache).pool_state(refs, generations, free_pop_order, free_count); });
-}
-
 int tvara_kv_block_read(tvara_kv_cache* cache, tvara_kv_handle h, void* out, size_t bytes) {
     return guard([&] { live(cache).block_read(handle(h), out, bytes); });
 }
@@ -238,40 +167,6 @@ int tvara_kv_block_checksums(tvara_kv_cache* cache, const tvara_kv_handle* handl
         for (size_t i = 0; i < count; ++i) hs[i] = handle(handles[i]);
         live(cache).checksums(hs.data(), count, out);
     });
-}
-
-uint64_t tvara_kv_sequence_create(tvara_kv_cache* cache) {
-    uint64_t id = 0;
-    guard([&] { id = live(cache).create_sequence(); });
-    return id;
-}
-
-int tvara_kv_sequence(tvara_kv_cache* cache, uint64_t sequence, size_t* length, tvara_kv_handle* blocks,
-                      size_t capacity, size_t* count) {
-    return guard([&] {
-        const auto& t = live(cache).sequence(sequence);
-        if (length) *length = t.length;
-        if (count) *count = t.blocks.size();
-        if (blocks) {
-            if (capacity < t.blocks.size()) throw std::invalid_argument("block list buffer too small");
-            for (size_t i = 0; i < t.blocks.size(); ++i) blocks[i] = exported(t.blocks[i]);
-        }
-    });
-}
-
-int tvara_kv_sequence_ids(tvara_kv_cache* cache, uint64_t* ids, size_t capacity, size_t* count) {
-    return guard([&] {
-        auto v = live(cache).sequence_ids();
-        if (count) *count = v.size();
-        if (ids) {
-            if (capacity < v.size()) throw std::invalid_argument("id buffer too small");
-            std::copy(v.begin(), v.end(), ids);
-        }
-    });
-}
-
-int tvara_kv_physical_block(tvara_kv_cache* cache, uint64_t sequence, size_t position, tvara_kv_handle* out) {
-    return guard([&] { *out = exported(live(cache).physical_block(sequence, position)); });
 }
 
 int tvara_kv_append(tvara_kv_cache* cache, uint64_t sequence, const float* keys, const float* values) {
@@ -302,36 +197,6 @@ int tvara_kv_read(tvara_kv_cache* cache, uint64_t sequence, size_t layer, size_t
 int tvara_kv_read_all(tvara_kv_cache* cache, uint64_t sequence, size_t layer, int value, float* out,
                       size_t capacity) {
     return guard([&] { live(cache).read_all(sequence, layer, value != 0, out, out ? capacity : 0); });
-}
-
-int tvara_kv_drop(tvara_kv_cache* cache, uint64_t sequence) {
-    return guard([&] { live(cache).drop(sequence); });
-}
-
-uint64_t tvara_kv_fork(tvara_kv_cache* cache, uint64_t sequence) {
-    uint64_t id = 0;
-    guard([&] { id = live(cache).fork(sequence); });
-    return id;
-}
-
-int tvara_kv_truncate(tvara_kv_cache* cache, uint64_t sequence, size_t length) {
-    return guard([&] { live(cache).truncate(sequence, length); });
-}
-
-int tvara_kv_audit(tvara_kv_cache* cache, const size_t* external, size_t count) {
-    return guard([&] { live(cache).audit(external, external ? count : 0); });
-}
-
-uint64_t tvara_kv_import_sequence(tvara_kv_cache* cache, const tvara_kv_handle* blocks, size_t block_count,
-                                  size_t source_length, size_t length) {
-    uint64_t id = 0;
-    guard([&] {
-        if (block_count && !blocks) throw std::invalid_argument("null snapshot blocks");
-        std::vector<Handle> hs(block_count);
-        for (size_t i = 0; i < block_count; ++i) hs[i] = handle(blocks[i]);
-        id = live(cache).import_sequence(hs.data(), block_count, source_length, length);
-    });
-    return id;
 }
 
 int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t layer, size_t heads,
@@ -486,8 +351,7 @@ void tvara_prefill_plan_destroy(tvara_prefill_plan* plan) { delete plan; }
 // per-handle lock are the reference's.
 
 tvara_model* tvara_model_open(const char* path, size_t blocks, size_t tokens) {
-    error_message.clear();
-    error_status = TVARA_OK;
+    tvara_amd::abi::clear();
     try {
         if (!path || !*path) throw std::invalid_argument("empty model path");
         auto m = std::make_unique<tvara_model>();
@@ -530,8 +394,7 @@ const char* tvara_model_metadata(tvara_model* model) {
 }
 
 uint64_t tvara_sequence_create(tvara_model* model) {
-    error_message.clear();
-    error_status = TVARA_OK;
+    tvara_amd::abi::clear();
     try {
         if (!model) throw std::invalid_argument("closed model");
         std::lock_guard<std::mutex> lock(model->mutex);
@@ -546,8 +409,7 @@ uint64_t tvara_sequence_create(tvara_model* model) {
 }
 
 int tvara_sequence_decode(tvara_model* model, uint64_t sequence, uint32_t token, float* logits, size_t count) {
-    error_message.clear();
-    error_status = TVARA_OK;
+    tvara_amd::abi::clear();
     try {
         if (!model || !logits || count != model->model->config().vocab)
             throw std::invalid_argument("invalid logit output buffer");
@@ -564,8 +426,7 @@ int tvara_sequence_decode(tvara_model* model, uint64_t sequence, uint32_t token,
 }
 
 int tvara_sequence_drop(tvara_model* model, uint64_t sequence) {
-    error_message.clear();
-    error_status = TVARA_OK;
+    tvara_amd::abi::clear();
     try {
         if (!model) throw std::invalid_argument("closed model");
         std::lock_guard<std::mutex> lock(model->mutex);
@@ -582,8 +443,7 @@ int tvara_sequence_drop(tvara_model* model, uint64_t sequence) {
 
 int tvara_sequence_decode_batch(tvara_model* model, uint64_t sequence, const uint32_t* tokens, size_t token_count,
                                 float* logits, size_t count) {
-    error_message.clear();
-    error_status = TVARA_OK;
+    tvara_amd::abi::clear();
     try {
         if (!model || (!tokens && token_count) || (!logits && count)) throw std::invalid_argument("invalid batch buffers");
         const size_t vocab = model->model->config().vocab;
@@ -612,8 +472,7 @@ int tvara_sequence_decode_batch(tvara_model* model, uint64_t sequence, const uin
 }
 
 int tvara_sequence_truncate(tvara_model* model, uint64_t sequence, size_t length) {
-    error_message.clear();
-    error_status = TVARA_OK;
+    tvara_amd::abi::clear();
     try {
         if (!model) throw std::invalid_argument("closed model");
         std::lock_guard<std::mutex> lock(model->mutex);
@@ -630,8 +489,7 @@ int tvara_sequence_truncate(tvara_model* model, uint64_t sequence, size_t length
 
 int tvara_sequences_decode(tvara_model* model, const uint64_t* sequences, const uint32_t* tokens, size_t count,
                            float* logits, size_t logits_count) {
-    error_message.clear();
-    error_status = TVARA_OK;
+    tvara_amd::abi::clear();
     try {
         if (!model || (count && (!sequences || !tokens || !logits))) throw std::invalid_argument("invalid batch buffers");
         const size_t vocab = model->model->config().vocab;
@@ -658,110 +516,6 @@ tvara_kv_cache* tvara_model_cache(tvara_model* model) {
         return nullptr;
     }
     return model->kv.get();
-}
-
-// ------------------------------------------------------------- prefix cache
-// RadixCache (radix.hpp:17-131) over a cache handle
-
-tvara_radix* tvara_radix_create(tvara_kv_cache* cache, const char* isolation) {
-    tvara_radix* out = nullptr;
-    guard([&] {
-        auto r = std::make_unique<tvara_radix>();
-        r->tree = std::make_unique<tvara_amd::RadixCache>(live(cache), isolation ? isolation : "");
-        out = r.release();
-    });
-    return out;
-}
-
-void tvara_radix_destroy(tvara_radix* radix) { delete radix; }
-
-namespace {
-tvara_amd::RadixCache& tree(tvara_radix* r) {
-    if (!r) throw std::invalid_argument("closed prefix cache");
-    return *r->tree;
-}
-}  // namespace
-
-int tvara_radix_insert(tvara_radix* radix, const int32_t* tokens, size_t count, uint64_t* node) {
-    return guard([&] {
-        if (!tokens && count) throw std::invalid_argument("invalid prefix tokens");
-        const uint64_t id = tree(radix).insert(tokens, count);
-        if (node) *node = id;
-    });
-}
-
-int tvara_radix_lookup(tvara_radix* radix, const int32_t* tokens, size_t count, uint64_t* node, size_t* matched) {
-    return guard([&] {
-        if (!tokens && count) throw std::invalid_argument("invalid prefix tokens");
-        const auto m = tree(radix).lookup(tokens, count);
-        if (node) *node = m.first;
-        if (matched) *matched = m.second;
-    });
-}
-
-int tvara_radix_attach(tvara_radix* radix, uint64_t node, uint64_t sequence) {
-    return guard([&] { tree(radix).attach(node, sequence); });
-}
-
-int tvara_radix_reuse(tvara_radix* radix, const int32_t* tokens, size_t count, int partial, uint64_t* sequence,
-                      size_t* length) {
-    return guard([&] {
-        if (!tokens && count) throw std::invalid_argument("invalid prefix tokens");
-        const auto r = tree(radix).reuse(tokens, count, partial != 0);
-        if (sequence) *sequence = r.first;
-        if (length) *length = r.second;
-    });
-}
-
-int tvara_radix_pin(tvara_radix* radix, uint64_t node) { return guard([&] { tree(radix).pin(node); }); }
-int tvara_radix_unpin(tvara_radix* radix, uint64_t node) { return guard([&] { tree(radix).unpin(node); }); }
-int tvara_radix_touch(tvara_radix* radix, uint64_t node) { return guard([&] { tree(radix).touch(node); }); }
-
-int tvara_radix_eviction_candidate(tvara_radix* radix, uint64_t* node) {
-    return guard([&] {
-        const auto c = tree(radix).eviction_candidate();
-        if (node) *node = c ? *c : 0;
-    });
-}
-
-int tvara_radix_evict_one(tvara_radix* radix, int* evicted) {
-    return guard([&] {
-        const bool e = tree(radix).evict_one();
-        if (evicted) *evicted = e ? 1 : 0;
-    });
-}
-
-int tvara_radix_reset(tvara_radix* radix) { return guard([&] { tree(radix).reset(); }); }
-
-int tvara_radix_size(tvara_radix* radix, size_t* size) {
-    return guard([&] {
-        const size_t n = tree(radix).size();
-        if (size) *size = n;
-    });
-}
-
-int tvara_radix_node(tvara_radix* radix, uint64_t id, uint64_t* parent, int32_t* edge, size_t edge_capacity,
-                     size_t* edge_length, size_t* pins, uint64_t* accessed, size_t* kv_length, size_t* kv_blocks,
-                     size_t* children) {
-    return guard([&] {
-        const tvara_amd::RadixNode& n = tree(radix).node(id);
-        if (parent) *parent = n.parent;
-        if (edge_length) *edge_length = n.edge.size();
-        if (edge) std::copy(n.edge.begin(), n.edge.begin() + std::min(edge_capacity, n.edge.size()), edge);
-        if (pins) *pins = n.pins;
-        if (accessed) *accessed = n.accessed;
-        if (kv_length) *kv_length = n.kv ? n.kv->length : 0;
-        if (kv_blocks) *kv_blocks = n.kv ? n.kv->blocks.size() : static_cast<size_t>(-1);
-        if (children) *children = n.children.size();
-    });
-}
-
-int tvara_radix_external_references(tvara_radix* radix, size_t* counts, size_t capacity) {
-    return guard([&] {
-        const auto c = tree(radix).external_references();
-        if (!counts || capacity < c.size()) throw std::invalid_argument("reference count buffer too small");
-        std::copy(c.begin(), c.end(), counts);
-    });
 }
 
 int tvara_profile_enable(int enabled) {

@@ -9,12 +9,9 @@
 #include <stdexcept>
 #include <string>
 
-namespace tvara_amd {
+#include "kv_ledger.hpp"
 
-// tvara::CacheExhausted (kv.hpp:34)
-struct CacheExhausted : std::runtime_error {
-    CacheExhausted() : std::runtime_error("KV cache exhausted") {}
-};
+namespace tvara_amd {
 
 inline void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
@@ -55,13 +52,6 @@ __host__ __device__ inline size_t q8_scale_offset(const BlockLayout& lay, int sl
            (static_cast<size_t>(slot) * ng + (group - h * ng)) * 2;
 }
 
-// Block initialisation: zero-fill (src < 0, BlockPool::allocate, kv.hpp:48)
-// or whole-block copy (copy-on-write, kv.hpp:99).
-struct BlockInitOp {
-    int64_t dst;
-    int64_t src;
-};
-
 // Block work passed in the kernel arguments (no upload) when a call has at
 // most kInlineOps of it: init ops as (dst, src or -1) int32 pairs, row ops as
 // (block, slot << 16 | input row) with slot and row below 65,536.
@@ -71,14 +61,6 @@ struct InlineInitOps {
 };
 struct InlineRowOps {
     int2 op[kInlineOps];
-};
-
-// One appended token: destination block, slot and the row of the input.
-struct RowOp {
-    int32_t block;
-    int32_t slot;
-    int32_t src_row;
-    int32_t pad;
 };
 
 // Decode work: one entry per attention row (a sequence for decode, a

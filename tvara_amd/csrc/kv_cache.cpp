@@ -1,9 +1,7 @@
-// Host side of the device paged KV cache.  The allocator and block tables
-// follow the reference's rules exactly (core/include/tvara/kv.hpp): LIFO free
-// list handing out 0, 1, 2, ... from a fresh pool, generation-tagged handles,
-// zero-on-allocate, copy-on-write of a shared partial tail, truncation that
-// keeps stale slots, and CacheExhausted leaving an append unapplied.  Block
-// bytes live in HBM and are only touched by the kernels in kv_kernels.hip.
+// Device half of the paged KV cache: block storage in one HBM allocation,
+// every byte movement done by the gfx950 kernels of kv_kernels.hip, and the
+// host bookkeeping (pool, tables, append planning) in KvLedger
+// (kv_ledger.cpp), which follows core/include/tvara/kv.hpp.
 #include "kv_cache.hpp"
 
 #include <algorithm>
@@ -23,32 +21,6 @@ size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 enum Slot { kInitOps = 0, kRowOps = 1, kKeys = 2, kValues = 3, kMisc = 4, kMiscOut = 5 };
 }  // namespace
-
-// ------------------------------------------------------------- geometry
-
-// CacheGeometry::kv_width (kv.hpp:14-17)
-size_t Geometry::kv_width() const {
-    if (!kv_heads || !head_dim || kv_heads > kMax / head_dim) throw std::invalid_argument("KV width overflow");
-    return kv_heads * head_dim;
-}
-
-// CacheGeometry::elements_per_block (kv.hpp:18-23)
-size_t Geometry::elements_per_block() const {
-    size_t count = kv_width();
-    for (size_t dim : {layers, tokens_per_block, size_t(2)}) {
-        if (!dim || count > kMax / dim) throw std::invalid_argument("KV block overflow");
-        count *= dim;
-    }
-    return count;
-}
-
-// CacheGeometry::validate (kv.hpp:24-28)
-void Geometry::validate() const {
-    const size_t elements = elements_per_block();
-    if (!max_blocks || max_blocks > 1000000 || elements > kMax / sizeof(float) / max_blocks ||
-        tokens_per_block > kMax / max_blocks)
-        throw std::invalid_argument("KV capacity overflow");
-}
 
 // -------------------------------------------------------------- buffers
 
@@ -109,43 +81,39 @@ static T* upload(DeviceCache& c, int slot, const T* data, size_t count) {
     return static_cast<T*>(dev);
 }
 
-// -------------------------------------------------------------- the pool
+// ------------------------------------------------------- the block store
 
-DeviceCache::DeviceCache(const Geometry& g, int format) : g_(g), format_(format) {
-    g_.validate();
+DeviceCache::DeviceCache(const Geometry& g, int format) : meta_(g), format_(format) {
+    const Geometry& geo = meta_.geometry();
     if (format != kF32 && format != kQ8) throw std::invalid_argument("unknown KV format");
-    const size_t kvw = g_.kv_width();
-    if (format == kQ8 && g_.head_dim % 32) throw std::invalid_argument("Q8_0 KV needs head_dim divisible by 32");
-    if (g_.max_blocks > static_cast<size_t>(std::numeric_limits<int32_t>::max()) ||
+    const size_t kvw = geo.kv_width();
+    if (format == kQ8 && geo.head_dim % 32) throw std::invalid_argument("Q8_0 KV needs head_dim divisible by 32");
+    if (geo.max_blocks > static_cast<size_t>(std::numeric_limits<int32_t>::max()) ||
         kvw > static_cast<size_t>(std::numeric_limits<int32_t>::max() / 16) ||
-        g_.layers > 65535 / 2 || g_.tokens_per_block > (1u << 20))
+        geo.layers > 65535 / 2 || geo.tokens_per_block > (1u << 20))
         throw std::invalid_argument("KV geometry outside the device kernels' index range");
     lay_.format = format;
-    lay_.layers = static_cast<int>(g_.layers);
-    lay_.kv_heads = static_cast<int>(g_.kv_heads);
-    lay_.head_dim = static_cast<int>(g_.head_dim);
-    lay_.tpb = static_cast<int>(g_.tokens_per_block);
+    lay_.layers = static_cast<int>(geo.layers);
+    lay_.kv_heads = static_cast<int>(geo.kv_heads);
+    lay_.head_dim = static_cast<int>(geo.head_dim);
+    lay_.tpb = static_cast<int>(geo.tokens_per_block);
     lay_.kv_width = static_cast<int>(kvw);
     if (format == kF32) {
-        lay_.section = g_.tokens_per_block * kvw * sizeof(float);
-        lay_.stride = round_up(g_.elements_per_block() * sizeof(float), 256);
+        lay_.section = geo.tokens_per_block * kvw * sizeof(float);
+        lay_.stride = round_up(geo.elements_per_block() * sizeof(float), 256);
     } else {
-        lay_.head_bytes = round_up(g_.tokens_per_block * g_.head_dim + g_.tokens_per_block * (g_.head_dim / 32) * 2, 16);
-        lay_.section = g_.kv_heads * lay_.head_bytes;
-        lay_.stride = round_up(2 * g_.layers * lay_.section, 256);
+        lay_.head_bytes =
+            round_up(geo.tokens_per_block * geo.head_dim + geo.tokens_per_block * (geo.head_dim / 32) * 2, 16);
+        lay_.section = geo.kv_heads * lay_.head_bytes;
+        lay_.stride = round_up(2 * geo.layers * lay_.section, 256);
     }
-    if (lay_.stride > kMax / g_.max_blocks) throw std::invalid_argument("KV capacity overflow");
+    if (lay_.stride > kMax / geo.max_blocks) throw std::invalid_argument("KV capacity overflow");
     int dev = 0;
     TVARA_HIP(hipGetDevice(&dev));
     TVARA_HIP(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
-    TVARA_HIP(hipMalloc(&pool_, lay_.stride * g_.max_blocks));
+    TVARA_HIP(hipMalloc(&pool_, lay_.stride * geo.max_blocks));
     TVARA_HIP(hipMalloc(&err_, sizeof(int)));
     TVARA_HIP(hipMemset(err_, 0, sizeof(int)));
-    refs_.assign(g_.max_blocks, 0);
-    gens_.assign(g_.max_blocks, 0);
-    zero_pending_.assign(g_.max_blocks, 0);
-    free_.reserve(g_.max_blocks);
-    for (size_t i = g_.max_blocks; i > 0; --i) free_.push_back(i - 1);  // kv.hpp:42
 }
 
 DeviceCache::~DeviceCache() {
@@ -155,104 +123,25 @@ DeviceCache::~DeviceCache() {
 }
 
 size_t DeviceCache::canonical_block_bytes() const {
-    const size_t elements = g_.elements_per_block();
+    const size_t elements = geometry().elements_per_block();
     return format_ == kF32 ? elements * sizeof(float) : elements / 32 * 34;
 }
 
 void DeviceCache::synchronize() { TVARA_HIP(hipStreamSynchronize(stream_)); }
 
-// BlockPool::validated (kv.hpp:68-72)
-const Handle& DeviceCache::validated(Handle h) const {
-    static thread_local Handle out;
-    if (h.id >= g_.max_blocks || !refs_[h.id] || gens_[h.id] != h.generation)
-        throw std::invalid_argument("stale or invalid KV handle");
-    out = h;
-    return out;
-}
-
-// BlockPool::allocate (kv.hpp:44-50) without the zero-fill
-Handle DeviceCache::take_free() {
-    if (free_.empty()) throw CacheExhausted();
-    const size_t id = free_.back();
-    if (gens_[id] == std::numeric_limits<uint64_t>::max()) throw std::runtime_error("KV generation exhausted");
-    free_.pop_back();
-    refs_[id] = 1;
-    ++gens_[id];
-    zero_pending_[id] = 0;
-    ++epoch_;
-    return {id, gens_[id]};
-}
-
-// BlockPool::allocate (kv.hpp:44-50).  The zero-fill is queued and runs, batched,
-// before the next device access of the cache.
-Handle DeviceCache::allocate() {
-    Handle h = take_free();
-    zero_pending_[h.id] = 1;
-    zero_list_.push_back(h.id);
-    return h;
-}
-
+// BlockPool::allocate's zero-fill (kv.hpp:48), batched over every block handed
+// out since the last device access
 void DeviceCache::flush() {
-    if (zero_list_.empty()) return;
-    std::vector<BlockInitOp> ops;
-    for (size_t id : zero_list_)
-        if (zero_pending_[id] && refs_[id]) {
-            ops.push_back({static_cast<int64_t>(id), -1});
-            zero_pending_[id] = 0;
-        }
-    zero_list_.clear();
-    if (ops.empty()) return;
+    const std::vector<int64_t> ids = meta_.take_pending_zero_fills();
+    if (ids.empty()) return;
+    std::vector<BlockInitOp> ops(ids.size());
+    for (size_t i = 0; i < ids.size(); ++i) ops[i] = {ids[i], -1};
     auto* d = upload(*this, kInitOps, ops.data(), ops.size());
     launch_block_init(pool_, lay_.stride, d, static_cast<int>(ops.size()), stream_);
 }
 
-// BlockPool::retain (kv.hpp:56)
-void DeviceCache::retain(Handle h) {
-    validated(h);
-    if (refs_[h.id] == kMax) throw std::runtime_error("KV reference overflow");
-    ++refs_[h.id];
-    ++epoch_;
-}
-
-// BlockPool::release (kv.hpp:57)
-void DeviceCache::release(Handle h) {
-    validated(h);
-    if (--refs_[h.id] == 0) free_.push_back(h.id);
-    ++epoch_;
-}
-
-// BlockPool::references (kv.hpp:58)
-size_t DeviceCache::references(Handle h) const {
-    validated(h);
-    return refs_[h.id];
-}
-
-// BlockPool::references_by_id (kv.hpp:59): blocks_.at() throws out_of_range
-size_t DeviceCache::references_by_id(size_t id) const {
-    if (id >= g_.max_blocks) throw std::out_of_range("KV block id out of range");
-    return refs_[id];
-}
-
-// BlockPool::audit (kv.hpp:61-64)
-void DeviceCache::pool_audit() const {
-    std::vector<bool> seen(g_.max_blocks);
-    for (size_t id : free_) {
-        if (id >= g_.max_blocks || seen[id] || refs_[id]) throw std::logic_error("KV free-list invariant");
-        seen[id] = true;
-    }
-    for (size_t i = 0; i < g_.max_blocks; ++i)
-        if (seen[i] != (refs_[i] == 0)) throw std::logic_error("KV allocation invariant");
-}
-
-void DeviceCache::pool_state(size_t* refs, uint64_t* generations, size_t* free_pop_order, size_t* free_count) const {
-    if (refs) std::copy(refs_.begin(), refs_.end(), refs);
-    if (generations) std::copy(gens_.begin(), gens_.end(), generations);
-    if (free_pop_order) std::copy(free_.rbegin(), free_.rend(), free_pop_order);
-    if (free_count) *free_count = free_.size();
-}
-
 void DeviceCache::block_read(Handle h, void* out, size_t bytes) {
-    validated(h);
+    meta_.check_live(h);
     if (!out || bytes != canonical_block_bytes()) throw std::invalid_argument("block buffer size mismatch");
     flush();
     if (format_ == kF32) {
@@ -266,7 +155,7 @@ void DeviceCache::block_read(Handle h, void* out, size_t bytes) {
 }
 
 void DeviceCache::block_write(Handle h, size_t offset, const void* data, size_t bytes) {
-    validated(h);
+    meta_.check_live(h);
     const size_t total = canonical_block_bytes();
     if (!data || offset > total || bytes > total - offset) throw std::invalid_argument("write outside block");
     flush();
@@ -285,7 +174,10 @@ void DeviceCache::block_write(Handle h, size_t offset, const void* data, size_t 
 
 void DeviceCache::checksums(const Handle* handles, size_t n, uint64_t* out) {
     std::vector<int64_t> ids(n);
-    for (size_t i = 0; i < n; ++i) ids[i] = static_cast<int64_t>(validated(handles[i]).id);
+    for (size_t i = 0; i < n; ++i) {
+        meta_.check_live(handles[i]);
+        ids[i] = static_cast<int64_t>(handles[i].id);
+    }
     if (!n) return;
     flush();
     auto* d = upload(*this, kMisc, ids.data(), n);
@@ -295,118 +187,48 @@ void DeviceCache::checksums(const Handle* handles, size_t n, uint64_t* out) {
     synchronize();
 }
 
-// ------------------------------------------------------------ the tables
-
-// PagedCache::create_sequence (kv.hpp:81)
-uint64_t DeviceCache::create_sequence() {
-    if (next_ == std::numeric_limits<uint64_t>::max()) throw std::runtime_error("sequence ID exhausted");
-    const uint64_t id = ++next_;
-    sequences_.emplace(id, Table{});
-    ++epoch_;
-    return id;
-}
-
-// PagedCache::sequence (kv.hpp:82-84)
-const Table& DeviceCache::sequence(uint64_t id) const {
-    auto it = sequences_.find(id);
-    if (it == sequences_.end()) throw std::invalid_argument("unknown KV sequence");
-    return it->second;
-}
-
-Table& DeviceCache::mutable_sequence(uint64_t id) { return const_cast<Table&>(sequence(id)); }
-
-std::vector<uint64_t> DeviceCache::sequence_ids() const {
-    std::vector<uint64_t> ids;
-    ids.reserve(sequences_.size());
-    for (auto& kv : sequences_) ids.push_back(kv.first);
-    return ids;
-}
-
-// PagedCache::physical_block (kv.hpp:85-87)
-Handle DeviceCache::physical_block(uint64_t id, size_t position) const {
-    const auto& t = sequence(id);
-    if (position >= t.length) throw std::invalid_argument("KV position beyond sequence");
-    return t.blocks.at(position / g_.tokens_per_block);
-}
-
-// Appends in order, each following PagedCache::append (kv.hpp:91-108) on the
-// host metadata, then runs the block work of all applied appends as two
+// Appends in order (KvLedger::plan_appends follows PagedCache::append,
+// kv.hpp:91-108), then runs the block work of all applied appends as two
 // launches: zero-fills and copy-on-write copies first, then the row writes.
-// Within one call no append writes a block another append copies from: a block
-// is written in place only when its reference count is 1, and reference counts
-// never grow during appends.
 size_t DeviceCache::append_batch(const uint64_t* seqs, size_t n, const float* keys, const float* values, bool device,
                                  size_t* applied_out) {
     if (n && (!seqs || !keys || !values)) throw std::invalid_argument("invalid paged KV append dimensions");
-    std::vector<BlockInitOp> init;
-    std::vector<RowOp> rows;
-    std::exception_ptr failure;
-    size_t applied = 0;
-    for (; applied < n; ++applied) {
-        try {
-            Table& t = mutable_sequence(seqs[applied]);
-            if (t.length >= g_.max_blocks * g_.tokens_per_block)
-                throw std::invalid_argument("invalid paged KV append dimensions");
-            const size_t slot = t.length % g_.tokens_per_block;
-            if (slot == 0) {  // kv.hpp:96
-                Handle h = take_free();
-                try {
-                    t.blocks.push_back(h);
-                } catch (...) {
-                    release(h);
-                    throw;
-                }
-                init.push_back({static_cast<int64_t>(h.id), -1});
-            } else if (refs_[t.blocks.back().id] > 1) {  // kv.hpp:97-101
-                const Handle original = t.blocks.back();
-                const Handle replacement = take_free();
-                init.push_back({static_cast<int64_t>(replacement.id), static_cast<int64_t>(original.id)});
-                t.blocks.back() = replacement;
-                release(original);
-            }
-            rows.push_back({static_cast<int32_t>(t.blocks.back().id), static_cast<int32_t>(slot),
-                            static_cast<int32_t>(applied), 0});
-            ++t.length;
-            ++epoch_;
-        } catch (...) {
-            failure = std::current_exception();
-            break;
-        }
-    }
+    AppendWork w = meta_.plan_appends(seqs, n);
+    const size_t applied = w.applied;
+    const Geometry& g = meta_.geometry();
     if (applied) {
         flush();
         // small batches pass their ops in the kernel arguments (no upload copy)
-        if (!init.empty() && init.size() <= static_cast<size_t>(kInlineOps) &&
-            g_.max_blocks <= static_cast<size_t>(std::numeric_limits<int32_t>::max())) {
+        if (!w.init.empty() && w.init.size() <= static_cast<size_t>(kInlineOps)) {
             InlineInitOps ops;
-            for (size_t i = 0; i < init.size(); ++i)
-                ops.op[i] = make_int2(static_cast<int>(init[i].dst), static_cast<int>(init[i].src));
-            launch_block_init_inline(pool_, lay_.stride, ops, static_cast<int>(init.size()), stream_);
-        } else if (!init.empty()) {
-            auto* d = upload(*this, kInitOps, init.data(), init.size());
-            launch_block_init(pool_, lay_.stride, d, static_cast<int>(init.size()), stream_);
+            for (size_t i = 0; i < w.init.size(); ++i)
+                ops.op[i] = make_int2(static_cast<int>(w.init[i].dst), static_cast<int>(w.init[i].src));
+            launch_block_init_inline(pool_, lay_.stride, ops, static_cast<int>(w.init.size()), stream_);
+        } else if (!w.init.empty()) {
+            auto* d = upload(*this, kInitOps, w.init.data(), w.init.size());
+            launch_block_init(pool_, lay_.stride, d, static_cast<int>(w.init.size()), stream_);
         }
         const float* k = keys;
         const float* v = values;
         if (!device) {
-            const size_t w = g_.layers * g_.kv_width();
-            k = upload(*this, kKeys, keys, applied * w);
-            v = upload(*this, kValues, values, applied * w);
+            const size_t width = g.layers * g.kv_width();
+            k = upload(*this, kKeys, keys, applied * width);
+            v = upload(*this, kValues, values, applied * width);
         }
-        if (format_ == kF32 && rows.size() <= static_cast<size_t>(kInlineOps) && g_.tokens_per_block <= 32768 &&
-            applied <= 65536 && g_.kv_width() % 4 == 0 &&
+        if (format_ == kF32 && w.rows.size() <= static_cast<size_t>(kInlineOps) && g.tokens_per_block <= 32768 &&
+            applied <= 65536 && g.kv_width() % 4 == 0 &&
             lay_.stride / 16 <= static_cast<size_t>(std::numeric_limits<int32_t>::max())) {
             InlineRowOps ops;
-            for (size_t i = 0; i < rows.size(); ++i)
-                ops.op[i] = make_int2(rows[i].block, (rows[i].slot << 16) | rows[i].src_row);
-            launch_append_rows_inline(pool_, lay_, ops, static_cast<int>(rows.size()), k, v, stream_);
+            for (size_t i = 0; i < w.rows.size(); ++i)
+                ops.op[i] = make_int2(w.rows[i].block, (w.rows[i].slot << 16) | w.rows[i].src_row);
+            launch_append_rows_inline(pool_, lay_, ops, static_cast<int>(w.rows.size()), k, v, stream_);
         } else {
-            auto* d = upload(*this, kRowOps, rows.data(), rows.size());
-            launch_append_rows(pool_, lay_, d, static_cast<int>(rows.size()), k, v, stream_);
+            auto* d = upload(*this, kRowOps, w.rows.data(), w.rows.size());
+            launch_append_rows(pool_, lay_, d, static_cast<int>(w.rows.size()), k, v, stream_);
         }
     }
     if (applied_out) *applied_out = applied;
-    if (failure) std::rethrow_exception(failure);
+    if (w.failure) std::rethrow_exception(w.failure);
     return applied;
 }
 
@@ -418,12 +240,12 @@ size_t DeviceCache::append_tokens(uint64_t seq, const float* keys, const float* 
 // PagedCache::read (kv.hpp:110-113)
 void DeviceCache::read(uint64_t id, size_t layer, size_t position, bool value, float* out) {
     const Handle h = physical_block(id, position);
-    if (layer >= g_.layers) throw std::invalid_argument("KV position outside block");
-    validated(h);
+    if (layer >= geometry().layers) throw std::invalid_argument("KV position outside block");
+    meta_.check_live(h);
     flush();
-    const int2 row = make_int2(static_cast<int>(h.id), static_cast<int>(position % g_.tokens_per_block));
+    const int2 row = make_int2(static_cast<int>(h.id), static_cast<int>(position % geometry().tokens_per_block));
     auto* d = upload(*this, kMisc, &row, 1);
-    const size_t w = g_.kv_width();
+    const size_t w = geometry().kv_width();
     auto* o = static_cast<float*>(scratch_[kMiscOut].ensure(w * sizeof(float)));
     launch_gather_rows(pool_, lay_, d, 1, static_cast<int>(layer), value ? 1 : 0, o, stream_);
     TVARA_HIP(hipMemcpyAsync(out, o, w * sizeof(float), hipMemcpyDeviceToHost, stream_));
@@ -433,15 +255,16 @@ void DeviceCache::read(uint64_t id, size_t layer, size_t position, bool value, f
 // PagedCache::read_all (kv.hpp:114-119)
 void DeviceCache::read_all(uint64_t id, size_t layer, bool value, float* out, size_t capacity) {
     const Table& t = sequence(id);
-    if (layer >= g_.layers) throw std::invalid_argument("invalid KV layer");
-    const size_t w = g_.kv_width();
+    const Geometry& g = geometry();
+    if (layer >= g.layers) throw std::invalid_argument("invalid KV layer");
+    const size_t w = g.kv_width();
     if (t.length * w > capacity) throw std::invalid_argument("read_all buffer too small");
     if (!t.length) return;
     std::vector<int2> rows(t.length);
     for (size_t p = 0; p < t.length; ++p) {
-        const Handle h = t.blocks[p / g_.tokens_per_block];
-        validated(h);
-        rows[p] = make_int2(static_cast<int>(h.id), static_cast<int>(p % g_.tokens_per_block));
+        const Handle h = t.blocks[p / g.tokens_per_block];
+        meta_.check_live(h);
+        rows[p] = make_int2(static_cast<int>(h.id), static_cast<int>(p % g.tokens_per_block));
     }
     flush();
     auto* d = upload(*this, kMisc, rows.data(), rows.size());
@@ -449,80 +272,6 @@ void DeviceCache::read_all(uint64_t id, size_t layer, bool value, float* out, si
     launch_gather_rows(pool_, lay_, d, static_cast<int>(t.length), static_cast<int>(layer), value ? 1 : 0, o, stream_);
     TVARA_HIP(hipMemcpyAsync(out, o, t.length * w * sizeof(float), hipMemcpyDeviceToHost, stream_));
     synchronize();
-}
-
-// PagedCache::drop (kv.hpp:121)
-void DeviceCache::drop(uint64_t id) {
-    Table& t = mutable_sequence(id);
-    for (const Handle& h : t.blocks) release(h);
-    sequences_.erase(id);
-    ++epoch_;
-}
-
-// shared tail of fork (kv.hpp:123-129) and import_sequence (kv.hpp:149-159)
-uint64_t DeviceCache::publish(const Handle* blocks, size_t count, size_t length) {
-    size_t retained = 0;
-    try {
-        for (; retained < count; ++retained) retain(blocks[retained]);
-        if (next_ == std::numeric_limits<uint64_t>::max()) throw std::runtime_error("sequence ID exhausted");
-        Table t;
-        t.blocks.assign(blocks, blocks + count);
-        t.length = length;
-        const uint64_t id = next_ + 1;
-        sequences_.emplace(id, std::move(t));
-        next_ = id;
-        ++epoch_;
-        return id;
-    } catch (...) {
-        for (size_t i = 0; i < retained; ++i) release(blocks[i]);
-        throw;
-    }
-}
-
-uint64_t DeviceCache::fork(uint64_t id) {
-    const Table copy = sequence(id);
-    return publish(copy.blocks.data(), copy.blocks.size(), copy.length);
-}
-
-// PagedCache::truncate (kv.hpp:131-136): released pages only; stale slots stay
-void DeviceCache::truncate(uint64_t id, size_t length) {
-    Table& t = mutable_sequence(id);
-    if (length > t.length) throw std::invalid_argument("cannot extend KV by truncating");
-    const size_t tpb = g_.tokens_per_block;
-    const size_t keep = length / tpb + (length % tpb ? 1 : 0);
-    for (size_t i = keep; i < t.blocks.size(); ++i) release(t.blocks[i]);
-    t.blocks.resize(keep);
-    t.length = length;
-    ++epoch_;
-}
-
-// PagedCache::audit (kv.hpp:138-146)
-void DeviceCache::audit(const size_t* external, size_t count) const {
-    pool_audit();
-    std::vector<size_t> counts(g_.max_blocks);
-    if (count && count != counts.size()) throw std::invalid_argument("external reference counts mismatch");
-    const size_t tpb = g_.tokens_per_block;
-    for (const auto& [id, t] : sequences_) {
-        (void)id;
-        const size_t expected = t.length / tpb + (t.length % tpb ? 1 : 0);
-        if (t.blocks.size() != expected) throw std::logic_error("KV block table length invariant");
-        for (const Handle& h : t.blocks) {
-            validated(h);
-            ++counts.at(h.id);
-        }
-    }
-    for (size_t i = 0; i < counts.size(); ++i)
-        if (counts[i] + (count ? external[i] : 0) != refs_[i]) throw std::logic_error("KV reference invariant");
-}
-
-// PagedCache::import_sequence (kv.hpp:149-159)
-uint64_t DeviceCache::import_sequence(const Handle* blocks, size_t count, size_t source_length, size_t length) {
-    if (length > source_length) throw std::invalid_argument("prefix exceeds snapshot");
-    const size_t tpb = g_.tokens_per_block;
-    const size_t need = length / tpb + (length % tpb ? 1 : 0);
-    if (count < need) throw std::invalid_argument("invalid prefix snapshot");
-    std::vector<Handle> prefix(blocks, blocks + need);
-    return publish(prefix.data(), prefix.size(), length);
 }
 
 // ------------------------------------------------------------------ plans

@@ -13,26 +13,6 @@
 
 namespace tvara_amd {
 
-// CacheGeometry (kv.hpp:12-29)
-struct Geometry {
-    size_t layers = 1, kv_heads = 1, head_dim = 4, tokens_per_block = 16, max_blocks = 64;
-    size_t kv_width() const;
-    size_t elements_per_block() const;
-    void validate() const;
-};
-
-// BlockHandle (kv.hpp:35)
-struct Handle {
-    size_t id = 0;
-    uint64_t generation = 0;
-};
-
-// BlockTable (kv.hpp:77)
-struct Table {
-    std::vector<Handle> blocks;
-    size_t length = 0;
-};
-
 // Grow-only device buffer.
 struct DeviceBuffer {
     void* ptr = nullptr;
@@ -58,35 +38,41 @@ public:
     DeviceCache(const DeviceCache&) = delete;
     DeviceCache& operator=(const DeviceCache&) = delete;
 
-    const Geometry& geometry() const { return g_; }
+    const Geometry& geometry() const { return meta_.geometry(); }
     int format() const { return format_; }
     const BlockLayout& layout() const { return lay_; }
     size_t canonical_block_bytes() const;
     char* pool() const { return pool_; }
     hipStream_t stream() const { return stream_; }
     void set_stream(hipStream_t s) { stream_ = s; }
-    uint64_t epoch() const { return epoch_; }
+    uint64_t epoch() const { return meta_.epoch(); }
     int compute_units() const { return cus_; }
     void synchronize();
 
+    // the host bookkeeping (pool and tables); prefix trees work on it directly
+    KvLedger& ledger() { return meta_; }
+    const KvLedger& ledger() const { return meta_; }
+
     // BlockPool (kv.hpp:36-75)
-    Handle allocate();
-    void retain(Handle h);
-    void release(Handle h);
-    size_t references(Handle h) const;
-    size_t references_by_id(size_t id) const;
-    size_t available() const { return free_.size(); }
-    void pool_audit() const;
-    void pool_state(size_t* refs, uint64_t* generations, size_t* free_pop_order, size_t* free_count) const;
+    Handle allocate() { return meta_.allocate(); }
+    void retain(Handle h) { meta_.retain(h); }
+    void release(Handle h) { meta_.release(h); }
+    size_t references(Handle h) const { return meta_.references(h); }
+    size_t references_by_id(size_t id) const { return meta_.references_by_id(id); }
+    size_t available() const { return meta_.available(); }
+    void pool_audit() const { meta_.pool_audit(); }
+    void pool_state(size_t* refs, uint64_t* generations, size_t* free_pop_order, size_t* free_count) const {
+        meta_.pool_state(refs, generations, free_pop_order, free_count);
+    }
     void block_read(Handle h, void* out, size_t bytes);
     void block_write(Handle h, size_t offset, const void* data, size_t bytes);
     void checksums(const Handle* handles, size_t n, uint64_t* out);
 
     // PagedCache (kv.hpp:78-165)
-    uint64_t create_sequence();
-    const Table& sequence(uint64_t id) const;
-    std::vector<uint64_t> sequence_ids() const;
-    Handle physical_block(uint64_t id, size_t position) const;
+    uint64_t create_sequence() { return meta_.create_sequence(); }
+    const Table& sequence(uint64_t id) const { return meta_.sequence(id); }
+    std::vector<uint64_t> sequence_ids() const { return meta_.sequence_ids(); }
+    Handle physical_block(uint64_t id, size_t position) const { return meta_.physical_block(id, position); }
     // appends one token to each listed sequence in order; *applied receives the
     // number applied before the failure of the first one that could not be,
     // which is rethrown
@@ -95,11 +81,13 @@ public:
     size_t append_tokens(uint64_t seq, const float* keys, const float* values, size_t count, bool device);
     void read(uint64_t id, size_t layer, size_t position, bool value, float* out);
     void read_all(uint64_t id, size_t layer, bool value, float* out, size_t capacity);
-    void drop(uint64_t id);
-    uint64_t fork(uint64_t id);
-    void truncate(uint64_t id, size_t length);
-    void audit(const size_t* external, size_t count) const;
-    uint64_t import_sequence(const Handle* blocks, size_t count, size_t source_length, size_t length);
+    void drop(uint64_t id) { meta_.drop(id); }
+    uint64_t fork(uint64_t id) { return meta_.fork(id); }
+    void truncate(uint64_t id, size_t length) { meta_.truncate(id, length); }
+    void audit(const size_t* external, size_t count) const { meta_.audit(external, count); }
+    uint64_t import_sequence(const Handle* blocks, size_t count, size_t source_length, size_t length) {
+        return meta_.import_sequence(blocks, count, source_length, length);
+    }
 
     // zero-fill blocks handed out by allocate() that are still live
     void flush();
@@ -109,25 +97,12 @@ public:
     int* error_flag() const { return err_; }
 
 private:
-    const Handle& validated(Handle h) const;
-    Handle take_free();  // pop the free list: refs=1, ++generation
-    Table& mutable_sequence(uint64_t id);
-    uint64_t publish(const Handle* blocks, size_t count, size_t length);
-
-    Geometry g_;
+    KvLedger meta_;
     int format_;
     BlockLayout lay_{};
     char* pool_ = nullptr;
     hipStream_t stream_ = nullptr;
-    uint64_t epoch_ = 0;
     int cus_ = 256;
-    std::vector<size_t> refs_;
-    std::vector<uint64_t> gens_;
-    std::vector<size_t> free_;
-    std::vector<uint8_t> zero_pending_;
-    std::vector<size_t> zero_list_;
-    std::map<uint64_t, Table> sequences_;
-    uint64_t next_ = 0;
     DeviceBuffer scratch_[6];
     PinnedBuffer pinned_[6];
     int* err_ = nullptr;

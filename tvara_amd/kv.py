@@ -37,15 +37,15 @@ class PagedCache:
     """PagedCache(CacheGeometry{layers, kv_heads, head_dim, tokens_per_block,
     max_blocks}) (kv.hpp:80) on one GPU; ``fmt`` selects f32 or Q8_0 blocks."""
 
-    def __init__(self, layers, kv_heads, head_dim, tokens_per_block, max_blocks, fmt=F32):
-        self.lib = _capi.lib()
+    def __init__(self, layers, kv_heads, head_dim, tokens_per_block, max_blocks, fmt=F32, lib=None):
+        self.lib = lib or _capi.lib()
         self.geometry = (layers, kv_heads, head_dim, tokens_per_block, max_blocks)
         self.layers, self.kv_heads, self.head_dim, self.tokens_per_block, self.max_blocks = self.geometry
         self.format = fmt
         self.kv_width = kv_heads * head_dim
         self.h = self.lib.tvara_kv_cache_create(layers, kv_heads, head_dim, tokens_per_block, max_blocks, fmt)
         if not self.h:
-            _capi.raise_last()
+            _capi.raise_last(self.lib)
         self.block_bytes = self.lib.tvara_kv_block_bytes(self.h)
 
     @classmethod
@@ -80,7 +80,7 @@ class PagedCache:
         self.close()
 
     def _check(self, rc):
-        _capi.check(rc)
+        _capi.check(rc, self.lib)
 
     @property
     def elements_per_block(self):
@@ -160,7 +160,7 @@ class PagedCache:
     def create_sequence(self):
         s = self.lib.tvara_kv_sequence_create(self.h)
         if not s:
-            _capi.raise_last()
+            _capi.raise_last(self.lib)
         return s
 
     def _sequence(self, seq):
@@ -256,7 +256,7 @@ class PagedCache:
     def fork(self, seq):
         s = self.lib.tvara_kv_fork(self.h, seq)
         if not s:
-            _capi.raise_last()
+            _capi.raise_last(self.lib)
         return s
 
     def truncate(self, seq, length):
@@ -273,7 +273,7 @@ class PagedCache:
         arr = (Handle * max(1, len(blocks)))(*[Handle(*b) for b in blocks])
         s = self.lib.tvara_kv_import_sequence(self.h, arr, len(blocks), source_length, length)
         if not s:
-            _capi.raise_last()
+            _capi.raise_last(self.lib)
         return s
 
     def state(self):

@@ -31,7 +31,7 @@ class RadixCache:
         self.lib = cache.lib
         self.h = self.lib.tvara_radix_create(cache.h, isolation.encode("utf-8"))
         if not self.h:
-            _capi.raise_last()
+            _capi.raise_last(self.lib)
         self.isolation = isolation
 
     def close(self):
@@ -42,62 +42,65 @@ class RadixCache:
     def __del__(self):
         self.close()
 
+    def _check(self, rc):
+        _capi.check(rc, self.lib)
+
     def size(self):
         n = _sz()
-        _capi.check(self.lib.tvara_radix_size(self.h, C.byref(n)))
+        self._check(self.lib.tvara_radix_size(self.h, C.byref(n)))
         return n.value
 
     def lookup(self, tokens):
         """(node, tokens matched) (radix.hpp:29-42)."""
         t, p = _tokens(tokens)
         node, matched = _u64(), _sz()
-        _capi.check(self.lib.tvara_radix_lookup(self.h, p, t.size, C.byref(node), C.byref(matched)))
+        self._check(self.lib.tvara_radix_lookup(self.h, p, t.size, C.byref(node), C.byref(matched)))
         return node.value, matched.value
 
     def insert(self, tokens):
         t, p = _tokens(tokens)
         node = _u64()
-        _capi.check(self.lib.tvara_radix_insert(self.h, p, t.size, C.byref(node)))
+        self._check(self.lib.tvara_radix_insert(self.h, p, t.size, C.byref(node)))
         return node.value
 
     def attach(self, node, sequence):
-        _capi.check(self.lib.tvara_radix_attach(self.h, node, sequence))
+        self._check(self.lib.tvara_radix_attach(self.h, node, sequence))
 
     def reuse(self, tokens, partial=False):
         """(new sequence, prefix length) (radix.hpp:90-96)."""
         t, p = _tokens(tokens)
         seq, length = _u64(), _sz()
-        _capi.check(self.lib.tvara_radix_reuse(self.h, p, t.size, int(partial), C.byref(seq), C.byref(length)))
+        self._check(self.lib.tvara_radix_reuse(self.h, p, t.size, int(partial), C.byref(seq), C.byref(length)))
         return seq.value, length.value
 
     def pin(self, node):
-        _capi.check(self.lib.tvara_radix_pin(self.h, node))
+        self._check(self.lib.tvara_radix_pin(self.h, node))
 
     def unpin(self, node):
-        _capi.check(self.lib.tvara_radix_unpin(self.h, node))
+        self._check(self.lib.tvara_radix_unpin(self.h, node))
 
     def touch(self, node):
-        _capi.check(self.lib.tvara_radix_touch(self.h, node))
+        self._check(self.lib.tvara_radix_touch(self.h, node))
 
     def eviction_candidate(self):
         node = _u64()
-        _capi.check(self.lib.tvara_radix_eviction_candidate(self.h, C.byref(node)))
+        self._check(self.lib.tvara_radix_eviction_candidate(self.h, C.byref(node)))
         return node.value or None
 
     def evict_one(self):
         e = C.c_int()
-        _capi.check(self.lib.tvara_radix_evict_one(self.h, C.byref(e)))
+        self._check(self.lib.tvara_radix_evict_one(self.h, C.byref(e)))
         return bool(e.value)
 
     def reset(self):
-        _capi.check(self.lib.tvara_radix_reset(self.h))
+        self._check(self.lib.tvara_radix_reset(self.h))
 
     def node(self, node_id):
         parent, elen, pins, acc, kvlen, kvb, ch = _u64(), _sz(), _sz(), _u64(), _sz(), _sz(), _sz()
-        _capi.check(self.lib.tvara_radix_node(self.h, node_id, C.byref(parent), None, 0, C.byref(elen), C.byref(pins),
+        self._check(self.lib.tvara_radix_node(self.h, node_id, C.byref(parent), None, 0, C.byref(elen), C.byref(pins),
                                               C.byref(acc), C.byref(kvlen), C.byref(kvb), C.byref(ch)))
         edge = np.zeros(max(1, elen.value), np.int32)
-        _capi.check(self.lib.tvara_radix_node(self.h, node_id, C.byref(parent), edge.ctypes.data_as(C.POINTER(C.c_int32)),
+        self._check(self.lib.tvara_radix_node(self.h, node_id, C.byref(parent), edge.ctypes.data_as(C.POINTER(C.c_int32)),
                                               elen.value, C.byref(elen), C.byref(pins), C.byref(acc), C.byref(kvlen),
                                               C.byref(kvb), C.byref(ch)))
         has_kv = kvb.value != (1 << 64) - 1
@@ -107,6 +110,6 @@ class RadixCache:
 
     def external_references(self):
         counts = np.zeros(self.cache.max_blocks, np.uint64)
-        _capi.check(self.lib.tvara_radix_external_references(self.h, counts.ctypes.data_as(C.POINTER(_sz)),
+        self._check(self.lib.tvara_radix_external_references(self.h, counts.ctypes.data_as(C.POINTER(_sz)),
                                                              counts.size))
         return [int(x) for x in counts]
