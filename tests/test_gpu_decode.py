@@ -64,6 +64,50 @@ def test_c2_llama32_batch(device, oracle):
         assert np.array_equal(out.numpy(), got)
 
 
+def test_plan_on_a_non_blocking_stream(device, oracle):
+    # The cache queues its appends, copies and zero-fills on its own stream
+    # (the null stream here); a plan launched on a non-blocking stream is not
+    # ordered against it by HIP.  The launch must still see every appended
+    # row, and block writes queued after it (a truncate, then appends that
+    # reuse the freed blocks) must not overtake its reads.
+    from tvara_amd import hip
+
+    heads, kv_heads, dim, tpb, n, length = 32, 8, 64, 16, 8, 3000
+    g = (1, kv_heads, dim, tpb, n * (length // tpb + 1) + 8)
+    dev, ref = device.PagedCache(*g), oracle.Cache(*g)
+    w = kv_heads * dim
+    seqs = []
+    for i in range(n):
+        k = synth.normal(40 + i, "k", length * w).reshape(length, w)
+        v = synth.normal(40 + i, "v", length * w).reshape(length, w)
+        sd, sr = dev.create_sequence(), ref.create_sequence()
+        dev.append_many(sd, k, v)  # queued, not waited for
+        ref.append_many(sr, k, v)
+        seqs.append((sd, sr))
+    q = synth.normal(49, "q", n * heads * dim).reshape(n, heads * dim)
+    want = np.stack([ref.fused_paged_attention(q[i], sr, 0, heads, 8192) for i, (_, sr) in enumerate(seqs)])
+    stream = hip.Stream(non_blocking=True)
+    dq = hip.DeviceArray.from_numpy(q)
+    for rnd in range(3):
+        say("non-blocking stream round", rnd)
+        plan = attention.DecodePlan(dev, [sd for sd, _ in seqs], heads, 8192)
+        out = hip.DeviceArray(q.shape)
+        plan.launch(0, dq.ptr, out.ptr, stream=stream.h)
+        # block writes queued behind the launch on the cache's stream
+        victim = dev.create_sequence()
+        junk = np.full((length, w), np.nan, np.float32)
+        dev.truncate(seqs[rnd][0], 0)
+        dev.append_many(victim, junk, junk)
+        plan.check()
+        got = out.numpy()
+        assert refmath.close(got, want, TOL), (rnd, refmath.max_rel(got, want))
+        # restore the truncated sequence for the next round
+        dev.drop(victim)
+        k = synth.normal(40 + rnd, "k", length * w).reshape(length, w)
+        v = synth.normal(40 + rnd, "v", length * w).reshape(length, w)
+        dev.append_many(seqs[rnd][0], k, v)
+
+
 def _single(device, oracle, heads, kv_heads, dim, tpb, length, seed, tail=False, visible=None, fmt=None,
             layers=1, layer=0):
     g = (layers, kv_heads, dim, tpb, length // tpb + 3)

@@ -27,6 +27,15 @@ using tvara_amd::Handle;
 struct tvara_kv_cache {
     std::unique_ptr<DeviceCache> owned;
     DeviceCache* cache = nullptr;
+    // The synchronous attention calls keep their last plan and reuse it while
+    // the cache and the call's rows are unchanged (a model's layers share one
+    // batch), and stage host buffers through pinned memory into grow-only
+    // device buffers: no allocation and no device-wide wait per call.
+    std::vector<uint64_t> decode_key, prefill_key;
+    AttnPlan decode_plan;
+    tvara_amd::PrefillPlan prefill_plan;
+    tvara_amd::DeviceBuffer io;
+    tvara_amd::PinnedBuffer io_in, io_out;
     tvara_kv_cache(const Geometry& g, int format)
         : owned(std::make_unique<DeviceCache>(g, format)), cache(owned.get()) {}
     explicit tvara_kv_cache(DeviceCache* lent) : cache(lent) {}
@@ -66,58 +75,24 @@ DeviceCache& live(tvara_kv_cache* c) {
     return *c->cache;
 }
 
-// ModelConfig::validate (model.hpp:13-19), the part attention depends on
-void check_config(const DeviceCache& c, size_t heads, size_t context) {
-    const Geometry& g = c.geometry();
-    if (!heads || !context || heads % g.kv_heads || g.head_dim % 2 || heads > 65535)
-        throw std::invalid_argument("invalid native model configuration");
-}
-
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Rows of fused_paged_attention calls (attention.hpp:57-83) for `count`
-// sequences: the argument checks of attention.hpp:59-63 and the visible cap.
-void decode_rows(const DeviceCache& c, const uint64_t* seqs, size_t count, size_t context, bool tail,
-                 const size_t* visible, std::vector<uint64_t>& seq_of_row, std::vector<size_t>& cached,
-                 std::vector<uint8_t>& tail_rows) {
-    for (size_t i = 0; i < count; ++i) {
-        const size_t length = c.sequence(seqs[i]).length;
-        if (length > context || (tail && length == context)) throw std::invalid_argument("invalid fused attention shape");
-        const size_t total = length + (tail ? 1 : 0);
-        const size_t vis = visible ? std::min(visible[i], total) : total;
-        if (!vis) throw std::invalid_argument("empty fused attention");
-        if (length > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
-            throw std::invalid_argument("sequence too long for the device kernels");
-        seq_of_row.push_back(seqs[i]);
-        cached.push_back(std::min(vis, length));
-        tail_rows.push_back(vis > length ? 1 : 0);
-    }
+// the identity of a synchronous attention call's plan: the cache's mutation
+// count and every argument the plan depends on
+std::vector<uint64_t> plan_key(const DeviceCache& c, std::initializer_list<uint64_t> scalars, const uint64_t* seqs,
+                               size_t count, const size_t* a, const size_t* b) {
+    std::vector<uint64_t> key{c.epoch(), count};
+    key.insert(key.end(), scalars);
+    key.insert(key.end(), seqs, seqs + count);
+    key.push_back(a ? 1 : 0);
+    if (a) key.insert(key.end(), a, a + count);
+    if (b) key.insert(key.end(), b, b + count);
+    return key;
 }
-
-// device copies of host arrays for the synchronous attention entry points
-struct Staged {
-    std::vector<void*> owned;
-    ~Staged() {
-        for (void* p : owned) (void)hipFree(p);
-    }
-    const float* in(const float* host, size_t n) {
-        if (!host) return nullptr;
-        void* d = nullptr;
-        TVARA_HIP(hipMalloc(&d, std::max<size_t>(n, 1) * sizeof(float)));
-        owned.push_back(d);
-        TVARA_HIP(hipMemcpy(d, host, n * sizeof(float), hipMemcpyHostToDevice));
-        return static_cast<const float*>(d);
-    }
-    float* out(size_t n) {
-        void* d = nullptr;
-        TVARA_HIP(hipMalloc(&d, std::max<size_t>(n, 1) * sizeof(float)));
-        owned.push_back(d);
-        return static_cast<float*>(d);
-    }
-};
 }  // namespace
 
 tvara_amd::KvLedger& tvara_amd::abi::ledger_of(tvara_kv_cache* cache) { return live(cache).ledger(); }
+tvara_amd::DeviceCache& tvara_amd::device_cache(tvara_kv_cache* cache) { return live(cache); }
 
 extern "C" {
 
@@ -204,7 +179,7 @@ int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t c
                       const size_t* visible, float* out, int device_ptrs) {
     return guard([&] {
         auto& c = live(cache);
-        check_config(c, heads, context);
+        tvara_amd::check_attention_config(c, heads, context);
         if (!count) return;
         if (!sequences || !q || !out || (tail_keys == nullptr) != (tail_values == nullptr))
             throw std::invalid_argument("invalid fused attention shape");
@@ -213,25 +188,41 @@ int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t c
         std::vector<uint64_t> seq_of_row;
         std::vector<size_t> cached;
         std::vector<uint8_t> tails;
-        decode_rows(c, sequences, count, context, tail, visible, seq_of_row, cached, tails);
-        AttnPlan plan;
-        plan.build(&c, seq_of_row, cached, tails, static_cast<int>(heads), 0);
+        tvara_amd::attention_rows(c, sequences, count, context, tail, visible, seq_of_row, cached, tails);
+        AttnPlan& plan = cache->decode_plan;
+        std::vector<uint64_t> key = plan_key(c, {heads, tail ? 1u : 0u}, sequences, count, visible, nullptr);
+        if (key != cache->decode_key || plan.cache != &c) {
+            cache->decode_key.clear();
+            plan.build(&c, seq_of_row, cached, tails, static_cast<int>(heads), 0);
+            cache->decode_key = std::move(key);
+        }
         const size_t hidden = heads * c.geometry().head_dim, kvw = c.geometry().kv_width();
+        hipStream_t s = c.stream();
         if (device_ptrs) {
             if (!aligned16(q) || !aligned16(out) || (tail && (!aligned16(tail_keys) || !aligned16(tail_values))))
                 throw std::invalid_argument("device buffers must be 16-byte aligned");
-            plan.launch(static_cast<int>(layer), q, tail_keys, tail_values, out, c.stream());
+            plan.launch(static_cast<int>(layer), q, tail_keys, tail_values, out, s);
             plan.check();
             return;
         }
-        Staged st;
-        const float* dq = st.in(q, count * hidden);
-        const float* dk = st.in(tail_keys, count * kvw);
-        const float* dv = st.in(tail_values, count * kvw);
-        float* dout = st.out(count * hidden);
-        plan.launch(static_cast<int>(layer), dq, dk, dv, dout, c.stream());
-        plan.check();
-        TVARA_HIP(hipMemcpy(out, dout, count * hidden * sizeof(float), hipMemcpyDeviceToHost));
+        // q | tail keys | tail values in one pinned buffer and one copy in;
+        // the output comes back through a second pinned buffer
+        const size_t nq = count * hidden, nt = tail ? count * kvw : 0;
+        auto* in = static_cast<float*>(cache->io_in.acquire((nq + 2 * nt) * sizeof(float)));
+        std::memcpy(in, q, nq * sizeof(float));
+        if (tail) {
+            std::memcpy(in + nq, tail_keys, nt * sizeof(float));
+            std::memcpy(in + nq + nt, tail_values, nt * sizeof(float));
+        }
+        const size_t out_at = (nq + 2 * nt + 3) / 4 * 4;  // 16-byte aligned
+        auto* d = static_cast<float*>(cache->io.ensure((out_at + nq) * sizeof(float)));
+        TVARA_HIP(hipMemcpyAsync(d, in, (nq + 2 * nt) * sizeof(float), hipMemcpyHostToDevice, s));
+        cache->io_in.release(s);
+        plan.launch(static_cast<int>(layer), d, tail ? d + nq : nullptr, tail ? d + nq + nt : nullptr, d + out_at, s);
+        auto* back = static_cast<float*>(cache->io_out.acquire(nq * sizeof(float)));
+        TVARA_HIP(hipMemcpyAsync(back, d + out_at, nq * sizeof(float), hipMemcpyDeviceToHost, s));
+        plan.check();  // waits for the stream, the copy out included
+        std::memcpy(out, back, nq * sizeof(float));
     });
 }
 
@@ -240,27 +231,39 @@ int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t 
                        int precision, int device_ptrs) {
     return guard([&] {
         auto& c = live(cache);
-        check_config(c, heads, context);
+        tvara_amd::check_attention_config(c, heads, context);
         if (!count) return;
         if (!sequences || !start || !rows || !queries || !out) throw std::invalid_argument("invalid causal prompt chunk");
         if (layer >= c.geometry().layers) throw std::invalid_argument("invalid fused attention shape");
         if (precision != TVARA_ATTN_F32 && precision != TVARA_ATTN_BF16)
             throw std::invalid_argument("unknown attention precision");
-        tvara_amd::PrefillPlan plan;
-        plan.build(&c, sequences, count, heads, context, start, rows, precision);
-        const size_t total_rows = plan.total_rows;
-        const size_t hidden = heads * c.geometry().head_dim;
-        if (device_ptrs && (!aligned16(queries) || !aligned16(out)))
-            throw std::invalid_argument("device buffers must be 16-byte aligned");
-        Staged st;
-        const float* dq = device_ptrs ? queries : st.in(queries, total_rows * hidden);
-        float* dout = device_ptrs ? out : st.out(total_rows * hidden);
-        plan.launch(static_cast<int>(layer), dq, dout, c.stream());
+        tvara_amd::PrefillPlan& plan = cache->prefill_plan;
+        std::vector<uint64_t> key =
+            plan_key(c, {heads, context, static_cast<uint64_t>(precision)}, sequences, count, start, rows);
+        if (key != cache->prefill_key || plan.cache != &c) {
+            cache->prefill_key.clear();
+            plan.build(&c, sequences, count, heads, context, start, rows, precision);
+            cache->prefill_key = std::move(key);
+        }
+        const size_t n = plan.total_rows * heads * c.geometry().head_dim;
+        hipStream_t s = c.stream();
+        if (device_ptrs) {
+            if (!aligned16(queries) || !aligned16(out)) throw std::invalid_argument("device buffers must be 16-byte aligned");
+            plan.launch(static_cast<int>(layer), queries, out, s);
+            plan.check();
+            return;
+        }
+        auto* in = static_cast<float*>(cache->io_in.acquire(n * sizeof(float)));
+        std::memcpy(in, queries, n * sizeof(float));
+        const size_t out_at = (n + 3) / 4 * 4;
+        auto* d = static_cast<float*>(cache->io.ensure((out_at + n) * sizeof(float)));
+        TVARA_HIP(hipMemcpyAsync(d, in, n * sizeof(float), hipMemcpyHostToDevice, s));
+        cache->io_in.release(s);
+        plan.launch(static_cast<int>(layer), d, d + out_at, s);
+        auto* back = static_cast<float*>(cache->io_out.acquire(n * sizeof(float)));
+        TVARA_HIP(hipMemcpyAsync(back, d + out_at, n * sizeof(float), hipMemcpyDeviceToHost, s));
         plan.check();
-        if (!device_ptrs)
-            TVARA_HIP(hipMemcpy(out, dout, total_rows * hidden * sizeof(float), hipMemcpyDeviceToHost));
-        else
-            c.synchronize();
+        std::memcpy(out, back, n * sizeof(float));
     });
 }
 
@@ -269,12 +272,12 @@ tvara_attn_plan* tvara_attn_plan_create(tvara_kv_cache* cache, const uint64_t* s
     tvara_attn_plan* out = nullptr;
     guard([&] {
         auto& c = live(cache);
-        check_config(c, heads, context);
+        tvara_amd::check_attention_config(c, heads, context);
         if (!count || !sequences) throw std::invalid_argument("empty attention plan");
         std::vector<uint64_t> seq_of_row;
         std::vector<size_t> cached;
         std::vector<uint8_t> tails;
-        decode_rows(c, sequences, count, context, with_tail != 0, visible, seq_of_row, cached, tails);
+        tvara_amd::attention_rows(c, sequences, count, context, with_tail != 0, visible, seq_of_row, cached, tails);
         auto p = std::make_unique<tvara_attn_plan>();
         p->context = context;
         p->plan.build(&c, seq_of_row, cached, tails, static_cast<int>(heads), 0);
@@ -319,7 +322,7 @@ tvara_prefill_plan* tvara_prefill_plan_create(tvara_kv_cache* cache, const uint6
     tvara_prefill_plan* out = nullptr;
     guard([&] {
         auto& c = live(cache);
-        check_config(c, heads, context);
+        tvara_amd::check_attention_config(c, heads, context);
         auto p = std::make_unique<tvara_prefill_plan>();
         p->plan.build(&c, sequences, count, heads, context, start, rows, precision);
         out = p.release();

@@ -118,6 +118,8 @@ DeviceCache::DeviceCache(const Geometry& g, int format) : meta_(g), format_(form
 
 DeviceCache::~DeviceCache() {
     (void)hipStreamSynchronize(stream_);
+    for (hipEvent_t e : ordered_)
+        if (e) (void)hipEventDestroy(e);
     if (pool_) (void)hipFree(pool_);
     if (err_) (void)hipFree(err_);
 }
@@ -130,14 +132,29 @@ size_t DeviceCache::canonical_block_bytes() const {
 void DeviceCache::synchronize() { TVARA_HIP(hipStreamSynchronize(stream_)); }
 
 // BlockPool::allocate's zero-fill (kv.hpp:48), batched over every block handed
-// out since the last device access
+// out since the last device access, kInlineOps blocks a launch
 void DeviceCache::flush() {
     const std::vector<int64_t> ids = meta_.take_pending_zero_fills();
-    if (ids.empty()) return;
-    std::vector<BlockInitOp> ops(ids.size());
-    for (size_t i = 0; i < ids.size(); ++i) ops[i] = {ids[i], -1};
-    auto* d = upload(*this, kInitOps, ops.data(), ops.size());
-    launch_block_init(pool_, lay_.stride, d, static_cast<int>(ops.size()), stream_);
+    for (size_t at = 0; at < ids.size(); at += kInlineOps) {
+        const size_t n = std::min<size_t>(kInlineOps, ids.size() - at);
+        InlineInitOps ops;
+        for (size_t i = 0; i < n; ++i) ops.op[i] = make_int2(static_cast<int>(ids[at + i]), -1);
+        launch_block_init_inline(pool_, lay_.stride, ops, static_cast<int>(n), stream_);
+    }
+}
+
+void DeviceCache::enter(hipStream_t s) {
+    if (s == stream_) return;
+    if (!ordered_[0]) TVARA_HIP(hipEventCreateWithFlags(&ordered_[0], hipEventDisableTiming));
+    TVARA_HIP(hipEventRecord(ordered_[0], stream_));
+    TVARA_HIP(hipStreamWaitEvent(s, ordered_[0], 0));
+}
+
+void DeviceCache::leave(hipStream_t s) {
+    if (s == stream_) return;
+    if (!ordered_[1]) TVARA_HIP(hipEventCreateWithFlags(&ordered_[1], hipEventDisableTiming));
+    TVARA_HIP(hipEventRecord(ordered_[1], s));
+    TVARA_HIP(hipStreamWaitEvent(stream_, ordered_[1], 0));
 }
 
 void DeviceCache::block_read(Handle h, void* out, size_t bytes) {
@@ -276,7 +293,30 @@ void DeviceCache::read_all(uint64_t id, size_t layer, bool value, float* out, si
 
 // ------------------------------------------------------------------ plans
 
-void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, const std::vector<size_t>& cached,
+void check_attention_config(const DeviceCache& c, size_t heads, size_t context) {
+    const Geometry& g = c.geometry();
+    if (!heads || !context || heads % g.kv_heads || g.head_dim % 2 || heads > 65535)
+        throw std::invalid_argument("invalid native model configuration");
+}
+
+void attention_rows(const DeviceCache& c, const uint64_t* seqs, size_t count, size_t context, bool tail,
+                    const size_t* visible, std::vector<uint64_t>& seq_of_row, std::vector<size_t>& cached,
+                    std::vector<uint8_t>& tail_rows) {
+    for (size_t i = 0; i < count; ++i) {
+        const size_t length = c.sequence(seqs[i]).length;
+        if (length > context || (tail && length == context)) throw std::invalid_argument("invalid fused attention shape");
+        const size_t total = length + (tail ? 1 : 0);
+        const size_t vis = visible ? std::min(visible[i], total) : total;
+        if (!vis) throw std::invalid_argument("empty fused attention");
+        if (length > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
+            throw std::invalid_argument("sequence too long for the device kernels");
+        seq_of_row.push_back(seqs[i]);
+        cached.push_back(std::min(vis, length));
+        tail_rows.push_back(vis > length ? 1 : 0);
+    }
+}
+
+void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, const std::vector<size_t>& cached,
                      const std::vector<uint8_t>& tail_rows, int h, size_t split_override) {
     cache = c;
     epoch = c->epoch();
@@ -287,7 +327,8 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     group = static_cast<int>(heads / g.kv_heads);
     rows = static_cast<int>(seq_of_row.size());
     std::map<uint64_t, int32_t> offset;
-    std::vector<int32_t> tab;
+    std::vector<int32_t>& tab = h_tables;
+    tab.clear();
     size_t total = 0;
     for (size_t r = 0; r < seq_of_row.size(); ++r) {
         total += cached[r];
@@ -335,9 +376,14 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
     // the decode kernels keep a split's block ids in one register per lane
     split = std::min(round_up(std::max<size_t>(split, 16), 16), kMaxSplitTokens);
     split_tokens = static_cast<int>(split);
-    std::vector<int4> ent(rows), work;
-    std::vector<int2> its;
-    std::vector<int32_t> work_ids;
+    std::vector<int4>& ent = h_entries;
+    std::vector<int4>& work = h_work;
+    std::vector<int2>& its = h_items;
+    std::vector<int32_t>& work_ids = h_work_blocks;
+    ent.assign(rows, int4{});
+    work.clear();
+    its.clear();
+    work_ids.clear();
     const bool blocks16 = g.tokens_per_block == 16;
     inline_ok = rows <= kInlineRows;
     need_merge = false;
@@ -362,29 +408,75 @@ void AttnPlan::build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, co
         kv_bytes += static_cast<size_t>(static_cast<double>(n + tail) * g.kv_width() * 2 * bytes_per_element);
     }
     items = static_cast<int>(its.size());
-    auto put = [&](DeviceBuffer& b, const void* data, size_t bytes) {
-        void* d = b.ensure(std::max<size_t>(bytes, 16));
-        if (bytes) TVARA_HIP(hipMemcpy(d, data, bytes, hipMemcpyHostToDevice));
+}
+
+void AttnPlan::place() {
+    size_t copied = 0;
+    const size_t total = region_bytes(&copied);
+    char* device = static_cast<char*>(region.ensure(total));
+    char* host = static_cast<char*>(staging.acquire(copied));
+    place_in(device, region.bytes, cache->stream(), host);
+    staging.release(cache->stream());
+}
+
+namespace {
+// packed layout of a plan in one region: every section starts on 256 bytes
+struct RegionLayout {
+    size_t tables, entries, items, work, work_blocks, row_done, err, copied, part_acc, part_ml, total;
+};
+
+RegionLayout region_layout(const AttnPlan& p) {
+    const Geometry& g = p.cache->geometry();
+    RegionLayout r{};
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        const size_t here = at;
+        at = round_up(at + std::max<size_t>(bytes, 1), 256);
+        return here;
     };
-    put(tables, tab.data(), tab.size() * sizeof(int32_t));
-    put(entries, ent.data(), ent.size() * sizeof(int4));
-    put(items_buf, its.data(), its.size() * sizeof(int2));
-    put(work_buf, work.data(), work.size() * sizeof(int4));
-    put(work_blocks, work_ids.data(), work_ids.size() * sizeof(int32_t));
-    if (need_merge) {
-        part_acc.ensure(static_cast<size_t>(items) * heads * g.head_dim * sizeof(float));
-        part_ml.ensure(static_cast<size_t>(items) * heads * 2 * sizeof(float));
-        // split counters of the in-kernel merge, one per (row, KV head) at
-        // most; every launch that counts leaves them at zero again, so only a
-        // new allocation is cleared
-        const size_t bytes = static_cast<size_t>(rows) * g.kv_heads * sizeof(int);
-        if (!row_done.ptr || row_done.bytes < bytes) {
-            row_done.ensure(bytes);
-            TVARA_HIP(hipMemset(row_done.ptr, 0, row_done.bytes));
-        }
-    }
-    err.ensure(sizeof(int));
-    TVARA_HIP(hipMemset(err.ptr, 0, sizeof(int)));
+    r.tables = take(p.h_tables.size() * sizeof(int32_t));
+    r.entries = take(p.h_entries.size() * sizeof(int4));
+    r.items = take(p.h_items.size() * sizeof(int2));
+    r.work = take(p.h_work.size() * sizeof(int4));
+    r.work_blocks = take(p.h_work_blocks.size() * sizeof(int32_t));
+    r.row_done = take(static_cast<size_t>(p.rows) * g.kv_heads * sizeof(int));
+    r.err = take(sizeof(int));
+    r.copied = at;
+    r.part_acc = take(p.need_merge ? static_cast<size_t>(p.items) * p.heads * g.head_dim * sizeof(float) : 0);
+    r.part_ml = take(p.need_merge ? static_cast<size_t>(p.items) * p.heads * 2 * sizeof(float) : 0);
+    r.total = at;
+    return r;
+}
+}  // namespace
+
+size_t AttnPlan::region_bytes(size_t* copied) const {
+    const RegionLayout r = region_layout(*this);
+    if (copied) *copied = r.copied;
+    return r.total;
+}
+
+// One host-to-device copy carries the tables, the work list and zeros for the
+// split counters and the error flag, which therefore start cleared whatever
+// the region held before.
+void AttnPlan::place_in(char* device, size_t capacity, hipStream_t s, char* host) {
+    const RegionLayout r = region_layout(*this);
+    if (r.total > capacity) throw std::invalid_argument("attention plan exceeds the no-allocation scratch");
+    std::memset(host, 0, r.copied);
+    auto put = [&](size_t at, const void* data, size_t bytes) {
+        if (bytes) std::memcpy(host + at, data, bytes);
+        return device + at;
+    };
+    dev.tables = reinterpret_cast<const int32_t*>(put(r.tables, h_tables.data(), h_tables.size() * sizeof(int32_t)));
+    dev.entries = reinterpret_cast<const int4*>(put(r.entries, h_entries.data(), h_entries.size() * sizeof(int4)));
+    dev.items = reinterpret_cast<const int2*>(put(r.items, h_items.data(), h_items.size() * sizeof(int2)));
+    dev.work = reinterpret_cast<const int4*>(put(r.work, h_work.data(), h_work.size() * sizeof(int4)));
+    dev.work_blocks = reinterpret_cast<const int32_t*>(
+        put(r.work_blocks, h_work_blocks.data(), h_work_blocks.size() * sizeof(int32_t)));
+    dev.row_done = need_merge ? reinterpret_cast<int*>(device + r.row_done) : nullptr;
+    dev.err = reinterpret_cast<int*>(device + r.err);
+    dev.part_acc = need_merge ? reinterpret_cast<float*>(device + r.part_acc) : nullptr;
+    dev.part_ml = need_merge ? reinterpret_cast<float*>(device + r.part_ml) : nullptr;
+    TVARA_HIP(hipMemcpyAsync(device, host, r.copied, hipMemcpyHostToDevice, s));
 }
 
 void AttnPlan::launch(int layer, const float* q, const float* tail_k, const float* tail_v, float* out, hipStream_t s) {
@@ -392,38 +484,43 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     if (layer < 0 || static_cast<size_t>(layer) >= cache->geometry().layers)
         throw std::invalid_argument("invalid fused attention shape");
     if (with_tail && (!tail_k || !tail_v)) throw std::invalid_argument("plan expects tail K/V");
+    if (!dev.tables) throw std::invalid_argument("attention plan is not placed");
     cache->flush();
+    cache->enter(s);
     DecodeArgs a{};
     a.pool = cache->pool();
     a.lay = cache->layout();
     a.layer = layer;
     a.heads = heads;
     a.group = group;
-    a.tables = static_cast<const int32_t*>(tables.ptr);
-    a.entries = static_cast<const int4*>(entries.ptr);
-    a.items = static_cast<const int2*>(items_buf.ptr);
+    a.tables = dev.tables;
+    a.entries = dev.entries;
+    a.items = dev.items;
     a.split_tokens = split_tokens;
-    a.work = static_cast<const int4*>(work_buf.ptr);
-    a.work_blocks = static_cast<const int32_t*>(work_blocks.ptr);
+    a.work = dev.work;
+    a.work_blocks = dev.work_blocks;
     a.q = q;
     a.tail_k = tail_k;
     a.tail_v = tail_v;
     a.out = out;
-    a.part_acc = static_cast<float*>(part_acc.ptr);
-    a.part_ml = static_cast<float*>(part_ml.ptr);
-    a.row_done = need_merge ? static_cast<int*>(row_done.ptr) : nullptr;
+    a.part_acc = dev.part_acc;
+    a.part_ml = dev.part_ml;
+    a.row_done = need_merge ? dev.row_done : nullptr;
     a.wave_splits = wave_splits;
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
-    a.err = static_cast<int*>(err.ptr);
+    a.err = dev.err;
     launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, s);
+    cache->leave(s);
+    last_stream = s;
 }
 
 void AttnPlan::check() {
     int flag = 0;
-    TVARA_HIP(hipDeviceSynchronize());
-    TVARA_HIP(hipMemcpy(&flag, err.ptr, sizeof(int), hipMemcpyDeviceToHost));
+    TVARA_HIP(hipMemcpyAsync(&flag, dev.err, sizeof(int), hipMemcpyDeviceToHost, last_stream));
+    TVARA_HIP(hipStreamSynchronize(last_stream));
     if (flag) {
-        TVARA_HIP(hipMemset(err.ptr, 0, sizeof(int)));
+        TVARA_HIP(hipMemsetAsync(dev.err, 0, sizeof(int), last_stream));
+        TVARA_HIP(hipStreamSynchronize(last_stream));
         throw std::invalid_argument("invalid online attention input");
     }
 }
@@ -496,6 +593,7 @@ void PrefillPlan::launch(int layer, const float* q, float* out, hipStream_t s) {
     }
     if (cache->epoch() != epoch) throw std::invalid_argument("attention plan is stale: the cache changed");
     cache->flush();
+    cache->enter(s);
     PrefillArgs a{};
     a.pool = cache->pool();
     a.lay = cache->layout();
@@ -509,6 +607,8 @@ void PrefillPlan::launch(int layer, const float* q, float* out, hipStream_t s) {
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
     a.err = static_cast<int*>(err.ptr);
     launch_prefill_bf16(a, count, max_rows, s);
+    cache->leave(s);
+    last_stream = s;
 }
 
 void PrefillPlan::check() {
@@ -517,10 +617,11 @@ void PrefillPlan::check() {
         return;
     }
     int flag = 0;
-    TVARA_HIP(hipDeviceSynchronize());
-    TVARA_HIP(hipMemcpy(&flag, err.ptr, sizeof(int), hipMemcpyDeviceToHost));
+    TVARA_HIP(hipMemcpyAsync(&flag, err.ptr, sizeof(int), hipMemcpyDeviceToHost, last_stream));
+    TVARA_HIP(hipStreamSynchronize(last_stream));
     if (flag) {
-        TVARA_HIP(hipMemset(err.ptr, 0, sizeof(int)));
+        TVARA_HIP(hipMemsetAsync(err.ptr, 0, sizeof(int), last_stream));
+        TVARA_HIP(hipStreamSynchronize(last_stream));
         throw std::invalid_argument("invalid online attention input");
     }
 }

@@ -89,8 +89,15 @@ public:
         return meta_.import_sequence(blocks, count, source_length, length);
     }
 
-    // zero-fill blocks handed out by allocate() that are still live
+    // zero-fill blocks handed out by allocate() that are still live (kernel
+    // launches with their ops in the arguments: no upload, no allocation)
     void flush();
+    // Work on another stream `s` that reads the pool: enter() makes `s` wait
+    // for everything queued on the cache's stream (appends, copies,
+    // zero-fills); leave() makes the cache's stream wait for what `s` has
+    // queued, so a later write to a block cannot overtake a read of it.
+    void enter(hipStream_t s);
+    void leave(hipStream_t s);
     // device scratch owned by the cache
     DeviceBuffer& scratch(int i) { return scratch_[i]; }
     PinnedBuffer& pinned(int i) { return pinned_[i]; }
@@ -103,12 +110,16 @@ private:
     char* pool_ = nullptr;
     hipStream_t stream_ = nullptr;
     int cus_ = 256;
+    hipEvent_t ordered_[2] = {nullptr, nullptr};
     DeviceBuffer scratch_[6];
     PinnedBuffer pinned_[6];
     int* err_ = nullptr;
 };
 
-// A batch of attention rows with resident block tables.
+// A batch of attention rows with resident block tables.  compute() builds the
+// host image of the plan (block ids, per-row entries, work items); place()
+// uploads it into buffers the plan owns, place_in() into one packed region of
+// caller-provided device memory (no allocation).
 struct AttnPlan {
     DeviceCache* cache = nullptr;
     uint64_t epoch = 0;
@@ -116,13 +127,50 @@ struct AttnPlan {
     int wave_splits = 0;  // > 0: splits per row = waves of one workgroup per (row, KV head)
     bool need_merge = false, with_tail = false, inline_ok = false;
     size_t kv_bytes = 0;  // algorithmic K/V bytes one launch reads
-    DeviceBuffer tables, entries, items_buf, work_buf, work_blocks, part_acc, part_ml, row_done, err;
     RowSplits inline_rows{};  // (first item, splits) per row when rows <= kInlineRows
+    // host image
+    std::vector<int32_t> h_tables;
+    std::vector<int4> h_entries, h_work;
+    std::vector<int2> h_items;
+    std::vector<int32_t> h_work_blocks;
+    // where the device copy lives
+    struct Placement {
+        const int32_t* tables = nullptr;
+        const int4* entries = nullptr;
+        const int2* items = nullptr;
+        const int4* work = nullptr;
+        const int32_t* work_blocks = nullptr;
+        float* part_acc = nullptr;
+        float* part_ml = nullptr;
+        int* row_done = nullptr;
+        int* err = nullptr;
+    } dev;
+    DeviceBuffer region;  // place(): the packed plan (grow-only)
+    PinnedBuffer staging;
+    hipStream_t last_stream = nullptr;
+
+    AttnPlan() = default;
+    AttnPlan(const AttnPlan&) = delete;
+    AttnPlan& operator=(const AttnPlan&) = delete;
+
     // Builds the plan for rows reading `cached[r]` tokens of `seq_of_row[r]`,
     // followed by the row's uncommitted tail token when tail_rows[r] != 0.
+    void compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, const std::vector<size_t>& cached,
+                 const std::vector<uint8_t>& tail_rows, int heads, size_t split_override);
+    // into the plan's own region, one asynchronous copy on the cache's stream
+    void place();
+    // bytes place_in needs, and the leading part of them it copies
+    size_t region_bytes(size_t* copied = nullptr) const;
+    // packs the image into `host` (at least the copied bytes; it must stay
+    // untouched until the copy on `s` has run) and copies it to `device`
+    void place_in(char* device, size_t capacity, hipStream_t s, char* host);
     void build(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, const std::vector<size_t>& cached,
-               const std::vector<uint8_t>& tail_rows, int heads, size_t split_override);
+               const std::vector<uint8_t>& tail_rows, int heads, size_t split_override) {
+        compute(c, seq_of_row, cached, tail_rows, heads, split_override);
+        place();
+    }
     void launch(int layer, const float* q, const float* tail_k, const float* tail_v, float* out, hipStream_t s);
+    // waits for the last launch's stream; a non-finite score throws
     void check();
 };
 
@@ -138,10 +186,29 @@ struct PrefillPlan {
     size_t total_rows = 0;
     AttnPlan rows_plan;
     DeviceBuffer tables, seqs, err;
+    hipStream_t last_stream = nullptr;
+    PrefillPlan() = default;
+    PrefillPlan(const PrefillPlan&) = delete;
+    PrefillPlan& operator=(const PrefillPlan&) = delete;
     void build(DeviceCache* c, const uint64_t* sequences, size_t count, size_t heads, size_t context,
                const size_t* start, const size_t* rows, int precision);
     void launch(int layer, const float* q, float* out, hipStream_t s);
     void check();
 };
 
+// ModelConfig::validate (model.hpp:13-19), the part attention depends on
+void check_attention_config(const DeviceCache& c, size_t heads, size_t context);
+
+// Rows of fused_paged_attention calls (attention.hpp:57-83) for `count`
+// sequences: the argument checks of attention.hpp:59-63 and the visible cap.
+void attention_rows(const DeviceCache& c, const uint64_t* seqs, size_t count, size_t context, bool tail,
+                    const size_t* visible, std::vector<uint64_t>& seq_of_row, std::vector<size_t>& cached,
+                    std::vector<uint8_t>& tail_rows);
+
+}  // namespace tvara_amd
+
+// the device cache behind a C ABI handle (capi.cpp); throws for NULL
+struct tvara_kv_cache;
+namespace tvara_amd {
+DeviceCache& device_cache(tvara_kv_cache* handle);
 }  // namespace tvara_amd

@@ -200,7 +200,7 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
 
     // attention rows: the cached tokens plus this token as the tail
     // (paged_model.hpp:22; attention.hpp:80)
-    AttnPlan plan;
+    AttnPlan& plan = step_plan_;
     plan.build(cache_.get(), {sequence}, {position}, {1}, static_cast<int>(c.heads), 0);
 
     for (size_t l = 0; l < c.layers; ++l) {
@@ -352,7 +352,7 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     // Per layer: the products write split sums, and each epilogue finishes
     // what follows its product (RoPE; the residual add with the next
     // RMSNorm; SwiGLU) and writes the next product's input.
-    AttnPlan plan;
+    AttnPlan& plan = batch_plan_;
     plan.build(cache_.get(), seqs, positions, std::vector<uint8_t>(n, 1), static_cast<int>(c.heads), 0);
     launch_resid_norm(nullptr, 0, x, at(layers_[0].attn_norm, 0), N, H, c.rms_epsilon, norm,
                       halves_for(layers_[0].qkv), unscale, s);

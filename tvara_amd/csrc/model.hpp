@@ -129,6 +129,9 @@ private:
     ModelConfig cfg_;
     std::string metadata_;
     std::unique_ptr<DeviceCache> cache_;
+    // the attention plans of a step, rebuilt per token into the same device
+    // region (no allocation once it is large enough)
+    AttnPlan step_plan_, batch_plan_;
     Weight embedding_, output_;
     DeviceBuffer final_norm_;
     bool has_output_ = false;

@@ -37,6 +37,9 @@ def runtime():
         h.hipGetErrorString.argtypes = [C.c_int]
         h.hipGetDeviceCount.argtypes = [C.POINTER(C.c_int)]
         h.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        h.hipStreamCreateWithFlags.argtypes = [C.POINTER(C.c_void_p), C.c_uint]
+        h.hipStreamSynchronize.argtypes = [C.c_void_p]
+        h.hipStreamDestroy.argtypes = [C.c_void_p]
         _hip = h
     return _hip
 
@@ -94,6 +97,25 @@ class DeviceArray:
 
     def __del__(self):
         self.free()
+
+
+class Stream:
+    """A HIP stream at the default priority; non_blocking streams do not wait
+    for the null stream (hipStreamNonBlocking)."""
+
+    def __init__(self, non_blocking=True):
+        p = C.c_void_p()
+        check(runtime().hipStreamCreateWithFlags(C.byref(p), 1 if non_blocking else 0))
+        self.h = p.value
+
+    def synchronize(self):
+        check(runtime().hipStreamSynchronize(self.h))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            runtime().hipStreamSynchronize(self.h)
+            runtime().hipStreamDestroy(self.h)
+            self.h = None
 
 
 class Event:
