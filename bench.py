@@ -1,16 +1,30 @@
-"""Paged decode attention benchmark on one MI355X.
+"""Benchmarks of the paged KV path on one MI355X.
 
-A step is one batched paged decode attention launch (decode kernel plus the
-split merge) over the Llama-3.2-1B attention shape: 64 sequences, 32 query /
-8 KV heads, head_dim 64, f32 KV, contexts uniform in [128, 4096], 16-token
-blocks scattered over a 65,536-block pool.  Inputs (K/V blocks, block tables,
-queries) are resident in HBM before the timed region.
+With no --workload the run covers every configuration of the path, one JSON
+line each, the headline last:
 
-Prints one JSON line: value = algorithmic bytes moved per step / step time
-(GB/s), plus decode tokens/s, the roofline of the decode kernel from HIP events
-around its own launches (a second pass of the same steps, so the event packets
-stay out of the throughput region), and the reference CPU path timed on this
-host.
+  c1     SmolLM2-135M decode: 1 sequence x 512 tokens, 9/3 heads, d=64, f32;
+  c3     KV-management stress: 256 sequences forked from a 1,024-token
+         prefix, 22 layers x 8 x 64 f32, one appended token per sequence a
+         step (c3cow: a 1,025-token prefix, so the first step copies 256
+         shared tail blocks);
+  c4     chunked prefill: 8 x (2,048 cached + 512-token causal chunk), 32/8
+         heads, d=64, bf16 MFMA;
+  c5     Llama-3-8B decode: 16 x 32,768 tokens, 32/8 heads, d=128, Q8_0;
+  c2     (headline, printed last) Llama-3.2-1B decode: 64 sequences, 32/8
+         heads, d=64, f32 KV, contexts uniform in [128, 4096], 16-token blocks
+         scattered over a 65,536-block pool.
+
+A decode step is one batched paged decode attention launch (decode kernel
+plus the split merge) with every input resident in HBM before the timed
+region; value = algorithmic bytes per step / step time.  The roofline is the
+dominant kernel's algorithmic bytes (or flops) over its own duration, from
+HIP events the library records around its launches in a second pass of the
+same steps.  Each line carries the reference's own CPU path (oracle/_ref,
+built from its sources) timed on this host: one warm-up, then the median of
+nine runs, on one thread and on every host thread the box grants, with the
+host's CPU model, core count, compiler, flags, AVX2 use and a STREAM-style
+triad bandwidth.
 """
 
 from __future__ import annotations
@@ -18,6 +32,8 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -27,62 +43,100 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16
 METRIC = "paged decode attn: achieved HBM GB/s (% of peak) + decode tokens/s, 1 MI355X"
 MODEL_LAYERS = {"llama-3.2-1b-decode-64x[128,4096]": 16, "smollm2-135m-decode-1x512": 30,
                 "llama-3-8b-q8_0-decode-16x32768": 32}
+DEFAULT_RUN = ["c1", "c3", "c3cow", "c4", "c5", "c2"]
+REF_FLAGS = "g++ -O2 -std=c++20 -fPIC (oracle/Makefile, target ref; the reference's recorded flags)"
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(w, seconds_cap=30.0):
-    """The reference's fused_paged_attention (oracle/_ref, built from the
-    reference headers) on one host thread over the same workload; the C
-    restatement of the oracle when _ref was not built."""
-    import numpy as np
+# ----------------------------------------------------------- CPU baseline
 
-    from oracle import pyoracle
-    from tvara_amd import workloads
+def host_threads():
+    """Host threads the CPU baseline uses: what the process may run on,
+    capped at 16 (a one-GPU box's CPU share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
 
-    kind = "reference" if pyoracle.ref_available() else "port"
-    make = pyoracle.RefCache if kind == "reference" else pyoracle.Cache
-    g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)
-    cache = make(*g)
-    seqs = workloads.fill_decode(cache, w)
-    q = w.queries()
-    times, done_seqs = [], 0
-    t_all = time.perf_counter()
-    for rep in range(3):
+
+_HOST = None
+
+
+def host_info():
+    """The host the CPU baseline ran on (recorded once per run)."""
+    global _HOST
+    if _HOST is None:
+        from oracle import pyoracle
+
+        model = "unknown"
+        try:
+            for line in Path("/proc/cpuinfo").read_text().splitlines():
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+        try:
+            gxx = subprocess.run(["g++", "-dumpfullversion"], capture_output=True, text=True).stdout.strip()
+        except OSError:
+            gxx = "unknown"
+        t = host_threads()
+        doubles = 1 << 24  # 128 MiB per array
+        _HOST = {"cpu": model, "nproc": os.cpu_count(), "threads_used": t, "compiler": f"g++ {gxx}",
+                 "flags": REF_FLAGS, "avx2_dot": pyoracle.ref_uses_avx2(),
+                 "triad_GBps_1thread": round(pyoracle.host_triad_gbs(doubles, 1), 2),
+                 f"triad_GBps_{t}threads": round(pyoracle.host_triad_gbs(doubles, t), 2)}
+        log("host:", json.dumps(_HOST))
+    return _HOST
+
+
+def median_of_9(run):
+    """One warm-up run, then the median of nine (tests/core/prefill_support.hpp:13-16)."""
+    run()
+    times = []
+    for _ in range(9):
         t0 = time.perf_counter()
-        n = 0
-        for i, s in enumerate(seqs):
-            cache.fused_paged_attention(q[i], s, 0, w.heads, w.context)
-            n += 1
-            if time.perf_counter() - t_all > seconds_cap:
-                break
-        times.append((time.perf_counter() - t0, n))
-        if time.perf_counter() - t_all > seconds_cap:
-            break
-    # median per-sequence-batch time scaled to the whole batch
-    per_pass = sorted(t * len(seqs) / n for t, n in times)[len(times) // 2]
-    done_seqs = times[-1][1]
-    value = w.kv_bytes() / per_pass / 1e9
-    del cache
-    return {
-        "value": round(value, 4),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": kind,
-        "sample": f"{len(times)} pass(es) of fused_paged_attention over {done_seqs} of {len(seqs)} sequences, "
-                  f"1 thread, median scaled to the batch; {per_pass * 1e3:.1f} ms per batch, "
-                  f"{len(seqs) / per_pass:.1f} decode tokens/s",
-        "ms_per_step": round(per_pass * 1e3, 3),
-    }
+        run()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
 
 
-MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16
+def cpu_result(unit, one, alln, threads, sample, work_per_run_one, work_per_run_all, extra=None):
+    """A cpu_baseline object: value and cores from the all-thread run (on
+    `threads` threads), the one-thread run beside it."""
+    t = threads
+    out = {"value": round(work_per_run_all / alln, 6), "unit": unit, "cores": t, "kind": "reference",
+           "sample": sample, "protocol": "1 warm-up, median of 9 runs",
+           "one_thread": {"value": round(work_per_run_one / one, 6), "unit": unit, "cores": 1,
+                          "ms_per_run": round(one * 1e3, 3)},
+           "all_threads": {"value": round(work_per_run_all / alln, 6), "unit": unit, "cores": t,
+                           "ms_per_run": round(alln * 1e3, 3)},
+           "host": host_info()}
+    if extra:
+        out.update(extra)
+    return out
 
+
+def ref_ready(args):
+    if args.no_cpu_baseline:
+        return False
+    from oracle import pyoracle
+
+    if not pyoracle.ref_available():
+        log("cpu baseline skipped: oracle/_ref is not built")
+        return False
+    return True
+
+
+# ------------------------------------------------------------- GPU timing
 
 def timed_steps(call, steps):
     """ms per step over `steps` back-to-back calls, bracketed by device
@@ -129,14 +183,193 @@ def hbm_traffic(workload, kernel):
     return None if entry is None else int(entry["bytes_per_launch"])
 
 
-def bench_prefill(args, w):
-    """Chunked prefill, 8 x (2,048 cached + 512 causal chunk), 32/8 heads, d=64
-    (or d=128): the bf16 MFMA kernel's TFLOP/s over the algorithmic 77.3 (154.6)
-    GFLOP."""
+# ----------------------------------------------------------------- decode
+
+# CPU samples per decode workload: sequences for the one-thread run, for the
+# all-thread run, and reference calls per run (a single short row repeats)
+CPU_DECODE_SAMPLE = {"c1": (1, 1, 50), "c2": (64, 64, 1), "c5": (1, 16, 1)}
+
+
+def cpu_rows(w, k, v):
+    """The rows the reference's cache holds for the CPU baseline: Q8_0
+    workloads take their dequantised values (the reference has no quantised
+    KV; Q8_0 dequantisation is quant.hpp:40-49)."""
+    if not w.q8:
+        return k, v
+    from oracle import pyoracle
+
+    return (pyoracle.dequantize_q8_0(pyoracle.quantize_q8_0(k)).reshape(k.shape),
+            pyoracle.dequantize_q8_0(pyoracle.quantize_q8_0(v)).reshape(v.shape))
+
+
+def cpu_decode(key, w, ref, rseqs, qh):
+    """The reference's fused_paged_attention over a sample of the batch: one
+    thread, then every host thread over sequences (std::thread in the shim)."""
+    n1, nall, calls = CPU_DECODE_SAMPLE.get(key, (1, min(w.sequences, host_threads()), 1))
+    threads = min(host_threads(), nall)
+
+    def run(n, th):
+        def go():
+            for _ in range(calls):
+                ref.fused_batch(rseqs[:n], qh[:n], 0, w.heads, w.context, th)
+        return go
+
+    one = median_of_9(run(n1, 1))
+    alln = median_of_9(run(nall, threads))
+    per_token = w.kv_bytes() / w.total_tokens
+    tokens = lambda n: sum(w.lengths[:n])  # noqa: E731
+    sample = (f"the reference's fused_paged_attention over {n1} (1 thread) and {nall} ({threads} threads) of "
+              f"the {w.sequences} sequences" + (f", {calls} calls a run" if calls > 1 else "") +
+              (", on the dequantised Q8_0 values (the reference has no quantised KV)" if w.q8 else "") +
+              "; GB/s counts the workload's algorithmic bytes of the rows processed")
+    return cpu_result("GB/s", one, alln, threads, sample, calls * tokens(n1) * per_token / 1e9,
+                      calls * tokens(nall) * per_token / 1e9,
+                      {"decode_tokens_per_s": round(calls * nall / alln, 2),
+                       "ms_per_step_one_thread": round(one / calls * w.sequences / n1 * 1e3, 3)})
+
+
+def bench_decode(args, key, w):
     import numpy as np
 
     from tvara_amd import attention, hip, kv, workloads
-    cache = kv.PagedCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks(), fmt=kv.Q8_0 if w.q8 else kv.F32)
+
+    log(f"workload {w.name}: {w.sequences} sequences, {w.total_tokens} tokens")
+    g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)
+    cache = kv.PagedCache(*g, fmt=kv.Q8_0 if w.q8 else kv.F32)
+    # the reference's cache takes the same rows (Q8_0 workloads: their
+    # dequantised values, as the reference has no quantised KV) in the same
+    # fill, so the inputs are generated once
+    ref, rseqs = None, []
+    if ref_ready(args):
+        from oracle import pyoracle
+
+        blocks = sum((n + w.tokens_per_block - 1) // w.tokens_per_block for n in w.lengths) + 8
+        ref = pyoracle.RefCache(w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, blocks)
+    t0 = time.perf_counter()
+    workloads.place_blocks(cache, w.placement())
+    seqs = []
+    for i in range(w.sequences):
+        k, v = w.keys(i), w.values(i)
+        s = cache.create_sequence()
+        cache.append_many(s, k, v)
+        seqs.append(s)
+        if ref is not None:
+            r = ref.create_sequence()
+            ref.append_many(r, *cpu_rows(w, k, v))
+            rseqs.append(r)
+    cache.synchronize()
+    log(f"filled in {time.perf_counter() - t0:.1f}s")
+    qh = w.queries()
+    q = hip.DeviceArray.from_numpy(qh)
+    out = hip.DeviceArray(q.shape)
+    plan = attention.DecodePlan(cache, seqs, w.heads, w.context)
+    log(f"plan: split {plan.split_tokens} tokens, {plan.items} work items")
+    for _ in range(args.warmup):
+        plan.launch(0, q.ptr, out.ptr)
+    plan.check()
+    hip.synchronize()
+
+    # the timed region: K launches on the cache's stream (the null stream)
+    step = lambda: plan.launch(0, q.ptr, out.ptr)  # noqa: E731
+    ms_per_step = timed_steps(step, args.steps)
+    plan.check()
+    kt = kernel_times(step, args.steps, ["paged_decode", "paged_decode_merge"])
+    kernel_avg_ms, launches = kt["paged_decode"]
+    merge_ms, merges = kt["paged_decode_merge"]
+    log(f"step {ms_per_step * 1e3:.1f} us; decode kernel {kernel_avg_ms * 1e3:.1f} us x{launches}; "
+        f"merge {merge_ms * 1e3:.1f} us x{merges}")
+    assert np.isfinite(out.numpy()).all()
+    # the same batch through the host-buffer entry point (queries in and
+    # outputs out over PCIe): reported beside the value, never as it
+    attention.decode_batch(cache, qh, seqs, 0, w.heads, w.context)
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        attention.decode_batch(cache, qh, seqs, 0, w.heads, w.context)
+    host_ms = (time.perf_counter() - t0) / reps * 1e3
+
+    kv_bytes = w.kv_bytes()
+    step_bytes = kv_bytes + w.qo_bytes() + w.table_bytes()
+    gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    kernel_bytes = kv_bytes + w.qo_bytes() // 2 + w.table_bytes()
+    kernel_gbs = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
+    tokens_per_s = w.sequences / (ms_per_step * 1e-3)
+    layers = MODEL_LAYERS.get(w.name, 1)
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0" if w.q8 else "f32",
+        "data": "synthetic: K/V/q ~ N(0,1) from a seeded splitmix64 stream, blocks at a seeded permutation",
+        "config": {"workload": w.name, "sequences": w.sequences, "heads": w.heads, "kv_heads": w.kv_heads,
+                   "head_dim": w.head_dim, "tokens_per_block": w.tokens_per_block, "total_tokens": w.total_tokens,
+                   "pool_blocks": w.pool_blocks, "split_tokens": plan.split_tokens, "work_items": plan.items},
+        "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "decode_tokens_per_s": round(tokens_per_s, 1),
+        "model_decode_tokens_per_s": round(tokens_per_s / layers, 1),
+        "model_layers": layers,
+        "host_buffers_ms_per_step": round(host_ms, 4),
+        "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(w.name, "paged_decode"),
+                     "kernel": "paged_decode", "kernel_avg_us": round(kernel_avg_ms * 1e3, 3),
+                     "merge_avg_us": round(merge_ms * 1e3, 3) if merges else 0.0,
+                     "algorithmic_bytes": kernel_bytes},
+        "cpu_baseline": None,
+    }
+    del plan, cache, q, out
+    if ref is not None:
+        t0 = time.perf_counter()
+        result["cpu_baseline"] = cpu_decode(key, w, ref, rseqs, qh)
+        log(f"cpu baseline in {time.perf_counter() - t0:.1f}s")
+    del ref
+    return result
+
+
+# ---------------------------------------------------------------- prefill
+
+def chunk_flops(w, first, count):
+    """Causal chunk rows first .. first+count-1 of one sequence: 4·d flops per
+    (row, head, visible key)."""
+    keys = sum(w.prefix + i + 1 for i in range(first, first + count))
+    return 4 * w.head_dim * w.heads * keys
+
+
+def cpu_prefill(w):
+    """The reference's fused_prompt_attention (FP64, row by row) over the first
+    chunk: its first 64 rows on one thread, all its rows in runs of 16 on
+    every host thread."""
+    from oracle import pyoracle
+    from tvara_amd import workloads
+
+    ref = pyoracle.RefCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks())
+    rs = workloads.fill_prefill(ref, w)[0]
+    qs = w.chunk_queries(0)
+    threads = host_threads()
+    n1 = 64
+    one = median_of_9(lambda: ref.prompt_batch(qs[:n1], rs, 0, w.prefix, n1, w.heads, w.context, n1, 1))
+    alln = median_of_9(lambda: ref.prompt_batch(qs, rs, 0, w.prefix, w.chunk, w.heads, w.context, 16, threads))
+    return cpu_result("TFLOP/s", one, alln, threads,
+                      f"the reference's fused_prompt_attention on chunk 0: rows 0-{n1 - 1} on 1 thread, all "
+                      f"{w.chunk} rows in runs of 16 on {threads} threads",
+                      chunk_flops(w, 0, n1) / 1e12, chunk_flops(w, 0, w.chunk) / 1e12)
+
+
+def bench_prefill(args, w):
+    """Chunked prefill: the bf16 MFMA kernel's TFLOP/s over the algorithmic
+    flops of the causal chunks."""
+    import numpy as np
+
+    from tvara_amd import attention, hip, kv, workloads
+
+    cache = kv.PagedCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks(),
+                          fmt=kv.Q8_0 if w.q8 else kv.F32)
     seqs = workloads.fill_prefill(cache, w)
     q = hip.DeviceArray.from_numpy(np.concatenate([w.chunk_queries(i) for i in range(w.sequences)]))
     out = hip.DeviceArray(q.shape)
@@ -154,63 +387,61 @@ def bench_prefill(args, w):
     assert np.isfinite(out.numpy()).all()
     tfs = w.flops() / (kernel_ms * 1e-3) / 1e12
     log(f"prefill kernel {kernel_ms * 1e3:.1f} us, call {ms_per_step * 1e3:.1f} us, {tfs:.1f} TFLOP/s")
-    cpu = None
-    if not args.no_cpu_baseline:
-        from oracle import pyoracle
-
-        if pyoracle.ref_available():
-            # the reference's fused_prompt_attention (its FP64 loop, one
-            # thread), sequence by sequence over about 80 GFLOP of the workload
-            ns = max(1, min(w.sequences, int(80e9 * w.sequences / w.flops())))
-            ref = pyoracle.RefCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks())
-            rseqs = workloads.fill_prefill(ref, w)[:ns]
-            t0 = time.perf_counter()
-            for i, rs in enumerate(rseqs):
-                ref.fused_prompt_attention(w.chunk_queries(i), rs, 0, w.prefix, w.chunk, w.heads, w.context)
-            cpu_s = time.perf_counter() - t0
-            cpu = {"value": round(w.flops() * ns / w.sequences / cpu_s / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
-                   "kind": "reference",
-                   "sample": f"{ns} of the {w.sequences} chunks ({w.chunk} rows, {w.heads} heads each) through "
-                             f"the reference's fused_prompt_attention, 1 thread: {cpu_s:.2f} s",
-                   "seconds": round(cpu_s, 3)}
-    print(json.dumps({
+    del plan, cache, q, out
+    cpu = cpu_prefill(w) if ref_ready(args) and not w.q8 else None
+    return {
         "metric": "paged chunked prefill attn: achieved TFLOP/s (MFMA utilisation), 1 MI355X",
         "value": round(w.flops() / (ms_per_step * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic: K/V/q ~ N(0,1)",
         "config": {"workload": w.name, "sequences": w.sequences, "prefix": w.prefix, "chunk": w.chunk,
-                   "heads": w.heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim},
+                   "heads": w.heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
+                   "kv": "q8_0" if w.q8 else "f32"},
         "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
                      "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
                      "traffic": hbm_traffic(w.name, "paged_prefill_bf16"), "kernel": "paged_prefill_bf16",
                      "kernel_avg_us": round(kernel_ms * 1e3, 3), "algorithmic_flops": w.flops()},
         "cpu_baseline": cpu,
-    }), flush=True)
+    }
 
 
-def bench_kv(args, cow):
-    """KV-management stress: 256 sequences forked from a shared 1,024-token
-    (or 1,025-token, copy-on-write) prefix, 22 layers x 8 x 64 f32; a step is
-    one batched append of one token to every sequence (host bookkeeping, the
-    zero-fill / copy-on-write launch and the row-copy launch).  K/V rows are
-    resident in HBM.  Bytes per step: the rows written, plus a block's zero
-    fill for every new block and a read and a write of a block for every
-    copy-on-write."""
-    import numpy as np
+# -------------------------------------------------------------- KV stress
 
-    from tvara_amd import hip, kv, workloads
+def cpu_kv(w, step_bytes):
+    """The reference's PagedCache: a run is one fork of the prefix for every
+    sequence and 32 append steps.  The cache is single-owner
+    (docs/kv-cache.md), so one thread."""
+    from oracle import pyoracle
 
-    w = workloads.kv_c3(unaligned=cow)
-    cache = kv.PagedCache(w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.max_blocks())
+    ref = pyoracle.RefCache(w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.max_blocks())
+    src = ref.create_sequence()
+    ref.append_many(src, w.tokens("prefix-k", w.prefix), w.tokens("prefix-v", w.prefix))
+    hk = [w.tokens(f"step{i}-k", w.sequences) for i in range(4)]
+    hv = [w.tokens(f"step{i}-v", w.sequences) for i in range(4)]
+    n_cpu = 32
+
+    def run():
+        rseqs = [ref.fork(src) for _ in range(w.sequences)]
+        for i in range(n_cpu):
+            ref.append_batch(rseqs, hk[i % 4], hv[i % 4])
+        for s in rseqs:
+            ref.drop(s)
+
+    per_run = median_of_9(run)
+    cpu_bytes = sum(step_bytes(i) for i in range(n_cpu))
+    return {"value": round(cpu_bytes / per_run / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "reference",
+            "sample": f"one fork of the prefix for {w.sequences} sequences and {n_cpu} append steps a run; "
+                      "the reference cache is single-owner, so one thread",
+            "protocol": "1 warm-up, median of 9 runs", "ms_per_step": round(per_run / n_cpu * 1e3, 4),
+            "host": host_info()}
+
+
+def kv_step_bytes(w):
+    """Algorithmic bytes of append step i: the rows written, a zero fill per
+    new block, a read and a write per copy-on-write block."""
     width = w.layers * w.kv_heads * w.head_dim
     block_bytes = w.tokens_per_block * width * 2 * 4
     row_bytes = width * 2 * 4
-    # four distinct step batches, used in turn (the contents do not change the work)
-    batches = [(hip.DeviceArray.from_numpy(w.tokens(f"step{i}-k", w.sequences)),
-                hip.DeviceArray.from_numpy(w.tokens(f"step{i}-v", w.sequences))) for i in range(4)]
-    steps_k = [batches[i % 4][0] for i in range(w.steps)]
-    steps_v = [batches[i % 4][1] for i in range(w.steps)]
-    pk, pv = w.tokens("prefix-k", w.prefix), w.tokens("prefix-v", w.prefix)
 
     def step_bytes(i):
         length = w.prefix + i
@@ -223,6 +454,29 @@ def bench_kv(args, cow):
             extra = 0
         return w.sequences * row_bytes + extra
 
+    return step_bytes
+
+
+def bench_kv(args, cow):
+    """KV-management stress: 256 sequences forked from a shared 1,024-token
+    (or 1,025-token, copy-on-write) prefix, 22 layers x 8 x 64 f32; a step is
+    one batched append of one token to every sequence (host bookkeeping, the
+    zero-fill / copy-on-write launch and the row-copy launch).  K/V rows are
+    resident in HBM.  Bytes per step: the rows written, plus a block's zero
+    fill for every new block and a read and a write of a block for every
+    copy-on-write."""
+    from tvara_amd import hip, kv, workloads
+
+    w = workloads.kv_c3(unaligned=cow)
+    cache = kv.PagedCache(w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.max_blocks())
+    step_bytes = kv_step_bytes(w)
+    # four distinct step batches, used in turn (the contents do not change the work)
+    batches = [(hip.DeviceArray.from_numpy(w.tokens(f"step{i}-k", w.sequences)),
+                hip.DeviceArray.from_numpy(w.tokens(f"step{i}-v", w.sequences))) for i in range(4)]
+    steps_k = [batches[i % 4][0] for i in range(w.steps)]
+    steps_v = [batches[i % 4][1] for i in range(w.steps)]
+    pk, pv = w.tokens("prefix-k", w.prefix), w.tokens("prefix-v", w.prefix)
+
     def setup():
         src = cache.create_sequence()
         cache.append_many(src, pk, pv)
@@ -231,7 +485,7 @@ def bench_kv(args, cow):
         cache.synchronize()
         return seqs
 
-    def run_pass(seqs, first, count, timed):
+    def run_pass(seqs, first, count):
         start, stop = hip.Event(), hip.Event()
         hip.synchronize()
         start.record()
@@ -244,14 +498,14 @@ def bench_kv(args, cow):
     # warm-up: whole passes, untimed
     for _ in range(max(1, args.warmup // w.steps)):
         seqs = setup()
-        run_pass(seqs, 0, w.steps, False)
+        run_pass(seqs, 0, w.steps)
         for s in seqs:
             cache.drop(s)
     total_ms, done, nbytes = 0.0, 0, 0
     while done < args.steps:
         seqs = setup()
         n = min(w.steps, args.steps - done)
-        total_ms += run_pass(seqs, 0, n, True)
+        total_ms += run_pass(seqs, 0, n)
         nbytes += sum(step_bytes(i) for i in range(n))
         done += n
         for s, r in zip(seqs, w.rollback()):  # speculative rollback (metadata only)
@@ -262,32 +516,9 @@ def bench_kv(args, cow):
     ms_per_step = total_ms / done
     gbs = nbytes / (total_ms * 1e-3) / 1e9
     log(f"{w.name}: {ms_per_step * 1e3:.1f} us per step, {gbs:.1f} GB/s")
-    cpu = None
-    if not args.no_cpu_baseline:
-        # the reference's PagedCache (oracle/_ref) on one host thread: one fork
-        # of the prefix and the first 32 append steps
-        from oracle import pyoracle
-
-        kind = "reference" if pyoracle.ref_available() else "port"
-        ref = (pyoracle.RefCache if kind == "reference" else pyoracle.Cache)(
-            w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.max_blocks())
-        src = ref.create_sequence()
-        ref.append_many(src, pk, pv)
-        rseqs = [ref.fork(src) for _ in range(w.sequences)]
-        ref.drop(src)
-        hk = [w.tokens(f"step{i}-k", w.sequences) for i in range(4)]
-        hv = [w.tokens(f"step{i}-v", w.sequences) for i in range(4)]
-        n_cpu = 32
-        t0 = time.perf_counter()
-        for i in range(n_cpu):
-            ref.append_batch(rseqs, hk[i % 4], hv[i % 4])
-        cpu_s = (time.perf_counter() - t0) / n_cpu
-        cpu_bytes = sum(step_bytes(i) for i in range(n_cpu)) / n_cpu
-        cpu = {"value": round(cpu_bytes / cpu_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
-               "sample": f"{n_cpu} append steps of 256 tokens after one fork of the prefix, 1 thread; "
-                         f"{cpu_s * 1e3:.2f} ms per step", "ms_per_step": round(cpu_s * 1e3, 4)}
-        del ref
-    print(json.dumps({
+    del cache, batches, steps_k, steps_v
+    cpu = cpu_kv(w, step_bytes) if ref_ready(args) else None
+    return {
         "metric": "paged KV management stress: us per append step + GB/s, 1 MI355X", "value": round(gbs, 2),
         "unit": "GB/s", "n_gpus": 1, "steps": done, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
@@ -299,8 +530,10 @@ def bench_kv(args, cow):
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "kv_append (step)",
                      "algorithmic_bytes_per_step": round(nbytes / done)},
         "cpu_baseline": cpu,
-    }), flush=True)
+    }
 
+
+# ------------------------------------------------------------------ model
 
 def bench_model(args):
     """Decode through the model-level C ABI on a Llama-3.2-1B-shaped GGUF file
@@ -366,26 +599,23 @@ def bench_model(args):
         log(f"single sequence {single_s * 1e3:.2f} ms/token; {nseq} sequences {batch_s * 1e3:.2f} ms/step, "
             f"{tps:.0f} tokens/s")
         cpu = None
-        if not args.no_cpu_baseline:
-            from oracle import pyoracle
-
-            if pyoracle.ref_available():
-                refso = ROOT / "oracle" / "_ref" / "libtvara_ref_capi.so"
-                t0 = time.perf_counter()
-                r = native.NativeModel(path, library=str(refso), max_blocks=16, block_tokens=16)
-                log(f"reference loaded in {time.perf_counter() - t0:.1f}s")
-                rs = r.new_sequence()
-                r.logits(rs, 1)
-                t0 = time.perf_counter()
-                for t in (2, 3, 4):
-                    r.logits(rs, t)
-                cpu_s = (time.perf_counter() - t0) / 3
-                r.close()
-                cpu = {"value": round(1 / cpu_s, 4), "unit": "tokens/s", "cores": 1, "kind": "reference",
-                       "sample": f"3 tokens of one sequence through the reference's tvara_sequence_decode (its "
-                                 f"f32 executor on the calling thread); {cpu_s:.2f} s per token",
-                       "s_per_token": round(cpu_s, 4)}
-        print(json.dumps({
+        if ref_ready(args):
+            refso = ROOT / "oracle" / "_ref" / "libtvara_ref_capi.so"
+            t0 = time.perf_counter()
+            r = native.NativeModel(path, library=str(refso), max_blocks=16, block_tokens=16)
+            log(f"reference loaded in {time.perf_counter() - t0:.1f}s")
+            rs = r.new_sequence()
+            r.logits(rs, 1)
+            t0 = time.perf_counter()
+            for t in (2, 3, 4):
+                r.logits(rs, t)
+            cpu_s = (time.perf_counter() - t0) / 3
+            r.close()
+            cpu = {"value": round(1 / cpu_s, 4), "unit": "tokens/s", "cores": 1, "kind": "reference",
+                   "sample": f"3 tokens of one sequence through the reference's tvara_sequence_decode (its "
+                             f"f32 executor on the calling thread); {cpu_s:.2f} s per token",
+                   "s_per_token": round(cpu_s, 4)}
+        return {
             "metric": "llama-3.2-1b-shaped decode through the model-level C ABI: tokens/s, 1 MI355X",
             "value": round(tps, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(batch_s * 1e3, 4), "higher_is_better": True, "scaling": "weak",
@@ -401,9 +631,45 @@ def bench_model(args):
                          "traffic": None, "kernel": "whole decode step (Q8_0 weights once + cached K/V)",
                          "algorithmic_bytes": step_bytes, "weight_bytes": weight_bytes, "kv_bytes": kv_bytes},
             "cpu_baseline": cpu,
-        }), flush=True)
+        }
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
+
+
+# ------------------------------------------------------------------- main
+
+def compact(r):
+    """The fields of a configuration line that precede the headline."""
+    cpu = r.get("cpu_baseline")
+    out = {"metric": r["metric"], "value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
+           "steps": r["steps"], "warmup": r["warmup"], "dtype": r["dtype"],
+           "config": {"workload": r["config"]["workload"]},
+           "roofline": {k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+           "cpu_baseline": None}
+    for k in ("kernel_avg_us", "merge_avg_us"):
+        if k in r["roofline"]:
+            out["roofline"][k] = r["roofline"][k]
+    if cpu:
+        out["cpu_baseline"] = {"value": cpu["value"], "unit": cpu["unit"], "cores": cpu["cores"], "kind": cpu["kind"]}
+        if "one_thread" in cpu:
+            out["cpu_baseline"]["one_thread"] = cpu["one_thread"]["value"]
+    return out
+
+
+def run_one(args, key):
+    from tvara_amd import workloads
+
+    if key in ("c4", "c4d128", "c4q8"):
+        make = {"c4": workloads.prefill_c4, "c4d128": workloads.prefill_8b, "c4q8": workloads.prefill_c4_q8}
+        return bench_prefill(args, make[key]())
+    if key in ("c3", "c3cow"):
+        return bench_kv(args, key == "c3cow")
+    if key == "llama1b":
+        return bench_model(args)
+    w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5,
+         "gqa8": workloads.decode_gqa8, "gqa8q8": lambda: workloads.decode_gqa8(q8=True),
+         "tiny": workloads.decode_tinyllama, "tinyq8": lambda: workloads.decode_tinyllama(q8=True)}[key]()
+    return bench_decode(args, key, w)
 
 
 def main():
@@ -411,8 +677,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c5", "gqa8", "gqa8q8", "tiny",
-                             "tinyq8", "llama1b"])
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c5", "gqa8", "gqa8q8",
+                             "tiny", "tinyq8", "llama1b"],
+                    help="one configuration; `all` (the default) runs c1, c3, c3cow, c4 and c5, one JSON line "
+                         "each, then the c2 headline line last")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -426,9 +695,7 @@ def main():
     if args.split_tokens:
         os.environ["TVARA_SPLIT_TOKENS"] = str(args.split_tokens)
 
-    import numpy as np
-
-    from tvara_amd import attention, hip, kv, workloads
+    from tvara_amd import hip
 
     if args.copy_mib:
         a, b = hip.DeviceArray((args.copy_mib << 18,)), hip.DeviceArray((args.copy_mib << 18,))
@@ -437,92 +704,14 @@ def main():
         hip.synchronize()
         log(f"copied {args.copy_mib} MiB x3")
         del a, b
-    if args.workload in ("c4", "c4d128", "c4q8"):
-        make = {"c4": workloads.prefill_c4, "c4d128": workloads.prefill_8b, "c4q8": workloads.prefill_c4_q8}
-        return bench_prefill(args, make[args.workload]())
-    if args.workload in ("c3", "c3cow"):
-        return bench_kv(args, args.workload == "c3cow")
-    if args.workload == "llama1b":
-        return bench_model(args)
-    w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5,
-         "gqa8": workloads.decode_gqa8, "gqa8q8": lambda: workloads.decode_gqa8(q8=True),
-         "tiny": workloads.decode_tinyllama, "tinyq8": lambda: workloads.decode_tinyllama(q8=True)}[args.workload]()
-    log(f"workload {w.name}: {w.sequences} sequences, {w.total_tokens} tokens")
-    g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)
-    cache = kv.PagedCache(*g, fmt=kv.Q8_0 if w.q8 else kv.F32)
-    t0 = time.perf_counter()
-    seqs = workloads.fill_decode(cache, w)
-    cache.synchronize()
-    log(f"filled in {time.perf_counter() - t0:.1f}s")
-    q = hip.DeviceArray.from_numpy(w.queries())
-    out = hip.DeviceArray(q.shape)
-    plan = attention.DecodePlan(cache, seqs, w.heads, w.context)
-    log(f"plan: split {plan.split_tokens} tokens, {plan.items} work items")
-    for _ in range(args.warmup):
-        plan.launch(0, q.ptr, out.ptr)
-    plan.check()
-    hip.synchronize()
-
-    # the timed region: K launches on the cache's stream (the null stream)
-    step = lambda: plan.launch(0, q.ptr, out.ptr)  # noqa: E731
-    ms_per_step = timed_steps(step, args.steps)
-    plan.check()
-    kt = kernel_times(step, args.steps, ["paged_decode", "paged_decode_merge"])
-    kernel_avg_ms, launches = kt["paged_decode"]
-    merge_ms, merges = kt["paged_decode_merge"]
-    log(f"step {ms_per_step * 1e3:.1f} us; decode kernel {kernel_avg_ms * 1e3:.1f} us x{launches}; "
-        f"merge {merge_ms * 1e3:.1f} us x{merges}")
-    assert np.isfinite(out.numpy()).all()
-    # the same batch through the host-buffer entry point (queries in and
-    # outputs out over PCIe, block tables uploaded per call): reported beside
-    # the value, never as it
-    qh = w.queries()
-    attention.decode_batch(cache, qh, seqs, 0, w.heads, w.context)
-    t0 = time.perf_counter()
-    for _ in range(20):
-        attention.decode_batch(cache, qh, seqs, 0, w.heads, w.context)
-    host_ms = (time.perf_counter() - t0) / 20 * 1e3
-
-    kv_bytes = w.kv_bytes()
-    step_bytes = kv_bytes + w.qo_bytes() + w.table_bytes()
-    gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
-    kernel_gbs = (kv_bytes + w.qo_bytes() // 2 + w.table_bytes()) / (kernel_avg_ms * 1e-3) / 1e9
-    tokens_per_s = w.sequences / (ms_per_step * 1e-3)
-    layers = MODEL_LAYERS.get(w.name, 1)
-    result = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "q8_0" if w.q8 else "f32",
-        "data": "synthetic: K/V/q ~ N(0,1) from a seeded splitmix64 stream, blocks at a seeded permutation",
-        "config": {"workload": w.name, "sequences": w.sequences, "heads": w.heads, "kv_heads": w.kv_heads,
-                   "head_dim": w.head_dim, "tokens_per_block": w.tokens_per_block, "total_tokens": w.total_tokens,
-                   "pool_blocks": w.pool_blocks, "split_tokens": plan.split_tokens, "work_items": plan.items},
-        "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "decode_tokens_per_s": round(tokens_per_s, 1),
-        "model_decode_tokens_per_s": round(tokens_per_s / layers, 1),
-        "model_layers": layers,
-        "host_buffers_ms_per_step": round(host_ms, 4),
-        "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(w.name, "paged_decode"),
-                     "kernel": "paged_decode", "kernel_avg_us": round(kernel_avg_ms * 1e3, 3),
-                     "algorithmic_bytes": kv_bytes + w.qo_bytes() // 2 + w.table_bytes()},
-    }
-    del plan, cache, q, out
-    if not args.no_cpu_baseline:
+    if args.workload != "all":
+        print(json.dumps(run_one(args, args.workload)), flush=True)
+        return
+    for key in DEFAULT_RUN:
         t0 = time.perf_counter()
-        result["cpu_baseline"] = cpu_baseline(w)
-        log(f"cpu baseline in {time.perf_counter() - t0:.1f}s")
-    else:
-        result["cpu_baseline"] = None
-    print(json.dumps(result), flush=True)
+        r = run_one(args, key)
+        log(f"{key} done in {time.perf_counter() - t0:.1f}s")
+        print(json.dumps(r if key == "c2" else compact(r)), flush=True)
 
 
 if __name__ == "__main__":

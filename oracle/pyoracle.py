@@ -120,6 +120,8 @@ def _load_oracle():
     lib.tvo_dequantize_q8_0.argtypes = [C.POINTER(C.c_uint8), _sz, _fp, _sz]
     lib.tvo_quantize_q8_0_block.argtypes = [_fp, C.POINTER(C.c_uint8)]
     lib.tvo_quantize_q8_0_block.restype = None
+    lib.tvo_quantize_q8_0.argtypes = [_fp, _sz, C.POINTER(C.c_uint8)]
+    lib.tvo_quantize_q8_0.restype = None
     return lib
 
 
@@ -157,12 +159,9 @@ def dequantize_q8_0(raw: np.ndarray) -> np.ndarray:
 
 def quantize_q8_0(x: np.ndarray) -> np.ndarray:
     """Encode float32 values (length a multiple of 32) into 34-byte Q8_0 groups."""
-    x = _f32(x).reshape(-1, 32)
+    x = np.ascontiguousarray(_f32(x).reshape(-1, 32))
     out = np.empty((x.shape[0], 34), np.uint8)
-    lib = oracle_lib()
-    for g in range(x.shape[0]):
-        row = np.ascontiguousarray(x[g])
-        lib.tvo_quantize_q8_0_block(_ptr(row), out[g].ctypes.data_as(C.POINTER(C.c_uint8)))
+    oracle_lib().tvo_quantize_q8_0(_ptr(x), x.shape[0], out.ctypes.data_as(C.POINTER(C.c_uint8)))
     return out.reshape(-1)
 
 
@@ -448,6 +447,11 @@ def ref_lib():
         lib.tvr_radix_external_references.argtypes = [C.c_void_p, C.POINTER(_sz), _sz]
         lib.tvr_half_to_float.restype = C.c_float
         lib.tvr_half_to_float.argtypes = [C.c_uint16]
+        lib.tvr_fused_batch.argtypes = [C.c_void_p, C.POINTER(_u64), _sz, _sz, _sz, _sz, _fp, _fp, C.c_int]
+        lib.tvr_prompt_batch.argtypes = [C.c_void_p, _u64, _sz, _sz, _sz, _sz, _sz, _fp, _fp, _sz, C.c_int]
+        lib.tvr_use_avx2.restype = C.c_int
+        lib.tvr_host_triad.restype = C.c_double
+        lib.tvr_host_triad.argtypes = [_sz, C.c_int, C.c_int]
         lib.tvr_dequantize_q8_0.argtypes = [C.POINTER(C.c_uint8), _sz, _fp, _sz]
         _ref = lib
     return _ref
@@ -635,6 +639,25 @@ class RefCache:
                                                        _ptr(tv), vis, int(scalar), _ptr(out)))
         return out
 
+    def fused_batch(self, seqs, q, layer, heads, context, threads=1):
+        """fused_paged_attention for every listed sequence on `threads`
+        std::threads (the CPU-baseline runner of bench.py)."""
+        seqs = np.ascontiguousarray(seqs, dtype=np.uint64)
+        q = _f32(q).reshape(seqs.size, heads * self.head_dim)
+        out = np.empty_like(q)
+        self._check(self.lib.tvr_fused_batch(self.h, seqs.ctypes.data_as(C.POINTER(_u64)), seqs.size, layer, heads,
+                                             context, _ptr(q), _ptr(out), threads))
+        return out
+
+    def prompt_batch(self, queries, seq, layer, start, count, heads, context, rows_per_unit, threads=1):
+        """fused_prompt_attention over rows start .. start+count-1 in runs of
+        rows_per_unit rows on `threads` std::threads."""
+        q = _f32(queries).reshape(-1)
+        out = np.empty(count * heads * self.head_dim, np.float32)
+        self._check(self.lib.tvr_prompt_batch(self.h, seq, layer, heads, context, start, count, _ptr(q), _ptr(out),
+                                              rows_per_unit, threads))
+        return out
+
     def fused_prompt_attention(self, queries, seq, layer, start, count, heads, context):
         q = _f32(queries).reshape(-1)
         out = np.empty(count * heads * self.head_dim, np.float32)
@@ -651,6 +674,16 @@ def ref_grouped_attention(q, keys, values, positions, heads, kv_heads, head_dim,
     if rc:
         raise _ERRORS.get(rc, OracleError)(lib.tvr_last_error().decode())
     return out
+
+
+def ref_uses_avx2() -> bool:
+    """Whether the reference's attention dot takes its AVX2 path on this host."""
+    return bool(ref_lib().tvr_use_avx2())
+
+
+def host_triad_gbs(doubles: int, threads: int, reps: int = 3) -> float:
+    """STREAM-style triad bandwidth of the host (GB/s, best of reps)."""
+    return ref_lib().tvr_host_triad(doubles, threads, reps) / 1e9
 
 
 def ref_half_to_float(h: int) -> float:

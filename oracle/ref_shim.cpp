@@ -13,10 +13,17 @@
 #include "tvara/radix.hpp"
 
 #include <algorithm>
+#include <atomic>
+#include <functional>
+#include <mutex>
+#include <stdexcept>
+#include <chrono>
 #include <cstring>
 #include <span>
 #include <new>
 #include <string>
+#include <thread>
+#include <vector>
 
 namespace {
 thread_local std::string last_error;
@@ -341,6 +348,91 @@ int tvr_radix_external_references(tvr_radix* r, std::size_t* counts, std::size_t
         if (cap < c.size()) throw std::invalid_argument("reference count buffer too small");
         std::copy(c.begin(), c.end(), counts);
     });
+}
+
+// ---- CPU-baseline runners (bench.py): the reference's own functions over a
+// batch, on `threads` std::threads taking work units from a shared counter.
+
+static void run_parallel(std::size_t units, int threads, const std::function<void(std::size_t)>& body) {
+    std::atomic<std::size_t> next{0};
+    std::atomic<bool> failed{false};
+    std::string error;
+    std::mutex lock;
+    auto worker = [&] {
+        for (std::size_t u; !failed && (u = next++) < units;) {
+            try {
+                body(u);
+            } catch (const std::exception& e) {
+                std::lock_guard<std::mutex> hold(lock);
+                failed = true;
+                error = e.what();
+            }
+        }
+    };
+    std::vector<std::thread> pool;
+    for (int t = 1; t < threads; ++t) pool.emplace_back(worker);
+    worker();
+    for (auto& t : pool) t.join();
+    if (failed) throw std::runtime_error(error);
+}
+
+// fused_paged_attention (attention.hpp:57-83) for every listed sequence, one
+// sequence a work unit; q and out are [count][heads * head_dim]
+int tvr_fused_batch(tvr_cache* c, const std::uint64_t* seqs, std::size_t count, std::size_t layer,
+                    std::size_t heads, std::size_t context, const float* q, float* out, int threads) {
+    return guard([&] {
+        const auto cfg = config(c->cache, heads, context);
+        run_parallel(count, threads, [&](std::size_t i) {
+            auto o = tvara::fused_paged_attention(std::span<const float>(q + i * cfg.hidden, cfg.hidden), c->cache,
+                                                  seqs[i], layer, cfg);
+            std::memcpy(out + i * cfg.hidden, o.data(), o.size() * sizeof(float));
+        });
+    });
+}
+
+// fused_prompt_attention (attention.hpp:85-89) over rows start .. start+count-1
+// of one sequence, in runs of `rows_per_unit` rows a work unit (each run is a
+// call of the reference function on its own rows)
+int tvr_prompt_batch(tvr_cache* c, std::uint64_t seq, std::size_t layer, std::size_t heads, std::size_t context,
+                     std::size_t start, std::size_t count, const float* queries, float* out,
+                     std::size_t rows_per_unit, int threads) {
+    return guard([&] {
+        const auto cfg = config(c->cache, heads, context);
+        const std::size_t units = (count + rows_per_unit - 1) / rows_per_unit;
+        run_parallel(units, threads, [&](std::size_t u) {
+            const std::size_t a = u * rows_per_unit, n = std::min(rows_per_unit, count - a);
+            auto o = tvara::fused_prompt_attention(std::span<const float>(queries + a * cfg.hidden, n * cfg.hidden),
+                                                   c->cache, seq, layer, start + a, n, cfg);
+            std::memcpy(out + a * cfg.hidden, o.data(), o.size() * sizeof(float));
+        });
+    });
+}
+
+// whether the reference's attention dot takes its AVX2 path here (simd.hpp:14-17)
+int tvr_use_avx2(void) { return tvara::use_avx2() ? 1 : 0; }
+
+// STREAM-style triad a = b + s*c over n doubles per array on `threads` threads
+// (each its own contiguous share), best of `reps`: bytes moved (3 x 8 x n) per
+// second.  The host's memory bandwidth, measured before any CPU fraction is
+// quoted.
+double tvr_host_triad(std::size_t n, int threads, int reps) {
+    std::vector<double> a(n), b(n, 1.0), c(n, 2.0);
+    double best = 0;
+    for (int r = 0; r < reps; ++r) {
+        const auto t0 = std::chrono::steady_clock::now();
+        std::vector<std::thread> pool;
+        for (int t = 0; t < threads; ++t)
+            pool.emplace_back([&, t] {
+                const std::size_t lo = n * t / threads, hi = n * (t + 1) / threads;
+                for (std::size_t i = lo; i < hi; ++i) a[i] = b[i] + 3.0 * c[i];
+            });
+        for (auto& th : pool) th.join();
+        const double s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        best = std::max(best, 24.0 * static_cast<double>(n) / s);
+    }
+    volatile double sink = a[n / 2];
+    (void)sink;
+    return best;
 }
 
 float tvr_half_to_float(std::uint16_t h) { return tvara::quant::half_to_float(h); }

@@ -732,3 +732,8 @@ void tvo_quantize_q8_0_block(const float* x, uint8_t* out) {
         out[2 + i] = (uint8_t)(int8_t)r;
     }
 }
+
+/* tvo_quantize_q8_0_block over `groups` consecutive groups of 32 floats. */
+void tvo_quantize_q8_0(const float* x, size_t groups, uint8_t* out) {
+    for (size_t g = 0; g < groups; ++g) tvo_quantize_q8_0_block(x + 32 * g, out + 34 * g);
+}

@@ -120,6 +120,7 @@ float tvo_half_to_float(uint16_t h);
 uint16_t tvo_double_to_half(double x);
 int tvo_dequantize_q8_0(const uint8_t* bytes, size_t nbytes, float* out, size_t count);
 void tvo_quantize_q8_0_block(const float* x32, uint8_t* out34);
+void tvo_quantize_q8_0(const float* x, size_t groups, uint8_t* out);
 
 #ifdef __cplusplus
 }

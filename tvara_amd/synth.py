@@ -14,6 +14,9 @@ on purpose: their outputs differ between standard libraries.
 
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
@@ -52,12 +55,24 @@ def uniform(seed: int, name: str, n: int, start: int = 0) -> np.ndarray:
     return (bits(seed, name, n, start) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
 
 
+def _workers() -> int:
+    """Host threads for large draws (the stream is counter-based, so chunks
+    are independent and the result does not depend on the count)."""
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    return max(1, min(16, cores))
+
+
 def normal(seed: int, name: str, n: int) -> np.ndarray:
     """N(0, 1) float32 values by Box-Muller over consecutive uniform pairs."""
     out = np.empty(n, np.float32)
     pairs = (n + 1) // 2
-    for lo in range(0, pairs, _CHUNK):
-        hi = min(pairs, lo + _CHUNK)
+    chunk = 1 << 18  # pairs per task
+
+    def fill(lo):
+        hi = min(pairs, lo + chunk)
         u = uniform(seed, name, 2 * (hi - lo), 2 * lo)
         radius = np.sqrt(-2.0 * np.log1p(-u[0::2]))
         angle = 2.0 * np.pi * u[1::2]
@@ -66,6 +81,14 @@ def normal(seed: int, name: str, n: int) -> np.ndarray:
         block[1::2] = radius * np.sin(angle)
         m = min(n, 2 * hi) - 2 * lo
         out[2 * lo : 2 * lo + m] = block[:m]
+
+    starts = range(0, pairs, chunk)
+    if len(starts) > 1:
+        with ThreadPoolExecutor(_workers()) as pool:
+            list(pool.map(fill, starts))
+    else:
+        for lo in starts:
+            fill(lo)
     return out
 
 
