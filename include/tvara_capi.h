@@ -282,6 +282,23 @@ TVARA_API int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequence
                                  size_t heads, size_t context, const size_t* start, const size_t* rows,
                                  const float* queries, float* out, int precision, int device_ptrs);
 
+/* tvara_attn_decode with device pointers that allocates nothing: no
+ * hipMalloc, hipFree or allocating library call.  No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * plan (block ids, rows, work items, split counters, error flag) and the
+ * split partials live in a fixed per-GPU device array of
+ * tvara_attn_decode_noalloc_limit() bytes (32 MiB, held until the process
+ * ends); a batch needing more fails with TVARA_INVALID.  Same arguments,
+ * kernels and results as tvara_attn_decode(..., device_ptrs = 1): q, the
+ * optional tails and out are 16-byte aligned device buffers; synchronous on
+ * the cache's stream.  Calls on one GPU share the array: the library
+ * serialises them and each waits for its own work, so none overlap on it. */
+TVARA_API int tvara_attn_decode_noalloc(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t layer,
+                                        size_t heads, size_t context, const float* q, const float* tail_keys,
+                                        const float* tail_values, const size_t* visible, float* out);
+TVARA_API size_t tvara_attn_decode_noalloc_limit(void);
+
 /* A decode plan keeps the listed sequences' block tables resident in HBM so
  * that repeated launches (the same batch over several layers, or timing)
  * upload nothing.  It records the cache's mutation count; launching it after

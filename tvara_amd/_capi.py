@@ -93,6 +93,9 @@ SIGNATURES = {
                                     C.c_int]),
     "tvara_attn_prefill": (C.c_int, [_vp, C.POINTER(_u64), _sz, _sz, _sz, _sz, C.POINTER(_sz), C.POINTER(_sz), _fp,
                                      _fp, C.c_int, C.c_int]),
+    "tvara_attn_decode_noalloc": (C.c_int, [_vp, C.POINTER(_u64), _sz, _sz, _sz, _sz, _vp, _vp, _vp,
+                                            C.POINTER(_sz), _vp]),
+    "tvara_attn_decode_noalloc_limit": (_sz, []),
     "tvara_attn_plan_create": (_vp, [_vp, C.POINTER(_u64), _sz, _sz, _sz, C.POINTER(_sz), C.c_int]),
     "tvara_attn_plan_decode": (C.c_int, [_vp, _sz, _vp, _vp, _vp, _vp, _vp]),
     "tvara_attn_plan_check": (C.c_int, [_vp]),
