@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "abi.hpp"
+#include "host_copy.hpp"
 #include "kv_cache.hpp"
 #include "model.hpp"
 
@@ -208,11 +209,16 @@ int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t c
         // q | tail keys | tail values in one pinned buffer and one copy in;
         // the output comes back through a second pinned buffer
         const size_t nq = count * hidden, nt = tail ? count * kvw : 0;
+        tvara_amd::HostCopier& copier = tvara_amd::HostCopier::shared();
+        std::lock_guard<std::mutex> hold(copier.lock());
         auto* in = static_cast<float*>(cache->io_in.acquire((nq + 2 * nt) * sizeof(float)));
-        std::memcpy(in, q, nq * sizeof(float));
+        auto stage = [&](float* to, const float* from, size_t n) {
+            copier.parallel_copy(reinterpret_cast<char*>(to), reinterpret_cast<const char*>(from), n * sizeof(float));
+        };
+        stage(in, q, nq);
         if (tail) {
-            std::memcpy(in + nq, tail_keys, nt * sizeof(float));
-            std::memcpy(in + nq + nt, tail_values, nt * sizeof(float));
+            stage(in + nq, tail_keys, nt);
+            stage(in + nq + nt, tail_values, nt);
         }
         const size_t out_at = (nq + 2 * nt + 3) / 4 * 4;  // 16-byte aligned
         auto* d = static_cast<float*>(cache->io.ensure((out_at + nq) * sizeof(float)));
@@ -222,7 +228,7 @@ int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t c
         auto* back = static_cast<float*>(cache->io_out.acquire(nq * sizeof(float)));
         TVARA_HIP(hipMemcpyAsync(back, d + out_at, nq * sizeof(float), hipMemcpyDeviceToHost, s));
         plan.check();  // waits for the stream, the copy out included
-        std::memcpy(out, back, nq * sizeof(float));
+        stage(out, back, nq);
     });
 }
 
@@ -253,8 +259,10 @@ int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t 
             plan.check();
             return;
         }
+        tvara_amd::HostCopier& copier = tvara_amd::HostCopier::shared();
+        std::lock_guard<std::mutex> hold(copier.lock());
         auto* in = static_cast<float*>(cache->io_in.acquire(n * sizeof(float)));
-        std::memcpy(in, queries, n * sizeof(float));
+        copier.parallel_copy(reinterpret_cast<char*>(in), reinterpret_cast<const char*>(queries), n * sizeof(float));
         const size_t out_at = (n + 3) / 4 * 4;
         auto* d = static_cast<float*>(cache->io.ensure((out_at + n) * sizeof(float)));
         TVARA_HIP(hipMemcpyAsync(d, in, n * sizeof(float), hipMemcpyHostToDevice, s));
@@ -263,7 +271,7 @@ int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t 
         auto* back = static_cast<float*>(cache->io_out.acquire(n * sizeof(float)));
         TVARA_HIP(hipMemcpyAsync(back, d + out_at, n * sizeof(float), hipMemcpyDeviceToHost, s));
         plan.check();
-        std::memcpy(out, back, n * sizeof(float));
+        copier.parallel_copy(reinterpret_cast<char*>(out), reinterpret_cast<const char*>(back), n * sizeof(float));
     });
 }
 

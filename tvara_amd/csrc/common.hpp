@@ -78,6 +78,16 @@ struct RowSplits {
     int2 r[kInlineRows];
 };
 
+// Launch order of a decode launch's work items when the plan has at most
+// kOrderedItems of them and one workgroup per item: workgroup s runs item
+// item[s] (n == 0: workgroup s runs item s).  Workgroups go to the XCDs
+// round-robin by id, so the order sets how many tokens each XCD streams.
+constexpr int kOrderedItems = 512;
+struct WorkOrder {
+    int n;
+    uint16_t item[kOrderedItems];
+};
+
 struct DecodeArgs {
     const char* pool;
     BlockLayout lay;
@@ -137,7 +147,7 @@ void launch_q8_to_canonical(const char* pool, const BlockLayout& lay, int64_t id
 void launch_canonical_to_q8(char* pool, const BlockLayout& lay, int64_t id, const uint8_t* in, hipStream_t s);
 // decode.hip
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
-                   hipStream_t s);
+                   const WorkOrder* order, hipStream_t s);
 int decode_waves(int kv_heads, int group, int format, int head_dim);
 int decode_slots(int kv_heads, int group, int format, int head_dim);  // waves' worth of work per work item
 int wave_split_waves(int rows, int kv_heads, int group, int format, int head_dim, int tpb, size_t max_tokens);

@@ -320,12 +320,16 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
 // the workgroup has waves), merged in LDS: no second launch and no global
 // round trip, for launches too small to fill the GPU.
 template <int D, int G, int LPT, int NB, bool kWS>
-__global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(const DecodeArgs a,
+                                                                                const WorkOrder order) {
     constexpr int E = D / LPT, NV = E / 4, TT = 64 / LPT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int groups = kWS ? 1 : a.lay.kv_heads / nwaves;
+    // the launch order (a kernel argument, so no dependent load) maps this
+    // workgroup to its work item
+    const int slot = static_cast<int>(blockIdx.x) / groups;
     const int item = kWS ? (static_cast<int>(blockIdx.x) / a.lay.kv_heads) * nwaves + wave
-                         : static_cast<int>(blockIdx.x) / groups;
+                         : (order.n ? static_cast<int>(order.item[slot]) : slot);
     const int kh = kWS ? static_cast<int>(blockIdx.x) % a.lay.kv_heads
                        : (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
     // the item's descriptor and block ids come in two independent loads
@@ -1258,20 +1262,25 @@ void launch_merge(const DecodeArgs& a, const RowSplits* inline_rows, int nrows, 
 }
 
 template <int D, int G, int LPT>
-void launch_f32(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
+void launch_f32(const DecodeArgs& a, int nitems, int waves, const WorkOrder& order, hipStream_t s) {
     const size_t lds = (static_cast<size_t>(waves) * 4 * G * D + waves * 2 * G) * sizeof(float);
     const dim3 grid(nitems * (a.lay.kv_heads / waves)), block(64 * waves);
     // two tiles in flight: a third needs more than the 256 VGPRs that keep two
     // waves per SIMD, and measured slower
-    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, false>, grid, block, lds, s, a);
+    WorkOrder o;
+    o.n = a.lay.kv_heads == waves && order.n == nitems ? order.n : 0;
+    if (o.n) std::copy(order.item, order.item + o.n, o.item);
+    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, false>, grid, block, lds, s, a, o);
 }
 
 template <int D, int G, int LPT>
 void launch_f32_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
     const int waves = a.wave_splits;
     const size_t lds = (static_cast<size_t>(waves) * 4 * G * D + waves * 2 * G) * sizeof(float);
+    WorkOrder o;
+    o.n = 0;
     launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, true>, dim3(nrows * a.lay.kv_heads), dim3(64 * waves), lds,
-           s, a);
+           s, a, o);
 }
 
 template <int D>
@@ -1336,7 +1345,7 @@ bool q8_mma_shape(int group, int format, int head_dim) {
 // (four at head_dim 64); five to eight take eight lanes a token at either
 // head_dim, so the queries and accumulators of a lane stay at 2 * G * D / 8.
 template <int D>
-bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
+bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, const WorkOrder& order, hipStream_t s) {
     constexpr int LPT = D == 64 ? 4 : 8;
     const int G = a.group;
     if (G > 8) return false;
@@ -1351,17 +1360,17 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, hipStream_t s) {
     }
     if (a.lay.format == kF32) {
         switch (G) {
-            case 1: launch_f32<D, 1, LPT>(a, nitems, waves, s); return true;
-            case 2: launch_f32<D, 2, LPT>(a, nitems, waves, s); return true;
-            case 3: launch_f32<D, 3, LPT>(a, nitems, waves, s); return true;
-            case 4: launch_f32<D, 4, LPT>(a, nitems, waves, s); return true;
+            case 1: launch_f32<D, 1, LPT>(a, nitems, waves, order, s); return true;
+            case 2: launch_f32<D, 2, LPT>(a, nitems, waves, order, s); return true;
+            case 3: launch_f32<D, 3, LPT>(a, nitems, waves, order, s); return true;
+            case 4: launch_f32<D, 4, LPT>(a, nitems, waves, order, s); return true;
             default: break;
         }
         switch (G) {
-            case 5: launch_f32<D, 5, 8>(a, nitems, waves, s); return true;
-            case 6: launch_f32<D, 6, 8>(a, nitems, waves, s); return true;
-            case 7: launch_f32<D, 7, 8>(a, nitems, waves, s); return true;
-            case 8: launch_f32<D, 8, 8>(a, nitems, waves, s); return true;
+            case 5: launch_f32<D, 5, 8>(a, nitems, waves, order, s); return true;
+            case 6: launch_f32<D, 6, 8>(a, nitems, waves, order, s); return true;
+            case 7: launch_f32<D, 7, 8>(a, nitems, waves, order, s); return true;
+            case 8: launch_f32<D, 8, 8>(a, nitems, waves, order, s); return true;
             default: break;
         }
         return false;
@@ -1460,7 +1469,13 @@ bool decode_fast_path(const DecodeArgs& a) {
 }
 
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
-                   hipStream_t s) {
+                   const WorkOrder* order, hipStream_t s) {
+    static const WorkOrder identity = [] {
+        WorkOrder o;
+        o.n = 0;
+        return o;
+    }();
+    const WorkOrder& ord = order ? *order : identity;
     if (nitems <= 0) return;
     if (a.wave_splits) {  // the plan chose wave splits (wave_split_shape): merged in LDS
         a.lay.head_dim == 64 ? dispatch_ws<64>(a, nrows, s) : dispatch_ws<128>(a, nrows, s);
@@ -1490,8 +1505,8 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
         bool done = false;
         if (fast) {
             const int waves = waves_for(b);
-            done = b.lay.head_dim == 64 ? dispatch_fast<64>(b, nitems, waves, s)
-                                        : dispatch_fast<128>(b, nitems, waves, s);
+            done = b.lay.head_dim == 64 ? dispatch_fast<64>(b, nitems, waves, ord, s)
+                                        : dispatch_fast<128>(b, nitems, waves, ord, s);
         }
         if (!done) {
             if (b.lay.head_dim > kGenericMaxDim) throw std::invalid_argument("head_dim above 512 is not supported");

@@ -57,8 +57,15 @@ void HostCopier::worker(int index) {
     }
 }
 
+// never destroyed: its threads wait on a condition variable until the
+// process ends, and nothing runs at static destruction
+HostCopier& HostCopier::shared() {
+    static HostCopier* copier = new HostCopier;
+    return *copier;
+}
+
 void HostCopier::parallel_copy(char* dst, const char* src, size_t bytes) {
-    const int parts = static_cast<int>(std::min<size_t>(threads_.size() + 1, std::max<size_t>(1, bytes >> 18)));
+    const int parts = static_cast<int>(std::min<size_t>(threads_.size() + 1, std::max<size_t>(1, bytes >> 17)));
     if (parts <= 1) {
         std::memcpy(dst, src, bytes);
         return;

@@ -24,16 +24,21 @@ public:
     // synchronous: returns when `bytes` from device `src` (after the work
     // already queued on `s`) are in host `dst`
     void from_device(void* dst, const void* src, size_t bytes, hipStream_t s);
+    // host-to-host copy split over the pool's threads (one thread below 128 KiB)
+    void parallel_copy(char* dst, const char* src, size_t bytes);
+
+    // a process-wide copier; calls on it are serialised by its own lock
+    static HostCopier& shared();
+    std::mutex& lock() { return use_; }
 
 private:
-    void parallel_copy(char* dst, const char* src, size_t bytes);
     void worker(int index);
 
     static constexpr size_t kChunk = size_t(4) << 20;
     void* pinned_[2] = {nullptr, nullptr};
     hipEvent_t done_[2] = {nullptr, nullptr};
     std::vector<std::thread> threads_;
-    std::mutex mu_;
+    std::mutex mu_, use_;
     std::condition_variable work_cv_, done_cv_;
     // the current job: part k of parts goes to worker k - 1 (part 0 stays on
     // the calling thread)

@@ -111,6 +111,7 @@ DeviceCache::DeviceCache(const Geometry& g, int format) : meta_(g), format_(form
     int dev = 0;
     TVARA_HIP(hipGetDevice(&dev));
     TVARA_HIP(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
+    if (hipDeviceGetAttribute(&xcds_, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || xcds_ < 1) xcds_ = 1;
     TVARA_HIP(hipMalloc(&pool_, lay_.stride * geo.max_blocks));
     TVARA_HIP(hipMalloc(&err_, sizeof(int)));
     TVARA_HIP(hipMemset(err_, 0, sizeof(int)));
@@ -408,6 +409,47 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
         kv_bytes += static_cast<size_t>(static_cast<double>(n + tail) * g.kv_width() * 2 * bytes_per_element);
     }
     items = static_cast<int>(its.size());
+    order.n = 0;
+    const bool one_group = decode_waves(static_cast<int>(g.kv_heads), group, c->format(),
+                                        static_cast<int>(g.head_dim)) == static_cast<int>(g.kv_heads);
+    if (!wave_splits && one_group && c->format() == kF32 && items <= kOrderedItems && c->xcds() > 1 &&
+        items >= c->xcds())
+        xcd_balance(c->xcds());
+}
+
+// Workgroup s runs on XCD s mod xcds, and every XCD streams from HBM through
+// its own L2: the launch order deals the items to the XCDs largest first,
+// each to the XCD with the fewest tokens so far that still has a free slot
+// (XCD x has ceil((items - x) / xcds) slots), so the XCDs stream about the
+// same number of tokens (the 64-sequence Llama-3.2-1B plan: the heaviest XCD
+// 7.6% above the mean in item order, 0.1% in this order).
+void AttnPlan::xcd_balance(int xcds) {
+    const int n = items;
+    std::vector<int> tokens(n), idx(n);
+    for (int i = 0; i < n; ++i) {
+        tokens[i] = h_work[i].z - h_work[i].y;
+        idx[i] = i;
+    }
+    std::stable_sort(idx.begin(), idx.end(), [&](int x, int y) { return tokens[x] > tokens[y]; });
+    std::vector<long long> load(xcds, 0);
+    std::vector<std::vector<int>> bins(xcds);
+    for (int i : idx) {
+        int best = -1;
+        for (int x = 0; x < xcds; ++x) {
+            const int cap = (n - x + xcds - 1) / xcds;
+            if (static_cast<int>(bins[x].size()) < cap && (best < 0 || load[x] < load[best])) best = x;
+        }
+        bins[best].push_back(i);
+        load[best] += tokens[i];
+    }
+    std::vector<uint8_t> seen(n, 0);
+    for (int s = 0; s < n; ++s) {
+        const int item = bins[s % xcds][s / xcds];
+        if (seen[item]) throw std::logic_error("decode launch order is not a permutation");
+        seen[item] = 1;
+        order.item[s] = static_cast<uint16_t>(item);
+    }
+    order.n = n;
 }
 
 void AttnPlan::place() {
@@ -509,7 +551,7 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.wave_splits = wave_splits;
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
     a.err = dev.err;
-    launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, s);
+    launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, order.n ? &order : nullptr, s);
     cache->leave(s);
     last_stream = s;
 }

@@ -47,6 +47,7 @@ public:
     void set_stream(hipStream_t s) { stream_ = s; }
     uint64_t epoch() const { return meta_.epoch(); }
     int compute_units() const { return cus_; }
+    int xcds() const { return xcds_; }  // XCDs (L2 domains) the workgroups are dealt over
     void synchronize();
 
     // the host bookkeeping (pool and tables); prefix trees work on it directly
@@ -109,7 +110,7 @@ private:
     BlockLayout lay_{};
     char* pool_ = nullptr;
     hipStream_t stream_ = nullptr;
-    int cus_ = 256;
+    int cus_ = 256, xcds_ = 1;
     hipEvent_t ordered_[2] = {nullptr, nullptr};
     DeviceBuffer scratch_[6];
     PinnedBuffer pinned_[6];
@@ -128,6 +129,7 @@ struct AttnPlan {
     bool need_merge = false, with_tail = false, inline_ok = false;
     size_t kv_bytes = 0;  // algorithmic K/V bytes one launch reads
     RowSplits inline_rows{};  // (first item, splits) per row when rows <= kInlineRows
+    WorkOrder order{};        // launch order of the items (n == 0: item order)
     // host image
     std::vector<int32_t> h_tables;
     std::vector<int4> h_entries, h_work;
@@ -159,6 +161,7 @@ struct AttnPlan {
                  const std::vector<uint8_t>& tail_rows, int heads, size_t split_override);
     // into the plan's own region, one asynchronous copy on the cache's stream
     void place();
+    void xcd_balance(int xcds);
     // bytes place_in needs, and the leading part of them it copies
     size_t region_bytes(size_t* copied = nullptr) const;
     // packs the image into `host` (at least the copied bytes; it must stay
