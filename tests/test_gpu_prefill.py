@@ -103,9 +103,14 @@ def test_bf16_c4_shape(device, oracle, make, fmt):
                                   w.context, precision="bf16").reshape(w.sequences, w.chunk, -1)
     f32 = attention.prefill_batch(dev, q, ds, [w.prefix] * w.sequences, [w.chunk] * w.sequences, 0, w.heads,
                                   w.context, precision="f32").reshape(w.sequences, w.chunk, -1)
-    rows = list(range(0, w.chunk, 37)) + [w.chunk - 1]
+    # every 37th row and the last, 24 seeded random rows per sequence, and a
+    # seeded run of 256 consecutive rows (whole query tiles) in one sequence
+    rng = np.random.default_rng(4242)
+    run_seq, run_at = int(rng.integers(w.sequences)), int(rng.integers(w.chunk - 256 + 1))
     want, gsel, fsel = [], [], []
     for i in range(w.sequences):
+        rows = sorted(set(range(0, w.chunk, 37)) | {w.chunk - 1} |
+                      set(rng.choice(w.chunk, 24, replace=False).tolist()))
         s = ref.create_sequence()
         k, v = w.keys(i), w.values(i)
         if q8:  # the oracle holds the dequantised values the Q8_0 blocks store
@@ -117,6 +122,12 @@ def test_bf16_c4_shape(device, oracle, make, fmt):
             want.append(ref.fused_prompt_attention(qi[r], s, 0, w.prefix + r, 1, w.heads, w.context))
             gsel.append(got[i, r])
             fsel.append(f32[i, r])
+        if i == run_seq:
+            run = ref.fused_prompt_attention(qi[run_at:run_at + 256], s, 0, w.prefix + run_at, 256, w.heads,
+                                             w.context).reshape(256, -1)
+            want.extend(run)
+            gsel.extend(got[i, run_at:run_at + 256])
+            fsel.extend(f32[i, run_at:run_at + 256])
         ref.drop(s)
     want = np.stack(want)
     assert refmath.close(np.stack(fsel), want, TOL_F32), refmath.max_rel(np.stack(fsel), want)

@@ -293,12 +293,18 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
     if (__any(st.bad) && lane == 0) *a.err = 1;
     if (nsplit > 1 && a.row_done) {
         __shared__ int last;
-        // every wave's partial stores complete before the count moves
+        // every wave waits for its own partial stores (gfx9's vmcnt counts
+        // stores) before the barrier; the signal fences keep the compiler
+        // from moving a store past the wait
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __syncthreads();
         if (threadIdx.x == 0) {
             int* done = a.row_done + static_cast<size_t>(row) * (a.lay.kv_heads / nwaves) + kh / nwaves;
-            const int prev = __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // release publishes this workgroup's partials at device scope;
+            // acquire orders the last arriver's reads of the others'
+            const int prev = __hip_atomic_fetch_add(done, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             last = prev == nsplit - 1;
             if (last) __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

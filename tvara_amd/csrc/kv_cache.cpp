@@ -605,7 +605,8 @@ void PrefillPlan::build(DeviceCache* c, const uint64_t* sequences, size_t n, siz
         return;
     }
     if (!prefill_bf16_supported(c->layout(), group))
-        throw std::invalid_argument("bf16 prefill needs f32 blocks of 16 tokens, head_dim 64, GQA group 1/2/4/8");
+        throw std::invalid_argument(
+            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, GQA group 1-8");
     std::vector<int32_t> tab;
     std::vector<int4> sq(n);
     size_t row0 = 0;
