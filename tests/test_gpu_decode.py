@@ -497,3 +497,50 @@ def test_ragged_rows_with_tail_only_rows(device, oracle, scale):
     want = np.stack([ref.fused_paged_attention(q[i], s, 0, heads, 1 << 20, tail_key=tk[i], tail_value=tv[i])
                      for i, s in enumerate(seqs)])
     assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+@pytest.mark.parametrize("kv_heads,group", [(8, 4), (8, 1), (8, 2), (8, 3), (8, 8), (4, 4), (4, 8), (16, 2), (16, 4),
+                                            (16, 7)])
+def test_row_major_kernel(device, oracle, monkeypatch, kv_heads, group):
+    # The row-major f32 kernel (head_dim 64; 4, 8 or 16 KV heads) takes launches
+    # of more than 128 work items.  64-token splits over rows of every kind
+    # (no cached token, one token, block edges, partial last blocks, long
+    # rows) with each row's uncommitted token as its last position; three
+    # launches in a row agree byte for byte and match the oracle.
+    from tvara_amd import hip
+
+    monkeypatch.setenv("TVARA_SPLIT_TOKENS", "64")
+    dim, tpb = 64, 16
+    heads = kv_heads * group
+    rng = np.random.default_rng(61 + kv_heads * 10 + group)
+    lengths = [0, 1, 15, 16, 17, 2047, 63, 64, 65, 100] + [int(x) for x in rng.integers(1, 1500, 14)]
+    g = (2, kv_heads, dim, tpb, sum((n + tpb - 1) // tpb for n in lengths) + 4)
+    dev, ref = device.PagedCache(*g), oracle.Cache(*g)
+    w = 2 * kv_heads * dim
+    seqs = []
+    for i, n in enumerate(lengths):
+        s, r = dev.create_sequence(), ref.create_sequence()
+        if n:
+            k = synth.normal(63, f"k{i}", n * w).reshape(n, w)
+            v = synth.normal(63, f"v{i}", n * w).reshape(n, w)
+            dev.append_many(s, k, v)
+            ref.append_many(r, k, v)
+        seqs.append(s)
+    rows = len(lengths)
+    q = synth.normal(63, "q", rows * heads * dim).reshape(rows, heads * dim)
+    tk = synth.normal(63, "tk", rows * kv_heads * dim).reshape(rows, kv_heads * dim)
+    tv = synth.normal(63, "tv", rows * kv_heads * dim).reshape(rows, kv_heads * dim)
+    dq, dtk, dtv = (hip.DeviceArray.from_numpy(x) for x in (q, tk, tv))
+    plan = attention.DecodePlan(dev, seqs, heads, 1 << 20, with_tail=True)
+    assert plan.items > 128
+    say("row-major", kv_heads, group, "items", plan.items)
+    outs = [hip.DeviceArray(q.shape) for _ in range(3)]
+    for o in outs:
+        plan.launch(1, dq.ptr, o.ptr, dtk.ptr, dtv.ptr)
+    plan.check()
+    got = [o.numpy() for o in outs]
+    for o in got[1:]:
+        assert np.array_equal(o, got[0])
+    want = np.stack([ref.fused_paged_attention(q[i], s, 1, heads, 1 << 20, tail_key=tk[i], tail_value=tv[i])
+                     for i, s in enumerate(seqs)])
+    assert refmath.close(got[0], want, TOL), refmath.max_rel(got[0], want)

@@ -107,6 +107,7 @@ struct DecodeArgs {
     // launches; null: merge_kernel merges)
     int* row_done;
     int wave_splits;  // > 0: each row's splits are the waves of one workgroup per (row, KV head)
+    int row_major;    // 1: decode_rows_kernel (one eight-wave workgroup per work item)
     const float* q;
     const float* tail_k;  // [rows][kv_width] or null
     const float* tail_v;
@@ -152,6 +153,11 @@ int decode_waves(int kv_heads, int group, int format, int head_dim);
 int decode_slots(int kv_heads, int group, int format, int head_dim);  // waves' worth of work per work item
 int wave_split_waves(int rows, int kv_heads, int group, int format, int head_dim, int tpb, size_t max_tokens);
 int decode_budget_per_cu(int group, int format, int head_dim);
+// Shapes the row-major f32 kernel takes (head_dim 64, 16-token blocks, 4, 8
+// or 16 KV heads, up to eight query heads each); plans of such a shape whose
+// launch has more than kRowMajorMinWorkgroups workgroups use it.
+bool decode_rows_shape(int kv_heads, int group, int format, int head_dim, int tpb);
+constexpr size_t kRowMajorMinWorkgroups = 128;
 // prefill.hip
 bool prefill_bf16_supported(const BlockLayout& lay, int group);
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s);

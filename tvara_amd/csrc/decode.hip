@@ -465,6 +465,340 @@ __global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(c
                                     nsplit, [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
 }
 
+// ------------------------------------- f32 blocks, row-major waves (head_dim 64)
+//
+// A workgroup of eight waves takes one work item for all of its KV heads
+// (kv_heads = 4P, P = 1, 2 or 4) and reads each 16-token block in steps of
+// 8 KiB of consecutive slot rows: load m of wave w covers floats
+// [(8m + w) * 256, +256) of the block's K (and V) section, i.e. slot row
+// m*R + w/P (R = 8/P rows a step, M = 2P loads per block and section) and
+// the half-, quarter- or whole row of KV heads hb..hb+3, hb = 4 (w % P).
+// Every workgroup-wide load is then one contiguous 8 KiB run (a 64 KiB block
+// in eight K and eight V loads), which HBM serves at 6.3 TB/s where the
+// head-major layout of decode_f32_kernel (16 strided 64-byte pieces a load)
+// gets 5.9 TB/s (MI355X, the C2 block placement, loads without arithmetic).
+//
+// Lane l of a wave owns columns 4(l%16)..+3 of KV head hb + l/16 in every row
+// it reads, so a DPP row (16 lanes) is one KV head.  A wave's R-way token
+// phase w/P sees every R-th token of the item; the phases' softmax states
+// are merged in LDS at the end of the item (log-sum-exp), by the phase-0
+// waves, which write the output row or the split's partial.
+//
+// Scores: the lane's partial dots for (row, query head) pairs are
+// transpose-reduced over the 16 lanes of the DPP row (row_mirror,
+// row_half_mirror, quad permutes), so after four levels each lane holds the
+// full score of one pair (VP = 16 pairs at a time; fewer pairs leave copies on
+// neighbouring lanes).  Online softmax in log2 units with the lazy rescale of
+// decode_f32_kernel; probabilities go back to the row with row_newbcast.
+
+// DPP row_ror:d (0 < d < 16)
+template <int D_>
+__device__ __forceinline__ float row_ror(float v) {
+    return dpp<0x120 + D_>(v);
+}
+
+// lane L of each DPP row receives lane L0 of that row
+template <int L0>
+__device__ __forceinline__ float row_bcast(float v) {
+    return dpp<0x150 + L0>(v);
+}
+
+// lane L of each DPP row receives lane (j << SH) & 15 of that row (j folds to
+// a constant once the caller's loops are unrolled)
+template <int SH>
+__device__ __forceinline__ float row_bcast_dyn(float v, int j) {
+    switch ((j << SH) & 15) {
+        case 0: return row_bcast<0>(v);
+        case 1: return row_bcast<1>(v);
+        case 2: return row_bcast<2>(v);
+        case 3: return row_bcast<3>(v);
+        case 4: return row_bcast<4>(v);
+        case 5: return row_bcast<5>(v);
+        case 6: return row_bcast<6>(v);
+        case 7: return row_bcast<7>(v);
+        case 8: return row_bcast<8>(v);
+        case 9: return row_bcast<9>(v);
+        case 10: return row_bcast<10>(v);
+        case 11: return row_bcast<11>(v);
+        case 12: return row_bcast<12>(v);
+        case 13: return row_bcast<13>(v);
+        case 14: return row_bcast<14>(v);
+        default: return row_bcast<15>(v);
+    }
+}
+
+// Pairing of the lanes of a DPP row that differ in lane bit BIT: row_mirror
+// (bit 3), row_half_mirror (bit 2), quad permutes (bits 1 and 0).  Partners
+// agree on every higher bit, so they hold the same values at each level.
+template <int BIT>
+constexpr int row_pair_ctrl() {
+    return BIT == 8 ? 0x140 : BIT == 4 ? 0x141 : BIT == 2 ? 0x4E : 0xB1;
+}
+
+template <int N, int BIT>
+__device__ __forceinline__ void row_sum_level(float (&a)[16], int i) {
+    constexpr int C = row_pair_ctrl<BIT>();
+    if constexpr (N > 1) {
+        // keep this lane's half of the values, plus the partner's copy of it
+        const bool up = (i & BIT) != 0;
+#pragma unroll
+        for (int j = 0; j < N / 2; ++j) a[j] = (up ? a[j + N / 2] : a[j]) + dpp<C>(up ? a[j] : a[j + N / 2]);
+    } else {
+        a[0] += dpp<C>(a[0]);
+    }
+    if constexpr (BIT > 1) row_sum_level<(N > 1 ? N / 2 : 1), BIT / 2>(a, i);
+}
+
+// Sum over the 16 lanes of a DPP row of N = 2^k values per lane (N <= 16):
+// lane i of the row returns the sum of value i >> (4 - k).
+template <int N>
+__device__ __forceinline__ float row_transpose_sum(const float (&v)[N], int i) {
+    float a[16];
+#pragma unroll
+    for (int j = 0; j < N; ++j) a[j] = v[j];
+    row_sum_level<N, 8>(a, i);
+    return a[0];
+}
+
+constexpr int pad_heads(int g) { return g == 1 ? 1 : g == 2 ? 2 : g <= 4 ? 4 : 8; }
+constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
+
+// LDS floats of a row-major decode workgroup: the partial accumulators and
+// (max, normaliser) pairs of the token phases 1 .. R-1
+__host__ __device__ constexpr size_t rows_lds_floats(int G, int P) {
+    return static_cast<size_t>(8 / P - 1) * P * 4 * G * (64 + 2);
+}
+
+template <int G, int P, int NB>
+__global__ __launch_bounds__(512) void decode_rows_kernel(const DecodeArgs a, const WorkOrder order) {
+    constexpr int D = 64, R = 8 / P, M = 2 * P;
+    constexpr int GP = pad_heads(G), LGP = ilog2(GP);
+    constexpr int MC = M * GP <= 16 ? M : 16 / GP;  // block rows scored together
+    constexpr int VP = MC * GP, SH = 4 - ilog2(VP);
+    static_assert(M % MC == 0 && VP <= 16, "row-major decode: shape");
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = lane & 15, kvrow = lane >> 4, c0 = 4 * i;
+    const int ph = wave / P, wp = wave % P, hb = wp * 4, kh = hb + kvrow;
+    // the value this lane holds after a transpose-sum: (row mq of the chunk,
+    // query head gq); `prim` marks the first of its copies
+    const int jq = i >> SH, gq = jq % GP, mq = jq / GP;
+    const bool prim = (i & ((1 << SH) - 1)) == 0;
+
+    const int slot = static_cast<int>(blockIdx.x);
+    const int item = order.n ? static_cast<int>(order.item[slot]) : slot;
+    const int4 it = a.work[item];  // row, first token, end token, tail | splits << 1
+    const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
+    const int nsplit = it.w >> 1;
+    const bool tail = (it.w & 1) != 0;
+    const int n = max(it.z - it.y, 0), nfull = n / 16;
+    const int kvw = a.lay.kv_width;
+
+    float q[G][4];
+    {
+        const float* qr = a.q + (static_cast<size_t>(it.x) * a.heads + static_cast<size_t>(kh) * G) * D + c0;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            // scaled in the score, not here (see decode_f32_kernel)
+            const float4 x = *reinterpret_cast<const float4*>(qr + g * D);
+            q[g][0] = x.x;
+            q[g][1] = x.y;
+            q[g][2] = x.z;
+            q[g][3] = x.w;
+        }
+    }
+    float acc[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[g][c] = 0.f;
+    float ms = -INFINITY, ls = 0.f;  // this lane's query head gq (on prim lanes)
+    bool bad = false;
+
+    const float* pool = reinterpret_cast<const float*>(a.pool);
+    const size_t bstride = a.lay.stride / sizeof(float);
+    const size_t kbase = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(ph) * kvw + hb * D + 4 * lane;
+    const size_t vsec = 16 * static_cast<size_t>(kvw), rstep = static_cast<size_t>(R) * kvw;
+
+    // rows m*R + ph of a full block (unconditional loads: a select on a load
+    // makes the compiler wait for it where the loop carries the registers)
+    auto load = [&](const float* base, float4 (&kk)[M], float4 (&vv)[M]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            kk[m] = stream_load(base + m * rstep);
+            vv[m] = stream_load(base + vsec + m * rstep);
+        }
+    };
+    // the same rows of a partial block: rows at or past `valid` read as zero
+    auto load_part = [&](const float* base, float4 (&kk)[M], float4 (&vv)[M], int valid) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const bool ok = m * R + ph < valid;
+            kk[m] = ok ? stream_load(base + m * rstep) : make_float4(0.f, 0.f, 0.f, 0.f);
+            vv[m] = ok ? stream_load(base + vsec + m * rstep) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto block_base = [&](int b) __attribute__((always_inline)) {
+        return pool + static_cast<size_t>(__builtin_amdgcn_readlane(bids, b)) * bstride + kbase;
+    };
+    auto process = [&](const float4 (&kk)[M], const float4 (&vv)[M], int valid) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ch = 0; ch < M / MC; ++ch) {
+            float part[VP];
+#pragma unroll
+            for (int mm = 0; mm < MC; ++mm)
+#pragma unroll
+                for (int g = 0; g < GP; ++g) {
+                    float d = 0.f;
+                    if (g < G) {
+                        const float4 k = kk[ch * MC + mm];
+                        d = fmaf(q[g][0], k.x, d);
+                        d = fmaf(q[g][1], k.y, d);
+                        d = fmaf(q[g][2], k.z, d);
+                        d = fmaf(q[g][3], k.w, d);
+                    }
+                    part[mm * GP + g] = d;
+                }
+            float sc = row_transpose_sum<VP>(part, i) * a.qscale;
+            const bool own = prim && gq < G && (ch * MC + mq) * R + ph < valid;
+            sc = own ? sc : -INFINITY;
+            bad |= own && !__builtin_isfinite(sc);
+            if (__any(own && sc > ms + kThreshold)) {
+                float mx = sc;
+#pragma unroll
+                for (int d = 1 << (SH + LGP); d < 16; d <<= 1) {
+                    if (d == 1) mx = fmaxf(mx, row_ror<1>(mx));
+                    if (d == 2) mx = fmaxf(mx, row_ror<2>(mx));
+                    if (d == 4) mx = fmaxf(mx, row_ror<4>(mx));
+                    if (d == 8) mx = fmaxf(mx, row_ror<8>(mx));
+                }
+                const float mnew = fmaxf(ms, mx);
+                const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(ms - mnew);
+                ms = mnew;
+                ls *= alpha;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float ag = row_bcast_dyn<SH>(alpha, g);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[g][c] *= ag;
+                }
+            }
+            const float p = own ? fast_exp2(sc - ms) : 0.f;
+            ls += p;
+#pragma unroll
+            for (int mm = 0; mm < MC; ++mm) {
+                const float4 v = vv[ch * MC + mm];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float pg = row_bcast_dyn<SH>(p, mm * GP + g);
+                    acc[g][0] = fmaf(pg, v.x, acc[g][0]);
+                    acc[g][1] = fmaf(pg, v.y, acc[g][1]);
+                    acc[g][2] = fmaf(pg, v.z, acc[g][2]);
+                    acc[g][3] = fmaf(pg, v.w, acc[g][3]);
+                }
+            }
+        }
+    };
+
+    // full blocks, NB in flight; unconditional prefetches (past the last
+    // full block they re-read it and the result is masked out), as in
+    // decode_f32_kernel
+    if (nfull > 0) {
+        const int last = nfull - 1;
+        float4 kb[NB][M], vb[NB][M];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            load(block_base(min(j, last)), kb[j], vb[j]);
+            asm volatile("" ::: "memory");  // issue order = use order
+        }
+        for (int b = 0; b < nfull; b += NB) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                process(kb[j], vb[j], b + j < nfull ? 16 : 0);
+                load(block_base(min(b + j + NB, last)), kb[j], vb[j]);
+                asm volatile("" ::: "memory");  // keep the prefetch here
+            }
+        }
+    }
+    float4 ka[M], va[M];
+    if (n > nfull * 16) {  // the partial last block: unused slots are never read
+        load_part(block_base(nfull), ka, va, n - nfull * 16);
+        process(ka, va, n - nfull * 16);
+    }
+    if (tail) {  // the row's uncommitted K/V is its last position (attention.hpp:80), row 0 of phase 0
+        const size_t toff = static_cast<size_t>(it.x) * kvw + hb * D + 4 * lane;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const bool ok = m == 0 && ph == 0;
+            ka[m] = ok ? *reinterpret_cast<const float4*>(a.tail_k + toff) : make_float4(0.f, 0.f, 0.f, 0.f);
+            va[m] = ok ? *reinterpret_cast<const float4*>(a.tail_v + toff) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        process(ka, va, 1);
+    }
+
+    // the phases' states: normalisers summed over this row's token lanes,
+    // phases 1 .. R-1 into LDS, combined by phase 0
+    float lt = ls;
+#pragma unroll
+    for (int d = 1 << (SH + LGP); d < 16; d <<= 1) {
+        if (d == 1) lt += row_ror<1>(lt);
+        if (d == 2) lt += row_ror<2>(lt);
+        if (d == 4) lt += row_ror<4>(lt);
+        if (d == 8) lt += row_ror<8>(lt);
+    }
+    float* accs = lds;
+    float* mls = lds + static_cast<size_t>(R - 1) * P * 4 * G * 64;
+    if (ph > 0) {
+        const int pw = ((ph - 1) * P + wp) * 4 + kvrow;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            *reinterpret_cast<float4*>(accs + (static_cast<size_t>(pw) * G + g) * 64 + c0) =
+                make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+        if (prim && mq == 0 && gq < G) {
+            mls[(pw * G + gq) * 2] = ms;
+            mls[(pw * G + gq) * 2 + 1] = lt;
+        }
+    }
+    __syncthreads();
+    if (ph == 0) {
+        const size_t head0 = static_cast<size_t>(kh) * G;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float m0 = row_bcast_dyn<SH>(ms, g), l0 = row_bcast_dyn<SH>(lt, g);
+            float mx = m0;
+#pragma unroll
+            for (int r = 1; r < R; ++r) mx = fmaxf(mx, mls[((((r - 1) * P + wp) * 4 + kvrow) * G + g) * 2]);
+            const float w0 = m0 == -INFINITY ? 0.f : fast_exp2(m0 - mx);
+            float l = w0 * l0;
+            float4 o = make_float4(w0 * acc[g][0], w0 * acc[g][1], w0 * acc[g][2], w0 * acc[g][3]);
+#pragma unroll
+            for (int r = 1; r < R; ++r) {
+                const int pw = ((r - 1) * P + wp) * 4 + kvrow;
+                const float mr = mls[(pw * G + g) * 2];
+                const float wr = mr == -INFINITY ? 0.f : fast_exp2(mr - mx);
+                l = fmaf(wr, mls[(pw * G + g) * 2 + 1], l);
+                const float4 x = *reinterpret_cast<const float4*>(accs + (static_cast<size_t>(pw) * G + g) * 64 + c0);
+                o.x = fmaf(wr, x.x, o.x);
+                o.y = fmaf(wr, x.y, o.y);
+                o.z = fmaf(wr, x.z, o.z);
+                o.w = fmaf(wr, x.w, o.w);
+            }
+            if (nsplit == 1) {
+                float* out = a.out + (static_cast<size_t>(it.x) * a.heads + head0 + g) * D + c0;
+                *reinterpret_cast<float4*>(out) = make_float4(o.x / l, o.y / l, o.z / l, o.w / l);
+            } else {
+                *reinterpret_cast<float4*>(a.part_acc + (static_cast<size_t>(item) * a.heads + head0 + g) * D + c0) = o;
+                if (i == 0) {
+                    float* pm = a.part_ml + (static_cast<size_t>(item) * a.heads + head0 + g) * 2;
+                    pm[0] = mx;
+                    pm[1] = l;
+                }
+            }
+        }
+    }
+    if (__any(bad) && lane == 0) *a.err = 1;
+}
+
 // ------------------------------------------------------------- Q8_0 blocks
 
 __device__ __forceinline__ void unpack_i8(uint4 w, float (&f)[16]) {
@@ -1279,6 +1613,39 @@ void launch_f32(const DecodeArgs& a, int nitems, int waves, const WorkOrder& ord
     launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, false>, grid, block, lds, s, a, o);
 }
 
+template <int G, int P>
+void launch_rows(const DecodeArgs& a, int nitems, const WorkOrder& order, hipStream_t s) {
+    WorkOrder o;
+    o.n = order.n == nitems ? order.n : 0;
+    if (o.n) std::copy(order.item, order.item + o.n, o.item);
+    launch("paged_decode", decode_rows_kernel<G, P, 2>, dim3(nitems), dim3(512), rows_lds_floats(G, P) * sizeof(float),
+           s, a, o);
+}
+
+template <int P>
+bool dispatch_rows_p(const DecodeArgs& a, int nitems, const WorkOrder& order, hipStream_t s) {
+    switch (a.group) {
+        case 1: launch_rows<1, P>(a, nitems, order, s); return true;
+        case 2: launch_rows<2, P>(a, nitems, order, s); return true;
+        case 3: launch_rows<3, P>(a, nitems, order, s); return true;
+        case 4: launch_rows<4, P>(a, nitems, order, s); return true;
+        case 5: launch_rows<5, P>(a, nitems, order, s); return true;
+        case 6: launch_rows<6, P>(a, nitems, order, s); return true;
+        case 7: launch_rows<7, P>(a, nitems, order, s); return true;
+        case 8: launch_rows<8, P>(a, nitems, order, s); return true;
+        default: return false;
+    }
+}
+
+bool dispatch_rows(const DecodeArgs& a, int nitems, const WorkOrder& order, hipStream_t s) {
+    switch (a.lay.kv_heads) {
+        case 4: return dispatch_rows_p<1>(a, nitems, order, s);
+        case 8: return dispatch_rows_p<2>(a, nitems, order, s);
+        case 16: return dispatch_rows_p<4>(a, nitems, order, s);
+        default: return false;
+    }
+}
+
 template <int D, int G, int LPT>
 void launch_f32_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
     const int waves = a.wave_splits;
@@ -1470,6 +1837,12 @@ int wave_split_waves(int rows, int kv_heads, int group, int format, int head_dim
 // (TVARA_INKERNEL_MERGE_MAX overrides it for tuning)
 constexpr int kInKernelMergeMaxWorkgroups = 128;
 
+bool decode_rows_shape(int kv_heads, int group, int format, int head_dim, int tpb) {
+    if (const char* env = std::getenv("TVARA_ROW_MAJOR"); env && std::atoi(env) == 0) return false;
+    return format == kF32 && head_dim == 64 && tpb == 16 && (kv_heads == 4 || kv_heads == 8 || kv_heads == 16) &&
+           group >= 1 && group <= 8;
+}
+
 bool decode_fast_path(const DecodeArgs& a) {
     return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128) && a.group <= 8;
 }
@@ -1486,6 +1859,17 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
     if (a.wave_splits) {  // the plan chose wave splits (wave_split_shape): merged in LDS
         a.lay.head_dim == 64 ? dispatch_ws<64>(a, nrows, s) : dispatch_ws<128>(a, nrows, s);
         TVARA_HIP(hipGetLastError());
+        return;
+    }
+    if (a.row_major) {  // the plan chose the row-major kernel: merge_kernel merges
+        DecodeArgs b = a;
+        b.row_done = nullptr;
+        if (!dispatch_rows(b, nitems, ord, s)) throw std::logic_error("row-major decode: unsupported shape");
+        TVARA_HIP(hipGetLastError());
+        if (need_merge) {
+            launch_merge(b, inline_rows, nrows, s);
+            TVARA_HIP(hipGetLastError());
+        }
         return;
     }
     // Small launches of the f32 and vector Q8_0 kernels merge a row's splits

@@ -355,6 +355,35 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
                         : wave_split_waves(rows, static_cast<int>(g.kv_heads), group, c->format(),
                                            static_cast<int>(g.head_dim), static_cast<int>(g.tokens_per_block), max_n);
     if (wave_splits) split = round_up((max_n + wave_splits - 1) / wave_splits, 16);
+    // The row-major f32 kernel (decode_rows_shape) runs one workgroup per
+    // item: its split is the shortest whose items fit one workgroup per CU,
+    // and it takes the launch when that is more than kRowMajorMinWorkgroups
+    // workgroups (smaller launches merge their splits in the kernel).
+    row_major = false;
+    auto items_at = [&](size_t sp) {
+        size_t n = 0;
+        for (size_t len : cached) n += std::max<size_t>(1, (len + sp - 1) / sp);
+        return n;
+    };
+    if (!wave_splits && decode_rows_shape(static_cast<int>(g.kv_heads), group, c->format(),
+                                          static_cast<int>(g.head_dim), static_cast<int>(g.tokens_per_block))) {
+        size_t sp = split;
+        if (!sp) {
+            const size_t budget = static_cast<size_t>(c->compute_units());
+            size_t lo = 4, hi = kMaxSplitTokens / 16;
+            while (lo < hi) {
+                const size_t mid = (lo + hi) / 2;
+                if (items_at(mid * 16) <= budget) hi = mid;
+                else lo = mid + 1;
+            }
+            sp = lo * 16;
+        }
+        sp = std::min(round_up(std::max<size_t>(sp, 16), 16), kMaxSplitTokens);
+        if (items_at(sp) > kRowMajorMinWorkgroups) {
+            row_major = true;
+            split = sp;
+        }
+    }
     if (!split) {
         const int gw = static_cast<int>(g.kv_heads), gd = static_cast<int>(g.head_dim);
         const size_t groups = static_cast<size_t>(decode_slots(gw, group, c->format(), gd)) /
@@ -410,7 +439,7 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     }
     items = static_cast<int>(its.size());
     order.n = 0;
-    const bool one_group = decode_waves(static_cast<int>(g.kv_heads), group, c->format(),
+    const bool one_group = row_major || decode_waves(static_cast<int>(g.kv_heads), group, c->format(),
                                         static_cast<int>(g.head_dim)) == static_cast<int>(g.kv_heads);
     if (!wave_splits && one_group && c->format() == kF32 && items <= kOrderedItems && c->xcds() > 1 &&
         items >= c->xcds())
@@ -549,6 +578,7 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.part_ml = dev.part_ml;
     a.row_done = need_merge ? dev.row_done : nullptr;
     a.wave_splits = wave_splits;
+    a.row_major = row_major ? 1 : 0;
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
     a.err = dev.err;
     launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, order.n ? &order : nullptr, s);

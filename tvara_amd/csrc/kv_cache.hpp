@@ -126,6 +126,7 @@ struct AttnPlan {
     uint64_t epoch = 0;
     int rows = 0, heads = 0, group = 0, items = 0, split_tokens = 0;
     int wave_splits = 0;  // > 0: splits per row = waves of one workgroup per (row, KV head)
+    bool row_major = false;  // the launch runs decode_rows_kernel (one workgroup per item)
     bool need_merge = false, with_tail = false, inline_ok = false;
     size_t kv_bytes = 0;  // algorithmic K/V bytes one launch reads
     RowSplits inline_rows{};  // (first item, splits) per row when rows <= kInlineRows
