@@ -4,6 +4,8 @@ With no --workload the run covers every configuration of the path, one JSON
 line each, the headline last:
 
   c1     SmolLM2-135M decode: 1 sequence x 512 tokens, 9/3 heads, d=64, f32;
+  t176   the reference's T176 cache case: 1 sequence x 1,025 tokens, 4/2
+         heads, d=32, f32 (latency beside the reference's published figure);
   c3     KV-management stress: 256 sequences forked from a 1,024-token
          prefix, 22 layers x 8 x 64 f32, one appended token per sequence a
          step (c3cow: a 1,025-token prefix, so the first step copies 256
@@ -47,7 +49,7 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16
 METRIC = "paged decode attn: achieved HBM GB/s (% of peak) + decode tokens/s, 1 MI355X"
 MODEL_LAYERS = {"llama-3.2-1b-decode-64x[128,4096]": 16, "smollm2-135m-decode-1x512": 30,
                 "llama-3-8b-q8_0-decode-16x32768": 32}
-DEFAULT_RUN = ["c1", "c3", "c3cow", "c4", "c5", "c2"]
+DEFAULT_RUN = ["c1", "t176", "c3", "c3cow", "c4", "c5", "c2"]
 REF_FLAGS = "g++ -O2 -std=c++20 -fPIC (oracle/Makefile, target ref; the reference's recorded flags)"
 
 
@@ -125,6 +127,20 @@ def cpu_result(unit, one, alln, threads, sample, work_per_run_one, work_per_run_
     return out
 
 
+# Where the default run parks the host baselines: every GPU measurement runs
+# first, back to back, so no configuration's timed steps follow seconds of an
+# idle GPU; the baselines then run and fill in their lines.
+DEFERRED = None
+
+
+def baseline(result, job):
+    """Fill result["cpu_baseline"] with job(), now or after the GPU runs."""
+    if DEFERRED is not None:
+        DEFERRED.append((result, job))
+    else:
+        result["cpu_baseline"] = job()
+
+
 def ref_ready(args):
     if args.no_cpu_baseline:
         return False
@@ -187,7 +203,10 @@ def hbm_traffic(workload, kernel):
 
 # CPU samples per decode workload: sequences for the one-thread run, for the
 # all-thread run, and reference calls per run (a single short row repeats)
-CPU_DECODE_SAMPLE = {"c1": (1, 1, 50), "c2": (64, 64, 1), "c5": (1, 16, 1)}
+CPU_DECODE_SAMPLE = {"c1": (1, 1, 50), "c2": (64, 64, 1), "c5": (1, 16, 1), "t176": (1, 1, 50)}
+# the reference's own published figure for the T176 cache case: one
+# fused_paged_attention call, median of 9 (bench/results/prefill/T176.json)
+T176_PUBLISHED_US = 523.7
 
 
 def cpu_rows(w, k, v):
@@ -312,6 +331,7 @@ def bench_decode(args, key, w):
                    "head_dim": w.head_dim, "tokens_per_block": w.tokens_per_block, "total_tokens": w.total_tokens,
                    "pool_blocks": w.pool_blocks, "split_tokens": plan.split_tokens, "work_items": plan.items},
         "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "latency_us": round(ms_per_step * 1e3, 2),
         "decode_tokens_per_s": round(tokens_per_s, 1),
         "model_decode_tokens_per_s": round(tokens_per_s / layers, 1),
         "model_layers": layers,
@@ -323,12 +343,20 @@ def bench_decode(args, key, w):
                      "algorithmic_bytes": kernel_bytes},
         "cpu_baseline": None,
     }
+    if key == "t176":
+        result["reference_published"] = {
+            "us_per_call": T176_PUBLISHED_US,
+            "source": "bench/results/prefill/T176.json cache_plain_us (the reference's own run: g++ 15.2 -O2, "
+                      "Windows, median of 9)"}
     del plan, cache, q, out
     if ref is not None:
-        t0 = time.perf_counter()
-        result["cpu_baseline"] = cpu_decode(key, w, ref, rseqs, qh)
-        log(f"cpu baseline in {time.perf_counter() - t0:.1f}s")
-    del ref
+        def job():
+            t0 = time.perf_counter()
+            c = cpu_decode(key, w, ref, rseqs, qh)
+            log(f"{w.name}: cpu baseline in {time.perf_counter() - t0:.1f}s")
+            return c
+
+        baseline(result, job)
     return result
 
 
@@ -388,8 +416,7 @@ def bench_prefill(args, w):
     tfs = w.flops() / (kernel_ms * 1e-3) / 1e12
     log(f"prefill kernel {kernel_ms * 1e3:.1f} us, call {ms_per_step * 1e3:.1f} us, {tfs:.1f} TFLOP/s")
     del plan, cache, q, out
-    cpu = cpu_prefill(w) if ref_ready(args) and not w.q8 else None
-    return {
+    result = {
         "metric": "paged chunked prefill attn: achieved TFLOP/s (MFMA utilisation), 1 MI355X",
         "value": round(w.flops() / (ms_per_step * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
@@ -401,8 +428,11 @@ def bench_prefill(args, w):
                      "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
                      "traffic": hbm_traffic(w.name, "paged_prefill_bf16"), "kernel": "paged_prefill_bf16",
                      "kernel_avg_us": round(kernel_ms * 1e3, 3), "algorithmic_flops": w.flops()},
-        "cpu_baseline": cpu,
+        "cpu_baseline": None,
     }
+    if ref_ready(args) and not w.q8:
+        baseline(result, lambda: cpu_prefill(w))
+    return result
 
 
 # -------------------------------------------------------------- KV stress
@@ -517,8 +547,7 @@ def bench_kv(args, cow):
     gbs = nbytes / (total_ms * 1e-3) / 1e9
     log(f"{w.name}: {ms_per_step * 1e3:.1f} us per step, {gbs:.1f} GB/s")
     del cache, batches, steps_k, steps_v
-    cpu = cpu_kv(w, step_bytes) if ref_ready(args) else None
-    return {
+    result = {
         "metric": "paged KV management stress: us per append step + GB/s, 1 MI355X", "value": round(gbs, 2),
         "unit": "GB/s", "n_gpus": 1, "steps": done, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
@@ -529,8 +558,11 @@ def bench_kv(args, cow):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "kv_append (step)",
                      "algorithmic_bytes_per_step": round(nbytes / done)},
-        "cpu_baseline": cpu,
+        "cpu_baseline": None,
     }
+    if ref_ready(args):
+        baseline(result, lambda: cpu_kv(w, step_bytes))
+    return result
 
 
 # ------------------------------------------------------------------ model
@@ -649,6 +681,9 @@ def compact(r):
     for k in ("kernel_avg_us", "merge_avg_us"):
         if k in r["roofline"]:
             out["roofline"][k] = r["roofline"][k]
+    for k in ("latency_us", "reference_published"):
+        if k in r:
+            out[k] = r[k]
     if cpu:
         out["cpu_baseline"] = {"value": cpu["value"], "unit": cpu["unit"], "cores": cpu["cores"], "kind": cpu["kind"]}
         if "one_thread" in cpu:
@@ -668,7 +703,8 @@ def run_one(args, key):
         return bench_model(args)
     w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5,
          "gqa8": workloads.decode_gqa8, "gqa8q8": lambda: workloads.decode_gqa8(q8=True),
-         "tiny": workloads.decode_tinyllama, "tinyq8": lambda: workloads.decode_tinyllama(q8=True)}[key]()
+         "tiny": workloads.decode_tinyllama, "tinyq8": lambda: workloads.decode_tinyllama(q8=True),
+         "t176": workloads.decode_t176}[key]()
     return bench_decode(args, key, w)
 
 
@@ -679,7 +715,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="all",
                     choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c5", "gqa8", "gqa8q8",
-                             "tiny", "tinyq8", "llama1b"],
+                             "tiny", "tinyq8", "t176", "llama1b"],
                     help="one configuration; `all` (the default) runs c1, c3, c3cow, c4 and c5, one JSON line "
                          "each, then the c2 headline line last")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -707,10 +743,21 @@ def main():
     if args.workload != "all":
         print(json.dumps(run_one(args, args.workload)), flush=True)
         return
+    global DEFERRED
+    DEFERRED = []
+    results = []
     for key in DEFAULT_RUN:
         t0 = time.perf_counter()
-        r = run_one(args, key)
+        # the lines before the headline warm up for at least 100 steps: the
+        # GPU clock ramps over the first few dozen launches after a fill (the
+        # headline keeps exactly --warmup, right after the others' GPU runs)
+        run_args = args if key == "c2" else argparse.Namespace(**{**vars(args), "warmup": max(args.warmup, 100)})
+        results.append((key, run_one(run_args, key)))
         log(f"{key} done in {time.perf_counter() - t0:.1f}s")
+    jobs, DEFERRED = DEFERRED, None
+    for r, job in jobs:
+        r["cpu_baseline"] = job()
+    for key, r in results:
         print(json.dumps(r if key == "c2" else compact(r)), flush=True)
 
 

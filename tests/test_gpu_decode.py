@@ -544,3 +544,65 @@ def test_row_major_kernel(device, oracle, monkeypatch, kv_heads, group):
     want = np.stack([ref.fused_paged_attention(q[i], s, 1, heads, 1 << 20, tail_key=tk[i], tail_value=tv[i])
                      for i, s in enumerate(seqs)])
     assert refmath.close(got[0], want, TOL), refmath.max_rel(got[0], want)
+
+
+@pytest.mark.parametrize("tpb", [32, 64, 256])
+@pytest.mark.parametrize("dim,kv_heads,group", [(32, 2, 2), (32, 4, 8), (64, 8, 4), (64, 2, 7), (128, 4, 4),
+                                                (128, 2, 8)])
+def test_large_blocks_fast_kernels(device, oracle, tpb, dim, kv_heads, group):
+    # f32 blocks of 32 to 256 tokens and head_dim 32 stream through the fast
+    # kernels (splits start on a block); lengths ending inside and on a block,
+    # with and without the uncommitted token, and a visible cap
+    for length, kw in [(1, {}), (tpb - 1, {}), (tpb, {"tail": True}), (3 * tpb + 5, {}),
+                       (2500, {"tail": True}), (2500, {"visible": 1300})]:
+        got, want = _single(device, oracle, kv_heads * group, kv_heads, dim, tpb, length, seed=tpb + length, **kw)
+        assert refmath.close(got, want, TOL), (length, kw, refmath.max_rel(got, want))
+
+
+@pytest.mark.parametrize("tpb", [32, 64])
+def test_row_major_large_blocks(device, oracle, monkeypatch, tpb):
+    # the row-major kernel over 32- and 64-token blocks: a 16-row tile is a
+    # quarter or half of a block
+    from tvara_amd import hip
+
+    monkeypatch.setenv("TVARA_SPLIT_TOKENS", "64")
+    kv_heads, dim, group = 8, 64, 4
+    heads = kv_heads * group
+    lengths = [1, 31, 32, 33, 63, 64, 65, 200, 1000, 3000] * 3
+    g = (1, kv_heads, dim, tpb, sum((n + tpb - 1) // tpb for n in lengths) + 4)
+    dev, ref = device.PagedCache(*g), oracle.Cache(*g)
+    w = kv_heads * dim
+    seqs = []
+    for i, n in enumerate(lengths):
+        s, r = dev.create_sequence(), ref.create_sequence()
+        k = synth.normal(71, f"k{i}", n * w).reshape(n, w)
+        v = synth.normal(71, f"v{i}", n * w).reshape(n, w)
+        dev.append_many(s, k, v)
+        ref.append_many(r, k, v)
+        seqs.append(s)
+    q = synth.normal(71, "q", len(lengths) * heads * dim).reshape(len(lengths), heads * dim)
+    plan = attention.DecodePlan(dev, seqs, heads, 1 << 20)
+    assert plan.items > 128
+    dq, out = hip.DeviceArray.from_numpy(q), hip.DeviceArray(q.shape)
+    plan.launch(0, dq.ptr, out.ptr)
+    plan.check()
+    want = np.stack([ref.fused_paged_attention(q[i], s, 0, heads, 1 << 20) for i, s in enumerate(seqs)])
+    got = out.numpy()
+    assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+def test_t176_shape(device, oracle):
+    # tests/core/prefill_t176.cpp: 1,025 appends of one K/V row to a 2-KV-head,
+    # head_dim 32 cache of 16-token blocks, one 4-head query (synth.signal is
+    # the reference's signal(), tests/core/prefill_support.hpp:11-13)
+    g = (1, 2, 32, 16, 128)
+    dev, ref = device.PagedCache(*g), oracle.Cache(*g)
+    k, v, q = synth.signal(64), synth.signal(64, 2), synth.signal(128, 3)
+    sd, sr = dev.create_sequence(), ref.create_sequence()
+    dev.append_many(sd, np.tile(k, (1025, 1)), np.tile(v, (1025, 1)))
+    ref.append_many(sr, np.tile(k, (1025, 1)), np.tile(v, (1025, 1)))
+    got = attention.fused_paged_attention(q, dev, sd, 0, 4, 2048)
+    want = ref.fused_paged_attention(q, sr, 0, 4, 2048)
+    # every key is the same row, so each head's output is that head's V row
+    assert np.allclose(want.reshape(4, 32), np.repeat(v.reshape(2, 32), 2, axis=0), rtol=1e-6, atol=1e-6)
+    assert refmath.close(got, want, TOL), refmath.max_rel(got, want)

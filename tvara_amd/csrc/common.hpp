@@ -157,6 +157,9 @@ int decode_budget_per_cu(int group, int format, int head_dim);
 // or 16 KV heads, up to eight query heads each); plans of such a shape whose
 // launch has more than kRowMajorMinWorkgroups workgroups use it.
 bool decode_rows_shape(int kv_heads, int group, int format, int head_dim, int tpb);
+// block sizes the f32 decode kernels stream directly (powers of two from 16
+// to 1,024 tokens); their splits start on a block
+bool decode_f32_blocks(int tpb);
 constexpr size_t kRowMajorMinWorkgroups = 128;
 // prefill.hip
 bool prefill_bf16_supported(const BlockLayout& lay, int group);

@@ -376,12 +376,15 @@ __global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(c
     // blocks); a tile's id is read from the owning lane, so the loop issues no
     // table loads
 
-    const size_t koff = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D + 4 * c;
-    const size_t voff = koff + 16 * static_cast<size_t>(kvw);
+    // blocks of tpb = 2^tsh tokens (16 to 1,024); a split starts on a block
+    const int tpb = a.lay.tpb, tsh = __builtin_ctz(static_cast<unsigned>(tpb));
+    const size_t koff = static_cast<size_t>(a.layer) * 2 * tpb * kvw + static_cast<size_t>(kh) * D + 4 * c;
+    const size_t voff = koff + static_cast<size_t>(tpb) * kvw;
 
     auto load = [&](int tb, float4 (&kk)[NV], float4 (&vv)[NV], bool ok) {
-        const int bid = __builtin_amdgcn_readlane(bids, (tb - t0) >> 4);
-        const float* base = pool + static_cast<size_t>(bid) * bstride + static_cast<size_t>((tb & 15) + tg) * kvw;
+        const int bid = __builtin_amdgcn_readlane(bids, (tb - t0) >> tsh);
+        const float* base =
+            pool + static_cast<size_t>(bid) * bstride + static_cast<size_t>((tb & (tpb - 1)) + tg) * kvw;
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
             kk[m] = ok ? stream_load(base + koff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -617,8 +620,10 @@ __global__ __launch_bounds__(512) void decode_rows_kernel(const DecodeArgs a, co
 
     const float* pool = reinterpret_cast<const float*>(a.pool);
     const size_t bstride = a.lay.stride / sizeof(float);
-    const size_t kbase = static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(ph) * kvw + hb * D + 4 * lane;
-    const size_t vsec = 16 * static_cast<size_t>(kvw), rstep = static_cast<size_t>(R) * kvw;
+    // blocks of tpb = 16 * 2^bsh tokens; the kernel's tiles are 16 rows
+    const int tpb = a.lay.tpb, bsh = __builtin_ctz(static_cast<unsigned>(tpb)) - 4;
+    const size_t kbase = static_cast<size_t>(a.layer) * 2 * tpb * kvw + static_cast<size_t>(ph) * kvw + hb * D + 4 * lane;
+    const size_t vsec = static_cast<size_t>(tpb) * kvw, rstep = static_cast<size_t>(R) * kvw;
 
     // rows m*R + ph of a full block (unconditional loads: a select on a load
     // makes the compiler wait for it where the loop carries the registers)
@@ -638,8 +643,10 @@ __global__ __launch_bounds__(512) void decode_rows_kernel(const DecodeArgs a, co
             vv[m] = ok ? stream_load(base + vsec + m * rstep) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
+    // tile b: rows 16 (b mod 2^bsh) .. of the split's block b >> bsh
     auto block_base = [&](int b) __attribute__((always_inline)) {
-        return pool + static_cast<size_t>(__builtin_amdgcn_readlane(bids, b)) * bstride + kbase;
+        return pool + static_cast<size_t>(__builtin_amdgcn_readlane(bids, b >> bsh)) * bstride +
+               static_cast<size_t>((b & ((1 << bsh) - 1)) * 16) * kvw + kbase;
     };
     auto process = [&](const float4 (&kk)[M], const float4 (&vv)[M], int valid) __attribute__((always_inline)) {
 #pragma unroll
@@ -1658,7 +1665,7 @@ void launch_f32_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
 
 template <int D>
 void dispatch_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
-    constexpr int LPT = D == 64 ? 4 : 8;
+    constexpr int LPT = D == 128 ? 8 : 4;
     switch (a.group) {
         case 1: launch_f32_ws<D, 1, LPT>(a, nrows, s); return;
         case 2: launch_f32_ws<D, 2, LPT>(a, nrows, s); return;
@@ -1666,7 +1673,7 @@ void dispatch_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
         case 4: launch_f32_ws<D, 4, LPT>(a, nrows, s); return;
         default: break;
     }
-    if constexpr (D == 64) {
+    if constexpr (D != 128) {
         switch (a.group) {
             case 5: launch_f32_ws<D, 5, 8>(a, nrows, s); return;
             case 6: launch_f32_ws<D, 6, 8>(a, nrows, s); return;
@@ -1719,16 +1726,18 @@ bool q8_mma_shape(int group, int format, int head_dim) {
 // head_dim, so the queries and accumulators of a lane stay at 2 * G * D / 8.
 template <int D>
 bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, const WorkOrder& order, hipStream_t s) {
-    constexpr int LPT = D == 64 ? 4 : 8;
+    constexpr int LPT = D == 128 ? 8 : 4;
     const int G = a.group;
     if (G > 8) return false;
-    if (a.lay.format != kF32) {
-        switch (q8_mma_heads(G, D)) {
+    if constexpr (D != 32) {
+        if (a.lay.format != kF32) {
+            switch (q8_mma_heads(G, D)) {
             case 1: launch_q8_mma<D, 1>(a, nitems, waves, s); return true;
             case 2: launch_q8_mma<D, 2>(a, nitems, waves, s); return true;
             case 3: launch_q8_mma<D, 3>(a, nitems, waves, s); return true;
             case 4: launch_q8_mma<D, 4>(a, nitems, waves, s); return true;
             default: break;
+            }
         }
     }
     if (a.lay.format == kF32) {
@@ -1748,12 +1757,14 @@ bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, const WorkOrder& 
         }
         return false;
     }
-    switch (G) {
-        case 1: launch_q8<D, 1>(a, nitems, waves, s); return true;
-        case 2: launch_q8<D, 2>(a, nitems, waves, s); return true;
-        case 3: launch_q8<D, 3>(a, nitems, waves, s); return true;
-        case 4: launch_q8<D, 4>(a, nitems, waves, s); return true;
-        default: break;
+    if constexpr (D != 32) {
+        switch (G) {
+            case 1: launch_q8<D, 1>(a, nitems, waves, s); return true;
+            case 2: launch_q8<D, 2>(a, nitems, waves, s); return true;
+            case 3: launch_q8<D, 3>(a, nitems, waves, s); return true;
+            case 4: launch_q8<D, 4>(a, nitems, waves, s); return true;
+            default: break;
+        }
     }
     if constexpr (LPT == 8) {  // the vector kernel's head slots: D/16 lanes a token
         switch (G) {
@@ -1823,7 +1834,7 @@ static int waves_for(const DecodeArgs& a) {
 // the usual decomposition.
 int wave_split_waves(int rows, int kv_heads, int group, int format, int head_dim, int tpb, size_t max_tokens) {
     if (const char* env = std::getenv("TVARA_WAVE_SPLITS"); env && std::atoi(env) == 0) return 0;
-    if (format != kF32 || tpb != 16 || (head_dim != 64 && head_dim != 128)) return 0;
+    if (format != kF32 || !decode_f32_blocks(tpb) || (head_dim != 32 && head_dim != 64 && head_dim != 128)) return 0;
     if (group > 8 || (head_dim == 128 && group > 4)) return 0;
     if (static_cast<size_t>(rows) * kv_heads > 32 || max_tokens > 1024) return 0;
     // one split of at least 64 tokens a wave, at most eight waves, the
@@ -1837,14 +1848,21 @@ int wave_split_waves(int rows, int kv_heads, int group, int format, int head_dim
 // (TVARA_INKERNEL_MERGE_MAX overrides it for tuning)
 constexpr int kInKernelMergeMaxWorkgroups = 128;
 
+bool decode_f32_blocks(int tpb) { return tpb >= 16 && tpb <= 1024 && (tpb & (tpb - 1)) == 0; }
+
 bool decode_rows_shape(int kv_heads, int group, int format, int head_dim, int tpb) {
     if (const char* env = std::getenv("TVARA_ROW_MAJOR"); env && std::atoi(env) == 0) return false;
-    return format == kF32 && head_dim == 64 && tpb == 16 && (kv_heads == 4 || kv_heads == 8 || kv_heads == 16) &&
+    return format == kF32 && head_dim == 64 && decode_f32_blocks(tpb) && (kv_heads == 4 || kv_heads == 8 || kv_heads == 16) &&
            group >= 1 && group <= 8;
 }
 
+// f32 blocks: head_dim 32, 64 or 128, any power-of-two block of 16 to 1,024
+// tokens; Q8_0 blocks: head_dim 64 or 128, 16-token blocks
 bool decode_fast_path(const DecodeArgs& a) {
-    return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128) && a.group <= 8;
+    if (a.group > 8) return false;
+    if (a.lay.format == kF32)
+        return decode_f32_blocks(a.lay.tpb) && (a.lay.head_dim == 32 || a.lay.head_dim == 64 || a.lay.head_dim == 128);
+    return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128);
 }
 
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
@@ -1857,7 +1875,9 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
     const WorkOrder& ord = order ? *order : identity;
     if (nitems <= 0) return;
     if (a.wave_splits) {  // the plan chose wave splits (wave_split_shape): merged in LDS
-        a.lay.head_dim == 64 ? dispatch_ws<64>(a, nrows, s) : dispatch_ws<128>(a, nrows, s);
+        a.lay.head_dim == 64    ? dispatch_ws<64>(a, nrows, s)
+        : a.lay.head_dim == 128 ? dispatch_ws<128>(a, nrows, s)
+                                : dispatch_ws<32>(a, nrows, s);
         TVARA_HIP(hipGetLastError());
         return;
     }
@@ -1895,8 +1915,9 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
         bool done = false;
         if (fast) {
             const int waves = waves_for(b);
-            done = b.lay.head_dim == 64 ? dispatch_fast<64>(b, nitems, waves, ord, s)
-                                        : dispatch_fast<128>(b, nitems, waves, ord, s);
+            done = b.lay.head_dim == 64    ? dispatch_fast<64>(b, nitems, waves, ord, s)
+                   : b.lay.head_dim == 128 ? dispatch_fast<128>(b, nitems, waves, ord, s)
+                                           : dispatch_fast<32>(b, nitems, waves, ord, s);
         }
         if (!done) {
             if (b.lay.head_dim > kGenericMaxDim) throw std::invalid_argument("head_dim above 512 is not supported");

@@ -339,6 +339,12 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     }
     if (tab.size() > static_cast<size_t>(std::numeric_limits<int32_t>::max()))
         throw std::invalid_argument("attention batch too large");
+    // The decode kernels that stream blocks directly (16-token blocks, and f32
+    // blocks of any power of two from 16 to 1,024 tokens) take work items
+    // that start on a block, with one id per block in the item's list.
+    const int tpb = static_cast<int>(g.tokens_per_block);
+    const bool listed = tpb == 16 || (c->format() == kF32 && decode_f32_blocks(tpb));
+    const size_t align = listed ? static_cast<size_t>(tpb) : 16;
     // Split length: the shortest (a multiple of 16 from 64 to 1,024 tokens)
     // whose launch fits the workgroup budget of the decode kernel that will
     // run (decode_budget_per_cu, measured on MI355X: the 64-sequence
@@ -354,7 +360,7 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     wave_splits = split ? 0
                         : wave_split_waves(rows, static_cast<int>(g.kv_heads), group, c->format(),
                                            static_cast<int>(g.head_dim), static_cast<int>(g.tokens_per_block), max_n);
-    if (wave_splits) split = round_up((max_n + wave_splits - 1) / wave_splits, 16);
+    if (wave_splits) split = round_up((max_n + wave_splits - 1) / wave_splits, align);
     // The row-major f32 kernel (decode_rows_shape) runs one workgroup per
     // item: its split is the shortest whose items fit one workgroup per CU,
     // and it takes the launch when that is more than kRowMajorMinWorkgroups
@@ -378,7 +384,7 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
             }
             sp = lo * 16;
         }
-        sp = std::min(round_up(std::max<size_t>(sp, 16), 16), kMaxSplitTokens);
+        sp = std::min(round_up(std::max<size_t>(sp, 16), align), kMaxSplitTokens);
         if (items_at(sp) > kRowMajorMinWorkgroups) {
             row_major = true;
             split = sp;
@@ -404,7 +410,7 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
         split = lo * 16;
     }
     // the decode kernels keep a split's block ids in one register per lane
-    split = std::min(round_up(std::max<size_t>(split, 16), 16), kMaxSplitTokens);
+    split = std::min(round_up(std::max<size_t>(split, 16), align), kMaxSplitTokens);
     split_tokens = static_cast<int>(split);
     std::vector<int4>& ent = h_entries;
     std::vector<int4>& work = h_work;
@@ -414,7 +420,6 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     work.clear();
     its.clear();
     work_ids.clear();
-    const bool blocks16 = g.tokens_per_block == 16;
     inline_ok = rows <= kInlineRows;
     need_merge = false;
     kv_bytes = 0;
@@ -431,8 +436,8 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
             its.push_back(make_int2(r, s));
             const int t0 = static_cast<int>(std::min(n, s * split)), t1 = static_cast<int>(std::min(n, (s + 1) * split));
             work.push_back(make_int4(r, t0, t1, ((tail && s == nsplit - 1) ? 1 : 0) | (nsplit << 1)));
-            const int nb = blocks16 ? (t1 - t0 + 15) / 16 : 0;
-            for (int j = 0; j < kMaxSplitBlocks; ++j) work_ids.push_back(j < nb ? tab[base + t0 / 16 + j] : 0);
+            const int nb = listed ? (t1 - t0 + tpb - 1) / tpb : 0;
+            for (int j = 0; j < kMaxSplitBlocks; ++j) work_ids.push_back(j < nb ? tab[base + t0 / tpb + j] : 0);
         }
         need_merge |= nsplit > 1 && !wave_splits;
         kv_bytes += static_cast<size_t>(static_cast<double>(n + tail) * g.kv_width() * 2 * bytes_per_element);

@@ -111,6 +111,13 @@ def decode_tinyllama(q8=False, sequences=64, length=2048):
     return DecodeWorkload(name, 32, 4, 64, [length] * sequences, blocks + 64, seed=7, q8=q8, context=1 << 17)
 
 
+def decode_t176():
+    """The reference's T176 cache case (tests/core/prefill_t176.cpp): one
+    sequence of 1,025 tokens, 4 query heads over 2 KV heads, head_dim 32,
+    16-token blocks, a 128-block cache."""
+    return DecodeWorkload("t176-decode-1x1025-d32", 4, 2, 32, [1025], 128, seed=8, context=2048)
+
+
 def place_blocks(cache, order):
     """Make the pool hand out block ids in `order`: allocate every block, then
     release them in reverse (the LIFO free list pops the last release first)."""
