@@ -207,7 +207,8 @@ int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t c
             return;
         }
         // q | tail keys | tail values in one pinned buffer and one copy in;
-        // the output comes back through a second pinned buffer
+        // the output comes back through a second pinned buffer, the error
+        // flag with it, so the call waits for the stream once
         const size_t nq = count * hidden, nt = tail ? count * kvw : 0;
         tvara_amd::HostCopier& copier = tvara_amd::HostCopier::shared();
         std::lock_guard<std::mutex> hold(copier.lock());
@@ -227,7 +228,9 @@ int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t c
         plan.launch(static_cast<int>(layer), d, tail ? d + nq : nullptr, tail ? d + nq + nt : nullptr, d + out_at, s);
         auto* back = static_cast<float*>(cache->io_out.acquire(nq * sizeof(float)));
         TVARA_HIP(hipMemcpyAsync(back, d + out_at, nq * sizeof(float), hipMemcpyDeviceToHost, s));
-        plan.check();  // waits for the stream, the copy out included
+        plan.queue_check();
+        TVARA_HIP(hipStreamSynchronize(s));
+        plan.finish_check();
         stage(out, back, nq);
     });
 }

@@ -64,8 +64,9 @@ HostCopier& HostCopier::shared() {
     return *copier;
 }
 
-void HostCopier::parallel_copy(char* dst, const char* src, size_t bytes) {
-    const int parts = static_cast<int>(std::min<size_t>(threads_.size() + 1, std::max<size_t>(1, bytes >> 17)));
+void HostCopier::parallel_copy(char* dst, const char* src, size_t bytes, int min_part_log2) {
+    const int parts =
+        static_cast<int>(std::min<size_t>(threads_.size() + 1, std::max<size_t>(1, bytes >> min_part_log2)));
     if (parts <= 1) {
         std::memcpy(dst, src, bytes);
         return;
@@ -109,7 +110,7 @@ void HostCopier::from_device(void* dst, const void* src, size_t bytes, hipStream
     for (size_t i = 0; i < n; ++i) {
         TVARA_HIP(hipEventSynchronize(done_[i % 2]));
         const size_t off = i * kChunk, len = std::min(kChunk, bytes - off);
-        parallel_copy(out + off, static_cast<const char*>(pinned_[i % 2]), len);
+        parallel_copy(out + off, static_cast<const char*>(pinned_[i % 2]), len, 17);
         if (i + 2 < n) issue(i + 2);
     }
 }

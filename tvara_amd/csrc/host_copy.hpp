@@ -24,8 +24,10 @@ public:
     // synchronous: returns when `bytes` from device `src` (after the work
     // already queued on `s`) are in host `dst`
     void from_device(void* dst, const void* src, size_t bytes, hipStream_t s);
-    // host-to-host copy split over the pool's threads (one thread below 128 KiB)
-    void parallel_copy(char* dst, const char* src, size_t bytes);
+    // host-to-host copy split over the pool's threads, parts of at least
+    // 2^min_part_log2 bytes (one thread copies 512 KiB in about 5 us, under
+    // the cost of waking the pool)
+    void parallel_copy(char* dst, const char* src, size_t bytes, int min_part_log2 = 21);
 
     // a process-wide copier; calls on it are serialised by its own lock
     static HostCopier& shared();

@@ -591,15 +591,35 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     last_stream = s;
 }
 
-void AttnPlan::check() {
-    int flag = 0;
-    TVARA_HIP(hipMemcpyAsync(&flag, dev.err, sizeof(int), hipMemcpyDeviceToHost, last_stream));
-    TVARA_HIP(hipStreamSynchronize(last_stream));
-    if (flag) {
+void AttnPlan::queue_check() {
+    auto* f = static_cast<int*>(flag.acquire(sizeof(int)));
+    TVARA_HIP(hipMemcpyAsync(f, dev.err, sizeof(int), hipMemcpyDeviceToHost, last_stream));
+}
+
+void AttnPlan::finish_check() {
+    if (*static_cast<const volatile int*>(flag.ptr)) {
         TVARA_HIP(hipMemsetAsync(dev.err, 0, sizeof(int), last_stream));
         TVARA_HIP(hipStreamSynchronize(last_stream));
         throw std::invalid_argument("invalid online attention input");
     }
+}
+
+void AttnPlan::check_into(int* host_flag) {
+    TVARA_HIP(hipMemcpyAsync(host_flag, dev.err, sizeof(int), hipMemcpyDeviceToHost, last_stream));
+    TVARA_HIP(hipStreamSynchronize(last_stream));
+    if (*host_flag) {
+        TVARA_HIP(hipMemsetAsync(dev.err, 0, sizeof(int), last_stream));
+        TVARA_HIP(hipStreamSynchronize(last_stream));
+        throw std::invalid_argument("invalid online attention input");
+    }
+}
+
+// the flag goes to pinned memory, so the copy is one DMA on the stream and
+// the call waits for the stream once
+void AttnPlan::check() {
+    queue_check();
+    TVARA_HIP(hipStreamSynchronize(last_stream));
+    finish_check();
 }
 
 void PrefillPlan::build(DeviceCache* c, const uint64_t* sequences, size_t n, size_t h, size_t context,

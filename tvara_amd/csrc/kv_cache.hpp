@@ -150,6 +150,7 @@ struct AttnPlan {
     } dev;
     DeviceBuffer region;  // place(): the packed plan (grow-only)
     PinnedBuffer staging;
+    PinnedBuffer flag;  // check(): the error flag's host copy
     hipStream_t last_stream = nullptr;
 
     AttnPlan() = default;
@@ -176,6 +177,13 @@ struct AttnPlan {
     void launch(int layer, const float* q, const float* tail_k, const float* tail_v, float* out, hipStream_t s);
     // waits for the last launch's stream; a non-finite score throws
     void check();
+    // the same, with the flag copied to caller-provided host memory (no
+    // pinned allocation)
+    void check_into(int* host_flag);
+    // queues the error flag's copy to pinned host memory on the last launch's
+    // stream; after the stream has drained, finish_check() reads it
+    void queue_check();
+    void finish_check();
 };
 
 // Chunked-prefill plan: sequences[i] attends its prompt rows start[i] ..

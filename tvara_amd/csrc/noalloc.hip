@@ -98,7 +98,8 @@ int tvara_attn_decode_noalloc(tvara_kv_cache* cache, const uint64_t* sequences, 
         hipStream_t s = c.stream();
         plan.place_in(base, tvara_amd::kScratchBytes, s, image.data());
         plan.launch(static_cast<int>(layer), q, tail_keys, tail_values, out, s);
-        plan.check();  // waits for the stream: the copy in and the launch are done
+        int flag = 0;
+        plan.check_into(&flag);  // waits for the stream: the copy in and the launch are done
     });
 }
 
