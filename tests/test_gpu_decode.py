@@ -606,3 +606,49 @@ def test_t176_shape(device, oracle):
     # every key is the same row, so each head's output is that head's V row
     assert np.allclose(want.reshape(4, 32), np.repeat(v.reshape(2, 32), 2, axis=0), rtol=1e-6, atol=1e-6)
     assert refmath.close(got, want, TOL), refmath.max_rel(got, want)
+
+
+@pytest.mark.parametrize("fmt_name,dim,kv_heads,group,split", [("F32", 64, 8, 4, 0), ("F32", 64, 4, 8, 0),
+                                                               ("F32", 64, 16, 2, 0), ("F32", 128, 8, 4, 0),
+                                                               ("F32", 64, 8, 4, 256), ("Q8_0", 128, 8, 4, 0),
+                                                               ("Q8_0", 64, 2, 4, 0)])
+def test_zero_query_counts_every_token(device, oracle, monkeypatch, fmt_name, dim, kv_heads, group, split):
+    # q = 0: every score is 0 and every weight exp2(0) = 1, so with V of
+    # integers (exact in f32 and in Q8_0 with one 127 per 32-column group) each
+    # output row is the exact mean of the row's V rows and its tail row, through
+    # any split and merge.  A dropped or repeated token moves the mean by at
+    # least 1/(2n) of a unit, far above the 1e-6 bar -- the 1e-4 bar of the
+    # N(0,1) tests can miss one token of 4,096.  Rows of the C2 length
+    # distribution (launches that fill the GPU: the row-major, int8-MFMA and
+    # head-major kernels with their split merges).
+    if split:
+        monkeypatch.setenv("TVARA_SPLIT_TOKENS", str(split))
+    fmt = getattr(device, fmt_name)
+    heads, tpb = kv_heads * group, 16
+    lengths = [int(x) for x in synth.integers(2, "ctx", 64, 128, 4096)[:48]] + [1, 15, 16, 17]
+    g = (1, kv_heads, dim, tpb, sum((n + tpb - 1) // tpb for n in lengths) + 4)
+    dev = device.PagedCache(*g, fmt=fmt)
+    w = kv_heads * dim
+    rng = np.random.default_rng(91 + dim + kv_heads + group)
+    seqs, vals = [], []
+    for i, n in enumerate(lengths):
+        v = rng.integers(-4, 5, size=(n, w)).astype(np.float32)
+        v[:, ::32] = 127.0
+        k = synth.normal(91, f"k{i}", n * w).reshape(n, w)
+        s = dev.create_sequence()
+        dev.append_many(s, k, v)
+        seqs.append(s)
+        vals.append(v)
+    rows = len(lengths)
+    tv = rng.integers(-4, 5, size=(rows, w)).astype(np.float32)
+    tk = synth.normal(91, "tk", rows * w).reshape(rows, w)
+    q = np.zeros((rows, heads * dim), np.float32)
+    plan = attention.DecodePlan(dev, seqs, heads, 1 << 20, with_tail=True)
+    say("zero query", fmt_name, dim, kv_heads, group, "items", plan.items, "split", plan.split_tokens)
+    got = attention.decode_batch(dev, q, seqs, 0, heads, 1 << 20, tail_keys=tk, tail_values=tv)
+    got = got.reshape(rows, heads, dim)
+    for i, n in enumerate(lengths):
+        want = (vals[i].astype(np.float64).sum(axis=0) + tv[i]) / (n + 1)
+        want = want.reshape(kv_heads, dim)
+        for h in range(heads):
+            assert np.allclose(got[i, h], want[h // group], rtol=1e-6, atol=1e-6), (i, n, h)

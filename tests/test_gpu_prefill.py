@@ -241,3 +241,57 @@ def test_chunk_invariant_under_future_tokens(device, precision, dim):
     after = attention.prefill_batch(dev, q, [s], [start], [rows], 0, heads, 4096, precision=precision)
     assert np.isfinite(before).all()
     assert np.array_equal(before, after)
+
+
+@pytest.mark.parametrize("precision", ["bf16", "f32"])
+@pytest.mark.parametrize("fmt", ["f32", "q8_0"])
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("group", [1, 3, 4, 8])
+def test_zero_query_averages_every_visible_key(device, oracle, group, dim, fmt, precision):
+    # With q = 0 every score is 0, every probability exp2(0) = 1 exactly, and
+    # with V of integers (exact in bf16, Q8_0 and every f32 partial sum) each
+    # output row is the exact mean of the V rows its causal mask admits.
+    # A dropped or repeated key moves the mean by at least 1/(2n) of a unit,
+    # far above the 1e-6 bar, so the mask boundary of every row, the chunk
+    # tiling, the GQA row mapping and the paged block walk are checked exactly
+    # (the bf16 bars above cannot see a single key among thousands).  The f32
+    # path (decode kernels, split merges) is exact here too.
+    heads, kv_heads = 2 * group, 2
+    w = kv_heads * dim
+    specs = [(1100, 1000, 100), (300, 0, 300), (77, 60, 17), (2100, 1600, 500)]
+    nb = sum((n + 15) // 16 for n, _, _ in specs) + 4
+    q8 = fmt == "q8_0"
+    dev = device.PagedCache(1, kv_heads, dim, 16, nb, fmt=device.Q8_0 if q8 else device.F32)
+    ref = oracle.Cache(1, kv_heads, dim, 16, nb)
+    rng = np.random.default_rng(83 + group + dim)
+    ds, rs, vals = [], [], []
+    for i, (n, _, _) in enumerate(specs):
+        k = synth.normal(83, f"k{i}", n * w).reshape(n, w)
+        # integers (exact in bf16); one 127 per 32-column group makes the
+        # Q8_0 scale exactly 1, so the blocks hold the same integers
+        v = rng.integers(-4, 5, size=(n, w)).astype(np.float32)
+        v[:, ::32] = 127.0
+        if q8:
+            k = oracle.dequantize_q8_0(oracle.quantize_q8_0(k)).reshape(n, w)
+            assert np.array_equal(oracle.dequantize_q8_0(oracle.quantize_q8_0(v)).reshape(n, w), v)
+        sd, sr = dev.create_sequence(), ref.create_sequence()
+        dev.append_many(sd, k, v)
+        ref.append_many(sr, k, v)
+        ds.append(sd)
+        rs.append(sr)
+        vals.append(v)
+    starts = [s for _, s, _ in specs]
+    counts = [r for _, _, r in specs]
+    rows = sum(counts)
+    q = np.zeros((rows, heads * dim), np.float32)
+    say("prefill zero query", group, dim, fmt, precision)
+    got = attention.prefill_batch(dev, q, ds, starts, counts, 0, heads, 4096, precision=precision)
+    got = got.reshape(rows, heads, dim)
+    at = 0
+    for i, (n, start, cnt) in enumerate(specs):
+        csum = np.cumsum(vals[i].reshape(n, kv_heads, dim).astype(np.float64), axis=0)
+        for r in range(cnt):
+            want = csum[start + r] / (start + r + 1)  # keys 0 .. start + r
+            for h in range(heads):
+                assert np.allclose(got[at + r, h], want[h // group], rtol=1e-6, atol=1e-6), (i, r, h)
+        at += cnt
