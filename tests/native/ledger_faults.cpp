@@ -370,6 +370,47 @@ static void faults() {
     check(total > 0, "no allocation was ever failed");
 }
 
+// The sequence map against std::map: random inserts and erases over a small
+// id range (many erased slots, repeated growth and same-size rehashes), every
+// id looked up after every step, the live set compared by for_each.
+static void sequence_map() {
+    for (uint64_t seed = 1; seed <= 4; ++seed) {
+        tvara_amd::SequenceMap m;
+        std::map<uint64_t, size_t> model;
+        Rng r{seed * 7777};
+        const uint64_t range = seed == 4 ? 5000 : 200;
+        for (int step = 0; step < 20000; ++step) {
+            const uint64_t id = 1 + r.below(range);
+            if (model.count(id)) {
+                check(m.erase(id), "erase of a live id failed", step);
+                model.erase(id);
+            } else {
+                tvara_amd::Table t;
+                t.length = static_cast<size_t>(step);
+                m.insert(id, std::move(t));
+                model[id] = static_cast<size_t>(step);
+            }
+            check(m.size() == model.size(), "sequence map size", step);
+            if (step % 97 == 0 || range <= 200) {
+                for (uint64_t k = 1; k <= range; k += (range <= 200 ? 1 : 13)) {
+                    const tvara_amd::Table* t = m.find(k);
+                    const auto it = model.find(k);
+                    check((t != nullptr) == (it != model.end()), "sequence map membership", static_cast<long>(k));
+                    if (t) check(t->length == it->second, "sequence map value", static_cast<long>(k));
+                }
+            }
+        }
+        size_t seen = 0;
+        m.for_each([&](uint64_t id, const tvara_amd::Table& t) {
+            check(model.count(id) && model[id] == t.length, "for_each entry", static_cast<long>(id));
+            ++seen;
+        });
+        check(seen == model.size(), "for_each count");
+        check(!m.erase(range + 1), "erase of an absent id");
+    }
+    std::printf("sequence map: 4 x 20000 random inserts and erases matched std::map\n");
+}
+
 static void gguf_files(int argc, char** argv) {
     for (int i = 2; i < argc; ++i) {
         try {
@@ -390,7 +431,10 @@ int main(int argc, char** argv) {
         gguf_files(argc, argv);
         return 0;
     }
-    if (mode == "all" || mode == "churn") churn();
+    if (mode == "all" || mode == "churn") {
+        sequence_map();
+        churn();
+    }
     if (mode == "all" || mode == "faults") {
         faults();
     }

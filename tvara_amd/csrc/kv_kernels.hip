@@ -13,6 +13,21 @@ namespace {
 
 constexpr int kThreads = 256;
 
+// Non-temporal 16-byte stores for block bytes: nothing in the same launch
+// reads them back, so they skip allocation in the caches (a later decode or
+// copy reads them from HBM).
+__device__ inline void store_stream(uint4* p, const uint4 v) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<u32x4*>(p));
+}
+
+__device__ inline void store_stream(float4* p, const float4 v) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(p));
+}
+
 // BlockPool::allocate zero-fill (kv.hpp:48) and PagedCache::append's
 // whole-block copy (kv.hpp:99); grid.y = op, grid.x strides the block.
 __global__ __launch_bounds__(kThreads) void block_init_kernel(char* pool, size_t stride,
@@ -24,11 +39,11 @@ __global__ __launch_bounds__(kThreads) void block_init_kernel(char* pool, size_t
     if (op.src >= 0) {
         const uint4* src = reinterpret_cast<const uint4*>(pool + static_cast<size_t>(op.src) * stride);
         for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < units; i += step)
-            dst[i] = src[i];
+            store_stream(dst + i, src[i]);
     } else {
         const uint4 zero = make_uint4(0, 0, 0, 0);
         for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < units; i += step)
-            dst[i] = zero;
+            store_stream(dst + i, zero);
     }
 }
 
@@ -41,11 +56,11 @@ __global__ __launch_bounds__(kThreads) void block_init_inline_kernel(char* pool,
     if (op.y >= 0) {
         const uint4* src = reinterpret_cast<const uint4*>(pool + static_cast<size_t>(op.y) * stride);
         for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < units; i += step)
-            dst[i] = src[i];
+            store_stream(dst + i, src[i]);
     } else {
         const uint4 zero = make_uint4(0, 0, 0, 0);
         for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < units; i += step)
-            dst[i] = zero;
+            store_stream(dst + i, zero);
     }
 }
 
@@ -54,7 +69,7 @@ __global__ __launch_bounds__(kThreads) void block_init_inline_kernel(char* pool,
 // kThreads 16-byte units of the token's rows over every (layer, kind); each
 // thread requests all its units before storing the first.  Requires
 // kv_width % 4 == 0.
-constexpr int kAppendUnroll = 8;
+constexpr int kAppendUnroll = 4;
 
 __global__ __launch_bounds__(kThreads) void append_rows_f32_inline_kernel(char* pool, BlockLayout lay,
                                                                           const InlineRowOps ops,
@@ -80,7 +95,7 @@ __global__ __launch_bounds__(kThreads) void append_rows_f32_inline_kernel(char* 
     }
 #pragma unroll
     for (int j = 0; j < kAppendUnroll; ++j)
-        if (u0 + j * kThreads < units) block[dst[j]] = x[j];
+        if (u0 + j * kThreads < units) store_stream(block + dst[j], x[j]);
 }
 
 // PagedCache::append row copies (kv.hpp:103-106): grid.x = layer*2+kind,

@@ -11,7 +11,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <exception>
-#include <map>
+#include <memory>
 #include <stdexcept>
 #include <vector>
 
@@ -40,6 +40,36 @@ struct Handle {
 struct Table {
     std::vector<Handle> blocks;
     size_t length = 0;
+};
+
+// Sequence id -> block table.  An append batch looks up every listed
+// sequence, so this is open addressing with linear probing over a power-of-two
+// array and a multiplicative hash (no division per lookup).  Ids are never 0
+// (the first is 1) nor ~0 (an exhausted counter throws first), which mark
+// empty and erased slots.  Tables sit behind unique_ptr, so a reference stays
+// valid while other sequences are added or erased.
+class SequenceMap {
+public:
+    SequenceMap() { rehash(64); }
+    Table* find(uint64_t id) const;
+    Table& insert(uint64_t id, Table&& t);  // id must not be present
+    bool erase(uint64_t id);
+    size_t size() const { return size_; }
+    template <class F>
+    void for_each(F&& f) const {
+        for (size_t i = 0; i < keys_.size(); ++i)
+            if (keys_[i] != kEmpty && keys_[i] != kErased) f(keys_[i], *vals_[i]);
+    }
+
+private:
+    static constexpr uint64_t kEmpty = 0, kErased = ~uint64_t(0);
+    size_t home(uint64_t id) const { return static_cast<size_t>((id * 0x9E3779B97F4A7C15ull) >> shift_); }
+    void rehash(size_t capacity);
+
+    std::vector<uint64_t> keys_;
+    std::vector<std::unique_ptr<Table>> vals_;
+    size_t size_ = 0, used_ = 0;  // live slots; live + erased slots
+    int shift_ = 64;
 };
 
 // Block initialisation: zero-fill (src < 0, BlockPool::allocate, kv.hpp:48)
@@ -118,7 +148,9 @@ private:
     std::vector<size_t> free_;  // popped from the back
     std::vector<uint8_t> zero_pending_;
     std::vector<size_t> zero_list_;
-    std::map<uint64_t, Table> sequences_;
+    size_t slot_mask_ = 0;  // tokens_per_block - 1 when it is a power of two
+    size_t max_tokens_ = 0;
+    SequenceMap sequences_;  // sequence_ids() sorts: the reference's std::map order
     uint64_t next_ = 0;
 };
 

@@ -23,6 +23,7 @@ F32 = _capi.KV_F32
 Q8_0 = _capi.KV_Q8_0
 
 _fp = C.POINTER(C.c_float)
+_u64p = C.POINTER(C.c_uint64)
 
 
 def _f32(a):
@@ -217,10 +218,13 @@ class PagedCache:
         return applied.value
 
     def append_batch_device(self, seqs, keys_ptr, values_ptr):
-        """As append_batch with K/V already in HBM ([n][layers*kv_width] f32)."""
-        seqs = np.ascontiguousarray(seqs, dtype=np.uint64)
+        """As append_batch with K/V already in HBM ([n][layers*kv_width] f32).
+        A scheduler that keeps its batch as a contiguous uint64 array saves the
+        per-call list conversion (about 10 us for 256 sequences)."""
+        if not (isinstance(seqs, np.ndarray) and seqs.dtype == np.uint64 and seqs.flags.c_contiguous):
+            seqs = np.ascontiguousarray(seqs, dtype=np.uint64)
         applied = C.c_size_t()
-        rc = self.lib.tvara_kv_append_batch(self.h, seqs.ctypes.data_as(C.POINTER(C.c_uint64)), seqs.size,
+        rc = self.lib.tvara_kv_append_batch(self.h, C.cast(seqs.ctypes.data, _u64p), seqs.size,
                                             C.cast(keys_ptr, _fp), C.cast(values_ptr, _fp), 1, C.byref(applied))
         self.last_applied = applied.value
         self._check(rc)
