@@ -207,8 +207,9 @@ int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t c
             return;
         }
         // q | tail keys | tail values in one pinned buffer and one copy in;
-        // the output comes back through a second pinned buffer, the error
-        // flag with it, so the call waits for the stream once
+        // the kernels write the output (and the error flag) straight into
+        // pinned host memory, so the call waits for the stream once and no
+        // copy comes back
         const size_t nq = count * hidden, nt = tail ? count * kvw : 0;
         tvara_amd::HostCopier& copier = tvara_amd::HostCopier::shared();
         std::lock_guard<std::mutex> hold(copier.lock());
@@ -221,13 +222,11 @@ int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences, size_t c
             stage(in + nq, tail_keys, nt);
             stage(in + nq + nt, tail_values, nt);
         }
-        const size_t out_at = (nq + 2 * nt + 3) / 4 * 4;  // 16-byte aligned
-        auto* d = static_cast<float*>(cache->io.ensure((out_at + nq) * sizeof(float)));
+        auto* d = static_cast<float*>(cache->io.ensure((nq + 2 * nt) * sizeof(float)));
         TVARA_HIP(hipMemcpyAsync(d, in, (nq + 2 * nt) * sizeof(float), hipMemcpyHostToDevice, s));
         cache->io_in.release(s);
-        plan.launch(static_cast<int>(layer), d, tail ? d + nq : nullptr, tail ? d + nq + nt : nullptr, d + out_at, s);
         auto* back = static_cast<float*>(cache->io_out.acquire(nq * sizeof(float)));
-        TVARA_HIP(hipMemcpyAsync(back, d + out_at, nq * sizeof(float), hipMemcpyDeviceToHost, s));
+        plan.launch(static_cast<int>(layer), d, tail ? d + nq : nullptr, tail ? d + nq + nt : nullptr, back, s);
         plan.queue_check();
         TVARA_HIP(hipStreamSynchronize(s));
         plan.finish_check();

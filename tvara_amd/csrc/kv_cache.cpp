@@ -596,21 +596,33 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.wave_splits = wave_splits;
     a.row_major = row_major ? 1 : 0;
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
-    a.err = dev.err;
+    a.err = pinned_err ? static_cast<int*>(flag.ptr) : dev.err;
     launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, order.n ? &order : nullptr, s);
     cache->leave(s);
     last_stream = s;
 }
 
+void AttnPlan::use_pinned_error() {
+    if (pinned_err) return;
+    *static_cast<volatile int*>(flag.acquire(sizeof(int))) = 0;
+    pinned_err = true;
+}
+
 void AttnPlan::queue_check() {
+    if (pinned_err) return;  // the kernels write the pinned flag themselves
     auto* f = static_cast<int*>(flag.acquire(sizeof(int)));
     TVARA_HIP(hipMemcpyAsync(f, dev.err, sizeof(int), hipMemcpyDeviceToHost, last_stream));
 }
 
 void AttnPlan::finish_check() {
-    if (*static_cast<const volatile int*>(flag.ptr)) {
-        TVARA_HIP(hipMemsetAsync(dev.err, 0, sizeof(int), last_stream));
-        TVARA_HIP(hipStreamSynchronize(last_stream));
+    auto* f = static_cast<volatile int*>(flag.ptr);
+    if (*f) {
+        if (pinned_err) {
+            *f = 0;
+        } else {
+            TVARA_HIP(hipMemsetAsync(dev.err, 0, sizeof(int), last_stream));
+            TVARA_HIP(hipStreamSynchronize(last_stream));
+        }
         throw std::invalid_argument("invalid online attention input");
     }
 }
@@ -625,8 +637,8 @@ void AttnPlan::check_into(int* host_flag) {
     }
 }
 
-// the flag goes to pinned memory, so the copy is one DMA on the stream and
-// the call waits for the stream once
+// the flag is (or is copied to) pinned memory, so the call waits for the
+// stream once
 void AttnPlan::check() {
     queue_check();
     TVARA_HIP(hipStreamSynchronize(last_stream));

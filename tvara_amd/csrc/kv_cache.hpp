@@ -150,7 +150,11 @@ struct AttnPlan {
     } dev;
     DeviceBuffer region;  // place(): the packed plan (grow-only)
     PinnedBuffer staging;
-    PinnedBuffer flag;  // check(): the error flag's host copy
+    PinnedBuffer flag;  // check(): the error flag's host copy, or the flag itself (pinned_err)
+    // the kernels set the error flag in pinned host memory (no copy back
+    // before a check); plans built by build() use it, the no-allocation path
+    // keeps the device flag
+    bool pinned_err = false;
     hipStream_t last_stream = nullptr;
 
     AttnPlan() = default;
@@ -173,7 +177,9 @@ struct AttnPlan {
                const std::vector<uint8_t>& tail_rows, int heads, size_t split_override) {
         compute(c, seq_of_row, cached, tail_rows, heads, split_override);
         place();
+        use_pinned_error();
     }
+    void use_pinned_error();
     void launch(int layer, const float* q, const float* tail_k, const float* tail_v, float* out, hipStream_t s);
     // waits for the last launch's stream; a non-finite score throws
     void check();
