@@ -232,14 +232,20 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) s[mt][nt] = f32x4{c0, c0, c0, c0};
             }
+            // every K operand of the tile is read before the first product, so
+            // the reads' latency is paid once
+            bf16x8 kop[KC][4];
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                    kop[kc][mt] = *reinterpret_cast<const bf16x8*>(&klds[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) {
-                    const bf16x8 kop =
-                        *reinterpret_cast<const bf16x8*>(&klds[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
-                    s[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[0][kc], s[mt][0], 0, 0, 0);
-                    s[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[1][kc], s[mt][1], 0, 0, 0);
+                    s[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[kc][mt], qop[0][kc], s[mt][0], 0, 0, 0);
+                    s[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[kc][mt], qop[1][kc], s[mt][1], 0, 0, 0);
                 }
             // the causal mask only on tiles that reach past a row's own position
             if (kbase + kKeys - 1 > start + pw0) {
