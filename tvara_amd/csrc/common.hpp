@@ -108,6 +108,10 @@ struct DecodeArgs {
     int* row_done;
     int wave_splits;  // > 0: each row's splits are the waves of one workgroup per (row, KV head)
     int row_major;    // 1: decode_rows_kernel (one eight-wave workgroup per work item)
+    // Query groups above eight run as slices: lay.kv_heads and group describe
+    // kv_share virtual KV heads per KV head, and virtual head v reads the K/V
+    // of head v / kv_share (1: no slicing)
+    int kv_share;
     const float* q;
     const float* tail_k;  // [rows][kv_width] or null
     const float* tail_v;

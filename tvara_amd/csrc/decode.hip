@@ -378,7 +378,8 @@ __global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(c
 
     // blocks of tpb = 2^tsh tokens (16 to 1,024); a split starts on a block
     const int tpb = a.lay.tpb, tsh = __builtin_ctz(static_cast<unsigned>(tpb));
-    const size_t koff = static_cast<size_t>(a.layer) * 2 * tpb * kvw + static_cast<size_t>(kh) * D + 4 * c;
+    const int kvh = kh / a.kv_share;  // the KV head whose K/V this (virtual) head reads
+    const size_t koff = static_cast<size_t>(a.layer) * 2 * tpb * kvw + static_cast<size_t>(kvh) * D + 4 * c;
     const size_t voff = koff + static_cast<size_t>(tpb) * kvw;
 
     auto load = [&](int tb, float4 (&kk)[NV], float4 (&vv)[NV], bool ok) {
@@ -455,8 +456,8 @@ __global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(c
     }
     if (tail) {  // the current token's uncommitted K/V is the last position (attention.hpp:80)
         const bool ok = tg == 0;
-        const float* tk = a.tail_k + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kh) * D + 4 * c;
-        const float* tv = a.tail_v + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kh) * D + 4 * c;
+        const float* tk = a.tail_k + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kvh) * D + 4 * c;
+        const float* tv = a.tail_v + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kvh) * D + 4 * c;
 #pragma unroll
         for (int m = 0; m < NV; ++m) {
             ka[m] = ok ? *reinterpret_cast<const float4*>(tk + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -863,10 +864,11 @@ __global__ __launch_bounds__(G > 4 ? 128 : 512) void decode_q8_kernel(const Deco
     // table loads
 
     const size_t sec = a.lay.section;
-    const size_t qcol = static_cast<size_t>(kh) * D + 16 * c;  // column in the f32 tail row
+    const int kvh = kh / a.kv_share;  // the KV head whose K/V this (virtual) head reads
+    const size_t qcol = static_cast<size_t>(kvh) * D + 16 * c;  // column in the f32 tail row
     // this head's run of the section: int8 [16][D], then fp16 scales [16][D/32]
-    const size_t qoff = static_cast<size_t>(kh) * a.lay.head_bytes + 16 * c;
-    const size_t soff = static_cast<size_t>(kh) * a.lay.head_bytes + 16 * D + (16 * c / 32) * 2;
+    const size_t qoff = static_cast<size_t>(kvh) * a.lay.head_bytes + 16 * c;
+    const size_t soff = static_cast<size_t>(kvh) * a.lay.head_bytes + 16 * D + (16 * c / 32) * 2;
     const size_t ksec = static_cast<size_t>(a.layer) * 2 * sec, vsec = ksec + sec;
 
     struct Tile {
@@ -1100,9 +1102,10 @@ __global__ __launch_bounds__(512) void decode_q8_mma_kernel(const DecodeArgs a) 
     const int nblk = (n + 15) >> 4;
     const size_t sec = a.lay.section;
     // this head's run of a section: int8 [16][D] then fp16 scales [16][NG]
-    const size_t ksec = static_cast<size_t>(a.layer) * 2 * sec + static_cast<size_t>(kh) * a.lay.head_bytes;
+    const int kvh = kh / a.kv_share;  // the KV head whose K/V this (virtual) head reads
+    const size_t ksec = static_cast<size_t>(a.layer) * 2 * sec + static_cast<size_t>(kvh) * a.lay.head_bytes;
     const size_t vsec = ksec + sec;
-    const size_t kcol = static_cast<size_t>(kh) * D;  // column of the f32 tail row
+    const size_t kcol = static_cast<size_t>(kvh) * D;  // column of the f32 tail row
 
     // Loads are contiguous: lane i takes bytes 16i (+1024m) of a head's int8
     // plane, and the 16 tokens' scales are one 16 * NG * 2 byte run.
@@ -1319,7 +1322,7 @@ constexpr int kGenericMaxDim = 512;
 __global__ __launch_bounds__(64) void decode_generic_kernel(const DecodeArgs a) {
     __shared__ float qs[kGenericMaxDim];
     const int lane = threadIdx.x;
-    const int h = blockIdx.y, kh = h / a.group;
+    const int h = blockIdx.y, kh = h / (a.group * a.kv_share);  // the KV head (group: a slice when kv_share > 1)
     const int D = a.lay.head_dim, kvw = a.lay.kv_width, tpb = a.lay.tpb;
     const int2 it = a.items[blockIdx.x];
     const int4 en = a.entries[it.x];

@@ -326,6 +326,14 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     for (uint8_t t : tail_rows) with_tail |= t != 0;
     const Geometry& g = c->geometry();
     group = static_cast<int>(heads / g.kv_heads);
+    kv_share = 1;
+    if (group > 8) {
+        int slice = 8;
+        while (group % slice) --slice;
+        kv_share = group / slice;
+    }
+    // the kernels' view: kv_share virtual KV heads per KV head
+    const int vkv = static_cast<int>(g.kv_heads) * kv_share, vgroup = group / kv_share;
     rows = static_cast<int>(seq_of_row.size());
     std::map<uint64_t, int32_t> offset;
     std::vector<int32_t>& tab = h_tables;
@@ -358,8 +366,8 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     size_t max_n = 0;
     for (size_t n : cached) max_n = std::max(max_n, n);
     wave_splits = split ? 0
-                        : wave_split_waves(rows, static_cast<int>(g.kv_heads), group, c->format(),
-                                           static_cast<int>(g.head_dim), static_cast<int>(g.tokens_per_block), max_n);
+                        : wave_split_waves(rows, vkv, vgroup, c->format(), static_cast<int>(g.head_dim),
+                                           static_cast<int>(g.tokens_per_block), max_n);
     if (wave_splits) split = round_up((max_n + wave_splits - 1) / wave_splits, align);
     // The row-major f32 kernel (decode_rows_shape) runs one workgroup per
     // item.  Its split starts from the shortest whose items fit one workgroup
@@ -377,8 +385,9 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
         for (size_t len : cached) n += std::max<size_t>(1, (len + sp - 1) / sp);
         return n;
     };
-    if (!wave_splits && decode_rows_shape(static_cast<int>(g.kv_heads), group, c->format(),
-                                          static_cast<int>(g.head_dim), static_cast<int>(g.tokens_per_block))) {
+    if (!wave_splits && kv_share == 1 &&
+        decode_rows_shape(static_cast<int>(g.kv_heads), group, c->format(), static_cast<int>(g.head_dim),
+                          static_cast<int>(g.tokens_per_block))) {
         size_t sp = split;
         if (!sp) {
             const size_t budget = static_cast<size_t>(c->compute_units());
@@ -402,11 +411,11 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
         }
     }
     if (!split) {
-        const int gw = static_cast<int>(g.kv_heads), gd = static_cast<int>(g.head_dim);
-        const size_t groups = static_cast<size_t>(decode_slots(gw, group, c->format(), gd)) /
-                              static_cast<size_t>(decode_waves(gw, group, c->format(), gd));
+        const int gd = static_cast<int>(g.head_dim);
+        const size_t groups = static_cast<size_t>(decode_slots(vkv, vgroup, c->format(), gd)) /
+                              static_cast<size_t>(decode_waves(vkv, vgroup, c->format(), gd));
         const size_t budget = static_cast<size_t>(c->compute_units()) *
-                              decode_budget_per_cu(group, c->format(), static_cast<int>(g.head_dim));
+                              decode_budget_per_cu(vgroup, c->format(), static_cast<int>(g.head_dim));
         auto workgroups = [&](size_t sp) {
             size_t n = 0;
             for (size_t len : cached) n += std::max<size_t>(1, (len + sp - 1) / sp);
@@ -455,8 +464,7 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     }
     items = static_cast<int>(its.size());
     order.n = 0;
-    const bool one_group = row_major || decode_waves(static_cast<int>(g.kv_heads), group, c->format(),
-                                        static_cast<int>(g.head_dim)) == static_cast<int>(g.kv_heads);
+    const bool one_group = row_major || decode_waves(vkv, vgroup, c->format(), static_cast<int>(g.head_dim)) == vkv;
     if (!wave_splits && one_group && c->format() == kF32 && items <= kOrderedItems && c->xcds() > 1 &&
         items >= c->xcds())
         xcd_balance(c->xcds());
@@ -526,7 +534,7 @@ RegionLayout region_layout(const AttnPlan& p) {
     r.items = take(p.h_items.size() * sizeof(int2));
     r.work = take(p.h_work.size() * sizeof(int4));
     r.work_blocks = take(p.h_work_blocks.size() * sizeof(int32_t));
-    r.row_done = take(static_cast<size_t>(p.rows) * g.kv_heads * sizeof(int));
+    r.row_done = take(static_cast<size_t>(p.rows) * g.kv_heads * p.kv_share * sizeof(int));
     r.err = take(sizeof(int));
     r.copied = at;
     r.part_acc = take(p.need_merge ? static_cast<size_t>(p.items) * p.heads * g.head_dim * sizeof(float) : 0);
@@ -577,9 +585,11 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     DecodeArgs a{};
     a.pool = cache->pool();
     a.lay = cache->layout();
+    a.lay.kv_heads *= kv_share;
+    a.kv_share = kv_share;
     a.layer = layer;
     a.heads = heads;
-    a.group = group;
+    a.group = group / kv_share;
     a.tables = dev.tables;
     a.entries = dev.entries;
     a.items = dev.items;

@@ -103,6 +103,14 @@ def decode_gqa8(q8=False, sequences=16, length=4096):
     return DecodeWorkload(name, 64, 8, 128, [length] * sequences, blocks + 64, seed=6, q8=q8, context=1 << 17)
 
 
+def decode_gqa16(q8=False, sequences=16, length=4096):
+    """Llama-3.1-405B's attention shape (128 query heads over 8 KV heads,
+    d=128): sixteen query heads per KV head, run as two slices of eight."""
+    blocks = sequences * length // 16
+    name = "llama-3.1-405b-attn-decode-16x4096" + ("-q8_0" if q8 else "")
+    return DecodeWorkload(name, 128, 8, 128, [length] * sequences, blocks + 64, seed=9, q8=q8, context=1 << 17)
+
+
 def decode_tinyllama(q8=False, sequences=64, length=2048):
     """TinyLlama-1.1B's attention shape (32 query heads over 4 KV heads, d=64):
     eight query heads per KV head at head_dim 64."""
