@@ -685,7 +685,7 @@ def compact(r):
     for k in ("kernel_avg_us", "merge_avg_us"):
         if k in r["roofline"]:
             out["roofline"][k] = r["roofline"][k]
-    for k in ("latency_us", "reference_published"):
+    for k in ("latency_us", "reference_published", "decode_tokens_per_s", "model_decode_tokens_per_s"):
         if k in r:
             out[k] = r[k]
     if cpu:
