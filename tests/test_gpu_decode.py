@@ -135,11 +135,13 @@ def _single(device, oracle, heads, kv_heads, dim, tpb, length, seed, tail=False,
 
 
 # groups above eight (16: Llama-3.1-405B's 128 / 8 heads) run as slices of at
-# most eight heads, each a virtual KV head of the fast kernels
+# most eight heads, each a virtual KV head of the fast kernels; head_dim 256
+# (Gemma) gives a token a 16-lane row, up to four heads a slice
 @pytest.mark.parametrize("dim,kv_heads,group", [(64, 8, 1), (64, 8, 2), (64, 3, 3), (64, 2, 4), (64, 4, 8), (64, 2, 7),
                                                 (64, 3, 5), (128, 8, 4), (128, 2, 8), (128, 4, 5), (8, 1, 8), (32, 2, 2),
                                                 (16, 4, 1), (64, 2, 16), (128, 2, 16), (64, 1, 12), (128, 1, 10),
-                                                (64, 1, 32), (32, 2, 9)])
+                                                (64, 1, 32), (32, 2, 9), (256, 2, 2), (256, 1, 4), (256, 1, 3),
+                                                (256, 2, 8)])
 @pytest.mark.parametrize("length", [1, 15, 16, 17, 100, 1031])
 def test_shapes_and_gqa_ratios(device, oracle, dim, kv_heads, group, length):
     say("decode shape", dim, kv_heads, group, length)
@@ -150,7 +152,7 @@ def test_shapes_and_gqa_ratios(device, oracle, dim, kv_heads, group, length):
 # Q8_0 groups of 32 columns never straddle a head: head_dim is a multiple of 32
 Q8_SHAPES = [(64, 8, 1), (64, 8, 2), (64, 3, 3), (64, 2, 4), (64, 4, 8), (64, 2, 6), (64, 2, 7), (128, 8, 4),
              (128, 2, 8), (128, 4, 5), (128, 2, 6), (128, 3, 7), (32, 2, 2), (32, 1, 8), (64, 2, 16), (128, 2, 16),
-             (128, 1, 12)]
+             (128, 1, 12), (256, 2, 2)]
 
 
 @pytest.mark.parametrize("dim,kv_heads,group", Q8_SHAPES)

@@ -67,6 +67,18 @@ __device__ __forceinline__ float transpose_reduce<8>(const float (&v)[8], int c)
     return transpose_reduce<4>(r, c & 3);
 }
 
+// Sixteen-lane groups (a DPP row, head_dim 256): lane c pairs with 15 - c
+// (row_mirror), which holds the other half of columns, then the eight-lane
+// reduce finishes within each half-row.
+template <>
+__device__ __forceinline__ float transpose_reduce<16>(const float (&v)[16], int c) {
+    const bool b8 = (c & 8) != 0;
+    float r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (b8 ? v[i + 8] : v[i]) + dpp<0x140>(b8 ? v[i] : v[i + 8]);
+    return transpose_reduce<8>(r, c & 7);
+}
+
 // value of lane (token group base + h)
 template <int LPT>
 __device__ __forceinline__ float group_bcast(float v, int h, int lane);
@@ -89,6 +101,21 @@ __device__ __forceinline__ float group_bcast<8>(float v, int h, int) {
     const int b = __builtin_bit_cast(int, group_bcast<4>(v, h & 3, 0));
     if (h < 4) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, 0x114, 0xF, 0xA, false));
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, 0x104, 0xF, 0x5, false));
+}
+
+// Sixteen-lane groups: row_newbcast broadcasts lane h of every row
+template <>
+__device__ __forceinline__ float group_bcast<16>(float v, int h, int) {
+    switch (h) {
+        case 0: return dpp<0x150>(v);
+        case 1: return dpp<0x151>(v);
+        case 2: return dpp<0x152>(v);
+        case 3: return dpp<0x153>(v);
+        case 4: return dpp<0x154>(v);
+        case 5: return dpp<0x155>(v);
+        case 6: return dpp<0x156>(v);
+        default: return dpp<0x157>(v);
+    }
 }
 
 __device__ __forceinline__ float wave_max_across(float v, int from) {
@@ -218,7 +245,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             float v = acc[h][e];
-            v += dpp<0x128>(v);             // row_ror:8
+            if constexpr (LPT < 16) v += dpp<0x128>(v);  // row_ror:8
             if constexpr (LPT == 4) v += dpp<0x124>(v);  // row_ror:4
             acc[h][e] = v;
         }
@@ -1729,56 +1756,67 @@ bool q8_mma_shape(int group, int format, int head_dim) {
 // head_dim, so the queries and accumulators of a lane stay at 2 * G * D / 8.
 template <int D>
 bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, const WorkOrder& order, hipStream_t s) {
-    constexpr int LPT = D == 128 ? 8 : 4;
+    constexpr int LPT = D == 256 ? 16 : (D == 128 ? 8 : 4);
     const int G = a.group;
     if (G > 8) return false;
-    if constexpr (D != 32) {
-        if (a.lay.format != kF32) {
-            switch (q8_mma_heads(G, D)) {
-            case 1: launch_q8_mma<D, 1>(a, nitems, waves, s); return true;
-            case 2: launch_q8_mma<D, 2>(a, nitems, waves, s); return true;
-            case 3: launch_q8_mma<D, 3>(a, nitems, waves, s); return true;
-            case 4: launch_q8_mma<D, 4>(a, nitems, waves, s); return true;
-            default: break;
-            }
-        }
-    }
-    if (a.lay.format == kF32) {
+    if constexpr (D == 256) {  // f32 blocks, a token per DPP row, up to four query heads per KV head
+        if (a.lay.format != kF32) return false;
         switch (G) {
             case 1: launch_f32<D, 1, LPT>(a, nitems, waves, order, s); return true;
             case 2: launch_f32<D, 2, LPT>(a, nitems, waves, order, s); return true;
             case 3: launch_f32<D, 3, LPT>(a, nitems, waves, order, s); return true;
             case 4: launch_f32<D, 4, LPT>(a, nitems, waves, order, s); return true;
-            default: break;
+            default: return false;
         }
-        switch (G) {
-            case 5: launch_f32<D, 5, 8>(a, nitems, waves, order, s); return true;
-            case 6: launch_f32<D, 6, 8>(a, nitems, waves, order, s); return true;
-            case 7: launch_f32<D, 7, 8>(a, nitems, waves, order, s); return true;
-            case 8: launch_f32<D, 8, 8>(a, nitems, waves, order, s); return true;
-            default: break;
+    } else {
+        if constexpr (D != 32) {
+            if (a.lay.format != kF32) {
+                switch (q8_mma_heads(G, D)) {
+                case 1: launch_q8_mma<D, 1>(a, nitems, waves, s); return true;
+                case 2: launch_q8_mma<D, 2>(a, nitems, waves, s); return true;
+                case 3: launch_q8_mma<D, 3>(a, nitems, waves, s); return true;
+                case 4: launch_q8_mma<D, 4>(a, nitems, waves, s); return true;
+                default: break;
+                }
+            }
+        }
+        if (a.lay.format == kF32) {
+            switch (G) {
+                case 1: launch_f32<D, 1, LPT>(a, nitems, waves, order, s); return true;
+                case 2: launch_f32<D, 2, LPT>(a, nitems, waves, order, s); return true;
+                case 3: launch_f32<D, 3, LPT>(a, nitems, waves, order, s); return true;
+                case 4: launch_f32<D, 4, LPT>(a, nitems, waves, order, s); return true;
+                default: break;
+            }
+            switch (G) {
+                case 5: launch_f32<D, 5, 8>(a, nitems, waves, order, s); return true;
+                case 6: launch_f32<D, 6, 8>(a, nitems, waves, order, s); return true;
+                case 7: launch_f32<D, 7, 8>(a, nitems, waves, order, s); return true;
+                case 8: launch_f32<D, 8, 8>(a, nitems, waves, order, s); return true;
+                default: break;
+            }
+            return false;
+        }
+        if constexpr (D != 32) {
+            switch (G) {
+                case 1: launch_q8<D, 1>(a, nitems, waves, s); return true;
+                case 2: launch_q8<D, 2>(a, nitems, waves, s); return true;
+                case 3: launch_q8<D, 3>(a, nitems, waves, s); return true;
+                case 4: launch_q8<D, 4>(a, nitems, waves, s); return true;
+                default: break;
+            }
+        }
+        if constexpr (LPT == 8) {  // the vector kernel's head slots: D/16 lanes a token
+            switch (G) {
+                case 5: launch_q8<D, 5>(a, nitems, waves, s); return true;
+                case 6: launch_q8<D, 6>(a, nitems, waves, s); return true;
+                case 7: launch_q8<D, 7>(a, nitems, waves, s); return true;
+                case 8: launch_q8<D, 8>(a, nitems, waves, s); return true;
+                default: break;
+            }
         }
         return false;
     }
-    if constexpr (D != 32) {
-        switch (G) {
-            case 1: launch_q8<D, 1>(a, nitems, waves, s); return true;
-            case 2: launch_q8<D, 2>(a, nitems, waves, s); return true;
-            case 3: launch_q8<D, 3>(a, nitems, waves, s); return true;
-            case 4: launch_q8<D, 4>(a, nitems, waves, s); return true;
-            default: break;
-        }
-    }
-    if constexpr (LPT == 8) {  // the vector kernel's head slots: D/16 lanes a token
-        switch (G) {
-            case 5: launch_q8<D, 5>(a, nitems, waves, s); return true;
-            case 6: launch_q8<D, 6>(a, nitems, waves, s); return true;
-            case 7: launch_q8<D, 7>(a, nitems, waves, s); return true;
-            case 8: launch_q8<D, 8>(a, nitems, waves, s); return true;
-            default: break;
-        }
-    }
-    return false;
 }
 
 }  // namespace
@@ -1864,7 +1902,8 @@ bool decode_rows_shape(int kv_heads, int group, int format, int head_dim, int tp
 bool decode_fast_path(const DecodeArgs& a) {
     if (a.group > 8) return false;
     if (a.lay.format == kF32)
-        return decode_f32_blocks(a.lay.tpb) && (a.lay.head_dim == 32 || a.lay.head_dim == 64 || a.lay.head_dim == 128);
+        return decode_f32_blocks(a.lay.tpb) && (a.lay.head_dim == 32 || a.lay.head_dim == 64 ||
+                                                a.lay.head_dim == 128 || (a.lay.head_dim == 256 && a.group <= 4));
     return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128);
 }
 
@@ -1920,6 +1959,7 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
             const int waves = waves_for(b);
             done = b.lay.head_dim == 64    ? dispatch_fast<64>(b, nitems, waves, ord, s)
                    : b.lay.head_dim == 128 ? dispatch_fast<128>(b, nitems, waves, ord, s)
+                   : b.lay.head_dim == 256 ? dispatch_fast<256>(b, nitems, waves, ord, s)
                                            : dispatch_fast<32>(b, nitems, waves, ord, s);
         }
         if (!done) {

@@ -111,6 +111,14 @@ def decode_gqa16(q8=False, sequences=16, length=4096):
     return DecodeWorkload(name, 128, 8, 128, [length] * sequences, blocks + 64, seed=9, q8=q8, context=1 << 17)
 
 
+def decode_gemma2(sequences=16, length=4096):
+    """Gemma-2-9B's attention shape (16 query heads over 8 KV heads, d=256):
+    a token's 256 columns take a 16-lane row."""
+    blocks = sequences * length // 16
+    return DecodeWorkload("gemma-2-9b-attn-decode-16x4096", 16, 8, 256, [length] * sequences, blocks + 64, seed=10,
+                          context=1 << 17)
+
+
 def decode_tinyllama(q8=False, sequences=64, length=2048):
     """TinyLlama-1.1B's attention shape (32 query heads over 4 KV heads, d=64):
     eight query heads per KV head at head_dim 64."""
