@@ -708,7 +708,7 @@ def run_one(args, key):
     w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5,
          "gqa8": workloads.decode_gqa8, "gqa8q8": lambda: workloads.decode_gqa8(q8=True),
          "gqa16": workloads.decode_gqa16, "gqa16q8": lambda: workloads.decode_gqa16(q8=True),
-         "gemma2": workloads.decode_gemma2,
+         "gemma2": workloads.decode_gemma2, "phi3": workloads.decode_phi3,
          "tiny": workloads.decode_tinyllama, "tinyq8": lambda: workloads.decode_tinyllama(q8=True),
          "t176": workloads.decode_t176}[key]()
     return bench_decode(args, key, w)
@@ -720,7 +720,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2",
+                    choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2", "phi3",
                              "tiny", "tinyq8", "t176", "llama1b"],
                     help="one configuration; `all` (the default) runs c1, c3, c3cow, c4 and c5, one JSON line "
                          "each, then the c2 headline line last")

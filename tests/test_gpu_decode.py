@@ -135,13 +135,14 @@ def _single(device, oracle, heads, kv_heads, dim, tpb, length, seed, tail=False,
 
 
 # groups above eight (16: Llama-3.1-405B's 128 / 8 heads) run as slices of at
-# most eight heads, each a virtual KV head of the fast kernels; head_dim 256
-# (Gemma) gives a token a 16-lane row, up to four heads a slice
+# most eight heads, each a virtual KV head of the fast kernels; head_dims 80,
+# 96 and 256 (Phi-2, Phi-3, Gemma) run it with up to four heads a slice
 @pytest.mark.parametrize("dim,kv_heads,group", [(64, 8, 1), (64, 8, 2), (64, 3, 3), (64, 2, 4), (64, 4, 8), (64, 2, 7),
                                                 (64, 3, 5), (128, 8, 4), (128, 2, 8), (128, 4, 5), (8, 1, 8), (32, 2, 2),
                                                 (16, 4, 1), (64, 2, 16), (128, 2, 16), (64, 1, 12), (128, 1, 10),
                                                 (64, 1, 32), (32, 2, 9), (256, 2, 2), (256, 1, 4), (256, 1, 3),
-                                                (256, 2, 8)])
+                                                (256, 2, 8), (96, 4, 1), (96, 2, 3), (96, 1, 8), (80, 4, 1),
+                                                (80, 1, 4)])
 @pytest.mark.parametrize("length", [1, 15, 16, 17, 100, 1031])
 def test_shapes_and_gqa_ratios(device, oracle, dim, kv_heads, group, length):
     say("decode shape", dim, kv_heads, group, length)

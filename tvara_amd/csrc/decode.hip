@@ -1756,16 +1756,24 @@ bool q8_mma_shape(int group, int format, int head_dim) {
 // head_dim, so the queries and accumulators of a lane stay at 2 * G * D / 8.
 template <int D>
 bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, const WorkOrder& order, hipStream_t s) {
-    constexpr int LPT = D == 256 ? 16 : (D == 128 ? 8 : 4);
+    // head_dims 80, 96 and 256 (Phi-2, Phi-3, Gemma): f32 blocks and up to
+    // four query heads per KV head (three at 80), a token on 4, 8 or 16 lanes
+    constexpr bool kF32Only = D == 80 || D == 96 || D == 256;
+    constexpr int LPT = D == 256 ? 16 : (D == 128 || D == 96 ? 8 : 4);
     const int G = a.group;
     if (G > 8) return false;
-    if constexpr (D == 256) {  // f32 blocks, a token per DPP row, up to four query heads per KV head
+    if constexpr (kF32Only) {
         if (a.lay.format != kF32) return false;
         switch (G) {
             case 1: launch_f32<D, 1, LPT>(a, nitems, waves, order, s); return true;
             case 2: launch_f32<D, 2, LPT>(a, nitems, waves, order, s); return true;
             case 3: launch_f32<D, 3, LPT>(a, nitems, waves, order, s); return true;
-            case 4: launch_f32<D, 4, LPT>(a, nitems, waves, order, s); return true;
+            case 4:  // at head_dim 80 four heads' registers (four lanes a token) would spill
+                if constexpr (D != 80) {
+                    launch_f32<D, 4, LPT>(a, nitems, waves, order, s);
+                    return true;
+                }
+                return false;
             default: return false;
         }
     } else {
@@ -1902,8 +1910,10 @@ bool decode_rows_shape(int kv_heads, int group, int format, int head_dim, int tp
 bool decode_fast_path(const DecodeArgs& a) {
     if (a.group > 8) return false;
     if (a.lay.format == kF32)
-        return decode_f32_blocks(a.lay.tpb) && (a.lay.head_dim == 32 || a.lay.head_dim == 64 ||
-                                                a.lay.head_dim == 128 || (a.lay.head_dim == 256 && a.group <= 4));
+        return decode_f32_blocks(a.lay.tpb) &&
+               (a.lay.head_dim == 32 || a.lay.head_dim == 64 || a.lay.head_dim == 128 ||
+                ((a.lay.head_dim == 96 || a.lay.head_dim == 256) && a.group <= 4) ||
+                (a.lay.head_dim == 80 && a.group <= 3));
     return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128);
 }
 
@@ -1960,6 +1970,8 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
             done = b.lay.head_dim == 64    ? dispatch_fast<64>(b, nitems, waves, ord, s)
                    : b.lay.head_dim == 128 ? dispatch_fast<128>(b, nitems, waves, ord, s)
                    : b.lay.head_dim == 256 ? dispatch_fast<256>(b, nitems, waves, ord, s)
+                   : b.lay.head_dim == 96  ? dispatch_fast<96>(b, nitems, waves, ord, s)
+                   : b.lay.head_dim == 80  ? dispatch_fast<80>(b, nitems, waves, ord, s)
                                            : dispatch_fast<32>(b, nitems, waves, ord, s);
         }
         if (!done) {

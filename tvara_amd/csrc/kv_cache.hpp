@@ -125,8 +125,9 @@ struct AttnPlan {
     DeviceCache* cache = nullptr;
     uint64_t epoch = 0;
     int rows = 0, heads = 0, group = 0, items = 0, split_tokens = 0;
-    // query groups above eight (four at f32 head_dim 256) run as kv_share
-    // slices of group / kv_share heads, each a virtual KV head
+    // query groups above eight (f32 blocks: four at head_dims 96 and 256,
+    // three at 80) run as kv_share slices of group / kv_share heads, each a
+    // virtual KV head
     int kv_share = 1;
     int wave_splits = 0;  // > 0: splits per row = waves of one workgroup per (row, KV head)
     bool row_major = false;  // the launch runs decode_rows_kernel (one workgroup per item)

@@ -119,6 +119,13 @@ def decode_gemma2(sequences=16, length=4096):
                           context=1 << 17)
 
 
+def decode_phi3(sequences=16, length=4096):
+    """Phi-3-mini's attention shape (32 query and 32 KV heads, d=96)."""
+    blocks = sequences * length // 16
+    return DecodeWorkload("phi-3-mini-attn-decode-16x4096", 32, 32, 96, [length] * sequences, blocks + 64, seed=11,
+                          context=1 << 17)
+
+
 def decode_tinyllama(q8=False, sequences=64, length=2048):
     """TinyLlama-1.1B's attention shape (32 query heads over 4 KV heads, d=64):
     eight query heads per KV head at head_dim 64."""
