@@ -72,7 +72,7 @@ def build(device, oracle, heads, kv_heads, dim, specs, seed, tpb=16, q8=False):
 
 @pytest.mark.parametrize("fmt", ["f32", "q8_0"])
 @pytest.mark.parametrize("dim", [64, 128])
-@pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8, 10, 16])  # 10, 16: slices of 5 and 8 heads
 def test_bf16_small_shapes(device, oracle, group, dim, fmt):
     heads, kv_heads = 2 * group, 2
     specs = [(137, 100, 37), (64, 0, 64), (20, 3, 17)]
@@ -246,7 +246,7 @@ def test_chunk_invariant_under_future_tokens(device, precision, dim):
 @pytest.mark.parametrize("precision", ["bf16", "f32"])
 @pytest.mark.parametrize("fmt", ["f32", "q8_0"])
 @pytest.mark.parametrize("dim", [64, 128])
-@pytest.mark.parametrize("group", [1, 3, 4, 8])
+@pytest.mark.parametrize("group", [1, 3, 4, 8, 12])
 def test_zero_query_averages_every_visible_key(device, oracle, group, dim, fmt, precision):
     # With q = 0 every score is 0, every probability exp2(0) = 1 exactly, and
     # with V of integers (exact in bf16, Q8_0 and every f32 partial sum) each

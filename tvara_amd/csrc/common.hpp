@@ -135,6 +135,9 @@ struct PrefillArgs {
     int* err;
     int chunk_tiles;  // query tiles per (sequence, KV head) pair (set by the launcher)
     int pairs;        // sequences x KV heads
+    // as DecodeArgs::kv_share: lay.kv_heads and group describe kv_share
+    // virtual KV heads per KV head (GQA groups above eight)
+    int kv_share;
 };
 
 // launchers (kernels.hip)

@@ -697,9 +697,17 @@ void PrefillPlan::build(DeviceCache* c, const uint64_t* sequences, size_t n, siz
         epoch = rows_plan.epoch;
         return;
     }
-    if (!prefill_bf16_supported(c->layout(), group))
+    // groups above eight: slices of at most eight query heads, each a virtual
+    // KV head of the tile kernel
+    kv_share = 1;
+    if (group > 8) {
+        int slice = 8;
+        while (group % slice) --slice;
+        kv_share = group / slice;
+    }
+    if (!prefill_bf16_supported(c->layout(), group / kv_share))
         throw std::invalid_argument(
-            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, GQA group 1-8");
+            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB) and head_dim 64 or 128");
     std::vector<int32_t> tab;
     std::vector<int4> sq(n);
     size_t row0 = 0;
@@ -733,9 +741,11 @@ void PrefillPlan::launch(int layer, const float* q, float* out, hipStream_t s) {
     PrefillArgs a{};
     a.pool = cache->pool();
     a.lay = cache->layout();
+    a.lay.kv_heads *= kv_share;
+    a.kv_share = kv_share;
     a.layer = layer;
     a.heads = heads;
-    a.group = group;
+    a.group = group / kv_share;
     a.tables = static_cast<const int32_t*>(tables.ptr);
     a.seqs = static_cast<const int4*>(seqs.ptr);
     a.q = q;

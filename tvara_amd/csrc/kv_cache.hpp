@@ -205,6 +205,7 @@ struct PrefillPlan {
     DeviceCache* cache = nullptr;
     uint64_t epoch = 0;
     int heads = 0, group = 0, count = 0, max_rows = 0, precision = 0;
+    int kv_share = 1;  // bf16: GQA groups above eight run as slices (as AttnPlan)
     size_t total_rows = 0;
     AttnPlan rows_plan;
     DeviceBuffer tables, seqs, err;

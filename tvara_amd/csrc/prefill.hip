@@ -137,8 +137,9 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     // K/V rows are read through a buffer descriptor per block (base = the
     // block's K run of this layer and head, V one section further, 32-bit lane
     // offsets, reads bounded by the block's end)
-    const size_t kbytes = kQ8 ? static_cast<size_t>(a.layer) * 2 * a.lay.section + static_cast<size_t>(kh) * a.lay.head_bytes
-                              : (static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kh) * D) * sizeof(float);
+    const int kvh = kh / a.kv_share;  // the KV head whose K/V this (virtual) head reads
+    const size_t kbytes = kQ8 ? static_cast<size_t>(a.layer) * 2 * a.lay.section + static_cast<size_t>(kvh) * a.lay.head_bytes
+                              : (static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kvh) * D) * sizeof(float);
     const int vsec = static_cast<int>(kQ8 ? a.lay.section : 16 * static_cast<size_t>(kvw) * sizeof(float));
     const int brange = static_cast<int>(a.lay.stride - kbytes);
     // register stages of K/V rows in flight: two (even / odd tiles) at head_dim
@@ -433,7 +434,8 @@ bool prefill_bf16_supported(const BlockLayout& lay, int group) {
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     if (!prefill_bf16_supported(a.lay, a.group))
         throw std::invalid_argument(
-            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, GQA group 1-8");
+            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, and a GQA "
+            "slice of 1-8 heads");
     if (nseqs <= 0 || max_rows <= 0) return;
     switch (a.group) {
         case 1: launch_g<1>(a, nseqs, max_rows, s); break;
