@@ -153,7 +153,7 @@ def test_shapes_and_gqa_ratios(device, oracle, dim, kv_heads, group, length):
 # Q8_0 groups of 32 columns never straddle a head: head_dim is a multiple of 32
 Q8_SHAPES = [(64, 8, 1), (64, 8, 2), (64, 3, 3), (64, 2, 4), (64, 4, 8), (64, 2, 6), (64, 2, 7), (128, 8, 4),
              (128, 2, 8), (128, 4, 5), (128, 2, 6), (128, 3, 7), (32, 2, 2), (32, 1, 8), (64, 2, 16), (128, 2, 16),
-             (128, 1, 12), (256, 2, 2)]
+             (128, 1, 12), (256, 2, 2), (256, 1, 4), (256, 2, 8)]
 
 
 @pytest.mark.parametrize("dim,kv_heads,group", Q8_SHAPES)

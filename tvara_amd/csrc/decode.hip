@@ -1756,14 +1756,28 @@ bool q8_mma_shape(int group, int format, int head_dim) {
 // head_dim, so the queries and accumulators of a lane stay at 2 * G * D / 8.
 template <int D>
 bool dispatch_fast(const DecodeArgs& a, int nitems, int waves, const WorkOrder& order, hipStream_t s) {
-    // head_dims 80, 96 and 256 (Phi-2, Phi-3, Gemma): f32 blocks and up to
-    // four query heads per KV head (three at 80), a token on 4, 8 or 16 lanes
+    // head_dims 80, 96 and 256 (Phi-2, Phi-3, Gemma): f32 blocks (and Q8_0 at
+    // 256) and up to four query heads per KV head (three at 80), a token on
+    // 4, 8 or 16 lanes
     constexpr bool kF32Only = D == 80 || D == 96 || D == 256;
     constexpr int LPT = D == 256 ? 16 : (D == 128 || D == 96 ? 8 : 4);
     const int G = a.group;
     if (G > 8) return false;
     if constexpr (kF32Only) {
-        if (a.lay.format != kF32) return false;
+        if (a.lay.format != kF32) {
+            // Q8_0 (head_dim a multiple of 32): the vector kernel, a token on
+            // D/16 = 16 lanes at 256
+            if constexpr (D == 256) {
+                switch (G) {
+                    case 1: launch_q8<D, 1>(a, nitems, waves, s); return true;
+                    case 2: launch_q8<D, 2>(a, nitems, waves, s); return true;
+                    case 3: launch_q8<D, 3>(a, nitems, waves, s); return true;
+                    case 4: launch_q8<D, 4>(a, nitems, waves, s); return true;
+                    default: break;
+                }
+            }
+            return false;
+        }
         switch (G) {
             case 1: launch_f32<D, 1, LPT>(a, nitems, waves, order, s); return true;
             case 2: launch_f32<D, 2, LPT>(a, nitems, waves, order, s); return true;
@@ -1914,7 +1928,7 @@ bool decode_fast_path(const DecodeArgs& a) {
                (a.lay.head_dim == 32 || a.lay.head_dim == 64 || a.lay.head_dim == 128 ||
                 ((a.lay.head_dim == 96 || a.lay.head_dim == 256) && a.group <= 4) ||
                 (a.lay.head_dim == 80 && a.group <= 3));
-    return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128);
+    return a.lay.tpb == 16 && (a.lay.head_dim == 64 || a.lay.head_dim == 128 || (a.lay.head_dim == 256 && a.group <= 4));
 }
 
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,

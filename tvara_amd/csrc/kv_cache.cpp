@@ -326,11 +326,11 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     for (uint8_t t : tail_rows) with_tail |= t != 0;
     const Geometry& g = c->geometry();
     group = static_cast<int>(heads / g.kv_heads);
-    // slices of at most eight query heads (f32 blocks at head_dims 96 and
-    // 256: four, at 80: three, what the fast kernel takes there)
+    // slices of at most eight query heads (head_dim 256 and f32 blocks at 96:
+    // four, at 80: three, what the fast kernels take there)
     kv_share = 1;
     int max_slice = 8;
-    if (c->format() == kF32 && (g.head_dim == 96 || g.head_dim == 256)) max_slice = 4;
+    if ((c->format() == kF32 && g.head_dim == 96) || g.head_dim == 256) max_slice = 4;
     if (c->format() == kF32 && g.head_dim == 80) max_slice = 3;
     if (group > max_slice) {
         int slice = max_slice;
