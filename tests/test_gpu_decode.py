@@ -200,6 +200,38 @@ def test_c5_q8_full_batch(device, oracle):
             say("row", i, "vs dequantised", refmath.max_rel(got[i], want), "vs f32", refmath.max_rel(got[i], orig))
 
 
+@pytest.mark.parametrize("make", [workloads.decode_gqa16, lambda: workloads.decode_gqa16(q8=True),
+                                  workloads.decode_gemma2, workloads.decode_phi3],
+                         ids=["gqa16-f32", "gqa16-q8_0", "gemma2-d256", "phi3-d96"])
+def test_wide_shapes_full_batch(device, oracle, make):
+    # the 16 x 4,096-token batches of the shapes the fast kernels take by
+    # slicing (Llama-3.1-405B's sixteen query heads per KV head) or by wider
+    # token groups (head_dim 256 and 96): every row against the oracle (Q8_0:
+    # on the dequantised values)
+    w = make()
+    say("decode", w.name)
+    fmt = device.Q8_0 if w.q8 else device.F32
+    dev = device.PagedCache(1, w.kv_heads, w.head_dim, 16, w.pool_blocks, fmt=fmt)
+    seqs = workloads.fill_decode(dev, w)
+    q = w.queries()
+    got = attention.decode_batch(dev, q, seqs, 0, w.heads, w.context)
+
+    def row(i):  # the oracle's calls release the GIL: rows run in threads
+        k, v = w.keys(i), w.values(i)
+        n = len(k)
+        if w.q8:
+            k = oracle.dequantize_q8_0(oracle.quantize_q8_0(k)).reshape(n, -1)
+            v = oracle.dequantize_q8_0(oracle.quantize_q8_0(v)).reshape(n, -1)
+        ref = oracle.Cache(1, w.kv_heads, w.head_dim, 16, n // 16 + 1)
+        s = ref.create_sequence()
+        ref.append_many(s, k, v)
+        return ref.fused_paged_attention(q[i], s, 0, w.heads, w.context)
+
+    with ThreadPoolExecutor(max_workers=8) as pool:
+        for i, want in enumerate(pool.map(row, range(w.sequences))):
+            assert refmath.close(got[i], want, TOL), (i, refmath.max_rel(got[i], want))
+
+
 @pytest.mark.parametrize("tpb", [7, 5, 4, 32, 1])
 def test_block_sizes(device, oracle, tpb):
     # block sizes that do not divide the length (prefill_t171.cpp, prefill_t180.cpp)
