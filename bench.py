@@ -27,6 +27,13 @@ built from its sources) timed on this host: one warm-up, then the median of
 nine runs, on one thread and on every host thread the box grants, with the
 host's CPU model, core count, compiler, flags, AVX2 use and a STREAM-style
 triad bandwidth.
+
+Other shapes, one line each with --workload: c4d128 and c4q8 (the chunks at
+head_dim 128 and over Q8_0 blocks), gqa8 / gqa8q8 (Llama-3-70B, eight query
+heads per KV head), gqa16 / gqa16q8 (Llama-3.1-405B, sixteen, run as two
+slices), tiny / tinyq8 (TinyLlama-1.1B), gemma2 (head_dim 256), phi3
+(head_dim 96) and llama1b (a Llama-3.2-1B-shaped model through the
+model-level C ABI).
 """
 
 from __future__ import annotations
