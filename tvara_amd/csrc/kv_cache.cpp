@@ -343,9 +343,7 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     std::map<uint64_t, int32_t> offset;
     std::vector<int32_t>& tab = h_tables;
     tab.clear();
-    size_t total = 0;
     for (size_t r = 0; r < seq_of_row.size(); ++r) {
-        total += cached[r];
         if (offset.count(seq_of_row[r])) continue;
         offset[seq_of_row[r]] = static_cast<int32_t>(tab.size());
         for (const Handle& b : c->sequence(seq_of_row[r]).blocks) tab.push_back(static_cast<int32_t>(b.id));

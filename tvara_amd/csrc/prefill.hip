@@ -157,7 +157,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 #pragma unroll
         for (int p = 0; p < SP; ++p) b[p] = tab[min(kt * kKeys + KPP * p + wkey, kmax - 1) >> 4];
     };
-    auto gload = [&](int kt, const int (&b)[SP], f32x4 (&kreg)[SP], f32x4 (&vreg)[SP]) {
+    // the tile's rows, from the block ids tabload put in b
+    auto gload = [&](const int (&b)[SP], f32x4 (&kreg)[SP], f32x4 (&vreg)[SP]) {
 #pragma unroll
         for (int p = 0; p < SP; ++p) {
             const char* blk =
@@ -337,21 +338,21 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     auto tile = [&](int t) { return min(t, ntiles - 1); };
     if constexpr (kStages == 2) {
         tabload(0, bA);
-        gload(0, bA, kA, vA);
+        gload(bA, kA, vA);
         tabload(tile(1), bB);
-        gload(tile(1), bB, kB, vB);
+        gload(bB, kB, vB);
         tabload(tile(2), bA);
         tabload(tile(3), bB);
         lstore(0, 0, kA, vA);
         __syncthreads();
         for (int kt = 0; kt < ntiles; kt += 2) {
-            gload(tile(kt + 2), bA, kA, vA);
+            gload(bA, kA, vA);
             tabload(tile(kt + 4), bA);
             compute(kt, 0);
             lstore(tile(kt + 1), 1, kB, vB);
             __syncthreads();
             if (kt + 1 >= ntiles) break;
-            gload(tile(kt + 3), bB, kB, vB);
+            gload(bB, kB, vB);
             tabload(tile(kt + 5), bB);
             compute(kt + 1, 1);
             lstore(tile(kt + 2), 0, kA, vA);
@@ -360,12 +361,12 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     } else {
         // one register stage: tile t + 1 is requested before tile t's products
         tabload(0, bA);
-        gload(0, bA, kA, vA);
+        gload(bA, kA, vA);
         tabload(tile(1), bA);
         lstore(0, 0, kA, vA);
         __syncthreads();
         for (int kt = 0; kt < ntiles; ++kt) {
-            gload(tile(kt + 1), bA, kA, vA);
+            gload(bA, kA, vA);
             tabload(tile(kt + 2), bA);
             compute(kt, kt & 1);
             lstore(tile(kt + 1), (kt + 1) & 1, kA, vA);
