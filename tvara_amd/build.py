@@ -31,6 +31,7 @@ FLAGS = [
     "-fPIC",
     "-fvisibility=hidden",
     "-Wall",
+    "-Wextra",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}",
