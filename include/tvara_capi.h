@@ -276,8 +276,9 @@ TVARA_API int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences
  * after the other, f32 [sum rows][heads * head_dim]; out likewise.
  * precision TVARA_ATTN_F32 keeps the reference's semantics; TVARA_ATTN_BF16
  * runs the causal tiles on MFMA with bf16 operands and f32 accumulation (f32 or
- * Q8_0 blocks of 16 tokens and head_dim 64 or 128, any number of query heads
- * per KV head; other shapes fail with TVARA_INVALID). */
+ * Q8_0 blocks of a power of two from 16 to 1,024 tokens and head_dim 64 or
+ * 128, any number of query heads per KV head; other shapes fail with
+ * TVARA_INVALID). */
 TVARA_API int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t layer,
                                  size_t heads, size_t context, const size_t* start, const size_t* rows,
                                  const float* queries, float* out, int precision, int device_ptrs);

@@ -89,6 +89,29 @@ def test_bf16_small_shapes(device, oracle, group, dim, fmt):
     assert ok, err
 
 
+@pytest.mark.parametrize("fmt", ["f32", "q8_0"])
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("tpb", [32, 64, 128, 1024])
+def test_bf16_block_sizes(device, oracle, tpb, dim, fmt):
+    """Blocks above 16 tokens: a 64-key tile lies inside one block (tpb >= 64)
+    or spans several (32); at 128 and 1,024 a block holds several tiles, so a
+    key's slot depends on the tile index as well as its row."""
+    heads, kv_heads = 8, 2
+    specs = [(1100, 900, 200), (300, 0, 300), (20, 3, 17)]
+    say("prefill bf16 tpb", tpb, "dim", dim, fmt)
+    dev, ref, ds, rs, qs = build(device, oracle, heads, kv_heads, dim, specs, seed=tpb + dim, tpb=tpb,
+                                 q8=fmt == "q8_0")
+    starts = [s for _, s, _ in specs]
+    counts = [r for _, _, r in specs]
+    got = attention.prefill_batch(dev, np.concatenate(qs), ds, starts, counts, 0, heads, 4096, precision="bf16")
+    f32 = attention.prefill_batch(dev, np.concatenate(qs), ds, starts, counts, 0, heads, 4096, precision="f32")
+    want = np.concatenate([ref.fused_prompt_attention(q, s, 0, st, c, heads, 4096).reshape(c, -1)
+                           for q, s, st, c in zip(qs, rs, starts, counts)])
+    assert refmath.close(f32, want, TOL_F32), refmath.max_rel(f32, want)
+    ok, err = bf16_ok(got, want, SHORT_ROWS)
+    assert ok, err
+
+
 @pytest.mark.parametrize("make,fmt", [(workloads.prefill_c4, "f32"), (workloads.prefill_8b, "f32"),
                                       (workloads.prefill_c4, "q8_0")], ids=["d64", "d128", "d64-q8_0"])
 def test_bf16_c4_shape(device, oracle, make, fmt):
@@ -219,6 +242,15 @@ def test_bf16_rejections(device):
         attention.prefill_batch(dev, q, [s], [10], [4], 0, 4, 64, precision="bf16")
     with pytest.raises(device.InvalidArgument):  # chunk past the cached tokens
         attention.prefill_batch(dev, q, [s], [18], [4], 0, 4, 64, precision="bf16")
+    q[1, 3] = 0.0
+    for tpb in (8, 24):  # bf16 tile kernels take power-of-two blocks of 16 to 1,024 tokens
+        dev = device.PagedCache(1, 2, 64, tpb, 8)
+        s = dev.create_sequence()
+        dev.append_many(s, x, x)
+        with pytest.raises(device.InvalidArgument):
+            attention.prefill_batch(dev, q, [s], [10], [4], 0, 4, 64, precision="bf16")
+        f32 = attention.prefill_batch(dev, q, [s], [10], [4], 0, 4, 64, precision="f32")
+        assert np.all(np.isfinite(f32))
 
 
 @pytest.mark.parametrize("precision", ["bf16", "f32"])

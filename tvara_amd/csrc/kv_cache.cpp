@@ -705,7 +705,8 @@ void PrefillPlan::build(DeviceCache* c, const uint64_t* sequences, size_t n, siz
     }
     if (!prefill_bf16_supported(c->layout(), group / kv_share))
         throw std::invalid_argument(
-            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB) and head_dim 64 or 128");
+            "bf16 prefill needs f32 or Q8_0 blocks of 16 to 1,024 tokens (a power of two, under 2 GiB) and head_dim "
+            "64 or 128");
     std::vector<int32_t> tab;
     std::vector<int4> sq(n);
     size_t row0 = 0;

@@ -4,9 +4,10 @@
 //
 // A workgroup takes 8 waves x 32 query rows of one (sequence, KV head); a row
 // is one (chunk position, query head of the GQA group), so the G heads that
-// share a KV head share every K/V tile.  Key tiles of 64 positions (4 paged
-// blocks) are read from the f32 pool by the first four waves, rounded to bf16
-// and staged in double-buffered LDS: K as [key][d], V transposed as [d][key].
+// share a KV head share every K/V tile.  Key tiles of 64 positions (four
+// blocks of 16 tokens, two of 32, or part of one larger block) are read from
+// the pool (f32 or Q8_0) by all the waves, rounded to bf16 and staged in
+// double-buffered LDS: K as [key][d], V transposed as [d][key].
 //
 // Each wave computes S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A = K from
 // LDS, B = Q^T held in registers), so the score of row r and key k sits in the
@@ -59,7 +60,9 @@ constexpr int kBufferWord3 = 0x00020000;
 
 // kQ8: Q8_0 blocks (the head's int8 plane and fp16 group scales), dequantised
 // to bf16 when staged; otherwise f32 blocks.
-template <int D, int G, int kWaves, bool kQ8>
+// TPB: 16 for blocks of 16 tokens (block arithmetic folded at compile time),
+// 0 for any power of two from 16 to 1,024 read from the layout
+template <int D, int G, int kWaves, bool kQ8, int TPB>
 __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const PrefillArgs a) {
     constexpr int PW = kRows / G;        // chunk positions per wave; rows PW*G .. 31 are padding (G = 3, 5, 6, 7)
     constexpr int QT = kWaves * PW;      // chunk positions per workgroup
@@ -124,23 +127,26 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     // before issuing its loads.
     const int skey = tid / LPR, col = 4 * (tid % LPR);
     const int wkey = __builtin_amdgcn_readfirstlane(skey);  // the wave's first row in a pass
-    // byte offset within the block's K (or V) run of this head of the lane's
-    // four columns (f32, or Q8_0 int8) and, for Q8_0, of their group's scale
-    auto roff = [&](int p) {
-        const int slot = (KPP * p + skey) & 15;
-        return static_cast<unsigned>(kQ8 ? slot * D + col : (slot * kvw + col) * static_cast<int>(sizeof(float)));
-    };
-    auto soff = [&](int p) {
-        const int slot = (KPP * p + skey) & 15;
-        return static_cast<unsigned>(16 * D + (slot * (D / 32) + col / 32) * 2);
-    };
+    // Blocks hold tpb = 2^tsh tokens (16 to 1,024).  The pass start
+    // kt * 64 + KPP * p is a multiple of KPP (a power of two) and skey < KPP,
+    // so key kt * 64 + KPP * p + skey sits in slot
+    // ((kt * 64 + KPP * p) & (tpb - 1)) + (skey & (tpb - 1)) of its block: the
+    // first term is wave-uniform and goes into the loads' scalar offsets, the
+    // second gives the loop-invariant lane offsets roff (the lane's four
+    // columns within the block's K or V run of this head: f32, or Q8_0 int8)
+    // and soff (Q8_0: their group's scale).
+    const int tpb = TPB ? TPB : a.lay.tpb, tsh = __builtin_ctz(static_cast<unsigned>(tpb));
+    const int lslot = skey & (tpb - 1);
+    const unsigned roff =
+        static_cast<unsigned>(kQ8 ? lslot * D + col : (lslot * kvw + col) * static_cast<int>(sizeof(float)));
+    const unsigned soff = static_cast<unsigned>(tpb * D + (lslot * (D / 32) + col / 32) * 2);
     // K/V rows are read through a buffer descriptor per block (base = the
     // block's K run of this layer and head, V one section further, 32-bit lane
     // offsets, reads bounded by the block's end)
     const int kvh = kh / a.kv_share;  // the KV head whose K/V this (virtual) head reads
     const size_t kbytes = kQ8 ? static_cast<size_t>(a.layer) * 2 * a.lay.section + static_cast<size_t>(kvh) * a.lay.head_bytes
-                              : (static_cast<size_t>(a.layer) * 2 * 16 * kvw + static_cast<size_t>(kvh) * D) * sizeof(float);
-    const int vsec = static_cast<int>(kQ8 ? a.lay.section : 16 * static_cast<size_t>(kvw) * sizeof(float));
+                              : (static_cast<size_t>(a.layer) * 2 * tpb * kvw + static_cast<size_t>(kvh) * D) * sizeof(float);
+    const int vsec = static_cast<int>(kQ8 ? a.lay.section : static_cast<size_t>(tpb) * kvw * sizeof(float));
     const int brange = static_cast<int>(a.lay.stride - kbytes);
     // register stages of K/V rows in flight: two (even / odd tiles) at head_dim
     // 64, one at 128, where two would not fit beside the accumulators
@@ -155,26 +161,28 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     // when staged, so a non-finite value there cannot reach a row as 0 * NaN.
     auto tabload = [&](int kt, int (&b)[SP]) {
 #pragma unroll
-        for (int p = 0; p < SP; ++p) b[p] = tab[min(kt * kKeys + KPP * p + wkey, kmax - 1) >> 4];
+        for (int p = 0; p < SP; ++p) b[p] = tab[min(kt * kKeys + KPP * p + wkey, kmax - 1) >> tsh];
     };
-    // the tile's rows, from the block ids tabload put in b
-    auto gload = [&](const int (&b)[SP], f32x4 (&kreg)[SP], f32x4 (&vreg)[SP]) {
+    // tile kt's rows, from the block ids tabload put in b
+    auto gload = [&](int kt, const int (&b)[SP], f32x4 (&kreg)[SP], f32x4 (&vreg)[SP]) {
 #pragma unroll
         for (int p = 0; p < SP; ++p) {
+            const int base = (kt * kKeys + KPP * p) & (tpb - 1);  // the pass's first slot in its block
+            const int rso = base * (kQ8 ? D : kvw * static_cast<int>(sizeof(float))), sso = base * (D / 32) * 2;
             const char* blk =
                 a.pool + static_cast<size_t>(__builtin_amdgcn_readfirstlane(b[p])) * a.lay.stride + kbytes;
             const __amdgpu_buffer_rsrc_t r =
                 __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(blk), 0, brange, kBufferWord3);
             if constexpr (kQ8) {  // four int8 and their scale's bits, dequantised when staged
-                const unsigned kq = __builtin_amdgcn_raw_buffer_load_b32(r, roff(p), 0, 0);
-                const unsigned ks = __builtin_amdgcn_raw_buffer_load_b16(r, soff(p), 0, 0);
-                const unsigned vq = __builtin_amdgcn_raw_buffer_load_b32(r, roff(p), vsec, 0);
-                const unsigned vs = __builtin_amdgcn_raw_buffer_load_b16(r, soff(p), vsec, 0);
+                const unsigned kq = __builtin_amdgcn_raw_buffer_load_b32(r, roff, rso, 0);
+                const unsigned ks = __builtin_amdgcn_raw_buffer_load_b16(r, soff, sso, 0);
+                const unsigned vq = __builtin_amdgcn_raw_buffer_load_b32(r, roff, vsec + rso, 0);
+                const unsigned vs = __builtin_amdgcn_raw_buffer_load_b16(r, soff, vsec + sso, 0);
                 kreg[p] = f32x4{__builtin_bit_cast(float, kq), __builtin_bit_cast(float, ks), 0.f, 0.f};
                 vreg[p] = f32x4{__builtin_bit_cast(float, vq), __builtin_bit_cast(float, vs), 0.f, 0.f};
             } else {
-                kreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff(p), 0, 0);
-                vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff(p), vsec, 0);
+                kreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff, rso, 0);
+                vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff, vsec + rso, 0);
             }
         }
     };
@@ -338,21 +346,21 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     auto tile = [&](int t) { return min(t, ntiles - 1); };
     if constexpr (kStages == 2) {
         tabload(0, bA);
-        gload(bA, kA, vA);
+        gload(0, bA, kA, vA);
         tabload(tile(1), bB);
-        gload(bB, kB, vB);
+        gload(tile(1), bB, kB, vB);
         tabload(tile(2), bA);
         tabload(tile(3), bB);
         lstore(0, 0, kA, vA);
         __syncthreads();
         for (int kt = 0; kt < ntiles; kt += 2) {
-            gload(bA, kA, vA);
+            gload(tile(kt + 2), bA, kA, vA);
             tabload(tile(kt + 4), bA);
             compute(kt, 0);
             lstore(tile(kt + 1), 1, kB, vB);
             __syncthreads();
             if (kt + 1 >= ntiles) break;
-            gload(bB, kB, vB);
+            gload(tile(kt + 3), bB, kB, vB);
             tabload(tile(kt + 5), bB);
             compute(kt + 1, 1);
             lstore(tile(kt + 2), 0, kA, vA);
@@ -361,12 +369,12 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     } else {
         // one register stage: tile t + 1 is requested before tile t's products
         tabload(0, bA);
-        gload(bA, kA, vA);
+        gload(0, bA, kA, vA);
         tabload(tile(1), bA);
         lstore(0, 0, kA, vA);
         __syncthreads();
         for (int kt = 0; kt < ntiles; ++kt) {
-            gload(bA, kA, vA);
+            gload(tile(kt + 1), bA, kA, vA);
             tabload(tile(kt + 2), bA);
             compute(kt, kt & 1);
             lstore(tile(kt + 1), (kt + 1) & 1, kA, vA);
@@ -396,7 +404,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 // eight waves per workgroup (measured on MI355X against four: 158 against 225
 // us on the 8 x (2,048 + 512) chunk; K/V tiles are re-read by half as many
 // workgroups) and 64-key tiles (128-key tiles measured 177 us)
-template <int D, int G, int W>
+template <int D, int G, int W, int TPB>
 void launch_gw(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     const bool q8 = a.lay.format == kQ8;
     constexpr int QT = W * (kRows / G);
@@ -406,37 +414,45 @@ void launch_gw(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     const int groups8 = (b.pairs + 7) / 8;  // ids = 8 XCDs x pair groups x chunk tiles
     const dim3 grid(8 * groups8 * b.chunk_tiles), block(64 * W);
     if (q8)
-        launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W, true>, grid, block, 0, s, b);
+        launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W, true, TPB>, grid, block, 0, s, b);
     else
-        launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W, false>, grid, block, 0, s, b);
+        launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W, false, TPB>, grid, block, 0, s, b);
 }
 
-// waves per workgroup (TVARA_PREFILL_WAVES: 4 or 8)
+// waves per workgroup (TVARA_PREFILL_WAVES: 4 or 8, for blocks of 16 tokens;
+// other block sizes take 8)
 template <int G>
 void launch_g(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     static const int waves = [] {
         const char* env = std::getenv("TVARA_PREFILL_WAVES");
         return env && std::atoi(env) == 4 ? 4 : 8;
     }();
-    if (a.lay.head_dim == 128)
-        waves == 4 ? launch_gw<128, G, 4>(a, nseqs, max_rows, s) : launch_gw<128, G, 8>(a, nseqs, max_rows, s);
-    else
-        waves == 4 ? launch_gw<64, G, 4>(a, nseqs, max_rows, s) : launch_gw<64, G, 8>(a, nseqs, max_rows, s);
+    if (a.lay.tpb != 16) {
+        if (a.lay.head_dim == 128)
+            launch_gw<128, G, 8, 0>(a, nseqs, max_rows, s);
+        else
+            launch_gw<64, G, 8, 0>(a, nseqs, max_rows, s);
+    } else if (a.lay.head_dim == 128) {
+        waves == 4 ? launch_gw<128, G, 4, 16>(a, nseqs, max_rows, s) : launch_gw<128, G, 8, 16>(a, nseqs, max_rows, s);
+    } else {
+        waves == 4 ? launch_gw<64, G, 4, 16>(a, nseqs, max_rows, s) : launch_gw<64, G, 8, 16>(a, nseqs, max_rows, s);
+    }
 }
 
 }  // namespace
 
 bool prefill_bf16_supported(const BlockLayout& lay, int group) {
     // the staging reads take 32-bit offsets within a block
-    return (lay.format == kF32 || lay.format == kQ8) && lay.tpb == 16 && (lay.head_dim == 64 || lay.head_dim == 128) &&
+    return (lay.format == kF32 || lay.format == kQ8) && decode_f32_blocks(lay.tpb) &&
+           (lay.head_dim == 64 || lay.head_dim == 128) &&
            lay.stride < (size_t(1) << 31) && group >= 1 && group <= 8;
 }
 
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     if (!prefill_bf16_supported(a.lay, a.group))
         throw std::invalid_argument(
-            "bf16 prefill needs f32 or Q8_0 blocks of 16 tokens (under 2 GiB), head_dim 64 or 128, and a GQA "
-            "slice of 1-8 heads");
+            "bf16 prefill needs f32 or Q8_0 blocks of 16 to 1,024 tokens (a power of two, under 2 GiB), "
+            "head_dim 64 or 128, and a GQA slice of 1-8 heads");
     if (nseqs <= 0 || max_rows <= 0) return;
     switch (a.group) {
         case 1: launch_g<1>(a, nseqs, max_rows, s); break;
