@@ -7,6 +7,8 @@
 // float one at a time are written with __fmul_rn / __fsub_rn / __fadd_rn so
 // the compiler does not contract them into FMAs; dot products and the RMS sum
 // accumulate in double and round once, as quant::dot_f32 and rms_norm do.
+#include <algorithm>
+
 #include "model.hpp"
 #include "q8.hpp"
 #include "device_util.hpp"
@@ -593,139 +595,144 @@ struct Q8BatchArgs {
     float* out;  // [gridDim.y][n_total][rows]
 };
 
-template <int RT, int CH>
-struct TilesChunk {
-    uint4 q[RT][CH / 2], d[RT][CH / 2];  // per group pair
-};
-
-template <int RT, int CH>
-__device__ __forceinline__ TilesChunk<RT, CH> q8_load_tiles(const Q8BatchArgs& a, int gbeg, int gend, int chunk,
-                                                            const int (&tile)[RT], int lane) {
-    TilesChunk<RT, CH> t;
-    const int plast = (gend - 1) / 2;
-#pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-        for (int c = 0; c < CH / 2; ++c) {
-            const int p = min((gbeg + chunk * CH) / 2 + c, plast);
-            const size_t blk = static_cast<size_t>(tile[r]) * a.pairs + p;
-            t.q[r][c] = a.q[blk * 64 + lane];
-            t.d[r][c] = *reinterpret_cast<const uint4*>(a.d + (blk * 16 + 4 * (lane >> 4)) * 2);
-        }
-    return t;
-}
-
-// the halves of chunk `chunk` (clamped) into hb[BPT]: element e of a chunk is
-// ((c*NT + vt)*2 + part)*64 + l, thread t takes e = t, t + 256, ...
-#define Q8_LOAD_HALVES(chunk)                                                                                       \
-    _Pragma("unroll") for (int i = 0; i < BPT; ++i) {                                                               \
-        const int e = threadIdx.x + 256 * i;                                                                        \
-        const int l = e & 63, part = (e >> 6) & 1, vt = (e >> 7) % NT, c = (e >> 7) / NT;                          \
-        const int g = min(gbeg + (chunk) * CH + c, gend - 1);                                                      \
-        hb[i] = reinterpret_cast<const u32x4*>(a.halves)[((static_cast<size_t>(a.vt0 + vt) * a.groups + g) * 2 + part) * \
-                                                         64 + l];                                                   \
-    }
-
-// A workgroup of four waves covers 4*RT row tiles and up to NT vector tiles
-// of 16 over a share of the groups; each wave owns RT row tiles.  K advances
-// in chunks of CH groups.  While chunk c is multiplied, the loads of chunk
-// c+1 are in flight: its halves into registers (written to the other LDS
-// buffer afterwards, one barrier per chunk) and its int8 tiles and scales
-// straight from HBM into registers.  The prefetch is unconditional (the last
-// chunk re-reads itself) so the compiler keeps it ahead of the arithmetic.
-template <int RT, int NT>
+// A workgroup of NT waves covers four row tiles (64 rows) over a share of the
+// groups; wave w owns vector tile w (16 vectors).  The operands are taken as
+// C^T = X W^T: A = the wave's fp16 activation halves (registers, straight
+// from global memory), B = the row tiles' int8 weights, converted to fp16 once
+// per workgroup and shared through LDS, so lane l accumulates weight row l%16
+// of each tile for vectors 4(l/16) + i and needs one scale per tile and
+// group.  K advances in chunks of two group pairs: the int8 tiles and scales
+// of chunk c + 2 are requested while chunk c is multiplied (two register
+// sets), staged into the other LDS buffer after it (one barrier per chunk);
+// the activations of chunk c + 1 are requested after chunk c's barrier.
+// Prefetches are unconditional (clamped to the last chunk) so that the
+// compiler keeps them ahead of the arithmetic.
+template <int NT>
 __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
-    constexpr int CH = 4;
-    constexpr int BU = CH * NT * 2 * 64;  // uint4 of halves per chunk
-    constexpr int BPT = BU / 256;
-    __shared__ u32x4 bs[2][BU];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int G = a.groups;
-    const int gbeg = blockIdx.y * a.groups_per_split;
-    const int gend = min(G, gbeg + a.groups_per_split);
-    const int nchunks = (gend - gbeg + CH - 1) / CH;
-    int tile[RT];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) tile[r] = min((static_cast<int>(blockIdx.x) * 4 + wave) * RT + r, a.tiles - 1);
+    constexpr int RT = 4, P = 2, CG = 2 * P;         // row tiles, pairs and groups per chunk
+    constexpr int NTH = 64 * NT;
+    constexpr int RAW = RT * P * 64;                 // uint4 of int8 per chunk
+    constexpr int WPT = (RAW + NTH - 1) / NTH;       // per thread
+    constexpr int DW = RT * P * 16;                  // scale dwords per chunk (16 rows x 2 groups each)
+    constexpr int DPT = (DW + NTH - 1) / NTH;        // per thread
+    __shared__ half8 ws[2][CG][RT][64];
+    __shared__ uint32_t wd[2][RT][P][16];
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+    const int gbeg = static_cast<int>(blockIdx.y) * a.groups_per_split;
+    const int gend = min(a.groups, gbeg + a.groups_per_split);
+    const int pbeg = gbeg / 2, plast = (gend - 1) / 2;
+    const int nchunks = (gend - gbeg + CG - 1) / CG;
+    const int t0 = static_cast<int>(blockIdx.x) * RT;
+    const u32x4* xsrc = reinterpret_cast<const u32x4*>(a.halves) + static_cast<size_t>(a.vt0 + wave) * a.groups * 2 * 64;
+    const uint32_t* dsrc = reinterpret_cast<const uint32_t*>(a.d);
 
-    float4v acc[RT][NT];
+    auto load_raw = [&](int chunk, uint4 (&raw)[WPT], uint32_t (&dr)[DPT]) {
 #pragma unroll
-    for (int r = 0; r < RT; ++r)
+        for (int i = 0; i < WPT; ++i) {
+            const int e = min(tid + NTH * i, RAW - 1);
+            const int r = (e >> 6) / P, p = (e >> 6) % P;
+            const int t = min(t0 + r, a.tiles - 1), pp = min(pbeg + chunk * P + p, plast);
+            raw[i] = a.q[(static_cast<size_t>(t) * a.pairs + pp) * 64 + (e & 63)];
+        }
 #pragma unroll
-        for (int v = 0; v < NT; ++v) acc[r][v] = float4v{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < DPT; ++i) {
+            const int e = min(tid + NTH * i, DW - 1);
+            const int r = e / (P * 16), p = (e / 16) % P;
+            const int t = min(t0 + r, a.tiles - 1), pp = min(pbeg + chunk * P + p, plast);
+            dr[i] = dsrc[(static_cast<size_t>(t) * a.pairs + pp) * 16 + (e & 15)];
+        }
+    };
+    auto stage = [&](int buf, const uint4 (&raw)[WPT], const uint32_t (&dr)[DPT]) {
+#pragma unroll
+        for (int i = 0; i < WPT; ++i) {
+            const int e = tid + NTH * i;
+            if (RAW % NTH && e >= RAW) break;
+            const int r = (e >> 6) / P, p = (e >> 6) % P, l = e & 63;
+            ws[buf][2 * p][r][l] = i8x8_to_half8(make_uint2(raw[i].x, raw[i].y));
+            ws[buf][2 * p + 1][r][l] = i8x8_to_half8(make_uint2(raw[i].z, raw[i].w));
+        }
+#pragma unroll
+        for (int i = 0; i < DPT; ++i) {
+            const int e = tid + NTH * i;
+            if (e < DW) wd[buf][e / (P * 16)][(e / 16) % P][e & 15] = dr[i];
+        }
+    };
+    auto load_x = [&](int chunk, u32x4 (&x)[CG][2]) {
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+            const int g = min(gbeg + chunk * CG + c, gend - 1);
+            x[c][0] = xsrc[(static_cast<size_t>(g) * 2) * 64 + lane];
+            x[c][1] = xsrc[(static_cast<size_t>(g) * 2 + 1) * 64 + lane];
+        }
+    };
+    float4v acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int chunk, int buf, const u32x4 (&x)[CG][2]) {
+        uint32_t dd[RT][P];
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int p = 0; p < P; ++p) dd[r][p] = wd[buf][r][p][lane & 15];
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+            const bool live = gbeg + chunk * CG + c < gend;  // uniform across the workgroup
+            const half8 xh = __builtin_bit_cast(half8, x[c][0]), xl = __builtin_bit_cast(half8, x[c][1]);
+            half8 w[RT];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) w[r] = ws[buf][c][r][lane];
+            float4v cc[RT];
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+                cc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, w[r], float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) cc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, w[r], cc[r], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const float d =
+                    live ? half_bits_to_float(static_cast<uint16_t>(dd[r][c / 2] >> (c % 2 ? 16 : 0))) : 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[r][i] = fmaf(d, cc[r][i], acc[r][i]);
+            }
+        }
+    };
 
-    // The halves of chunk c+1 sit in registers during chunk c: they go to LDS
-    // at the top of the next iteration, before the loads of chunk c+2 are
-    // issued, so a load is never consumed in the iteration that issued it.
-    // The int8 tiles and scales of chunk c+1 load into the register set that
-    // chunk c does not use: the loop is unrolled by two over sets ta / tb.
-    u32x4 hb[BPT];
-    Q8_LOAD_HALVES(0)
-#pragma unroll
-    for (int i = 0; i < BPT; ++i) bs[0][threadIdx.x + 256 * i] = hb[i];
-    Q8_LOAD_HALVES(min(1, nchunks - 1))
-    TilesChunk<RT, CH> ta = q8_load_tiles<RT, CH>(a, gbeg, gend, 0, tile, lane), tb;
+    uint4 rA[WPT], rB[WPT];
+    uint32_t dA[DPT], dB[DPT];
+    u32x4 xA[CG][2], xB[CG][2];
+    const int c1 = min(1, nchunks - 1);
+    load_raw(0, rA, dA);
+    load_x(0, xA);
+    load_raw(c1, rB, dB);
+    stage(0, rA, dA);
+    load_x(c1, xB);
     __syncthreads();
-
-#define Q8_CHUNK(chunk, CUR, NXT)                                                                                   \
-    {                                                                                                               \
-        const int buf = (chunk) & 1;                                                                                \
-        _Pragma("unroll") for (int i = 0; i < BPT; ++i) bs[buf ^ 1][threadIdx.x + 256 * i] = hb[i];                 \
-        Q8_LOAD_HALVES(min((chunk) + 2, nchunks - 1))                                                              \
-        NXT = q8_load_tiles<RT, CH>(a, gbeg, gend, min((chunk) + 1, nchunks - 1), tile, lane);                     \
-        _Pragma("unroll") for (int c = 0; c < CH; ++c) {                                                            \
-            if (gbeg + (chunk) * CH + c < gend) { /* uniform across the workgroup */                                \
-                half8 am[RT];                                                                                       \
-                float dv[RT][4];                                                                                    \
-                _Pragma("unroll") for (int r = 0; r < RT; ++r) {                                                    \
-                    const uint4 qp = CUR.q[r][c / 2], dp = CUR.d[r][c / 2];                                         \
-                    am[r] = i8x8_to_half8(c % 2 ? make_uint2(qp.z, qp.w) : make_uint2(qp.x, qp.y));                 \
-                    const int sh = c % 2 ? 16 : 0;                                                                  \
-                    dv[r][0] = half_bits_to_float(static_cast<uint16_t>(dp.x >> sh));                               \
-                    dv[r][1] = half_bits_to_float(static_cast<uint16_t>(dp.y >> sh));                               \
-                    dv[r][2] = half_bits_to_float(static_cast<uint16_t>(dp.z >> sh));                               \
-                    dv[r][3] = half_bits_to_float(static_cast<uint16_t>(dp.w >> sh));                               \
-                }                                                                                                   \
-                _Pragma("unroll") for (int v = 0; v < NT; ++v) {                                                    \
-                    const half8 bh = __builtin_bit_cast(half8, bs[buf][((c * NT + v) * 2) * 64 + lane]);            \
-                    const half8 bl = __builtin_bit_cast(half8, bs[buf][((c * NT + v) * 2 + 1) * 64 + lane]);        \
-                    _Pragma("unroll") for (int r = 0; r < RT; ++r) {                                                \
-                        float4v cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[r], bh, float4v{0.f, 0.f, 0.f, 0.f}, \
-                                                                            0, 0, 0);                               \
-                        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[r], bl, cc, 0, 0, 0);                        \
-                        _Pragma("unroll") for (int i = 0; i < 4; ++i) acc[r][v][i] =                                \
-                            fmaf(dv[r][i], cc[i], acc[r][v][i]);                                                    \
-                    }                                                                                               \
-                }                                                                                                   \
-            }                                                                                                       \
-        }                                                                                                           \
-        __syncthreads();                                                                                            \
+    for (int k = 0;; k += 2) {
+        load_raw(min(k + 2, nchunks - 1), rA, dA);
+        compute(k, 0, xA);
+        stage(1, rB, dB);
+        __syncthreads();
+        if (k + 1 >= nchunks) break;
+        load_x(min(k + 2, nchunks - 1), xA);
+        load_raw(min(k + 3, nchunks - 1), rB, dB);
+        compute(k + 1, 1, xB);
+        stage(0, rA, dA);
+        __syncthreads();
+        if (k + 2 >= nchunks) break;
+        load_x(min(k + 3, nchunks - 1), xB);
     }
-
-    for (int chunk = 0;; chunk += 2) {
-        Q8_CHUNK(chunk, ta, tb)
-        if (chunk + 1 >= nchunks) break;
-        Q8_CHUNK(chunk + 1, tb, ta)
-        if (chunk + 2 >= nchunks) break;
-    }
-#undef Q8_CHUNK
-    // lane l holds rows 4(l/16)+i of each tile, vector l%16 of each vector tile
+    // lane l holds row l%16 of each tile for vectors 4(l/16) + i of its tile
     float* out = a.out + static_cast<size_t>(blockIdx.y) * a.n_total * a.rows;
 #pragma unroll
-    for (int v = 0; v < NT; ++v) {
-        const int jl = v * 16 + (lane & 15);
+    for (int i = 0; i < 4; ++i) {
+        const int jl = wave * 16 + 4 * (lane >> 4) + i;
         if (jl >= a.n) continue;
         const int j = a.vt0 * 16 + jl;
         const float us = a.unscale[j];
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
-            const int t = (static_cast<int>(blockIdx.x) * 4 + wave) * RT + r;
-            if (t >= a.tiles) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = t * 16 + 4 * (lane >> 4) + i;
-                if (row < a.rows) out[static_cast<size_t>(j) * a.rows + row] = acc[r][v][i] * us;
-            }
+            const int row = (t0 + r) * 16 + (lane & 15);
+            if (t0 + r < a.tiles && row < a.rows) out[static_cast<size_t>(j) * a.rows + row] = acc[r][i] * us;
         }
     }
 }
@@ -1009,30 +1016,20 @@ void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg,
 }
 
 namespace {
-template <int RT>
-void launch_batch_q8_rt(int nt, dim3 grid, hipStream_t s, const Q8BatchArgs& a) {
-    switch (nt) {
-        case 1: launch("model_matvec_q8", batch_q8_kernel<RT, 1>, grid, dim3(256), 0, s, a); break;
-        case 2: launch("model_matvec_q8", batch_q8_kernel<RT, 2>, grid, dim3(256), 0, s, a); break;
-        case 3: launch("model_matvec_q8", batch_q8_kernel<RT, 3>, grid, dim3(256), 0, s, a); break;
-        default: launch("model_matvec_q8", batch_q8_kernel<RT, 4>, grid, dim3(256), 0, s, a); break;
-    }
-}
-
-// row tiles per wave and groups per K split of the batched Q8_0 product: two
-// tiles per wave for the largest matrices; the groups are split only while
-// the launch has fewer than one workgroup per CU, and never below 16 a split
+// groups per K split of the batched Q8_0 product (workgroups of four row
+// tiles): the groups are split while the launch has fewer than 512
+// workgroups (two per CU), in whole chunks of four groups, never below eight
+// groups and into at most eight splits (the epilogues read every split)
 struct Q8Plan {
-    int rt, gx, per, splits;
+    int gx, per, splits;
 };
 Q8Plan q8_plan(const Weight& w) {
     Q8Plan p{};
     const int tiles = w.tiles(), groups = w.groups();
-    p.rt = tiles >= 2048 ? 2 : 1;
-    p.gx = (tiles + 4 * p.rt - 1) / (4 * p.rt);
-    const int want = p.gx >= 256 ? 1 : std::min((256 + p.gx - 1) / p.gx, std::max(1, groups / 16));
+    p.gx = (tiles + 3) / 4;
+    const int want = p.gx >= 512 ? 1 : std::min({(512 + p.gx - 1) / p.gx, std::max(1, groups / 8), 8});
     p.per = (groups + want - 1) / want;
-    p.per += p.per % 2;  // splits start on a group pair
+    p.per = (p.per + 3) / 4 * 4;  // whole chunks, so splits start on a group pair
     p.splits = (groups + p.per - 1) / p.per;
     return p;
 }
@@ -1074,10 +1071,12 @@ void launch_batch_product(const Weight& w, const float* x, const _Float16* halve
             a.groups_per_split = p.per;
             a.out = out;
             const dim3 grid(p.gx, p.splits);
-            if (p.rt == 2)
-                launch_batch_q8_rt<2>((nj + 15) / 16, grid, s, a);
-            else
-                launch_batch_q8_rt<1>((nj + 15) / 16, grid, s, a);
+            switch ((nj + 15) / 16) {  // one wave per vector tile
+                case 1: launch("model_matvec_q8", batch_q8_kernel<1>, grid, dim3(64), 0, s, a); break;
+                case 2: launch("model_matvec_q8", batch_q8_kernel<2>, grid, dim3(128), 0, s, a); break;
+                case 3: launch("model_matvec_q8", batch_q8_kernel<3>, grid, dim3(192), 0, s, a); break;
+                default: launch("model_matvec_q8", batch_q8_kernel<4>, grid, dim3(256), 0, s, a); break;
+            }
         }
     } else {
         if (w.cols % kTileK) throw std::invalid_argument("batched matvec needs a row width divisible by 32");
