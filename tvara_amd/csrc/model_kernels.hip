@@ -743,10 +743,28 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
 // kernels add the splits in order (from 0.f, as one split's value is itself)
 // and apply what follows the product in the layer.
 
-__device__ __forceinline__ float split_total(const float* p, int splits, size_t stride, size_t at) {
+// The sum runs in split order.  The partials are read N at a time (N = 1, 2
+// or 4 when that covers every split, else 8), all N requested before the
+// first add; clamped indices keep the loads unconditional, and a select (not
+// an add of 0.f) skips the surplus ones.
+template <int N>
+__device__ __forceinline__ float split_sum(const float* p, int splits, size_t stride, size_t at) {
     float s = 0.f;
-    for (int k = 0; k < splits; ++k) s += p[k * stride + at];
+    for (int k0 = 0; k0 < splits; k0 += N) {
+        float v[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) v[k] = p[static_cast<size_t>(min(k0 + k, splits - 1)) * stride + at];
+#pragma unroll
+        for (int k = 0; k < N; ++k) s = k0 + k < splits ? s + v[k] : s;
+    }
     return s;
+}
+
+__device__ __forceinline__ float split_total(const float* p, int splits, size_t stride, size_t at) {
+    if (splits == 1) return split_sum<1>(p, splits, stride, at);
+    if (splits == 2) return split_sum<2>(p, splits, stride, at);
+    if (splits <= 4) return split_sum<4>(p, splits, stride, at);
+    return split_sum<8>(p, splits, stride, at);
 }
 
 // Q|K|V rows of vector j: q and k rotated by row j's (cos, sin)
