@@ -112,6 +112,67 @@ def test_bf16_block_sizes(device, oracle, tpb, dim, fmt):
     assert ok, err
 
 
+def bf16_rne(x):
+    """float32 -> the nearest bfloat16 (ties to even), as float32."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("tpb", [16, 64])
+@pytest.mark.parametrize("fmt", ["f32", "q8_0"])
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("group", [1, 4, 8])
+def test_bf16_against_bf16_operands(device, oracle, group, dim, fmt, tpb):
+    """The MFMA path against the FP64 oracle run on the operands the kernel
+    actually multiplies: K and V rounded to bf16 (Q8_0: d * q rounded), and
+    the query bf16(q * log2(e)/sqrt(d)) carried back to natural units.  The
+    scores then agree to f32 summation error, and what is left is the bf16
+    rounding of the probabilities, p~ = p (1 + e), |e| <= u = 2^-9, which
+    enters numerator and normaliser alike:
+        |o~ - o| = |sum w e (v - o)| / (1 + sum w e) <= u (max|v| + |o|) / (1 - u).
+    A dropped or duplicated key in a short row, a wrong scale or a stale
+    running maximum breaks this bound by far."""
+    heads, kv_heads = 2 * group, 2
+    specs = [(137, 100, 37), (64, 0, 64), (20, 3, 17), (300, 250, 50)]
+    say("prefill bf16 operands group", group, "dim", dim, fmt, "tpb", tpb)
+    nb = sum((n + tpb - 1) // tpb for n, _, _ in specs) + 4
+    q8 = fmt == "q8_0"
+    dev = device.PagedCache(1, kv_heads, dim, tpb, nb, fmt=device.Q8_0 if q8 else device.F32)
+    ref = oracle.Cache(1, kv_heads, dim, tpb, nb)
+    w, seed = kv_heads * dim, 100 + group + dim + tpb
+    qscale = np.float32(1.4426950408889634 / np.sqrt(float(dim)))
+    ds, rs, qs, qo, vmax = [], [], [], [], 0.0
+    for i, (n, start, rows) in enumerate(specs):
+        k = synth.normal(seed, f"k{i}", n * w).reshape(n, w)
+        v = synth.normal(seed, f"v{i}", n * w).reshape(n, w)
+        kr, vr = k, v
+        if q8:
+            kr = oracle.dequantize_q8_0(oracle.quantize_q8_0(k)).reshape(n, w)
+            vr = oracle.dequantize_q8_0(oracle.quantize_q8_0(v)).reshape(n, w)
+        kr, vr = bf16_rne(kr), bf16_rne(vr)
+        vmax = max(vmax, float(np.abs(vr).max()))
+        sd, sr = dev.create_sequence(), ref.create_sequence()
+        dev.append_many(sd, k, v)
+        ref.append_many(sr, kr, vr)
+        ds.append(sd)
+        rs.append(sr)
+        q = synth.normal(seed, f"q{i}", rows * heads * dim).reshape(rows, heads * dim)
+        qs.append(q)
+        qb = bf16_rne((q * qscale).astype(np.float32))
+        qo.append((qb.astype(np.float64) * np.sqrt(float(dim)) / 1.4426950408889634).astype(np.float32))
+    starts = [s for _, s, _ in specs]
+    counts = [r for _, _, r in specs]
+    got = attention.prefill_batch(dev, np.concatenate(qs), ds, starts, counts, 0, heads, 4096, precision="bf16")
+    want = np.concatenate([ref.fused_prompt_attention(q, s, 0, st, c, heads, 4096).reshape(c, -1)
+                           for q, s, st, c in zip(qo, rs, starts, counts)])
+    u = 2.0 ** -9
+    bound = u * (vmax + np.abs(want).astype(np.float64)) / (1 - u) + 1e-5
+    err = np.abs(np.asarray(got, np.float64) - want)
+    assert np.all(err <= bound), (float((err / bound).max()), float(err.max()))
+    say("bf16 operands: worst error / bound", float((err / bound).max()), "max error", float(err.max()))
+
+
 @pytest.mark.parametrize("make,fmt", [(workloads.prefill_c4, "f32"), (workloads.prefill_8b, "f32"),
                                       (workloads.prefill_c4, "q8_0")], ids=["d64", "d128", "d64-q8_0"])
 def test_bf16_c4_shape(device, oracle, make, fmt):
