@@ -595,8 +595,8 @@ struct Q8BatchArgs {
     float* out;  // [gridDim.y][n_total][rows]
 };
 
-// A workgroup of NT waves covers four row tiles (64 rows) over a share of the
-// groups; wave w owns vector tile w (16 vectors).  The operands are taken as
+// A workgroup of NT waves covers RT row tiles (RT x 16 rows) over a share of
+// the groups; wave w owns vector tile w (16 vectors).  The operands are taken as
 // C^T = X W^T: A = the wave's fp16 activation halves (registers, straight
 // from global memory), B = the row tiles' int8 weights, converted to fp16 once
 // per workgroup and shared through LDS, so lane l accumulates weight row l%16
@@ -607,9 +607,9 @@ struct Q8BatchArgs {
 // the activations of chunk c + 1 are requested after chunk c's barrier.
 // Prefetches are unconditional (clamped to the last chunk) so that the
 // compiler keeps them ahead of the arithmetic.
-template <int NT>
+template <int NT, int RT>
 __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
-    constexpr int RT = 4, P = 2, CG = 2 * P;         // row tiles, pairs and groups per chunk
+    constexpr int P = 2, CG = 2 * P;                 // pairs and groups per chunk
     constexpr int NTH = 64 * NT;
     constexpr int RAW = RT * P * 64;                 // uint4 of int8 per chunk
     constexpr int WPT = (RAW + NTH - 1) / NTH;       // per thread
@@ -1034,17 +1034,30 @@ void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg,
 }
 
 namespace {
-// groups per K split of the batched Q8_0 product (workgroups of four row
-// tiles): the groups are split while the launch has fewer than 512
-// workgroups (two per CU), in whole chunks of four groups, never below eight
-// groups and into at most eight splits (the epilogues read every split)
+// one wave per vector tile
+template <int RT>
+void launch_batch_q8(int nt, dim3 grid, hipStream_t s, const Q8BatchArgs& a) {
+    switch (nt) {
+        case 1: launch("model_matvec_q8", batch_q8_kernel<1, RT>, grid, dim3(64), 0, s, a); break;
+        case 2: launch("model_matvec_q8", batch_q8_kernel<2, RT>, grid, dim3(128), 0, s, a); break;
+        case 3: launch("model_matvec_q8", batch_q8_kernel<3, RT>, grid, dim3(192), 0, s, a); break;
+        default: launch("model_matvec_q8", batch_q8_kernel<4, RT>, grid, dim3(256), 0, s, a); break;
+    }
+}
+
+// row tiles per workgroup and groups per K split of the batched Q8_0
+// product: four row tiles from 1,024 tiles up, else two (more workgroups for
+// the smaller matrices); the groups are split while the launch has fewer than
+// 512 workgroups (two per CU), in whole chunks of four groups, never below
+// eight groups and into at most eight splits (the epilogues read every split)
 struct Q8Plan {
-    int gx, per, splits;
+    int rt, gx, per, splits;
 };
 Q8Plan q8_plan(const Weight& w) {
     Q8Plan p{};
     const int tiles = w.tiles(), groups = w.groups();
-    p.gx = (tiles + 3) / 4;
+    p.rt = tiles >= 1024 ? 4 : 2;
+    p.gx = (tiles + p.rt - 1) / p.rt;
     const int want = p.gx >= 512 ? 1 : std::min({(512 + p.gx - 1) / p.gx, std::max(1, groups / 8), 8});
     p.per = (groups + want - 1) / want;
     p.per = (p.per + 3) / 4 * 4;  // whole chunks, so splits start on a group pair
@@ -1089,12 +1102,10 @@ void launch_batch_product(const Weight& w, const float* x, const _Float16* halve
             a.groups_per_split = p.per;
             a.out = out;
             const dim3 grid(p.gx, p.splits);
-            switch ((nj + 15) / 16) {  // one wave per vector tile
-                case 1: launch("model_matvec_q8", batch_q8_kernel<1>, grid, dim3(64), 0, s, a); break;
-                case 2: launch("model_matvec_q8", batch_q8_kernel<2>, grid, dim3(128), 0, s, a); break;
-                case 3: launch("model_matvec_q8", batch_q8_kernel<3>, grid, dim3(192), 0, s, a); break;
-                default: launch("model_matvec_q8", batch_q8_kernel<4>, grid, dim3(256), 0, s, a); break;
-            }
+            if (p.rt == 4)
+                launch_batch_q8<4>((nj + 15) / 16, grid, s, a);
+            else
+                launch_batch_q8<2>((nj + 15) / 16, grid, s, a);
         }
     } else {
         if (w.cols % kTileK) throw std::invalid_argument("batched matvec needs a row width divisible by 32");
