@@ -658,6 +658,15 @@ void AttnPlan::check() {
     finish_check();
 }
 
+void AttnPlan::check_after(hipEvent_t after) {
+    if (!pinned_err) {
+        check();
+        return;
+    }
+    TVARA_HIP(hipEventSynchronize(after));
+    finish_check();
+}
+
 void PrefillPlan::build(DeviceCache* c, const uint64_t* sequences, size_t n, size_t h, size_t context,
                         const size_t* start, const size_t* rows, int prec) {
     cache = c;

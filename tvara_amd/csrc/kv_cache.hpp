@@ -187,6 +187,10 @@ struct AttnPlan {
     void launch(int layer, const float* q, const float* tail_k, const float* tail_v, float* out, hipStream_t s);
     // waits for the last launch's stream; a non-finite score throws
     void check();
+    // the same, waiting only for `after` (an event recorded after the last
+    // launch) when the kernels write the pinned flag; work queued behind the
+    // launch keeps running
+    void check_after(hipEvent_t after);
     // the same, with the flag copied to caller-provided host memory (no
     // pinned allocation)
     void check_into(int* host_flag);

@@ -283,6 +283,20 @@ void DeviceModel::ensure_batch(size_t n) {
     batch_cap_ = n;
 }
 
+void DeviceModel::StepEvents::ensure() {
+    if (!copy) TVARA_HIP(hipStreamCreateWithFlags(&copy, hipStreamNonBlocking));
+    if (!attn) TVARA_HIP(hipEventCreateWithFlags(&attn, hipEventDisableTiming));
+    for (hipEvent_t& e : band)
+        if (!e) TVARA_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+}
+
+DeviceModel::StepEvents::~StepEvents() {
+    for (hipEvent_t e : band)
+        if (e) (void)hipEventDestroy(e);
+    if (attn) (void)hipEventDestroy(attn);
+    if (copy) (void)hipStreamDestroy(copy);
+}
+
 void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens, size_t n, float* logits_host) {
     if (!n) return;
     const ModelConfig& c = cfg_;
@@ -354,6 +368,7 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     // RMSNorm; SwiGLU) and writes the next product's input.
     AttnPlan& plan = batch_plan_;
     plan.build(cache_.get(), seqs, positions, std::vector<uint8_t>(n, 1), static_cast<int>(c.heads), 0);
+    step_events_.ensure();
     launch_resid_norm(nullptr, 0, x, at(layers_[0].attn_norm, 0), N, H, c.rms_epsilon, norm,
                       halves_for(layers_[0].qkv), unscale, s);
     for (size_t l = 0; l < c.layers; ++l) {
@@ -364,6 +379,7 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
         launch_qkv_epilogue(part, batch_splits(L.qkv), N, static_cast<int>(c.heads), static_cast<int>(c.kv_heads), D,
                             c.interleaved_rope, at(brope_, 0), q, kl, vl, s);
         plan.launch(static_cast<int>(l), q, kl, vl, attn, s);
+        if (l + 1 == c.layers) TVARA_HIP(hipEventRecord(step_events_.attn, s));
         if (L.out.q8) launch_split_halves(attn, N, H, halves, unscale, s);
         launch_batch_product(L.out, attn, halves, unscale, N, part, s);
         launch_resid_norm(part, batch_splits(L.out), x, at(L.ffn_norm, 0), N, H, c.rms_epsilon, norm,
@@ -376,14 +392,31 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
         launch_resid_norm(part, batch_splits(L.down), x, last ? at(final_norm_, 0) : at(layers_[l + 1].attn_norm, 0), N,
                           H, c.rms_epsilon, norm, halves_for(last ? logits_w : layers_[l + 1].qkv), unscale, s);
     }
+    // Large logits (8 MiB and up, unsplit Q8_0) are computed in bands of row
+    // tiles, each copied to the host while the next is computed.  Every way
+    // the step can fail (the attention's error flag, the append's pool) is
+    // settled before the first byte reaches the caller's buffer.
     const int vocab = static_cast<int>(c.vocab);
-    if (batch_splits(logits_w) == 1) {
+    constexpr int kBands = StepEvents::kBands;
+    const bool banded =
+        logits_w.q8 && batch_splits(logits_w) == 1 && n * c.vocab * sizeof(float) >= (size_t(8) << 20);
+    size_t bounds[kBands + 1];
+    int bands = 0;
+    if (banded) {
+        const int tiles = logits_w.tiles(), per = (tiles + kBands - 1) / kBands;
+        for (int t = 0; t < tiles; t += per) {
+            launch_batch_product_tiles(logits_w, t, std::min(tiles, t + per), halves, unscale, N, at(blogits_, 0), s);
+            TVARA_HIP(hipEventRecord(step_events_.band[bands], s));
+            bounds[bands++] = static_cast<size_t>(t) * 16;
+        }
+        bounds[bands] = c.vocab;
+    } else if (batch_splits(logits_w) == 1) {
         launch_batch_product(logits_w, norm, halves, unscale, N, at(blogits_, 0), s);
     } else {
         launch_batch_product(logits_w, norm, halves, unscale, N, part, s);
         launch_split_sum(part, batch_splits(logits_w), N, vocab, at(blogits_, 0), s);
     }
-    plan.check();
+    plan.check_after(step_events_.attn);
     launch_interleave_layers(at(bk_, 0), at(bkapp_, 0), static_cast<int>(c.layers), N, KV, s);
     launch_interleave_layers(at(bv_, 0), at(bvapp_, 0), static_cast<int>(c.layers), N, KV, s);
     size_t applied = 0;
@@ -393,7 +426,11 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
         for (size_t i = 0; i < applied; ++i) cache_->truncate(seqs[i], positions[i]);  // all or nothing
         throw;
     }
-    copier_.from_device(logits_host, blogits_.ptr, n * c.vocab * sizeof(float), s);
+    if (banded)
+        copier_.bands_from_device(logits_host, at(blogits_, 0), n, c.vocab, bounds, step_events_.band, bands,
+                                  step_events_.copy);
+    else
+        copier_.from_device(logits_host, blogits_.ptr, n * c.vocab * sizeof(float), s);
 }
 
 }  // namespace tvara_amd

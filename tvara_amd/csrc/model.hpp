@@ -66,6 +66,11 @@ void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg,
 int batch_splits(const Weight& w);
 void launch_batch_product(const Weight& w, const float* x, const _Float16* halves, const float* unscale, int n,
                           float* out, hipStream_t s);
+// the rows of row tiles [tile0, tile1) of an unsplit Q8_0 product (out as for
+// launch_batch_product, rows at their place), so a product can be issued in
+// bands
+void launch_batch_product_tiles(const Weight& w, int tile0, int tile1, const _Float16* halves, const float* unscale,
+                                int n, float* out, hipStream_t s);
 void launch_split_halves(const float* x, int n, int cols, _Float16* halves, float* unscale, hipStream_t s);
 void launch_split_sum(const float* p, int splits, int n, int rows, float* out, hipStream_t s);
 // the split sums of the fused QKV product into q, k (rotated by row j's
@@ -145,6 +150,21 @@ private:
     size_t part_rows_ = 0;  // largest splits x rows of a batched product
     PinnedBuffer bhost_;
     HostCopier copier_;
+    // the batched step's synchronisation: an event after the last layer's
+    // attention (the plan's check waits on it, not on the whole stream), one
+    // per band of the logits product, and the stream the bands' copies to the
+    // host cross on while later bands are computed
+    struct StepEvents {
+        static constexpr int kBands = 4;
+        hipStream_t copy = nullptr;
+        hipEvent_t attn = nullptr, band[kBands] = {};
+        void ensure();
+        StepEvents() = default;
+        StepEvents(const StepEvents&) = delete;
+        StepEvents& operator=(const StepEvents&) = delete;
+        ~StepEvents();
+    };
+    StepEvents step_events_;
     size_t batch_cap_ = 0;
     void ensure_batch(size_t n);
 };

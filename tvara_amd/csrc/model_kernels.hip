@@ -588,8 +588,9 @@ struct Q8BatchArgs {
     const uint16_t* d;
     const uint4* halves;  // 8 fp16 per lane, see put_halves
     const float* unscale;
-    int rows, tiles, groups, pairs;
-    int n, vt0;  // vectors in this launch, first vector tile
+    int rows, tiles, groups, pairs;  // tiles: one past the last row tile of this launch
+    int tile0;                       // its first row tile (blockIdx.x counts from it)
+    int n, vt0;                      // vectors in this launch, first vector tile
     int n_total;
     int groups_per_split;
     float* out;  // [gridDim.y][n_total][rows]
@@ -622,7 +623,7 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
     const int gend = min(a.groups, gbeg + a.groups_per_split);
     const int pbeg = gbeg / 2, plast = (gend - 1) / 2;
     const int nchunks = (gend - gbeg + CG - 1) / CG;
-    const int t0 = static_cast<int>(blockIdx.x) * RT;
+    const int t0 = a.tile0 + static_cast<int>(blockIdx.x) * RT;
     const u32x4* xsrc = reinterpret_cast<const u32x4*>(a.halves) + static_cast<size_t>(a.vt0 + wave) * a.groups * 2 * 64;
     const uint32_t* dsrc = reinterpret_cast<const uint32_t*>(a.d);
 
@@ -1123,6 +1124,37 @@ void launch_batch_product(const Weight& w, const float* x, const _Float16* halve
             a.j0 = j0;
             launch("model_matvec", batch_matvec_kernel, dim3(p.tiles, p.splits), dim3(256), 0, s, a);
         }
+    }
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_batch_product_tiles(const Weight& w, int tile0, int tile1, const _Float16* halves, const float* unscale,
+                                int n, float* out, hipStream_t s) {
+    const Q8Plan p = q8_plan(w);
+    if (!w.q8 || p.splits != 1 || tile0 < 0 || tile0 >= tile1 || tile1 > w.tiles())
+        throw std::invalid_argument("row-tile range of a batched product needs an unsplit Q8_0 matrix");
+    for (int j0 = 0; j0 < n; j0 += 64) {
+        const int nj = std::min(64, n - j0);
+        Q8BatchArgs a{};
+        a.q = static_cast<const uint4*>(w.q.ptr);
+        a.d = static_cast<const uint16_t*>(w.d.ptr);
+        a.halves = reinterpret_cast<const uint4*>(halves);
+        a.unscale = unscale;
+        a.rows = w.rows;
+        a.tiles = tile1;
+        a.tile0 = tile0;
+        a.groups = w.groups();
+        a.pairs = w.pairs();
+        a.n = nj;
+        a.vt0 = j0 / 16;
+        a.n_total = n;
+        a.groups_per_split = p.per;
+        a.out = out;
+        const dim3 grid((tile1 - tile0 + p.rt - 1) / p.rt, 1);
+        if (p.rt == 4)
+            launch_batch_q8<4>((nj + 15) / 16, grid, s, a);
+        else
+            launch_batch_q8<2>((nj + 15) / 16, grid, s, a);
     }
     TVARA_HIP(hipGetLastError());
 }
