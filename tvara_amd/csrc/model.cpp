@@ -348,10 +348,13 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     auto* host = static_cast<char*>(bhost_.acquire(tok_bytes + n * c.head_dim() * sizeof(float)));
     std::memcpy(host, tokens, n * sizeof(uint32_t));
     auto* cs = reinterpret_cast<float*>(host + tok_bytes);
+    // rotary()'s angle position / theta^(2i/D), with the power taken once per
+    // i (the same float values; the GPU waits for this table)
+    std::vector<float> inv_freq(D / 2);
+    for (int i = 0; i < D / 2; ++i) inv_freq[i] = std::pow(c.rope_theta, static_cast<float>(2 * i) / static_cast<float>(D));
     for (size_t j = 0; j < n; ++j)
         for (int i = 0; i < D / 2; ++i) {
-            const float angle = static_cast<float>(positions[j]) /
-                                std::pow(c.rope_theta, static_cast<float>(2 * i) / static_cast<float>(D));
+            const float angle = static_cast<float>(positions[j]) / inv_freq[i];
             cs[j * D + 2 * i] = std::cos(angle);
             cs[j * D + 2 * i + 1] = std::sin(angle);
         }
