@@ -201,15 +201,16 @@ def test_nonfinite_q8_0_scale_rejected(tmp_path, ref_capi, scale):
 
 @pytest.mark.parametrize("nseq,embed,vocab", [(3, gf.T_F32, 96), (20, gf.T_F32, 96), (41, gf.T_Q8_0, 96),
                                                (70, gf.T_Q8_0, 96), (64, gf.T_Q8_0, 16390),
-                                               (64, gf.T_Q8_0, 32800)])
+                                               (64, gf.T_Q8_0, 32800), (20, gf.T_Q8_0, 131072)])
 def test_sequences_decode_matches_serial_reference(tmp_path, ref_capi, nseq, embed, vocab):
     # one pass for many sequences (tvara_sequences_decode) against the
     # reference decoding each sequence on its own; 41 and 70 sequences take
     # partial and multiple 64-vector passes of the batched Q8_0 products.  The
     # 16,390-row tied logits matrix (1,025 row tiles, the last one partial)
     # takes the four-tile workgroups that the model's largest products use;
-    # at 32,800 rows (8.4 MB of logits for 64 sequences) the logits are
-    # computed and copied to the host in four bands of row tiles.
+    # at 32,800 rows (8.4 MB of logits for 64 sequences) and 131,072 rows
+    # (10.5 MB for 20 sequences, two-wave workgroups) the logits are computed
+    # and copied to the host in four bands of row tiles.
     spec = gf.LlamaSpec(matrix_type=gf.T_Q8_0, embed_type=embed, output=embed == gf.T_F32, hidden=128,
                         intermediate=256, heads=8, kv_heads=2, vocab=vocab)
     path = spec.write(tmp_path / "m.gguf")
