@@ -429,10 +429,13 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
         for (size_t i = 0; i < applied; ++i) cache_->truncate(seqs[i], positions[i]);  // all or nothing
         throw;
     }
-    if (banded)
+    if (banded) {
         copier_.bands_from_device(logits_host, at(blogits_, 0), n, c.vocab, bounds, step_events_.band, bands,
                                   step_events_.copy);
-    else
+        // calls that return host data leave the stream drained (the append
+        // kernels behind the logits ended long before the last band's copy)
+        TVARA_HIP(hipStreamSynchronize(s));
+    } else
         copier_.from_device(logits_host, blogits_.ptr, n * c.vocab * sizeof(float), s);
 }
 
