@@ -202,6 +202,7 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
     // (paged_model.hpp:22; attention.hpp:80)
     AttnPlan& plan = step_plan_;
     plan.build(cache_.get(), {sequence}, {position}, {1}, static_cast<int>(c.heads), 0);
+    step_events_.ensure();
 
     for (size_t l = 0; l < c.layers; ++l) {
         Layer& L = layers_[l];
@@ -216,6 +217,7 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
                         c.interleaved_rope, s);
         }
         plan.launch(static_cast<int>(l), q, kl, vl, attn, s);
+        if (l + 1 == c.layers) TVARA_HIP(hipEventRecord(step_events_.attn, s));
         const MatvecSegment o[1] = {{x, H, x}};
         matvec(L.out, attn, o, 1, s);
         if (L.gate_up.interleaved) {  // SwiGLU in the product's epilogue, into gate
@@ -231,7 +233,10 @@ void DeviceModel::decode(uint64_t sequence, size_t token, float* logits_host) {
     }
     const MatvecSegment lg[1] = {{at(logits_, 0), static_cast<int>(c.vocab), nullptr}};
     matvec(has_output_ ? output_ : embedding_, x, lg, 1, s, at(final_norm_, 0));
-    plan.check();  // a non-finite score fails the token before anything is appended
+    // a non-finite score fails the token before anything is appended; the
+    // check waits for the last layer's attention only, so the append is
+    // planned while the GPU finishes the layer and the logits
+    plan.check_after(step_events_.attn);
     // the token's K/V for every layer, appended after all layers succeeded
     // (paged_model.hpp:27)
     cache_->append_batch(&sequence, 1, at(kall_, 0), at(vall_, 0), true);
