@@ -138,7 +138,9 @@ uint64_t PrefixTree::insert(const int32_t* tokens, size_t n) {
     const uint64_t leaf = done < n ? mint() : 0;
     const uint64_t leaf_parent = inner ? inner : s.at;
 
-    arena_.reserve(arena_.size() + 2 + arena_.size() / 2);
+    // room for the two nodes this call may add; growth is geometric, so a
+    // long run of inserts reallocates the arena O(log n) times
+    if (arena_.capacity() - arena_.size() < 2) arena_.reserve(arena_.size() + 2 + arena_.size() / 2);
     if (leaf && tokens_.capacity() - tokens_.size() < n - done)
         tokens_.reserve(std::max(2 * tokens_.capacity(), tokens_.size() + n - done));
     EdgeKey added[2];
@@ -292,8 +294,18 @@ bool PrefixTree::evict_one() {
     if (idle_.empty()) return false;
     Node& victim = at(idle_.begin()->second);
     Node& parent = at(victim.parent);
-    if (parent.id && parent.children == 1 && !parent.pins) idle_.emplace(parent.stamp, parent.id);
-    release_snapshot(victim);
+    // the parent becomes a leaf: its index entry is made first (the only
+    // allocation here) and taken back if the victim's snapshot cannot be
+    // released (a handle gone stale outside the tree), which leaves the
+    // victim in place as the reference does
+    const bool parent_idle = parent.id && parent.children == 1 && !parent.pins;
+    if (parent_idle) idle_.emplace(parent.stamp, parent.id);
+    try {
+        release_snapshot(victim);
+    } catch (...) {
+        if (parent_idle) idle_.erase({parent.stamp, parent.id});
+        throw;
+    }
     edges_.erase({victim.parent, tokens_[victim.edge_at]});
     index_out(victim);
     --parent.children;
