@@ -66,8 +66,10 @@ TVARA_API const char* tvara_last_error(void);
 /* ---- model-level exports: the reference's 11 (c_api.h:13-24), same
  * signatures, return conventions (NULL / 0 / -1 with tvara_last_error set),
  * messages and per-handle lock (c_api.cpp:35-78).  The model runs on the GPU:
- * GGUF weights dequantised to f32 in HBM, every layer of a token on device,
- * the KV cache in this library's paged pool. */
+ * Q8_0 weight matrices stay quantised in HBM (34 bytes per 32 weights,
+ * repacked into MFMA operand order), other GGUF types are dequantised to f32
+ * at load, every layer of a token runs on device, and the KV cache lives in
+ * this library's paged pool. */
 
 /* tvara_model_open (c_api.cpp:36-40): load a Llama GGUF file; the KV pool holds
  * max_blocks blocks of block_tokens tokens */
@@ -285,8 +287,10 @@ TVARA_API int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequence
 
 /* tvara_attn_decode with device pointers that allocates nothing: no
  * hipMalloc, hipFree or allocating library call.  No counterpart in the
- * reference; it is for callers that cannot allocate device memory (code under
- * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * reference; it is for callers that cannot allocate device memory (serving
+ * loops, harnesses that forbid hipMalloc).  It is not for graph capture: the
+ * call copies its plan from host memory and waits for its own work, so it
+ * must not be called while the cache's stream is capturing.  The
  * plan (block ids, rows, work items, split counters, error flag) and the
  * split partials live in a fixed per-GPU device array of
  * tvara_attn_decode_noalloc_limit() bytes (32 MiB, held until the process

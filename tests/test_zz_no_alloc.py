@@ -90,3 +90,35 @@ def test_noalloc_rejects_batches_above_the_scratch(device):
     rc = _decode(lib, "tvara_attn_decode_noalloc", cache, [s] * rows, 1, 4096, q, None, None, None, out)
     assert rc == _capi.INVALID
     assert "no-allocation scratch" in _capi.last_error()
+
+
+def _free_bytes():
+    hip.synchronize()
+    free, total = C.c_size_t(), C.c_size_t()
+    hip.check(hip.runtime().hipMemGetInfo(C.byref(free), C.byref(total)))
+    return free.value
+
+
+def test_noalloc_leaves_device_memory_unchanged(device):
+    """The device's free memory is the same before and after the no-allocation
+    call on a fresh cache and batch, while tvara_attn_decode on the same batch
+    then grows its plan buffers (the control: the probe sees an allocation of
+    the batch's size)."""
+    w = workloads.decode_c2()
+    say("no-alloc free-memory probe", w.name)
+    g = (w.layers, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks)
+    cache = device.PagedCache(*g)
+    seqs = workloads.fill_decode(cache, w)
+    q = hip.DeviceArray.from_numpy(w.queries())
+    out = hip.DeviceArray((len(seqs), w.heads * w.head_dim))
+    lib = cache.lib
+    before = _free_bytes()
+    for _ in range(3):
+        _capi.check(_decode(lib, "tvara_attn_decode_noalloc", cache, seqs, w.heads, w.context, q, None, None, None,
+                            out))
+    after = _free_bytes()
+    assert after == before, (before, after)
+    _capi.check(_decode(lib, "tvara_attn_decode", cache, seqs, w.heads, w.context, q, None, None, None, out))
+    control = _free_bytes()
+    say("free bytes: before", before, "after no-alloc", after, "after tvara_attn_decode", control)
+    assert control < after, (after, control)

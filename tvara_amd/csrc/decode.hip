@@ -169,20 +169,22 @@ __device__ __forceinline__ float token_group_sum(float v) {
 
 // Reduce the token groups of a wave and write the split's result: the
 // normalised output when the row has one split, otherwise the partial
-// (acc, m, l) that merge_kernel combines.  (Merging in the last workgroup to
-// finish a row needs a device-scope release per workgroup; on gfx950 each one
-// writes back the XCD's L2 and they serialise, which costs far more than a
-// second launch.)  `col(c, e4)` is the head-local column of lane slot c's
-// e4-th float4.
-// The last workgroup of a row's splits merges them (a.row_done set).  Each
-// workgroup stores its partials with agent-scope relaxed atomic stores (they
-// reach the point of coherence shared by the XCDs' L2s), waits for them, and
-// counts its split with an agent-scope atomic; the workgroup that completes
-// the count reads every partial with agent-scope loads, combines them in
-// split order (the result does not depend on which workgroup finished last)
-// and resets the counter for the next launch.  No release fence is needed, so
-// no XCD's L2 is written back (a device-scope release per workgroup cost more
-// than a second launch).  Launches that share a plan must not overlap.
+// (acc, m, l) that merge_kernel combines.  `col(c, e4)` is the head-local
+// column of lane slot c's e4-th float4.
+// With a.row_done set, the last workgroup of a row's splits merges them in
+// the same launch.  Each workgroup stores its partials with agent-scope
+// relaxed atomic stores, waits for them (vmcnt counts stores on gfx9), and
+// counts its split with one agent-scope acquire-release fetch_add.  On gfx950
+// the release half writes the XCD's L2 back before the add, so the partials
+// reach memory shared by all eight XCDs; the acquire half invalidates the
+// finishing workgroup's L2 before it reads every partial with agent-scope
+// loads.  The merge combines the splits in split order (the result does not
+// depend on which workgroup finished last) and resets the counter for the
+// next launch.  The L2 write-backs serialise across workgroups, so the
+// launcher enables this only for launches of at most
+// kInKernelMergeMaxWorkgroups workgroups, where it saves the second launch;
+// larger launches take merge_kernel.
+// Launches that share a plan must not overlap.
 template <int D, int G>
 __device__ __forceinline__ void merge_row_splits(const DecodeArgs& a, int lane, int kh, int first, int row,
                                                  int nsplit) {

@@ -1,6 +1,7 @@
-// tvara_attn_decode for callers that cannot allocate device memory (code
-// under HIP graph capture, serving loops, harnesses that forbid hipMalloc):
-// the same plan and kernels, with the plan's device half (block ids, rows,
+// tvara_attn_decode for callers that cannot allocate device memory (serving
+// loops, harnesses that forbid hipMalloc; not graph capture: the call copies
+// its plan from host memory and synchronises the cache's stream): the same
+// plan and kernels, with the plan's device half (block ids, rows,
 // work items, split counters, error flag, split partials) in a file-scope
 // device array instead of library-owned buffers.
 //
