@@ -388,3 +388,57 @@ def test_zero_query_averages_every_visible_key(device, oracle, group, dim, fmt, 
             for h in range(heads):
                 assert np.allclose(got[at + r, h], want[h // group], rtol=1e-6, atol=1e-6), (i, r, h)
         at += cnt
+
+
+def _every_kernel(monkeypatch, run):
+    """run() under TVARA_PREFILL_PIPE = 0 (prefill_bf16_kernel) and 1 (the
+    software-pipelined kernel)."""
+    out = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("TVARA_PREFILL_PIPE", flag)
+        out.append(run())
+    monkeypatch.delenv("TVARA_PREFILL_PIPE")
+    return out
+
+
+def _same_bits(plain, *others):
+    return all(np.array_equal(plain.view(np.uint32), o.view(np.uint32)) for o in others)
+
+
+@pytest.mark.parametrize("make,fmt", [(workloads.prefill_c4, "f32"), (workloads.prefill_c4, "q8_0"),
+                                      (workloads.prefill_8b, "f32")], ids=["d64", "d64-q8_0", "d128"])
+def test_pipelined_kernel_matches_plain_kernel(device, monkeypatch, make, fmt):
+    """The pipelined kernels perform the plain kernel's products, exponentials
+    and rescales in the same order, so the whole chunked-prefill batch must
+    agree bit for bit (the plain kernel is pinned to the oracle above)."""
+    w = make()
+    say("pipelined vs plain prefill", w.name, fmt)
+    g = (1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks())
+    dev = device.PagedCache(*g, fmt=device.Q8_0 if fmt == "q8_0" else device.F32)
+    ds = workloads.fill_prefill(dev, w)
+    q = np.concatenate([w.chunk_queries(i) for i in range(w.sequences)])
+    plain, pipe = _every_kernel(monkeypatch, lambda: attention.prefill_batch(
+        dev, q, ds, [w.prefix] * w.sequences, [w.chunk] * w.sequences, 0, w.heads, w.context, precision="bf16"))
+    assert np.isfinite(plain).all()
+    assert _same_bits(plain, pipe)
+
+
+@pytest.mark.parametrize("tpb", [16, 32, 1024])
+@pytest.mark.parametrize("group", [1, 3, 4, 8])
+def test_pipelined_kernel_ragged_chunks(device, oracle, monkeypatch, group, tpb):
+    """Ragged chunks (a row alone, chunks ending inside a tile, a chunk with no
+    cached prefix, odd and even tile counts) through every kernel: equal bits,
+    and the pipelined ones within the short-row bars of the oracle."""
+    heads, kv_heads, dim = 2 * group, 2, 64
+    specs = [(1, 0, 1), (65, 64, 1), (200, 137, 63), (129, 0, 129), (700, 300, 400)]
+    say("pipelined prefill ragged, group", group, "tpb", tpb)
+    dev, ref, ds, rs, qs = build(device, oracle, heads, kv_heads, dim, specs, seed=31 + group, tpb=tpb)
+    starts = [s for _, s, _ in specs]
+    counts = [r for _, _, r in specs]
+    plain, pipe = _every_kernel(monkeypatch, lambda: attention.prefill_batch(
+        dev, np.concatenate(qs), ds, starts, counts, 0, heads, 4096, precision="bf16"))
+    assert _same_bits(plain, pipe)
+    want = np.concatenate([ref.fused_prompt_attention(q, s, 0, st, c, heads, 4096).reshape(c, -1)
+                           for q, s, st, c in zip(qs, rs, starts, counts)])
+    ok, err = bf16_ok(pipe, want, SHORT_ROWS)
+    assert ok, err

@@ -83,8 +83,14 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     // XCD-aware order: workgroups are dispatched to the 8 XCDs round-robin by
     // id, so the chunk tiles of one (sequence, KV head) pair get ids of one
     // residue mod 8 and share that XCD's L2 for their common K/V tiles.
+    // Within an XCD the ids run from the last chunk tile to the first (the
+    // most keys to the fewest), pairs fastest: the dispatcher hands the next
+    // id to the first CU that frees up, so the heaviest tiles start first and
+    // the lightest fill in behind them (measured: 111.6 against 114.5 us on
+    // the 8 x (2,048 + 512) chunk).
     const int id = static_cast<int>(blockIdx.x), xcd = id & 7, k = id >> 3;
-    const int pair = (k / a.chunk_tiles) * 8 + xcd, ct = k % a.chunk_tiles;
+    const int groups8 = (a.pairs + 7) >> 3;
+    const int pair = (k % groups8) * 8 + xcd, ct = a.chunk_tiles - 1 - k / groups8;
     if (pair >= a.pairs) return;
     const int kh = pair % a.lay.kv_heads;
     const int4 sd = a.seqs[pair / a.lay.kv_heads];  // table offset, start, rows, first query row
@@ -401,42 +407,405 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     if (__any(bad) && lane == 0) *a.err = 1;
 }
 
-// eight waves per workgroup (measured on MI355X against four: 158 against 225
-// us on the 8 x (2,048 + 512) chunk; K/V tiles are re-read by half as many
-// workgroups) and 64-key tiles (128-key tiles measured 177 us)
-template <int D, int G, int W, int TPB>
-void launch_gw(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
+// The same tiles and arithmetic, software-pipelined within each wave.
+// Iteration kt issues tile kt+1's S^T MFMAs beside the exponentials of tile
+// kt, then tile kt's PV MFMAs beside the scan of tile kt+1's scores.  The
+// rescale test takes each lane's own maximum: some lane's maximum exceeds the
+// threshold exactly when some row's does, so the cross-lane reduction runs
+// only on the rare tile that raises a running maximum.  Every product,
+// exponential and rescale is the one prefill_bf16_kernel performs, in the
+// same order, so the two kernels give the same bits.
+//
+// On MI355X this gains about 3% on the 8 x (2,048 + 512) chunk: a SIMD's
+// MFMA and vector work add up rather than overlap (16 MFMAs and 32
+// exponentials of one wave take 443 cycles against 264 and 275 apart, 405 of
+// 240 and 255 with two waves per SIMD), so the order within a wave matters
+// little.  What sets the time is the sum per 64-key tile and wave: 36 MFMAs
+// (576 cycles), 24 LDS operand reads, 32 exponentials and the staging.
+//
+// LDS keeps K one tile ahead of V: iteration kt reads K of tile kt+1 (buffer
+// (kt+1)&1) and V of tile kt (buffer kt&1), and writes K of tile kt+2 and V
+// of tile kt+1 into the other two, so one barrier per tile suffices.  The
+// rows written in iteration kt were requested from HBM one iteration before.
+template <int D, int G, int kWaves, int NT, bool kQ8, int TPB>
+__global__ __launch_bounds__(64 * kWaves) void prefill_pipe_kernel(const PrefillArgs a) {
+    constexpr int WR = 16 * NT;  // rows per wave: NT tiles of 16
+    constexpr int PW = WR / G;
+    constexpr int QT = kWaves * PW;
+    constexpr int KC = D / 32;
+    constexpr int DT = D / 16;
+    constexpr int KSTR = D + 8;
+    constexpr int VSTR = D + 16;
+    static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+    constexpr int LPR = D / 4;
+    constexpr int KPP = 64 * kWaves / LPR;
+    constexpr int SP = kKeys / KPP;
+    static_assert(SP >= 1 && SP * KPP == kKeys, "the staging map covers whole key rows");
+    __shared__ __attribute__((aligned(16))) __bf16 klds[2][kKeys * KSTR];
+    __shared__ __attribute__((aligned(16))) __bf16 vlds[2][kKeys * VSTR];
+
+    // the wave index is uniform: in a scalar register, every branch on a
+    // wave's rows and every block-table lookup is scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, r16 = lane & 15;
+    // workgroup order as in prefill_bf16_kernel
+    const int id = static_cast<int>(blockIdx.x), xcd = id & 7, k = id >> 3;
+    const int groups8 = (a.pairs + 7) >> 3;
+    const int pair = (k % groups8) * 8 + xcd, ct = a.chunk_tiles - 1 - k / groups8;
+    if (pair >= a.pairs) return;
+    const int kh = pair % a.lay.kv_heads;
+    const int4 sd = a.seqs[pair / a.lay.kv_heads];
+    const int start = sd.y, nrows = sd.z;
+    const int q0 = ct * QT;
+    if (q0 >= nrows) return;
+    const int kmax = start + min(q0 + QT, nrows);
+    const int ntiles = (kmax + kKeys - 1) / kKeys;
+    const int pw0 = q0 + wave * PW;
+    const int wave_kmax = pw0 < nrows ? start + min(pw0 + PW, nrows) : 0;
+    const int wtiles = (wave_kmax + kKeys - 1) / kKeys;  // tiles this wave's rows see (0: no rows)
+    const int kvw = a.lay.kv_width;
+    const int32_t* tab = a.tables + sd.x;
+
+    bf16x8 qop[NT][KC];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int r = 16 * nt + r16, pos = pw0 + r / G, head = kh * G + r % G;
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+            float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+            if (pos < nrows && r < PW * G) {
+                const float* qp = a.q + (static_cast<size_t>(sd.w + pos) * a.heads + head) * D + 32 * kc + 8 * g;
+                x0 = *reinterpret_cast<const float4*>(qp);
+                x1 = *reinterpret_cast<const float4*>(qp + 4);
+            }
+            const float s = a.qscale;
+            const bf16x4 lo = to_bf16(make_float4(x0.x * s, x0.y * s, x0.z * s, x0.w * s));
+            const bf16x4 hi = to_bf16(make_float4(x1.x * s, x1.y * s, x1.z * s, x1.w * s));
+            qop[nt][kc] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+    }
+
+    // staging map and block addressing as in prefill_bf16_kernel
+    const int skey = tid / LPR, col = 4 * (tid % LPR);
+    const int wkey = __builtin_amdgcn_readfirstlane(skey);
+    const int tpb = TPB ? TPB : a.lay.tpb, tsh = __builtin_ctz(static_cast<unsigned>(tpb));
+    const int lslot = skey & (tpb - 1);
+    const unsigned roff =
+        static_cast<unsigned>(kQ8 ? lslot * D + col : (lslot * kvw + col) * static_cast<int>(sizeof(float)));
+    const unsigned soff = static_cast<unsigned>(tpb * D + (lslot * (D / 32) + col / 32) * 2);
+    const int kvh = kh / a.kv_share;
+    const size_t kbytes = kQ8 ? static_cast<size_t>(a.layer) * 2 * a.lay.section + static_cast<size_t>(kvh) * a.lay.head_bytes
+                              : (static_cast<size_t>(a.layer) * 2 * tpb * kvw + static_cast<size_t>(kvh) * D) * sizeof(float);
+    const int vsec = static_cast<int>(kQ8 ? a.lay.section : static_cast<size_t>(tpb) * kvw * sizeof(float));
+    const int brange = static_cast<int>(a.lay.stride - kbytes);
+    // Loads are unconditional: rows past the chunk's reach read the last
+    // reachable block (see prefill_bf16_kernel); tiles past the last re-read it.
+    auto tile = [&](int t) { return min(t, ntiles - 1); };
+    auto blocks = [&](int kt, int (&b)[SP]) {
+#pragma unroll
+        for (int p = 0; p < SP; ++p) b[p] = tab[min(kt * kKeys + KPP * p + wkey, kmax - 1) >> tsh];
+    };
+    // one half (K: sec 0, V: sec vsec) of tile kt's rows
+    auto load = [&](int kt, const int (&b)[SP], int sec, f32x4 (&reg)[SP]) {
+#pragma unroll
+        for (int p = 0; p < SP; ++p) {
+            const int base = (kt * kKeys + KPP * p) & (tpb - 1);
+            const int rso = base * (kQ8 ? D : kvw * static_cast<int>(sizeof(float))), sso = base * (D / 32) * 2;
+            const char* blk =
+                a.pool + static_cast<size_t>(__builtin_amdgcn_readfirstlane(b[p])) * a.lay.stride + kbytes;
+            const __amdgpu_buffer_rsrc_t r =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(blk), 0, brange, kBufferWord3);
+            if constexpr (kQ8) {
+                const unsigned q = __builtin_amdgcn_raw_buffer_load_b32(r, roff, sec + rso, 0);
+                const unsigned sc = __builtin_amdgcn_raw_buffer_load_b16(r, soff, sec + sso, 0);
+                reg[p] = f32x4{__builtin_bit_cast(float, q), __builtin_bit_cast(float, sc), 0.f, 0.f};
+            } else {
+                reg[p] = __builtin_amdgcn_raw_buffer_load_b128(r, roff, sec + rso, 0);
+            }
+        }
+    };
+    auto values = [](f32x4 x) {
+        if constexpr (kQ8) {
+            const float x0 = x[0], x1 = x[1];
+            const uint32_t q = __builtin_bit_cast(uint32_t, x0);
+            const float d = half_bits_to_float(static_cast<uint16_t>(__builtin_bit_cast(uint32_t, x1)));
+            return f32x4{sbyte_to_float<0>(q) * d, sbyte_to_float<1>(q) * d, sbyte_to_float<2>(q) * d,
+                         sbyte_to_float<3>(q) * d};
+        } else {
+            return x;
+        }
+    };
+    auto kstore = [&](int buf, const f32x4 (&reg)[SP]) {
+#pragma unroll
+        for (int p = 0; p < SP; ++p)
+            *reinterpret_cast<bf16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = to_bf16(values(reg[p]));
+    };
+    auto vstore = [&](int kt, int buf, f32x4 (&reg)[SP]) {
+        if (kt * kKeys + kKeys > kmax) {  // the chunk's last tile: zero V past its reach
+#pragma unroll
+            for (int p = 0; p < SP; ++p)
+                if (kt * kKeys + KPP * p + skey >= kmax) reg[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int p = 0; p < SP; ++p)
+            *reinterpret_cast<bf16x4*>(&vlds[buf][(KPP * p + skey) * VSTR + col]) = to_bf16(values(reg[p]));
+    };
+
+    f32x4 acc[DT + 1][NT];
+#pragma unroll
+    for (int dt = 0; dt <= DT; ++dt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const __bf16 one = r16 == 0 ? static_cast<__bf16>(1.f) : static_cast<__bf16>(0.f);
+    const bf16x8 ones = bf16x8{one, one, one, one, one, one, one, one};
+    float m[NT];
+    int lim[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        m[nt] = -INFINITY;
+        lim[nt] = start + pw0 + (16 * nt + r16) / G;
+    }
+
+    typedef f32x4 Scores[4][NT];
+    typedef bf16x8 KOps[KC][4];
+    typedef bf16x8 VOps[2][DT];
+    // every K operand of the tile in K buffer kb, and every V operand (V^T by
+    // transposing reads, in the probabilities' key order: lane (g, i) gets
+    // column 16dt + i of keys 4g + j and 16 + 4g + j of key half kc) of the
+    // tile in V buffer vb
+    auto kops = [&](int kb, KOps& k) {
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                k[kc][mt] = *reinterpret_cast<const bf16x8*>(&klds[kb][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
+    };
+    auto vops = [&](int vb, VOps& v) {
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const __bf16* vrow = &vlds[vb][(32 * kc + 4 * g + (r16 >> 2)) * VSTR + 16 * dt + 4 * (r16 & 3)];
+                const bf16x4 lo = tr16_read(vrow);
+                const bf16x4 hi = tr16_read(vrow + 16 * VSTR);
+                v[kc][dt] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+    };
+    // S^T of row tile nt: accumulators starting at -m (0 before the first tile)
+    auto scores = [&](const KOps& k, Scores& s, int nt, bool first) {
+        const float c = first ? 0.f : -m[nt];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) s[mt][nt] = f32x4{c, c, c, c};
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k[kc][mt], qop[nt][kc], s[mt][nt], 0, 0, 0);
+    };
+    // the causal mask, for tiles that reach past a row's own position
+    auto mask = [&](int kbase, Scores& s) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (kbase + 16 * mt + 4 * g + i > lim[nt]) s[mt][nt][i] = -INFINITY;
+    };
+    auto lane_max = [](const Scores& s, int nt) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nt][i]);
+        return mx;
+    };
+    // raise each row's running maximum to the tile's (the tile's scores are
+    // relative to the old one) and rescale what was accumulated
+    auto rescale = [&](Scores& s) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const float up = fmaxf(cross_row_max(lane_max(s, nt)), 0.f);
+            const float alpha = fast_exp2(-up);
+            m[nt] += up;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) s[mt][nt] -= up;
+#pragma unroll
+            for (int dt = 0; dt <= DT; ++dt) acc[dt][nt] *= alpha;
+        }
+    };
+    // P^T (B operand of O^T = V^T P^T) for key half kc and row tile nt
+    auto probs = [](const Scores& s, int nt, int kc) {
+        float p[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[h][i] = fast_exp2(s[2 * kc + h][nt][i]);
+        const bf16x4 lo = to_bf16(make_float4(p[0][0], p[0][1], p[0][2], p[0][3]));
+        const bf16x4 hi = to_bf16(make_float4(p[1][0], p[1][1], p[1][2], p[1][3]));
+        return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    // Prologue: K and V of tile 0 and K of tile 1 in LDS, tile 0's scores in
+    // registers.  Staging then runs K one tile ahead of V: iteration kt
+    // writes K of tile kt+2 and V of tile kt+1, whose rows were requested
+    // from HBM one iteration earlier (requesting them two iterations earlier,
+    // in alternating register sets, measured no faster).
+    f32x4 kreg[SP], vreg[SP];
+    int bK[SP], bV[SP];  // block ids of the next loads (K of tile kt+3, V of tile kt+2)
+    Scores s;            // the current tile's scores, score - m, updated in place
+    {
+        f32x4 k0[SP], v0[SP], k1[SP];
+        int b0[SP], b1[SP], b2[SP];
+        blocks(0, b0);
+        blocks(tile(1), b1);
+        blocks(tile(2), b2);
+        load(0, b0, 0, k0);
+        load(0, b0, vsec, v0);
+        load(tile(1), b1, 0, k1);
+        load(tile(2), b2, 0, kreg);
+        load(tile(1), b1, vsec, vreg);
+        blocks(tile(3), bK);
+        blocks(tile(2), bV);
+        kstore(0, k0);
+        vstore(0, 0, v0);
+        kstore(1, k1);
+    }
+    __syncthreads();
+    if (wtiles > 0) {
+        KOps k;
+        kops(0, k);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) scores(k, s, nt, true);
+        if (kKeys - 1 > start + pw0) mask(0, s);
+        // every row sees key 0 in tile 0, so its maximum is finite
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            m[nt] = cross_row_max(lane_max(s, nt));
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) s[mt][nt] -= m[nt];
+        }
+    }
+    __syncthreads();  // tile 0's K is read before iteration 0 overwrites it
+
+    // Iteration kt (cb = kt & 1: reads K of tile kt+1 from buffer nb, V of
+    // tile kt from buffer cb; writes K of tile kt+2 to cb and V of tile kt+1
+    // to nb).  The row tiles go in two halves: half h's probabilities of tile
+    // kt leave s as bf16, then tile kt+1's scores for those rows are computed
+    // into the same registers while the other half is exponentiated.  Tile
+    // kt+1's scores are computed even past the wave's last tile (from
+    // whatever K buffer nb then holds, never used), so that every product and
+    // exponential of the iteration shares one basic block and one schedule.
+    constexpr int H = NT / 2;
+    auto step = [&](int kt, const int cb) {
+        const int nb = cb ^ 1;
+        if (kt < wtiles) {
+            KOps k;
+            VOps v;
+            kops(nb, k);
+            vops(cb, v);
+            bf16x8 pop[2][NT];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int nt = h * H; nt < h * H + H; ++nt) {
+                    pop[0][nt] = probs(s, nt, 0);
+                    pop[1][nt] = probs(s, nt, 1);
+                }
+#pragma unroll
+                for (int nt = h * H; nt < h * H + H; ++nt) scores(k, s, nt, false);
+            }
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt)
+                        acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v[kc][dt], pop[kc][nt], acc[dt][nt], 0, 0, 0);
+                    acc[DT][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[kc][nt], acc[DT][nt], 0, 0, 0);
+                }
+            const int kn = (kt + 1) * kKeys;
+            if (kn + kKeys - 1 > start + pw0) mask(kn, s);  // a tile reaching past a row's own position
+            bool up = false;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) up |= lane_max(s, nt) > kThreshold;
+            if (kt + 1 < wtiles && __any(up)) rescale(s);
+        }
+        kstore(cb, kreg);
+        vstore(tile(kt + 1), nb, vreg);
+        load(tile(kt + 3), bK, 0, kreg);
+        load(tile(kt + 2), bV, vsec, vreg);
+        blocks(tile(kt + 4), bK);
+        blocks(tile(kt + 3), bV);
+        __syncthreads();
+    };
+    // Both halves always run (the second's products are skipped past the
+    // last tile by kt < wtiles; its staging then re-reads the last tile):
+    // a break between them would give the loop a path on which the first
+    // half's loads are still in flight at the top, and the compiler would
+    // wait for them there.
+    for (int kt = 0; kt < ntiles; kt += 2) {
+        step(kt, 0);
+        step(kt + 1, 1);
+    }
+
+    bool bad = false;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const float l = __shfl(acc[DT][nt][0], r16);
+        const int r = 16 * nt + r16, pos = pw0 + r / G, head = kh * G + r % G;
+        if (pos >= nrows || r >= PW * G) continue;
+        float* o = a.out + (static_cast<size_t>(sd.w + pos) * a.heads + head) * D + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const f32x4 v = acc[dt][nt] / l;
+            bad |= !__builtin_isfinite(v[0]) || !__builtin_isfinite(v[1]) || !__builtin_isfinite(v[2]) ||
+                   !__builtin_isfinite(v[3]);
+            *reinterpret_cast<float4*>(o + 16 * dt) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    if (__any(bad) && lane == 0) *a.err = 1;
+}
+
+// Kernel choice, TVARA_PREFILL_PIPE (read on every launch, so one process
+// can compare them; results are bit-identical): 0 prefill_bf16_kernel, 1
+// prefill_pipe_kernel; unset, the pipelined kernel at head_dim 64 and the
+// plain one at 128, where the pipelined kernel's operand sets do not fit in
+// registers beside its accumulators.  Both run eight waves of 32 rows, 256
+// rows per workgroup, over 64-key tiles (eight waves of the plain kernel
+// measured 158 against 225 us for four on the 8 x (2,048 + 512) chunk;
+// 128-key tiles 177 us).
+template <int D, int G, int TPB>
+void launch_gt(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
+    const char* env = std::getenv("TVARA_PREFILL_PIPE");
+    const bool pipe = env ? std::atoi(env) != 0 : D == 64;
     const bool q8 = a.lay.format == kQ8;
-    constexpr int QT = W * (kRows / G);
+    constexpr int W = 8, QT = W * (kRows / G);  // chunk positions per workgroup
     PrefillArgs b = a;
     b.chunk_tiles = (max_rows + QT - 1) / QT;
     b.pairs = nseqs * a.lay.kv_heads;
-    const int groups8 = (b.pairs + 7) / 8;  // ids = 8 XCDs x pair groups x chunk tiles
+    const int groups8 = (b.pairs + 7) / 8;  // ids = 8 XCDs x chunk tiles x pair groups
     const dim3 grid(8 * groups8 * b.chunk_tiles), block(64 * W);
-    if (q8)
+    if (pipe) {
+        if (q8)
+            launch("paged_prefill_bf16", prefill_pipe_kernel<D, G, W, 2, true, TPB>, grid, block, 0, s, b);
+        else
+            launch("paged_prefill_bf16", prefill_pipe_kernel<D, G, W, 2, false, TPB>, grid, block, 0, s, b);
+    } else if (q8) {
         launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W, true, TPB>, grid, block, 0, s, b);
-    else
+    } else {
         launch("paged_prefill_bf16", prefill_bf16_kernel<D, G, W, false, TPB>, grid, block, 0, s, b);
+    }
 }
 
-// waves per workgroup (TVARA_PREFILL_WAVES: 4 or 8, for blocks of 16 tokens;
-// other block sizes take 8)
+// blocks of 16 tokens fold the block arithmetic at compile time; other
+// powers of two read it from the layout
 template <int G>
 void launch_g(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
-    static const int waves = [] {
-        const char* env = std::getenv("TVARA_PREFILL_WAVES");
-        return env && std::atoi(env) == 4 ? 4 : 8;
-    }();
-    if (a.lay.tpb != 16) {
-        if (a.lay.head_dim == 128)
-            launch_gw<128, G, 8, 0>(a, nseqs, max_rows, s);
-        else
-            launch_gw<64, G, 8, 0>(a, nseqs, max_rows, s);
-    } else if (a.lay.head_dim == 128) {
-        waves == 4 ? launch_gw<128, G, 4, 16>(a, nseqs, max_rows, s) : launch_gw<128, G, 8, 16>(a, nseqs, max_rows, s);
-    } else {
-        waves == 4 ? launch_gw<64, G, 4, 16>(a, nseqs, max_rows, s) : launch_gw<64, G, 8, 16>(a, nseqs, max_rows, s);
-    }
+    if (a.lay.head_dim == 128)
+        a.lay.tpb == 16 ? launch_gt<128, G, 16>(a, nseqs, max_rows, s) : launch_gt<128, G, 0>(a, nseqs, max_rows, s);
+    else
+        a.lay.tpb == 16 ? launch_gt<64, G, 16>(a, nseqs, max_rows, s) : launch_gt<64, G, 0>(a, nseqs, max_rows, s);
 }
 
 }  // namespace
