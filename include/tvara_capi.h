@@ -255,6 +255,12 @@ TVARA_API int tvara_kv_drop(tvara_kv_cache* cache, uint64_t sequence);
 TVARA_API uint64_t tvara_kv_fork(tvara_kv_cache* cache, uint64_t sequence);
 /* PagedCache::truncate (kv.hpp:131-136) */
 TVARA_API int tvara_kv_truncate(tvara_kv_cache* cache, uint64_t sequence, size_t length);
+/* `count` truncations, in order: sequence i to lengths[i] tokens, as a loop
+ * over PagedCache::truncate (kv.hpp:131-136) would apply them (a batch's
+ * speculative rollback in one call).  On failure of truncation k, 0..k-1
+ * stay applied, k changes nothing, and *applied = k. */
+TVARA_API int tvara_kv_truncate_batch(tvara_kv_cache* cache, const uint64_t* sequences, const size_t* lengths,
+                                      size_t count, size_t* applied);
 /* PagedCache::audit (kv.hpp:138-146); external may be NULL (count 0) */
 TVARA_API int tvara_kv_audit(tvara_kv_cache* cache, const size_t* external, size_t count);
 /* PagedCache::import_sequence (kv.hpp:149-159) from a snapshot's handles; 0 on failure */

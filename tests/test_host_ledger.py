@@ -135,3 +135,45 @@ def test_sanitized_gguf_reader(host_build, tmp_path, request):
         assert line.startswith("error: "), (label, line)
         if ref_capi.exists():
             assert line[len("error: "):] == tm.opened_error(path, str(ref_capi)), label
+
+
+def test_truncate_batch_matches_single_truncations(host_lib):
+    """tvara_kv_truncate_batch against a loop of tvara_kv_truncate on a twin
+    cache: the same pool state after a valid batch, and after a batch whose
+    third entry fails (a length past the sequence's end) the same state as
+    the first two single calls, with the failure's class and the applied
+    count reported."""
+    import numpy as np
+
+    from tvara_amd._capi import InvalidArgument
+
+    geometry = (2, 1, 4, 4, 40)
+    caches = [_make(host_lib)(*geometry) for _ in range(2)]
+    ids = []
+    for c in caches:
+        base = c.create_sequence()
+        for t in range(10):
+            c.append(base, np.full(8, t, np.float32), np.full(8, -t, np.float32))
+        seqs = [base] + [c.fork(base) for _ in range(3)]
+        for j, s in enumerate(seqs[1:]):
+            for t in range(j + 2):
+                c.append(s, np.full(8, 100 + t, np.float32), np.full(8, 200 + t, np.float32))
+        ids.append(seqs)
+    assert ids[0] == ids[1]
+    seqs = ids[0]
+    lengths = [7, 12, 3, 9]
+    assert caches[0].truncate_batch(seqs, lengths) == 4
+    for s, n in zip(seqs, lengths):
+        caches[1].truncate(s, n)
+    assert caches[0].state() == caches[1].state()
+    bad = [5, 4, 99, 1]
+    with pytest.raises(InvalidArgument) as err:
+        caches[0].truncate_batch(seqs, bad)
+    assert caches[0].last_applied == 2
+    for s, n in zip(seqs[:2], bad[:2]):
+        caches[1].truncate(s, n)
+    with pytest.raises(InvalidArgument) as err1:
+        caches[1].truncate(seqs[2], bad[2])
+    assert str(err.value) == str(err1.value)
+    assert caches[0].state() == caches[1].state()
+    assert caches[0].truncate_batch([], []) == 0

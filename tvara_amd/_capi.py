@@ -87,6 +87,7 @@ SIGNATURES = {
     "tvara_kv_drop": (C.c_int, [_vp, _u64]),
     "tvara_kv_fork": (_u64, [_vp, _u64]),
     "tvara_kv_truncate": (C.c_int, [_vp, _u64, _sz]),
+    "tvara_kv_truncate_batch": (C.c_int, [_vp, C.POINTER(_u64), C.POINTER(_sz), _sz, C.POINTER(_sz)]),
     "tvara_kv_audit": (C.c_int, [_vp, C.POINTER(_sz), _sz]),
     "tvara_kv_import_sequence": (_u64, [_vp, C.POINTER(Handle), _sz, _sz, _sz]),
     "tvara_attn_decode": (C.c_int, [_vp, C.POINTER(_u64), _sz, _sz, _sz, _sz, _fp, _fp, _fp, C.POINTER(_sz), _fp,

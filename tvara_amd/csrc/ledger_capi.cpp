@@ -131,6 +131,20 @@ int tvara_kv_truncate(tvara_kv_cache* cache, uint64_t sequence, size_t length) {
     return guard([&] { ledger_of(cache).truncate(sequence, length); });
 }
 
+// PagedCache::truncate (kv.hpp:131-136) over a list, in order; a failure at
+// entry k leaves entries 0..k-1 applied and reports k in *applied
+int tvara_kv_truncate_batch(tvara_kv_cache* cache, const uint64_t* sequences, const size_t* lengths, size_t count,
+                            size_t* applied) {
+    size_t done = 0;
+    const int rc = guard([&] {
+        if (count && (!sequences || !lengths)) throw std::invalid_argument("null truncation batch");
+        KvLedger& ledger = ledger_of(cache);
+        for (; done < count; ++done) ledger.truncate(sequences[done], lengths[done]);
+    });
+    if (applied) *applied = done;
+    return rc;
+}
+
 int tvara_kv_audit(tvara_kv_cache* cache, const size_t* external, size_t count) {
     return guard([&] { ledger_of(cache).audit(external, external ? count : 0); });
 }
