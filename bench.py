@@ -13,6 +13,8 @@ line each, the headline last:
   c4     chunked prefill: 8 x (2,048 cached + 512-token causal chunk), 32/8
          heads, d=64, bf16 MFMA;
   c5     Llama-3-8B decode: 16 x 32,768 tokens, 32/8 heads, d=128, Q8_0;
+  llama1b  a Llama-3.2-1B-shaped model with random Q8_0 weights through the
+         model-level C ABI: 64 sequences a step, and one sequence alone;
   c2     (headline, printed last) Llama-3.2-1B decode: 64 sequences, 32/8
          heads, d=64, f32 KV, contexts uniform in [128, 4096], 16-token blocks
          scattered over a 65,536-block pool.
@@ -28,12 +30,12 @@ nine runs, on one thread and on every host thread the box grants, with the
 host's CPU model, core count, compiler, flags, AVX2 use and a STREAM-style
 triad bandwidth.
 
-Other shapes, one line each with --workload: c4d128 and c4q8 (the chunks at
-head_dim 128 and over Q8_0 blocks), gqa8 / gqa8q8 (Llama-3-70B, eight query
+Other shapes, one line each with --workload: c4d128, c4q8 and c4f32 (the
+chunks at head_dim 128, over Q8_0 blocks, and in f32 through the decode
+kernels), gqa8 / gqa8q8 (Llama-3-70B, eight query
 heads per KV head), gqa16 / gqa16q8 (Llama-3.1-405B, sixteen, run as two
 slices), tiny / tinyq8 (TinyLlama-1.1B), gemma2 (head_dim 256), phi3
-(head_dim 96) and llama1b (a Llama-3.2-1B-shaped model through the
-model-level C ABI).
+(head_dim 96).
 """
 
 from __future__ import annotations
@@ -56,7 +58,7 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16
 METRIC = "paged decode attn: achieved HBM GB/s (% of peak) + decode tokens/s, 1 MI355X"
 MODEL_LAYERS = {"llama-3.2-1b-decode-64x[128,4096]": 16, "smollm2-135m-decode-1x512": 30,
                 "llama-3-8b-q8_0-decode-16x32768": 32}
-DEFAULT_RUN = ["c1", "t176", "c3", "c3cow", "c4", "c5", "c2"]
+DEFAULT_RUN = ["c1", "t176", "c3", "c3cow", "c4", "c5", "llama1b", "c2"]
 REF_FLAGS = "g++ -O2 -std=c++20 -fPIC (oracle/Makefile, target ref; the reference's recorded flags)"
 
 
@@ -196,14 +198,40 @@ def kernel_times(call, steps, names):
     return out
 
 
+TRAFFIC_FILE = "profiles/hbm_traffic.json"
+
+
+def _traffic_entries():
+    f = ROOT / TRAFFIC_FILE
+    return json.loads(f.read_text()) if f.exists() else {}
+
+
 def hbm_traffic(workload, kernel):
-    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    (profiles/hbm_traffic.json, written from those runs), or None."""
-    f = ROOT / "profiles" / "hbm_traffic.json"
-    if not f.exists():
-        return None
-    entry = json.loads(f.read_text()).get(f"{workload}/{kernel}")
-    return None if entry is None else int(entry["bytes_per_launch"])
+    """The roofline's traffic fields: HBM bytes per launch of `kernel` on
+    `workload` as counted by two rocprofv3 --pmc runs (FETCH_SIZE, then
+    WRITE_SIZE, scaled by the copy-kernel calibration) and recorded in
+    profiles/hbm_traffic.json; read from that file, not measured in this run."""
+    entry = _traffic_entries().get(f"{workload}/{kernel}")
+    if entry is None:
+        return {"traffic": None, "traffic_source": f"no {TRAFFIC_FILE} entry for {workload}/{kernel}"}
+    return {"traffic": int(entry["bytes_per_launch"]),
+            "traffic_source": f"{TRAFFIC_FILE} {workload}/{entry.get('kernel', kernel)}: FETCH_SIZE + WRITE_SIZE "
+                              "per dispatch from rocprofv3 --pmc runs, not this run"}
+
+
+def kv_traffic(workload, steps):
+    """C3's traffic per append step: the append kernel's bytes per launch
+    plus the zero-fill / copy kernel's bytes per launch times its launches
+    per pass over the pass's steps (profiles/hbm_traffic.json)."""
+    e = _traffic_entries()
+    ap, bi = e.get(f"{workload}/kv_append"), e.get(f"{workload}/kv_block_init")
+    if ap is None or bi is None:
+        return {"traffic": None, "traffic_source": f"no {TRAFFIC_FILE} entries for {workload}"}
+    per_step = ap["bytes_per_launch"] + bi["bytes_per_launch"] * bi["launches_per_pass"] / steps
+    return {"traffic": int(round(per_step)),
+            "traffic_source": f"{TRAFFIC_FILE} {workload}: FETCH_SIZE + WRITE_SIZE of {ap['kernel']} per launch "
+                              f"plus {bi['kernel']} x {bi['launches_per_pass']} launches per {steps}-step pass, "
+                              "from rocprofv3 --pmc runs, not this run"}
 
 
 # ----------------------------------------------------------------- decode
@@ -302,6 +330,13 @@ def bench_decode(args, key, w):
     kt = kernel_times(step, args.steps, ["paged_decode", "paged_decode_merge"])
     kernel_avg_ms, launches = kt["paged_decode"]
     merge_ms, merges = kt["paged_decode_merge"]
+    kernel_source = "start/stop events the runtime stamps on each launch, a second pass of the same steps"
+    if not merges and kernel_avg_ms > ms_per_step:
+        # a one-launch step (the split merge runs in the kernel): the events'
+        # own packets can lengthen a launch of a few microseconds past the
+        # step that contains it, so the step time bounds the kernel
+        kernel_avg_ms = ms_per_step
+        kernel_source = "the step time: the step is this one launch (its event-bracketed duration was longer)"
     log(f"step {ms_per_step * 1e3:.1f} us; decode kernel {kernel_avg_ms * 1e3:.1f} us x{launches}; "
         f"merge {merge_ms * 1e3:.1f} us x{merges}")
     assert np.isfinite(out.numpy()).all()
@@ -344,8 +379,9 @@ def bench_decode(args, key, w):
         "model_layers": layers,
         "host_buffers_ms_per_step": round(host_ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), "traffic": hbm_traffic(w.name, "paged_decode"),
+                     "frac": round(kernel_gbs / HBM_PEAK_GBS, 4), **hbm_traffic(w.name, "paged_decode"),
                      "kernel": "paged_decode", "kernel_avg_us": round(kernel_avg_ms * 1e3, 3),
+                     "kernel_time_source": kernel_source,
                      "merge_avg_us": round(merge_ms * 1e3, 3) if merges else 0.0,
                      "algorithmic_bytes": kernel_bytes},
         "cpu_baseline": None,
@@ -396,9 +432,15 @@ def cpu_prefill(w):
                       chunk_flops(w, 0, n1) / 1e12, chunk_flops(w, 0, w.chunk) / 1e12)
 
 
-def bench_prefill(args, w):
-    """Chunked prefill: the bf16 MFMA kernel's TFLOP/s over the algorithmic
-    flops of the causal chunks."""
+FP32_PEAK_TFS = 157.3  # MI355X dense fp32 (matrix)
+
+
+def bench_prefill(args, w, precision="bf16"):
+    """Chunked prefill: TFLOP/s over the algorithmic flops of the causal
+    chunks.  bf16: the MFMA kernel.  f32 (the reference's arithmetic, within
+    1e-4): every chunk row runs as a decode row whose visible length stops at
+    its own position (attention.hpp:85-89), through the decode kernels and the
+    split merge; its dominant kernel is priced against the fp32 peak."""
     import numpy as np
 
     from tvara_amd import attention, hip, kv, workloads
@@ -411,30 +453,37 @@ def bench_prefill(args, w):
     # one plan per prompt chunk (as an executor keeps it for every layer); a
     # step is one launch of it
     plan = attention.PrefillPlan(cache, seqs, [w.prefix] * w.sequences, [w.chunk] * w.sequences, w.heads, w.context,
-                                 "bf16")
+                                 precision)
     call = lambda: plan.launch(0, q.ptr, out.ptr)  # noqa: E731
     for _ in range(args.warmup):
         call()
     plan.check()
-    ms_per_step = timed_steps(call, args.steps)
-    kernel_ms, _ = kernel_times(call, args.steps, ["paged_prefill_bf16"])["paged_prefill_bf16"]
+    steps = args.steps if precision == "bf16" else max(1, min(args.steps, 20))
+    ms_per_step = timed_steps(call, steps)
+    kernel = "paged_prefill_bf16" if precision == "bf16" else "paged_decode"
+    kt = kernel_times(call, steps, [kernel, "paged_decode_merge"])
+    kernel_ms, _ = kt[kernel]
+    merge_ms, merges = kt["paged_decode_merge"]
     plan.check()
     assert np.isfinite(out.numpy()).all()
     tfs = w.flops() / (kernel_ms * 1e-3) / 1e12
-    log(f"prefill kernel {kernel_ms * 1e3:.1f} us, call {ms_per_step * 1e3:.1f} us, {tfs:.1f} TFLOP/s")
+    log(f"prefill ({precision}) kernel {kernel_ms * 1e3:.1f} us, call {ms_per_step * 1e3:.1f} us, {tfs:.1f} TFLOP/s")
     del plan, cache, q, out
+    peak = MFMA_BF16_PEAK_TFS if precision == "bf16" else FP32_PEAK_TFS
+    name = w.name if precision == "bf16" else w.name + "-f32"
     result = {
-        "metric": "paged chunked prefill attn: achieved TFLOP/s (MFMA utilisation), 1 MI355X",
+        "metric": "paged chunked prefill attn: achieved TFLOP/s (MFMA utilisation), 1 MI355X"
+        if precision == "bf16" else "paged chunked prefill attn, f32 (reference arithmetic): achieved TFLOP/s, 1 MI355X",
         "value": round(w.flops() / (ms_per_step * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic: K/V/q ~ N(0,1)",
-        "config": {"workload": w.name, "sequences": w.sequences, "prefix": w.prefix, "chunk": w.chunk,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": precision, "data": "synthetic: K/V/q ~ N(0,1)",
+        "config": {"workload": name, "sequences": w.sequences, "prefix": w.prefix, "chunk": w.chunk,
                    "heads": w.heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
-                   "kv": "q8_0" if w.q8 else "f32"},
-        "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
-                     "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
-                     "traffic": hbm_traffic(w.name, "paged_prefill_bf16"), "kernel": "paged_prefill_bf16",
-                     "kernel_avg_us": round(kernel_ms * 1e3, 3), "algorithmic_flops": w.flops()},
+                   "kv": "q8_0" if w.q8 else "f32", "precision": precision},
+        "roofline": {"bound": "mfma" if precision == "bf16" else "fp32", "achieved": round(tfs, 2), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(tfs / peak, 4), **hbm_traffic(name, kernel),
+                     "kernel": kernel, "kernel_avg_us": round(kernel_ms * 1e3, 3),
+                     "merge_avg_us": round(merge_ms * 1e3, 3) if merges else 0.0, "algorithmic_flops": w.flops()},
         "cpu_baseline": None,
     }
     if ref_ready(args) and not w.q8:
@@ -525,13 +574,24 @@ def bench_kv(args, cow):
         cache.synchronize()
         return seqs
 
-    def run_pass(seqs, first, count):
+    # the seeded rollback: every sequence back by 0-64 tokens from the
+    # length a pass leaves (the scheduler knows its sequences' lengths)
+    kept = np.asarray([w.prefix + w.steps - r for r in w.rollback()], np.uintp)
+
+    def run_pass(seqs):
+        """One whole pass: the 128 append steps, then the seeded 0-64 token
+        speculative rollback of every sequence (metadata only, one batched
+        truncation), between two events on the cache's stream.  The stop
+        event is recorded once the host has issued every append and the
+        rollback, so the interval covers the host's work where it outlasts
+        the GPU's."""
         batch = np.asarray(seqs, np.uint64)  # the batch as a scheduler holds it
         start, stop = hip.Event(), hip.Event()
         hip.synchronize()
         start.record()
-        for i in range(first, first + count):
+        for i in range(w.steps):
             cache.append_batch_device(batch, steps_k[i].ptr, steps_v[i].ptr)
+        cache.truncate_batch(batch, kept)
         stop.record()
         hip.synchronize()
         return start.elapsed_ms(stop)
@@ -539,21 +599,20 @@ def bench_kv(args, cow):
     # warm-up: whole passes, untimed
     for _ in range(max(1, args.warmup // w.steps)):
         seqs = setup()
-        run_pass(seqs, 0, w.steps)
+        run_pass(seqs)
         for s in seqs:
             cache.drop(s)
-    total_ms, done, nbytes = 0.0, 0, 0
-    while done < args.steps:
+    # timed: whole passes only, as many as --steps asks for (at least one)
+    passes = max(1, -(-args.steps // w.steps))
+    total_ms = 0.0
+    for _ in range(passes):
         seqs = setup()
-        n = min(w.steps, args.steps - done)
-        total_ms += run_pass(seqs, 0, n)
-        nbytes += sum(step_bytes(i) for i in range(n))
-        done += n
-        for s, r in zip(seqs, w.rollback()):  # speculative rollback (metadata only)
-            cache.truncate(s, cache.length(s) - r)
+        total_ms += run_pass(seqs)
         cache.audit()
         for s in seqs:
             cache.drop(s)
+    done = passes * w.steps
+    nbytes = passes * sum(step_bytes(i) for i in range(w.steps))
     ms_per_step = total_ms / done
     gbs = nbytes / (total_ms * 1e-3) / 1e9
     log(f"{w.name}: {ms_per_step * 1e3:.1f} us per step, {gbs:.1f} GB/s")
@@ -564,11 +623,12 @@ def bench_kv(args, cow):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic: K/V rows from a seeded splitmix64 stream (floats in [1, 2))",
         "config": {"workload": w.name, "sequences": w.sequences, "prefix": w.prefix, "steps_per_pass": w.steps,
+                   "passes": passes, "rollback": "seeded 0-64 tokens per sequence, inside the timed pass",
                    "layers": w.layers, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
                    "tokens_per_block": w.tokens_per_block},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "kv_append (step)",
-                     "algorithmic_bytes_per_step": round(nbytes / done)},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "kernel": "kv_append (step)",
+                     "algorithmic_bytes_per_step": round(nbytes / done), **kv_traffic(w.name, w.steps)},
         "cpu_baseline": None,
     }
     if ref_ready(args):
@@ -671,7 +731,8 @@ def bench_model(args):
             "single_sequence_weight_GBps": round(weight_bytes / single_s / 1e9, 1),
             "roofline": {"bound": "hbm", "achieved": round(step_bytes / batch_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(step_bytes / batch_s / 1e9 / HBM_PEAK_GBS, 4),
-                         "traffic": None, "kernel": "whole decode step (Q8_0 weights once + cached K/V)",
+                         "traffic": None, "traffic_source": "not counted: a step is about 180 launches of 20 kernels",
+                         "kernel": "whole decode step (Q8_0 weights once + cached K/V)",
                          "algorithmic_bytes": step_bytes, "weight_bytes": weight_bytes, "kv_bytes": kv_bytes},
             "cpu_baseline": cpu,
         }
@@ -689,7 +750,7 @@ def compact(r):
            "config": {"workload": r["config"]["workload"]},
            "roofline": {k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
            "cpu_baseline": None}
-    for k in ("kernel_avg_us", "merge_avg_us"):
+    for k in ("kernel", "kernel_avg_us", "merge_avg_us", "kernel_time_source", "traffic_source"):
         if k in r["roofline"]:
             out["roofline"][k] = r["roofline"][k]
     for k in ("latency_us", "reference_published", "decode_tokens_per_s", "model_decode_tokens_per_s"):
@@ -705,9 +766,10 @@ def compact(r):
 def run_one(args, key):
     from tvara_amd import workloads
 
-    if key in ("c4", "c4d128", "c4q8"):
-        make = {"c4": workloads.prefill_c4, "c4d128": workloads.prefill_8b, "c4q8": workloads.prefill_c4_q8}
-        return bench_prefill(args, make[key]())
+    if key in ("c4", "c4d128", "c4q8", "c4f32"):
+        make = {"c4": workloads.prefill_c4, "c4d128": workloads.prefill_8b, "c4q8": workloads.prefill_c4_q8,
+                "c4f32": workloads.prefill_c4}
+        return bench_prefill(args, make[key](), "f32" if key == "c4f32" else "bf16")
     if key in ("c3", "c3cow"):
         return bench_kv(args, key == "c3cow")
     if key == "llama1b":
@@ -727,10 +789,10 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2", "phi3",
+                    choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c4f32", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2", "phi3",
                              "tiny", "tinyq8", "t176", "llama1b"],
-                    help="one configuration; `all` (the default) runs c1, c3, c3cow, c4 and c5, one JSON line "
-                         "each, then the c2 headline line last")
+                    help="one configuration; `all` (the default) runs c1, t176, c3, c3cow, c4, c5 and llama1b, "
+                         "one JSON line each, then the c2 headline line last")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--copy-mib", type=int, default=0,
