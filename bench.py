@@ -13,6 +13,9 @@ line each, the headline last:
   c4     chunked prefill: 8 x (2,048 cached + 512-token causal chunk), 32/8
          heads, d=64, bf16 MFMA;
   c5     Llama-3-8B decode: 16 x 32,768 tokens, 32/8 heads, d=128, Q8_0;
+  prefix the prefix cache: the reference's radix benchmark (10,000 lookups
+         with a KV restore, 75% hits), ns per request beside its published
+         933 ns;
   llama1b  a Llama-3.2-1B-shaped model with random Q8_0 weights through the
          model-level C ABI: 64 sequences a step, and one sequence alone;
   c2     (headline, printed last) Llama-3.2-1B decode: 64 sequences, 32/8
@@ -58,7 +61,7 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16
 METRIC = "paged decode attn: achieved HBM GB/s (% of peak) + decode tokens/s, 1 MI355X"
 MODEL_LAYERS = {"llama-3.2-1b-decode-64x[128,4096]": 16, "smollm2-135m-decode-1x512": 30,
                 "llama-3-8b-q8_0-decode-16x32768": 32}
-DEFAULT_RUN = ["c1", "t176", "c3", "c3cow", "c4", "c5", "llama1b", "c2"]
+DEFAULT_RUN = ["c1", "t176", "c3", "c3cow", "c4", "c5", "prefix", "llama1b", "c2"]
 REF_FLAGS = "g++ -O2 -std=c++20 -fPIC (oracle/Makefile, target ref; the reference's recorded flags)"
 
 
@@ -636,6 +639,73 @@ def bench_kv(args, cow):
     return result
 
 
+# ----------------------------------------------------------- prefix cache
+
+PREFIX_PUBLISHED_NS = 933.08  # bench/results/radix-prefix.json: 9,330,800 ns for 10,000 requests
+
+
+def prefix_driver():
+    """bench_prefix.cpp built into build/release (by build() or here, when
+    missing or older than its source)."""
+    src = ROOT / "bench_prefix.cpp"
+    exe = ROOT / "build" / "release" / "bench_prefix"
+    if not exe.exists() or exe.stat().st_mtime < src.stat().st_mtime:
+        exe.parent.mkdir(parents=True, exist_ok=True)
+        subprocess.run(["g++", "-O2", "-std=c++17", "-o", str(exe), str(src), "-ldl"], check=True)
+    return exe
+
+
+def run_prefix_driver(kind, library, runs=9):
+    res = subprocess.run([str(prefix_driver()), kind, str(library), str(runs)], capture_output=True, text=True,
+                         timeout=300)
+    if res.returncode != 0:
+        raise RuntimeError(f"bench_prefix {kind} failed ({res.returncode}): {res.stderr[-2000:]}")
+    return json.loads(res.stdout)
+
+
+def bench_prefix(args):
+    """The prefix cache: the reference's radix benchmark (bench/radix_prefix.cpp:
+    10,000 lookups with a KV restore of an 8-token prefix, 75% hits) through
+    this library's C ABI, timed in C++ as the reference times it.  Host
+    metadata only (the prefix tree and the block ledger): no kernel runs."""
+    from tvara_amd import _capi
+
+    mine = run_prefix_driver("tvara", _capi.find_library())
+    ns = statistics.median(mine["runs_ns"]) / mine["requests"]
+    log(f"prefix cache: {ns:.1f} ns per request (median of {len(mine['runs_ns'])} runs of 10,000)")
+    result = {
+        "metric": "prefix cache lookup + KV restore: ns per request (10,000 requests, 75% hits), 1 MI355X host",
+        "value": round(ns, 2), "unit": "ns/request", "n_gpus": 1, "steps": mine["requests"],
+        "warmup": mine["requests"], "ms_per_step": round(ns * 1e-6, 8), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int32 tokens",
+        "data": "the reference's fixture: an 8-token prefix in 4-token blocks; every fourth request misses",
+        "config": {"workload": "radix-prefix-10000x8-75pct", "requests": mine["requests"], "hits": mine["hits"],
+                   "saved_prefill_tokens": mine["saved_prefill_tokens"], "runs": len(mine["runs_ns"]),
+                   "runs_ns": mine["runs_ns"]},
+        "reference_published": {"ns_per_request": PREFIX_PUBLISHED_NS,
+                                "source": "bench/results/radix-prefix.json (host A: Intel Family 6 Model 61, "
+                                          "Windows 11, one run)"},
+        "roofline": {"bound": "host", "achieved": None, "peak": None, "unit": "ns/request", "frac": None,
+                     "traffic": None, "traffic_source": "none: no device memory is touched",
+                     "kernel": "none: host metadata (prefix tree and block ledger)"},
+        "cpu_baseline": None,
+    }
+    if ref_ready(args):
+        def job():
+            from oracle import pyoracle
+
+            ref = run_prefix_driver("ref", pyoracle.REF_PATH)
+            rns = statistics.median(ref["runs_ns"]) / ref["requests"]
+            assert (ref["hits"], ref["saved_prefill_tokens"]) == (mine["hits"], mine["saved_prefill_tokens"])
+            return {"value": round(rns, 2), "unit": "ns/request", "cores": 1, "kind": "reference",
+                    "sample": "the same 10,000 requests through the reference's RadixCache and PagedCache built "
+                              "from its headers (oracle/_ref), timed by the same driver",
+                    "protocol": "1 warm-up run, median of 9 runs", "runs_ns": ref["runs_ns"], "host": host_info()}
+
+        baseline(result, job)
+    return result
+
+
 # ------------------------------------------------------------------ model
 
 def bench_model(args):
@@ -774,6 +844,8 @@ def run_one(args, key):
         return bench_kv(args, key == "c3cow")
     if key == "llama1b":
         return bench_model(args)
+    if key == "prefix":
+        return bench_prefix(args)
     w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5,
          "gqa8": workloads.decode_gqa8, "gqa8q8": lambda: workloads.decode_gqa8(q8=True),
          "gqa16": workloads.decode_gqa16, "gqa16q8": lambda: workloads.decode_gqa16(q8=True),
@@ -790,8 +862,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="all",
                     choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c4f32", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2", "phi3",
-                             "tiny", "tinyq8", "t176", "llama1b"],
-                    help="one configuration; `all` (the default) runs c1, t176, c3, c3cow, c4, c5 and llama1b, "
+                             "tiny", "tinyq8", "t176", "llama1b", "prefix"],
+                    help="one configuration; `all` (the default) runs c1, t176, c3, c3cow, c4, c5, prefix and llama1b, "
                          "one JSON line each, then the c2 headline line last")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-tokens", type=int, default=0)

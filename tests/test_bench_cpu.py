@@ -33,3 +33,27 @@ def test_decode_baseline_record(ref):
     host = r["host"]
     assert host["nproc"] >= 1 and host["compiler"].startswith("g++") and isinstance(host["avx2_dot"], bool)
     assert host["triad_GBps_1thread"] > 0
+
+
+def test_prefix_driver_replays_the_reference_workload(ref):
+    """bench_prefix.cpp through the library's own ledger and prefix tree (the
+    HIP-free host build) and through the reference's RadixCache: both give
+    the counts the reference's benchmark records (bench/results/
+    radix-prefix.json: 7,500 hits, 60,000 saved of 80,000 requested tokens)."""
+    import shutil
+    import subprocess
+
+    import pytest
+
+    if not shutil.which("g++") or not shutil.which("make"):
+        pytest.skip("g++ / make not available")
+    native = Path(__file__).resolve().parents[0] / "native"
+    res = subprocess.run(["make", "-C", str(native)], capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    from oracle import pyoracle
+
+    for kind, lib in (("tvara", native / "_build" / "libtvara_host.so"), ("ref", pyoracle.REF_PATH)):
+        r = bench.run_prefix_driver(kind, lib, runs=2)
+        assert (r["requests"], r["hits"], r["saved_prefill_tokens"], r["requested_tokens"]) == (10000, 7500, 60000,
+                                                                                                 80000), (kind, r)
+        assert len(r["runs_ns"]) == 2 and min(r["runs_ns"]) > 0
