@@ -598,16 +598,25 @@ def test_large_blocks_fast_kernels(device, oracle, tpb, dim, kv_heads, group):
         assert refmath.close(got, want, TOL), (length, kw, refmath.max_rel(got, want))
 
 
-@pytest.mark.parametrize("tpb", [32, 64])
+@pytest.mark.parametrize("tpb", [32, 64, 128, 1024])
 def test_row_major_large_blocks(device, oracle, monkeypatch, tpb):
-    # the row-major kernel over 32- and 64-token blocks: a 16-row tile is a
-    # quarter or half of a block
+    # the row-major kernel over 32- to 1,024-token blocks: a 16-row tile is a
+    # quarter or half of a block at 32 and 64; at 128 and 1,024 a 64-token
+    # split covers part of one block, so a tile's block and its offset inside
+    # it both come from the tile index
     from tvara_amd import hip
 
     monkeypatch.setenv("TVARA_SPLIT_TOKENS", "64")
     kv_heads, dim, group = 8, 64, 4
     heads = kv_heads * group
-    lengths = [1, 31, 32, 33, 63, 64, 65, 200, 1000, 3000] * 3
+    # splits are whole blocks, so the larger blocks need more tokens to give
+    # the row-major kernel its launch of more than 128 work items
+    if tpb <= 64:
+        lengths = [1, 31, 32, 33, 63, 64, 65, 200, 1000, 3000] * 3
+    elif tpb == 128:
+        lengths = [1, 31, 32, 33, 63, 64, 65, 200, 1000, 3000] * 4
+    else:
+        lengths = [1, tpb - 1, tpb, tpb + 1, 2 * tpb - 1, 2 * tpb, 2 * tpb + 1, 3000, 5000, 9000] * 5
     g = (1, kv_heads, dim, tpb, sum((n + tpb - 1) // tpb for n in lengths) + 4)
     dev, ref = device.PagedCache(*g), oracle.Cache(*g)
     w = kv_heads * dim
