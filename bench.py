@@ -708,6 +708,9 @@ def bench_prefix(args):
 
 # ------------------------------------------------------------------ model
 
+PREFILL_PROMPT = 2048
+
+
 def bench_model(args):
     """Decode through the model-level C ABI on a Llama-3.2-1B-shaped GGUF file
     with random Q8_0 weights (tied embedding): one sequence token by token
@@ -729,10 +732,25 @@ def bench_model(args):
         log(f"wrote {path.stat().st_size / 1e9:.2f} GB GGUF in {time.perf_counter() - t0:.1f}s")
         nseq, prompt = 64, 128
         t0 = time.perf_counter()
-        m = native.NativeModel(path, max_blocks=nseq * ((prompt + args.steps + args.warmup + 64) // 16 + 1) + 64,
-                               block_tokens=16)
+        m = native.NativeModel(path, max_blocks=nseq * ((prompt + args.steps + args.warmup + 64) // 16 + 1) +
+                               PREFILL_PROMPT // 16 + 64, block_tokens=16)
         log(f"loaded in {time.perf_counter() - t0:.1f}s")
         rng = np.random.default_rng(3)
+        # one 2,048-token prompt through tvara_sequence_prefill (passes of 512
+        # tokens), rolled back between repetitions
+        sp = m.new_sequence()
+        ptoks = rng.integers(0, spec.vocab, PREFILL_PROMPT)
+        m.prefill(sp, ptoks[:600])
+        m.truncate(sp, 0)
+        prefill_runs = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            last = m.prefill(sp, ptoks)
+            prefill_runs.append(time.perf_counter() - t0)
+            m.truncate(sp, 0)
+        assert np.isfinite(last).all()
+        m.drop_sequence(sp)
+        prefill_s = statistics.median(prefill_runs)
         # one sequence, token by token
         s1 = m.new_sequence()
         for t in rng.integers(0, spec.vocab, 8):
@@ -770,7 +788,8 @@ def bench_model(args):
         step_bytes = weight_bytes + kv_bytes
         tps = nseq / batch_s
         log(f"single sequence {single_s * 1e3:.2f} ms/token; {nseq} sequences {batch_s * 1e3:.2f} ms/step, "
-            f"{tps:.0f} tokens/s")
+            f"{tps:.0f} tokens/s; a {PREFILL_PROMPT}-token prompt in {prefill_s * 1e3:.2f} ms "
+            f"({PREFILL_PROMPT / prefill_s:.0f} tokens/s)")
         cpu = None
         if ref_ready(args):
             refso = ROOT / "oracle" / "_ref" / "libtvara_ref_capi.so"
@@ -798,6 +817,10 @@ def bench_model(args):
                        "layers": spec.layers, "hidden": spec.hidden, "heads": spec.heads,
                        "kv_heads": spec.kv_heads, "intermediate": spec.intermediate, "vocab": spec.vocab},
             "single_sequence_ms_per_token": round(single_s * 1e3, 4),
+            "prompt_prefill": {"tokens": PREFILL_PROMPT, "ms": round(prefill_s * 1e3, 3),
+                               "tokens_per_s": round(PREFILL_PROMPT / prefill_s, 1),
+                               "call": "tvara_sequence_prefill, passes of 512 tokens, median of 5",
+                               "token_loop_tokens_per_s": round(1 / single_s, 1)},
             "single_sequence_weight_GBps": round(weight_bytes / single_s / 1e9, 1),
             "roofline": {"bound": "hbm", "achieved": round(step_bytes / batch_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(step_bytes / batch_s / 1e9 / HBM_PEAK_GBS, 4),
@@ -823,7 +846,8 @@ def compact(r):
     for k in ("kernel", "kernel_avg_us", "merge_avg_us", "kernel_time_source", "traffic_source"):
         if k in r["roofline"]:
             out["roofline"][k] = r["roofline"][k]
-    for k in ("latency_us", "reference_published", "decode_tokens_per_s", "model_decode_tokens_per_s"):
+    for k in ("latency_us", "reference_published", "decode_tokens_per_s", "model_decode_tokens_per_s",
+              "prompt_prefill"):
         if k in r:
             out[k] = r[k]
     if cpu:

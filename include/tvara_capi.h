@@ -91,9 +91,20 @@ TVARA_API int tvara_sequence_decode(tvara_model* model, uint64_t sequence, uint3
 /* c_api.cpp:56-59 */
 TVARA_API int tvara_sequence_drop(tvara_model* model, uint64_t sequence);
 /* c_api.cpp:61-73: token_count decodes (count == token_count * vocab); all
- * tokens are checked first and a failure truncates back to the entry length */
+ * tokens are checked first and a failure truncates back to the entry length.
+ * The tokens run as one pass per chunk of up to 512: batched products (each
+ * weight row read once per chunk), each layer's K/V written into the cache,
+ * then the chunk's causal attention over it; the logits are those of
+ * token_count single decodes (f32 arithmetic throughout). */
 TVARA_API int tvara_sequence_decode_batch(tvara_model* model, uint64_t sequence, const uint32_t* tokens,
                                           size_t token_count, float* logits, size_t count);
+/* A prompt: tvara_sequence_decode_batch with only the last token's logits
+ * returned (count == vocab, token_count >= 1), the same checks, messages and
+ * rollback.  Replaces the per-token loop of NativeSchedulerBackend.prefill
+ * (python/tvara/scheduler.py:197-199), which keeps the last token's logits;
+ * no counterpart in the reference ABI. */
+TVARA_API int tvara_sequence_prefill(tvara_model* model, uint64_t sequence, const uint32_t* tokens,
+                                     size_t token_count, float* logits, size_t count);
 /* c_api.cpp:76-78 (PagedCache::truncate, kv.hpp:131-136) */
 TVARA_API int tvara_sequence_truncate(tvara_model* model, uint64_t sequence, size_t length);
 

@@ -276,6 +276,114 @@ def test_sequences_decode_odd_width_falls_back(tmp_path, ref_capi):
         got = mine.decode_sequences(sm, toks)
         ok, err = close(got, np.stack([ref.logits(r, t) for r, t in zip(sr, toks)]))
         assert ok, err
+    # decode_batch and prefill decode such a model token by token
+    ok, err = close(mine.decode_batch(sm[0], [4, 5, 6]), ref.decode_batch(sr[0], [4, 5, 6]))
+    assert ok, err
+    ok, err = close(mine.prefill(sm[1], [7, 8, 9]), ref.decode_batch(sr[1], [7, 8, 9])[-1])
+    assert ok, err
+
+
+CHUNK_SPECS = {
+    "f32": dict(context=1200),
+    "q8_0-gqa4": dict(matrix_type=gf.T_Q8_0, heads=8, kv_heads=2, hidden=128, intermediate=256, context=1200),
+    "q8_0-tied-ragged": dict(matrix_type=gf.T_Q8_0, embed_type=gf.T_Q8_0, output=False, vocab=100, hidden=96,
+                             intermediate=160, heads=3, kv_heads=1, context=1200),
+    "f16-split": dict(matrix_type=gf.T_F16, rope_layout="split", context=1200),
+}
+
+
+@pytest.mark.parametrize("name", list(CHUNK_SPECS))
+@pytest.mark.parametrize("block_tokens", [4, 16])
+def test_decode_batch_chunks_match_reference(tmp_path, ref_capi, name, block_tokens):
+    # tvara_sequence_decode_batch runs a chunk of tokens as one pass (batched
+    # products, each layer's K/V written into the cache, causal attention over
+    # it) where the reference decodes token by token: a batch starting
+    # mid-block, one of 1,100 tokens (passes of 512, 512 and 76 rows), a
+    # rollback into the middle of it and a continuation, every logit row
+    # against the reference's
+    spec = gf.LlamaSpec(**CHUNK_SPECS[name])
+    path = spec.write(tmp_path / f"{name}.gguf")
+    mine = native.NativeModel(path, max_blocks=1200 // block_tokens + 8, block_tokens=block_tokens)
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=1200 // block_tokens + 8, block_tokens=block_tokens)
+    sm, sr = mine.new_sequence(), ref.new_sequence()
+    rng = np.random.default_rng(3)
+    tokens = [int(t) for t in rng.integers(0, spec.vocab, 1200)]
+    worst = 0.0
+    for t in tokens[:3]:
+        ok, err = close(mine.logits(sm, t), ref.logits(sr, t))
+        assert ok, err
+    for lo, hi in [(3, 9), (9, 1109)]:
+        say(name, block_tokens, "batch", lo, hi)
+        got, want = mine.decode_batch(sm, tokens[lo:hi]), ref.decode_batch(sr, tokens[lo:hi])
+        ok, err = close(got, want)
+        worst = max(worst, err)
+        assert ok, (lo, hi, err, int(np.argmax(np.max(np.abs(got - want), axis=1))))
+    mine.truncate(sm, 600)
+    ref.truncate(sr, 600)
+    got, want = mine.decode_batch(sm, tokens[1109:1150]), ref.decode_batch(sr, tokens[1109:1150])
+    ok, err = close(got, want)
+    worst = max(worst, err)
+    assert ok, err
+    ok, err = close(mine.logits(sm, 7), ref.logits(sr, 7))
+    assert ok, err
+    say(name, block_tokens, "worst relative logit error", worst)
+
+
+def test_prefill_matches_reference_last_logits(tmp_path, ref_capi):
+    # tvara_sequence_prefill: the last token's logits of a chunked pass, with
+    # decode_batch's checks, messages and rollback
+    spec = gf.LlamaSpec(matrix_type=gf.T_Q8_0, heads=8, kv_heads=2, hidden=128, intermediate=256, context=64)
+    path = spec.write(tmp_path / "m.gguf")
+    mine = native.NativeModel(path, max_blocks=10, block_tokens=4)  # 40 tokens fit
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=10, block_tokens=4)
+    sm, sr = mine.new_sequence(), ref.new_sequence()
+    ok, err = close(mine.prefill(sm, [5]), ref.decode_batch(sr, [5])[-1])
+    assert ok, err
+    prompt = [int(t) for t in np.random.default_rng(9).integers(0, spec.vocab, 25)]
+    ok, err = close(mine.prefill(sm, prompt), ref.decode_batch(sr, prompt)[-1])
+    assert ok, err
+    cache = mine.cache()
+    assert cache.length(sm) == 26
+    with pytest.raises(ValueError, match="empty prompt"):
+        mine.prefill(sm, [])
+    assert errors(mine, mine.prefill, sm, [1, 2, spec.vocab]) == "invalid batch token"
+    assert cache.length(sm) == 26
+    # 26 + 20 > 40 pool tokens: the pool runs out partway; nothing stays appended
+    more = list(range(1, 21))
+    em, er = errors(mine, mine.prefill, sm, more), errors(ref, ref.decode_batch, sr, more)
+    assert em == er and em is not None, (em, er)
+    assert cache.length(sm) == 26
+    ok, err = close(mine.logits(sm, 3), ref.logits(sr, 3))
+    assert ok, err
+    # 27 cached + 38 > 64: the context check, as decode_batch's
+    long = [2] * 38
+    assert errors(mine, mine.prefill, sm, long) == errors(ref, ref.decode_batch, sr, long) == "batch exceeds context"
+
+
+def test_decode_batch_on_a_fork_copies_on_write(tmp_path, ref_capi):
+    # a chunk appended to a fork whose last block is shared and partly full:
+    # the block is copied on write before the chunk's rows land, and the
+    # forked-from sequence still decodes as before
+    spec = gf.LlamaSpec(matrix_type=gf.T_Q8_0, heads=8, kv_heads=2, hidden=128, intermediate=256, context=128)
+    path = spec.write(tmp_path / "m.gguf")
+    mine = native.NativeModel(path, max_blocks=64, block_tokens=4)
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=64, block_tokens=4)
+    rng = np.random.default_rng(4)
+    prefix = [int(t) for t in rng.integers(0, spec.vocab, 10)]
+    tail = [int(t) for t in rng.integers(0, spec.vocab, 30)]
+    other = [int(t) for t in rng.integers(0, spec.vocab, 7)]
+    a, ra, rf = mine.new_sequence(), ref.new_sequence(), ref.new_sequence()
+    mine.decode_batch(a, prefix)
+    ref.decode_batch(ra, prefix)
+    ref.decode_batch(rf, prefix)
+    cache = mine.cache()
+    f = cache.fork(a)
+    shared = cache.blocks(a)[-1]
+    ok, err = close(mine.decode_batch(f, tail), ref.decode_batch(rf, tail))
+    assert ok, err
+    assert cache.blocks(a)[-1] == shared and cache.blocks(f)[-1] != shared
+    ok, err = close(mine.decode_batch(a, other), ref.decode_batch(ra, other))
+    assert ok, err
 
 
 class _SerialBackend:

@@ -38,6 +38,7 @@ SIGNATURES = {
     "tvara_sequence_decode": (C.c_int, [_vp, _u64, C.c_uint32, _fp, _sz]),
     "tvara_sequence_drop": (C.c_int, [_vp, _u64]),
     "tvara_sequence_decode_batch": (C.c_int, [_vp, _u64, C.POINTER(C.c_uint32), _sz, _fp, _sz]),
+    "tvara_sequence_prefill": (C.c_int, [_vp, _u64, C.POINTER(C.c_uint32), _sz, _fp, _sz]),
     "tvara_sequence_truncate": (C.c_int, [_vp, _u64, _sz]),
     "tvara_sequences_decode": (C.c_int, [_vp, C.POINTER(_u64), C.POINTER(C.c_uint32), _sz, _fp, _sz]),
     "tvara_model_cache": (_vp, [_vp]),

@@ -468,10 +468,41 @@ int tvara_sequence_decode_batch(tvara_model* model, uint64_t sequence, const uin
         if (token_count > model->model->config().context - length) throw std::invalid_argument("batch exceeds context");
         for (size_t i = 0; i < token_count; ++i)
             if (tokens[i] >= vocab) throw std::invalid_argument("invalid batch token");
+        // the reference decodes token by token (c_api.cpp:68); the chunk pass
+        // gives the same logits with every weight row read once per chunk
         try {
-            for (size_t i = 0; i < token_count; ++i) model->model->decode(sequence, tokens[i], logits + i * vocab);
+            model->model->decode_chunk(sequence, tokens, token_count, logits, false);
         } catch (...) {
             cache.truncate(sequence, length);  // no partial batch stays in the cache (c_api.cpp:68-70)
+            throw;
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        failed(TVARA_ERROR, e.what());
+        return -1;
+    } catch (...) {
+        failed(TVARA_ERROR, "unknown batch error");
+        return -1;
+    }
+}
+
+int tvara_sequence_prefill(tvara_model* model, uint64_t sequence, const uint32_t* tokens, size_t token_count,
+                           float* logits, size_t count) {
+    tvara_amd::abi::clear();
+    try {
+        if (!model || (!tokens && token_count) || !logits) throw std::invalid_argument("invalid batch buffers");
+        const size_t vocab = model->model->config().vocab;
+        if (!token_count || count != vocab) throw std::invalid_argument("invalid batch dimensions");
+        std::lock_guard<std::mutex> lock(model->mutex);
+        auto& cache = model->model->cache();
+        const size_t length = cache.sequence(sequence).length;
+        if (token_count > model->model->config().context - length) throw std::invalid_argument("batch exceeds context");
+        for (size_t i = 0; i < token_count; ++i)
+            if (tokens[i] >= vocab) throw std::invalid_argument("invalid batch token");
+        try {
+            model->model->decode_chunk(sequence, tokens, token_count, logits, true);
+        } catch (...) {
+            cache.truncate(sequence, length);
             throw;
         }
         return 0;

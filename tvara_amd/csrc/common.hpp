@@ -147,6 +147,9 @@ void launch_append_rows_inline(char* pool, const BlockLayout& lay, const InlineR
                                const float* values, hipStream_t s);
 void launch_append_rows(char* pool, const BlockLayout& lay, const RowOp* ops, int n, const float* keys,
                         const float* values, hipStream_t s);
+// one layer's K and V rows ([n][kv_width] floats) into the f32 slots of ops
+void launch_write_layer_rows(char* pool, const BlockLayout& lay, const RowOp* ops, int n, int layer,
+                             const float* keys, const float* values, hipStream_t s);
 void launch_gather_rows(const char* pool, const BlockLayout& lay, const int2* rows, int n, int layer, int kind,
                         float* out, hipStream_t s);
 void launch_checksums(const char* pool, const BlockLayout& lay, const int64_t* ids, int n, uint64_t* out,

@@ -215,17 +215,7 @@ size_t DeviceCache::append_batch(const uint64_t* seqs, size_t n, const float* ke
     const size_t applied = w.applied;
     const Geometry& g = meta_.geometry();
     if (applied) {
-        flush();
-        // small batches pass their ops in the kernel arguments (no upload copy)
-        if (!w.init.empty() && w.init.size() <= static_cast<size_t>(kInlineOps)) {
-            InlineInitOps ops;
-            for (size_t i = 0; i < w.init.size(); ++i)
-                ops.op[i] = make_int2(static_cast<int>(w.init[i].dst), static_cast<int>(w.init[i].src));
-            launch_block_init_inline(pool_, lay_.stride, ops, static_cast<int>(w.init.size()), stream_);
-        } else if (!w.init.empty()) {
-            auto* d = upload(*this, kInitOps, w.init.data(), w.init.size());
-            launch_block_init(pool_, lay_.stride, d, static_cast<int>(w.init.size()), stream_);
-        }
+        run_block_init(w.init);
         const float* k = keys;
         const float* v = values;
         if (!device) {
@@ -253,6 +243,40 @@ size_t DeviceCache::append_batch(const uint64_t* seqs, size_t n, const float* ke
 size_t DeviceCache::append_tokens(uint64_t seq, const float* keys, const float* values, size_t count, bool device) {
     std::vector<uint64_t> seqs(count, seq);
     return append_batch(seqs.data(), count, keys, values, device);
+}
+
+void DeviceCache::run_block_init(const std::vector<BlockInitOp>& init) {
+    flush();
+    // small batches pass their ops in the kernel arguments (no upload copy)
+    if (!init.empty() && init.size() <= static_cast<size_t>(kInlineOps)) {
+        InlineInitOps ops;
+        for (size_t i = 0; i < init.size(); ++i)
+            ops.op[i] = make_int2(static_cast<int>(init[i].dst), static_cast<int>(init[i].src));
+        launch_block_init_inline(pool_, lay_.stride, ops, static_cast<int>(init.size()), stream_);
+    } else if (!init.empty()) {
+        auto* d = upload(*this, kInitOps, init.data(), init.size());
+        launch_block_init(pool_, lay_.stride, d, static_cast<int>(init.size()), stream_);
+    }
+}
+
+// The ledger half of `count` appends to one sequence (PagedCache::append,
+// kv.hpp:91-108, per token), with the rows left to write_layer_rows.
+const RowOp* DeviceCache::reserve_tokens(uint64_t seq, size_t count) {
+    if (format_ != kF32) throw std::invalid_argument("layer-wise appends need f32 blocks");
+    if (!count) return nullptr;
+    std::vector<uint64_t> seqs(count, seq);
+    AppendWork w = meta_.plan_appends(seqs.data(), count);
+    if (w.applied) run_block_init(w.init);
+    if (w.failure) std::rethrow_exception(w.failure);
+    return upload(*this, kRowOps, w.rows.data(), w.rows.size());
+}
+
+void DeviceCache::write_layer_rows(const RowOp* ops, size_t n, int layer, const float* keys, const float* values) {
+    if (!n) return;
+    if (format_ != kF32 || !ops || !keys || !values || layer < 0 || layer >= lay_.layers ||
+        n > static_cast<size_t>(std::numeric_limits<int>::max()))
+        throw std::invalid_argument("invalid paged KV append dimensions");
+    launch_write_layer_rows(pool_, lay_, ops, static_cast<int>(n), layer, keys, values, stream_);
 }
 
 // PagedCache::read (kv.hpp:110-113)

@@ -80,6 +80,18 @@ public:
     size_t append_batch(const uint64_t* seqs, size_t n, const float* keys, const float* values, bool device,
                         size_t* applied = nullptr);
     size_t append_tokens(uint64_t seq, const float* keys, const float* values, size_t count, bool device);
+    // Layer-wise appends (f32 blocks): appends `count` tokens to `seq` in the
+    // ledger and runs their block work (zero-fills, copy-on-write copies) but
+    // writes no rows; the returned device list gives each token's (block,
+    // slot), in order, for write_layer_rows().  The tokens hold stale bytes
+    // until every layer's rows are written, so the caller writes them before
+    // anything reads them, or truncates.  On failure the block work of the
+    // appends that took effect still runs, then the error is rethrown and the
+    // caller truncates.
+    const RowOp* reserve_tokens(uint64_t seq, size_t count);
+    // layer `layer`'s K and V rows ([n][kv_width] floats, row i for the
+    // token of ops[i]) into their slots
+    void write_layer_rows(const RowOp* ops, size_t n, int layer, const float* keys, const float* values);
     void read(uint64_t id, size_t layer, size_t position, bool value, float* out);
     void read_all(uint64_t id, size_t layer, bool value, float* out, size_t capacity);
     void drop(uint64_t id) { meta_.drop(id); }
@@ -105,6 +117,9 @@ public:
     int* error_flag() const { return err_; }
 
 private:
+    // zero-fills and copy-on-write copies of planned appends, on the stream
+    void run_block_init(const std::vector<BlockInitOp>& init);
+
     KvLedger meta_;
     int format_;
     BlockLayout lay_{};

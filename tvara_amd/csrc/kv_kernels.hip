@@ -118,6 +118,27 @@ __global__ __launch_bounds__(kThreads) void append_rows_f32_kernel(char* pool, B
     }
 }
 
+// One layer's rows of reserved tokens (DeviceCache::reserve_tokens): grid.x =
+// op, grid.y = kind; source rows are [src_row][kv_width].  Plain stores: the
+// attention of the same layer reads them next.
+__global__ __launch_bounds__(kThreads) void write_layer_rows_kernel(char* pool, BlockLayout lay,
+                                                                    const RowOp* __restrict__ ops, int layer,
+                                                                    const float* __restrict__ keys,
+                                                                    const float* __restrict__ values) {
+    const RowOp op = ops[blockIdx.x];
+    const int kind = blockIdx.y;
+    const float* src = (kind ? values : keys) + static_cast<size_t>(op.src_row) * lay.kv_width;
+    float* dst = reinterpret_cast<float*>(pool + static_cast<size_t>(op.block) * lay.stride) +
+                 (static_cast<size_t>(layer * 2 + kind) * lay.tpb + op.slot) * lay.kv_width;
+    if ((lay.kv_width & 3) == 0) {
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+        float4* d4 = reinterpret_cast<float4*>(dst);
+        for (int i = threadIdx.x; i < lay.kv_width / 4; i += blockDim.x) d4[i] = s4[i];
+    } else {
+        for (int i = threadIdx.x; i < lay.kv_width; i += blockDim.x) dst[i] = src[i];
+    }
+}
+
 // Quantise-on-append into Q8_0 with the encoder of tools/make_api_fixture.py:131-137:
 // one 32-lane half-wave per group; scale = max|x|/127 in f64, q = clip(rint(x/f32(scale)),
 // -127, 127) with an IEEE f32 division, d = f16(scale) rounded to nearest even.
@@ -309,6 +330,15 @@ void launch_append_rows(char* pool, const BlockLayout& lay, const RowOp* ops, in
             launch("kv_append_rows", append_rows_q8_kernel, dim3(lay.layers * 2, count), dim3(threads), 0, s, pool,
                    lay, ops + base, keys, values);
     }
+    TVARA_HIP(hipGetLastError());
+}
+
+void launch_write_layer_rows(char* pool, const BlockLayout& lay, const RowOp* ops, int n, int layer,
+                             const float* keys, const float* values, hipStream_t s) {
+    if (n <= 0) return;
+    const int threads = lay.kv_width >= 1024 ? 256 : (lay.kv_width >= 256 ? 128 : 64);
+    launch("kv_append_rows", write_layer_rows_kernel, dim3(n, 2), dim3(threads), 0, s, pool, lay, ops, layer, keys,
+           values);
     TVARA_HIP(hipGetLastError());
 }
 

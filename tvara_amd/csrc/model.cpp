@@ -320,9 +320,7 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     }
     if (n > static_cast<size_t>(std::numeric_limits<int>::max() / std::max<size_t>(c.vocab, c.hidden)))
         throw std::invalid_argument("decode batch too large");
-    if (c.hidden % 32 || c.intermediate % 32 || c.hidden > 16384 || c.intermediate > 16384) {
-        // the batched products tile K by 32 and the epilogues hold a row of
-        // up to 16,384 in registers: decode the sequences one by one
+    if (!batched_widths()) {
         size_t done = 0;
         try {
             for (; done < n; ++done) decode(seqs[done], tokens[done], logits_host + done * c.vocab);
@@ -334,27 +332,46 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     }
     ensure_batch(n);
     hipStream_t s = cache_->stream();
-    const int N = static_cast<int>(n);
-    const int H = static_cast<int>(c.hidden), I = static_cast<int>(c.intermediate);
-    const int KV = static_cast<int>(c.kv_width()), D = static_cast<int>(c.head_dim());
-    float* x = at(bx_, 0);
-    float* norm = at(bnorm_, 0);
-    float* q = at(bq_, 0);
-    float* attn = at(battn_, 0);
-    float* gate = at(bgate_, 0);
-    float* part = at(bpart_, 0);
-    auto* halves = static_cast<_Float16*>(bhalves_.ptr);
-    float* unscale = at(bunscale_, 0);
-    auto halves_for = [&](const Weight& w) { return w.q8 ? halves : nullptr; };
-    const Weight& logits_w = has_output_ ? output_ : embedding_;
+    const int N = static_cast<int>(n), KV = static_cast<int>(c.kv_width());
+    stage_rows(tokens, positions.data(), n);
+    // each row reads its sequence's cached tokens, then its own token as the tail
+    AttnPlan& plan = batch_plan_;
+    plan.build(cache_.get(), seqs, positions, std::vector<uint8_t>(n, 1), static_cast<int>(c.heads), 0);
+    layer_stack(n, [&](int l, const float* q, float* kl, float* vl, float* attn) {
+        plan.launch(l, q, kl, vl, attn, s);
+    });
+    const LogitsBands bands = launch_logits(n, 0);
+    plan.check_after(step_events_.attn);
+    launch_interleave_layers(at(bk_, 0), at(bkapp_, 0), static_cast<int>(c.layers), N, KV, s);
+    launch_interleave_layers(at(bv_, 0), at(bvapp_, 0), static_cast<int>(c.layers), N, KV, s);
+    size_t applied = 0;
+    try {
+        cache_->append_batch(seqs.data(), n, at(bkapp_, 0), at(bvapp_, 0), true, &applied);
+    } catch (...) {
+        for (size_t i = 0; i < applied; ++i) cache_->truncate(seqs[i], positions[i]);  // all or nothing
+        throw;
+    }
+    copy_logits(bands, n, logits_host);
+}
 
+bool DeviceModel::batched_widths() const {
+    // the batched products tile K by 32 and the epilogues hold a row of up to
+    // 16,384 in registers; other widths decode token by token
+    const ModelConfig& c = cfg_;
+    return c.hidden % 32 == 0 && c.intermediate % 32 == 0 && c.hidden <= 16384 && c.intermediate <= 16384;
+}
+
+void DeviceModel::stage_rows(const uint32_t* tokens, const size_t* positions, size_t n) {
+    const ModelConfig& c = cfg_;
+    hipStream_t s = cache_->stream();
+    const int D = static_cast<int>(c.head_dim());
     // tokens and each row's (cos, sin) go up through one pinned staging area
     const size_t tok_bytes = (n * sizeof(uint32_t) + 15) / 16 * 16;
     auto* host = static_cast<char*>(bhost_.acquire(tok_bytes + n * c.head_dim() * sizeof(float)));
     std::memcpy(host, tokens, n * sizeof(uint32_t));
     auto* cs = reinterpret_cast<float*>(host + tok_bytes);
-    // rotary()'s angle position / theta^(2i/D), with the power taken once per
-    // i (the same float values; the GPU waits for this table)
+    // rotary()'s angle position / theta^(2i/D) (model.hpp:66-68), with the
+    // power taken once per i (the same float values)
     std::vector<float> inv_freq(D / 2);
     for (int i = 0; i < D / 2; ++i) inv_freq[i] = std::pow(c.rope_theta, static_cast<float>(2 * i) / static_cast<float>(D));
     for (size_t j = 0; j < n; ++j)
@@ -366,17 +383,32 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
     TVARA_HIP(hipMemcpyAsync(btok_.ptr, host, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     TVARA_HIP(hipMemcpyAsync(brope_.ptr, cs, n * c.head_dim() * sizeof(float), hipMemcpyHostToDevice, s));
     bhost_.release(s);
+    const int N = static_cast<int>(n), H = static_cast<int>(c.hidden);
     if (embedding_.q8)
-        launch_gather_embedding_q8(embedding_, static_cast<const uint32_t*>(btok_.ptr), 0, N, x, s);
+        launch_gather_embedding_q8(embedding_, static_cast<const uint32_t*>(btok_.ptr), 0, N, at(bx_, 0), s);
     else
-        launch_gather_embedding(at(embedding_.f32, 0), static_cast<const uint32_t*>(btok_.ptr), N, H, x, s);
+        launch_gather_embedding(at(embedding_.f32, 0), static_cast<const uint32_t*>(btok_.ptr), N, H, at(bx_, 0), s);
+}
 
+void DeviceModel::layer_stack(size_t n, const Attend& attend) {
+    const ModelConfig& c = cfg_;
+    hipStream_t s = cache_->stream();
+    const int N = static_cast<int>(n);
+    const int H = static_cast<int>(c.hidden), I = static_cast<int>(c.intermediate), D = static_cast<int>(c.head_dim());
+    float* x = at(bx_, 0);
+    float* norm = at(bnorm_, 0);
+    float* q = at(bq_, 0);
+    float* attn = at(battn_, 0);
+    float* gate = at(bgate_, 0);
+    float* part = at(bpart_, 0);
+    auto* halves = static_cast<_Float16*>(bhalves_.ptr);
+    float* unscale = at(bunscale_, 0);
+    auto halves_for = [&](const Weight& w) { return w.q8 ? halves : nullptr; };
+    const Weight& logits_w = has_output_ ? output_ : embedding_;
+    step_events_.ensure();
     // Per layer: the products write split sums, and each epilogue finishes
     // what follows its product (RoPE; the residual add with the next
     // RMSNorm; SwiGLU) and writes the next product's input.
-    AttnPlan& plan = batch_plan_;
-    plan.build(cache_.get(), seqs, positions, std::vector<uint8_t>(n, 1), static_cast<int>(c.heads), 0);
-    step_events_.ensure();
     launch_resid_norm(nullptr, 0, x, at(layers_[0].attn_norm, 0), N, H, c.rms_epsilon, norm,
                       halves_for(layers_[0].qkv), unscale, s);
     for (size_t l = 0; l < c.layers; ++l) {
@@ -386,7 +418,7 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
         launch_batch_product(L.qkv, norm, halves, unscale, N, part, s);
         launch_qkv_epilogue(part, batch_splits(L.qkv), N, static_cast<int>(c.heads), static_cast<int>(c.kv_heads), D,
                             c.interleaved_rope, at(brope_, 0), q, kl, vl, s);
-        plan.launch(static_cast<int>(l), q, kl, vl, attn, s);
+        attend(static_cast<int>(l), q, kl, vl, attn);
         if (l + 1 == c.layers) TVARA_HIP(hipEventRecord(step_events_.attn, s));
         if (L.out.q8) launch_split_halves(attn, N, H, halves, unscale, s);
         launch_batch_product(L.out, attn, halves, unscale, N, part, s);
@@ -400,48 +432,109 @@ void DeviceModel::decode_many(const uint64_t* sequences, const uint32_t* tokens,
         launch_resid_norm(part, batch_splits(L.down), x, last ? at(final_norm_, 0) : at(layers_[l + 1].attn_norm, 0), N,
                           H, c.rms_epsilon, norm, halves_for(last ? logits_w : layers_[l + 1].qkv), unscale, s);
     }
+}
+
+DeviceModel::LogitsBands DeviceModel::launch_logits(size_t n, size_t row0) {
+    const ModelConfig& c = cfg_;
+    hipStream_t s = cache_->stream();
+    const int N = static_cast<int>(n);
+    const Weight& logits_w = has_output_ ? output_ : embedding_;
+    const float* norm = at(bnorm_, row0 * c.hidden);
+    auto* halves = static_cast<_Float16*>(bhalves_.ptr);
+    float* unscale = at(bunscale_, 0);
+    // rows after the first of the final norm: their halves again, from vector 0
+    if (row0 && logits_w.q8) launch_split_halves(norm, N, static_cast<int>(c.hidden), halves, unscale, s);
     // Large logits (8 MiB and up, unsplit Q8_0) are computed in bands of row
-    // tiles, each copied to the host while the next is computed.  Every way
-    // the step can fail (the attention's error flag, the append's pool) is
-    // settled before the first byte reaches the caller's buffer.
+    // tiles, each copied to the host while the next is computed.
+    LogitsBands b;
     const int vocab = static_cast<int>(c.vocab);
     constexpr int kBands = StepEvents::kBands;
-    const bool banded =
-        logits_w.q8 && batch_splits(logits_w) == 1 && n * c.vocab * sizeof(float) >= (size_t(8) << 20);
-    size_t bounds[kBands + 1];
-    int bands = 0;
-    if (banded) {
+    b.banded = logits_w.q8 && batch_splits(logits_w) == 1 && n * c.vocab * sizeof(float) >= (size_t(8) << 20);
+    if (b.banded) {
         const int tiles = logits_w.tiles(), per = (tiles + kBands - 1) / kBands;
         for (int t = 0; t < tiles; t += per) {
             launch_batch_product_tiles(logits_w, t, std::min(tiles, t + per), halves, unscale, N, at(blogits_, 0), s);
-            TVARA_HIP(hipEventRecord(step_events_.band[bands], s));
-            bounds[bands++] = static_cast<size_t>(t) * 16;
+            TVARA_HIP(hipEventRecord(step_events_.band[b.bands], s));
+            b.bounds[b.bands++] = static_cast<size_t>(t) * 16;
         }
-        bounds[bands] = c.vocab;
+        b.bounds[b.bands] = c.vocab;
     } else if (batch_splits(logits_w) == 1) {
         launch_batch_product(logits_w, norm, halves, unscale, N, at(blogits_, 0), s);
     } else {
+        float* part = at(bpart_, 0);
         launch_batch_product(logits_w, norm, halves, unscale, N, part, s);
         launch_split_sum(part, batch_splits(logits_w), N, vocab, at(blogits_, 0), s);
     }
-    plan.check_after(step_events_.attn);
-    launch_interleave_layers(at(bk_, 0), at(bkapp_, 0), static_cast<int>(c.layers), N, KV, s);
-    launch_interleave_layers(at(bv_, 0), at(bvapp_, 0), static_cast<int>(c.layers), N, KV, s);
-    size_t applied = 0;
-    try {
-        cache_->append_batch(seqs.data(), n, at(bkapp_, 0), at(bvapp_, 0), true, &applied);
-    } catch (...) {
-        for (size_t i = 0; i < applied; ++i) cache_->truncate(seqs[i], positions[i]);  // all or nothing
-        throw;
-    }
-    if (banded) {
-        copier_.bands_from_device(logits_host, at(blogits_, 0), n, c.vocab, bounds, step_events_.band, bands,
+    return b;
+}
+
+void DeviceModel::copy_logits(const LogitsBands& b, size_t n, float* logits_host) {
+    const ModelConfig& c = cfg_;
+    hipStream_t s = cache_->stream();
+    if (b.banded) {
+        copier_.bands_from_device(logits_host, at(blogits_, 0), n, c.vocab, b.bounds, step_events_.band, b.bands,
                                   step_events_.copy);
-        // calls that return host data leave the stream drained (the append
-        // kernels behind the logits ended long before the last band's copy)
+        // calls that return host data leave the stream drained (work queued
+        // behind the logits ended long before the last band's copy)
         TVARA_HIP(hipStreamSynchronize(s));
     } else
         copier_.from_device(logits_host, blogits_.ptr, n * c.vocab * sizeof(float), s);
+}
+
+void DeviceModel::decode_chunk(uint64_t sequence, const uint32_t* tokens, size_t n, float* logits_host,
+                               bool last_only) {
+    if (!n) return;
+    const ModelConfig& c = cfg_;
+    const size_t position = cache_->sequence(sequence).length;
+    for (size_t i = 0; i < n; ++i)
+        if (tokens[i] >= c.vocab) throw std::invalid_argument("paged decode exceeds token/context limits");
+    if (n > c.context || position > c.context - n)
+        throw std::invalid_argument("paged decode exceeds token/context limits");
+    if (n == 1 || !batched_widths()) {
+        std::vector<float> scratch(last_only && n > 1 ? c.vocab : 0);
+        for (size_t i = 0; i < n; ++i) {
+            float* out = last_only ? (i + 1 == n ? logits_host : scratch.data()) : logits_host + i * c.vocab;
+            decode(sequence, tokens[i], out);
+        }
+        return;
+    }
+    const size_t rows = std::min(n, kChunkRows);
+    if (rows > static_cast<size_t>(std::numeric_limits<int>::max() / std::max<size_t>(c.vocab, c.hidden)))
+        throw std::invalid_argument("decode batch too large");
+    ensure_batch(rows);
+    hipStream_t s = cache_->stream();
+    const int heads = static_cast<int>(c.heads);
+    std::vector<size_t> positions(rows);
+    std::vector<uint64_t> seq_of_row(rows, sequence);
+    for (size_t c0 = 0; c0 < n; c0 += rows) {
+        const size_t m = std::min(rows, n - c0);
+        positions.resize(m);
+        seq_of_row.resize(m);
+        for (size_t j = 0; j < m; ++j) positions[j] = position + c0 + j;
+        stage_rows(tokens + c0, positions.data(), m);
+        // the chunk's tokens join the sequence now (their blocks zero-filled or
+        // copied on write); every layer writes its K/V rows into their slots
+        // before its attention reads them
+        const RowOp* slots = cache_->reserve_tokens(sequence, m);
+        // row j sees the cached tokens and the chunk up to itself
+        // (fused_prompt_attention, attention.hpp:85-89)
+        for (size_t j = 0; j < m; ++j) positions[j] += 1;
+        AttnPlan& plan = batch_plan_;
+        plan.build(cache_.get(), seq_of_row, positions, {}, heads, 0);
+        layer_stack(m, [&](int l, const float* q, float* kl, float* vl, float* attn) {
+            cache_->write_layer_rows(slots, m, l, kl, vl);
+            plan.launch(l, q, nullptr, nullptr, attn, s);
+        });
+        const bool last = c0 + m == n;
+        if (last_only && !last) {
+            plan.check_after(step_events_.attn);
+            continue;
+        }
+        const size_t out_rows = last_only ? 1 : m;
+        const LogitsBands bands = launch_logits(out_rows, m - out_rows);
+        plan.check_after(step_events_.attn);
+        copy_logits(bands, out_rows, last_only ? logits_host : logits_host + c0 * c.vocab);
+    }
 }
 
 }  // namespace tvara_amd

@@ -4,6 +4,7 @@
 // in HBM and every step of a token on the GPU.
 #pragma once
 
+#include <functional>
 #include <memory>
 #include <string>
 #include <vector>
@@ -121,6 +122,14 @@ public:
     // one token for each of n distinct sequences in one pass: the logits of n
     // independent decode() calls; on failure no sequence changes
     void decode_many(const uint64_t* sequences, const uint32_t* tokens, size_t n, float* logits_host);
+    // n consecutive tokens at the end of `sequence` in one pass per chunk of
+    // up to kChunkRows tokens (the batched products, each layer's K/V written
+    // into the cache, then the rows' causal attention over it): the logits of
+    // n decode() calls, of every token or, with last_only, of the last one
+    // only.  On failure the sequence may hold part of the tokens; the caller
+    // truncates it.
+    void decode_chunk(uint64_t sequence, const uint32_t* tokens, size_t n, float* logits_host, bool last_only);
+    static constexpr size_t kChunkRows = 512;
 
 private:
     struct Layer {
@@ -167,6 +176,29 @@ private:
     StepEvents step_events_;
     size_t batch_cap_ = 0;
     void ensure_batch(size_t n);
+    // the widths the batched products and epilogues take
+    bool batched_widths() const;
+    // tokens and each row's (cos, sin) to the device, then the rows'
+    // embeddings into bx_
+    void stage_rows(const uint32_t* tokens, const size_t* positions, size_t n);
+    // The layer stack over the n rows staged in bx_: per layer the fused QKV
+    // product and its epilogue (q, k, v rows; RoPE), then attend(layer, q, k,
+    // v, out), then the output, gate|up and down products with their
+    // epilogues.  Records step_events_.attn after the last attention and
+    // leaves every row's final RMSNorm in bnorm_ (halves for a Q8_0 logits
+    // matrix).
+    using Attend = std::function<void(int, const float*, float*, float*, float*)>;
+    void layer_stack(size_t n, const Attend& attend);
+    // the logits of final-norm rows row0 .. row0 + n - 1 into blogits_, in
+    // bands of row tiles for large outputs
+    struct LogitsBands {
+        bool banded = false;
+        int bands = 0;
+        size_t bounds[StepEvents::kBands + 1] = {};
+    };
+    LogitsBands launch_logits(size_t n, size_t row0);
+    // blogits_ [n][vocab] to the host (synchronous)
+    void copy_logits(const LogitsBands& b, size_t n, float* logits_host);
 };
 
 }  // namespace tvara_amd

@@ -122,6 +122,28 @@ class NativeModel:
                 self._raise_error()
         return output
 
+    def prefill(self, sequence, tokens):
+        """Logits [vocab] of the last of `tokens`, decoded in order at the end
+        of `sequence` (tvara_sequence_prefill: one pass per chunk); on failure
+        the sequence is truncated back to its entry length.  A library without
+        the export (the reference's) decodes token by token."""
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        if not toks.size:
+            raise ValueError("empty prompt")
+        fn = getattr(self._library, "tvara_sequence_prefill", None)
+        if fn is None or fn.argtypes is None:  # not bound: a build of the reference's 11 exports
+            with self._lock:
+                for token in toks:
+                    out = self.logits(sequence, int(token))
+            return out
+        output = np.empty(self.vocab_size, dtype=np.float32)
+        with self._lock:
+            self._check_open()
+            if fn(self._handle, sequence, toks.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), toks.size,
+                  output.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), output.size):
+                self._raise_error()
+        return output
+
     def decode_sequences(self, sequences, tokens):
         """One token for each of several distinct sequences in one pass
         (tvara_sequences_decode): logits [len(sequences), vocab]."""

@@ -1,12 +1,14 @@
-"""NativeSchedulerBackend (python/tvara/scheduler.py:186-214) with the
-iteration batch decoded on the GPU in one tvara_sequences_decode call.
+"""NativeSchedulerBackend (python/tvara/scheduler.py:186-214) with a prompt
+decoded in chunked passes (tvara_sequence_prefill) and the iteration batch
+decoded on the GPU in one tvara_sequences_decode call.
 
 The interface, the greedy token choice and the error behaviour are the
 reference's: keys are served in order, a key whose pending logits are not
 finite raises ValueError("Nonfinite model logits") after every key before it
-was decoded, and a failing decode leaves the keys before it decoded.  The
-batched call is all-or-nothing, so a failed batch is replayed key by key to
-reach exactly that state.  A key listed twice is decoded twice, the second
+was decoded, and a failing decode leaves the keys (or prompt tokens) before it
+decoded.  The batched calls are all-or-nothing, so a failed call is replayed
+token by token to reach exactly that state (and that outcome: a replay that
+completes is a success).  A key listed twice is decoded twice, the second
 time from the logits of the first.
 """
 
@@ -25,8 +27,15 @@ class NativeSchedulerBackend:
         self.sequences[key] = self.model._new_sequence()
 
     def prefill(self, key, tokens):
-        for token in tokens:
-            self.pending[key] = self.model.logits(self.sequences[key], token)
+        tokens = list(tokens)
+        if not tokens:
+            return
+        try:
+            self.pending[key] = self.model.prefill(self.sequences[key], tokens)
+        except Exception:
+            # nothing was decoded: replay one by one for the reference's partial state
+            for token in tokens:
+                self.pending[key] = self.model.logits(self.sequences[key], token)
 
     def _decode_run(self, keys, tokens):
         try:
@@ -35,7 +44,7 @@ class NativeSchedulerBackend:
             # nothing was decoded: replay one by one for the reference's partial state
             for key, token in zip(keys, tokens):
                 self.pending[key] = self.model.logits(self.sequences[key], token)
-            raise
+            return
         for i, key in enumerate(keys):
             self.pending[key] = out[i]
 
