@@ -410,34 +410,14 @@ __global__ __launch_bounds__(W * 64) void matvec_q8_kernel(const Q8MatvecArgs a)
     __shared__ double red[W][RT][16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int P = a.pairs, G = a.groups, C = a.cols;
-    if (a.norm_w) {
-        double sq = 0;
-        for (int k = threadIdx.x; k < C; k += W * 64) sq += static_cast<double>(a.v[k]) * a.v[k];
-        for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
-        if (lane == 0) red[wave][0][0] = sq;
-        __syncthreads();
-        double t = 0;
-        for (int w = 0; w < W; ++w) t += red[w][0][0];
-        const float inv = static_cast<float>(1.0 / sqrt(t / static_cast<double>(C) + static_cast<double>(a.eps)));
-        for (int k = threadIdx.x; k < C; k += W * 64) vs[k] = __fmul_rn(__fmul_rn(a.v[k], inv), a.norm_w[k]);
-        __syncthreads();  // red is reused below
-    } else {
-        for (int k = 4 * threadIdx.x; k < C; k += 4 * W * 64)
-            *reinterpret_cast<float4*>(vs + k) = *reinterpret_cast<const float4*>(a.v + k);
-    }
-    __syncthreads();
     const int per = (P + W - 1) / W;
     const int p0 = min(P, wave * per), p1 = min(P, p0 + per);
     int tl[RT];
 #pragma unroll
     for (int r = 0; r < RT; ++r) tl[r] = min(static_cast<int>(blockIdx.x) * RT + r, a.tiles - 1);
-    const float* vp = vs + 8 * (lane >> 4);
-    double acc[RT];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) acc[r] = 0;
-    for (int p = p0; p < p1; p += U) {
-        uint4 qq[RT][U];
-        uint32_t dd[RT][U];
+    // U pairs of every tile from pair p on, clamped to the wave's last pair
+    // (a wave without pairs reads pair P - 1 and adds nothing)
+    auto load = [&](int p, uint4 (&qq)[RT][U], uint32_t (&dd)[RT][U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int pc = min(p + u, p1 - 1);
@@ -448,6 +428,66 @@ __global__ __launch_bounds__(W * 64) void matvec_q8_kernel(const Q8MatvecArgs a)
                 dd[r][u] = a.d[blk * 16 + (lane & 15)];
             }
         }
+    };
+    // the first step's weights are requested before the input is staged
+    uint4 qq[RT][U];
+    uint32_t dd[RT][U];
+    load(p0, qq, dd);
+    if (a.norm_w) {
+        // one pass over the input and the norm weights, both staged in LDS as
+        // float4s (two per thread a step, all four loads requested first);
+        // each thread then rescales the elements it staged
+        float* ws = vs + C;
+        constexpr int S = 4 * W * 64;
+        double sq = 0;
+        for (int k0 = 4 * static_cast<int>(threadIdx.x); k0 < C; k0 += 2 * S) {
+            const int k1 = min(k0 + S, C - 4);
+            const float4 x0 = *reinterpret_cast<const float4*>(a.v + k0);
+            const float4 w0 = *reinterpret_cast<const float4*>(a.norm_w + k0);
+            const float4 x1 = *reinterpret_cast<const float4*>(a.v + k1);
+            const float4 w1 = *reinterpret_cast<const float4*>(a.norm_w + k1);
+            sq += static_cast<double>(x0.x) * x0.x + static_cast<double>(x0.y) * x0.y +
+                  static_cast<double>(x0.z) * x0.z + static_cast<double>(x0.w) * x0.w;
+            *reinterpret_cast<float4*>(vs + k0) = x0;
+            *reinterpret_cast<float4*>(ws + k0) = w0;
+            if (k0 + S < C) {
+                sq += static_cast<double>(x1.x) * x1.x + static_cast<double>(x1.y) * x1.y +
+                      static_cast<double>(x1.z) * x1.z + static_cast<double>(x1.w) * x1.w;
+                *reinterpret_cast<float4*>(vs + k1) = x1;
+                *reinterpret_cast<float4*>(ws + k1) = w1;
+            }
+        }
+        for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+        if (lane == 0) red[wave][0][0] = sq;
+        __syncthreads();
+        double t = 0;
+        for (int w = 0; w < W; ++w) t += red[w][0][0];
+        const float inv = static_cast<float>(1.0 / sqrt(t / static_cast<double>(C) + static_cast<double>(a.eps)));
+        for (int k = 4 * static_cast<int>(threadIdx.x); k < C; k += S) {
+            float4 x = *reinterpret_cast<const float4*>(vs + k);
+            const float4 w = *reinterpret_cast<const float4*>(ws + k);
+            x.x = __fmul_rn(__fmul_rn(x.x, inv), w.x);
+            x.y = __fmul_rn(__fmul_rn(x.y, inv), w.y);
+            x.z = __fmul_rn(__fmul_rn(x.z, inv), w.z);
+            x.w = __fmul_rn(__fmul_rn(x.w, inv), w.w);
+            *reinterpret_cast<float4*>(vs + k) = x;
+        }
+        __syncthreads();  // red is reused below
+    } else {
+        for (int k = 4 * threadIdx.x; k < C; k += 4 * W * 64)
+            *reinterpret_cast<float4*>(vs + k) = *reinterpret_cast<const float4*>(a.v + k);
+    }
+    __syncthreads();
+    const float* vp = vs + 8 * (lane >> 4);
+    double acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) acc[r] = 0;
+    for (int p = p0; p < p1; p += U) {
+        // the next step's weights are in flight while this step is summed
+        // (unconditional, clamped: the last step re-reads its own pairs)
+        uint4 nq[RT][U];
+        uint32_t nd[RT][U];
+        load(min(p + U, p1 - 1), nq, nd);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int pc = min(p + u, p1 - 1);
@@ -467,6 +507,13 @@ __global__ __launch_bounds__(W * 64) void matvec_q8_kernel(const Q8MatvecArgs a)
                 acc[r] += live ? t : 0.0;
             }
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                qq[r][u] = nq[r][u];
+                dd[r][u] = nd[r][u];
+            }
     }
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
@@ -1011,13 +1058,17 @@ void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg,
     a.rope_rows = rope_rows;
     a.swiglu = w.interleaved ? 1 : 0;
     // two tiles per workgroup (sharing the staged input) when there are
-    // many; waves per workgroup so that about 4,096 waves share the pairs,
-    // at most sixteen and no more than there are pairs
+    // many.  Waves per workgroup: one step of pairs each (four), at most
+    // sixteen; launches of a thousand workgroups and more take two (MI355X,
+    // Llama-3.2-1B shapes: 3,072 x 2,048 rows in 6.2 us at eight waves
+    // against 7.4 at sixteen; 8,192 columns in 9.1 us at sixteen; the
+    // 128,256-row logits in 58 us at two waves against 65 at one)
     const int rt = a.tiles >= 1024 ? 2 : 1;
     const int wgs = (a.tiles + rt - 1) / rt;
-    const int want = std::max(1, std::min(a.pairs, 4096 / std::max(wgs, 1)));
+    const int want = wgs >= 1024 ? 2 : std::max(1, std::min(16, (a.pairs + 3) / 4));
     const dim3 grid(wgs);
-    const size_t lds = static_cast<size_t>(w.cols) * sizeof(float);
+    // the input, and the norm weights beside it when the product normalises
+    const size_t lds = static_cast<size_t>(w.cols) * sizeof(float) * (norm_w ? 2 : 1);
     auto go = [&](auto kernel, int waves) { launch("model_matvec_q8", kernel, grid, dim3(64 * waves), lds, s, a); };
     if (rt == 2) {
         if (want >= 8) go(matvec_q8_kernel<8, 2>, 8);
