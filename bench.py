@@ -61,7 +61,7 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16
 METRIC = "paged decode attn: achieved HBM GB/s (% of peak) + decode tokens/s, 1 MI355X"
 MODEL_LAYERS = {"llama-3.2-1b-decode-64x[128,4096]": 16, "smollm2-135m-decode-1x512": 30,
                 "llama-3-8b-q8_0-decode-16x32768": 32}
-DEFAULT_RUN = ["c1", "t176", "c3", "c3cow", "c4", "c5", "prefix", "llama1b", "c2"]
+DEFAULT_RUN = ["c1", "t176", "c3", "c3cow", "c4", "c5", "prefix", "conv", "llama1b", "c2"]
 REF_FLAGS = "g++ -O2 -std=c++20 -fPIC (oracle/Makefile, target ref; the reference's recorded flags)"
 
 
@@ -706,6 +706,134 @@ def bench_prefix(args):
     return result
 
 
+# ---------------------------------------------------------- conversations
+
+CONV_PUBLISHED = {"prefill_speedup": 3.554, "reused_token_fraction": 0.7524, "prompt_tokens": 3675,
+                  "reused_prompt_tokens": 2765, "turn_hits": 16,
+                  "source": "bench/results/prefix-cache-traces.json (the reference's CPU executor on its tiny-random "
+                            "Llama fixture; Intel Family 6 Model 61, Windows 11; median of 3)"}
+CONV_ISOLATION = "tiny-random-llama/synthetic-ids/tenant-a"
+
+
+def conversation_runs(model, traces, repeats, modes, tree_for=None):
+    """Median prefill seconds, counts and outputs of each mode over `repeats`
+    runs, the order alternating per repetition as the reference's tool does
+    (tools/run_prefix_cache_traces.py:105-118)."""
+    from tvara_amd import workloads
+
+    runs = {mode: [] for mode in modes}
+    for rep in range(repeats):
+        for mode in (modes if rep % 2 == 0 else modes[::-1]):
+            tree = tree_for() if mode == "radix" else None
+            try:
+                runs[mode].append(workloads.replay_conversations(model, traces, mode, tree=tree))
+            finally:
+                if tree is not None:
+                    tree.close()
+    return runs
+
+
+def conversation_summary(runs):
+    import numpy as np
+
+    out = {}
+    first = None
+    equal = True
+    for mode, reps in runs.items():
+        turns = [t for trace in reps[0] for t in trace]
+        seconds = [sum(t["prefill_seconds"] for trace in rep for t in trace) for rep in reps]
+        out[mode] = {"prompt_tokens": sum(t["prompt_tokens"] for t in turns),
+                     "reused_prompt_tokens": sum(t["reused_tokens"] for t in turns),
+                     "turn_hits": sum(t["reused_tokens"] > 0 for t in turns),
+                     "prefill_seconds_median": round(statistics.median(seconds), 6),
+                     "prefill_seconds": [round(x, 6) for x in seconds]}
+        out[mode]["reused_token_fraction"] = round(out[mode]["reused_prompt_tokens"] / out[mode]["prompt_tokens"], 4)
+        for rep in reps:
+            flat = [t for trace in rep for t in trace]
+            if first is None:
+                first = flat
+            equal = equal and all(a["reply"] == b["reply"] and np.array_equal(a["logits"], b["logits"])
+                                  for a, b in zip(first, flat))
+    off = out["off"]["prefill_seconds_median"]
+    for mode in out:
+        out[mode]["prefill_speedup"] = round(off / out[mode]["prefill_seconds_median"], 3)
+    return out, equal
+
+
+def bench_conversations(args):
+    """Prefix reuse on the reference's conversation traces (docs/prefix-cache.md:
+    13-23; tools/run_prefix_cache_traces.py): four seeded conversations of five
+    turns (a 64-token shared system prompt, 16-48-token user turns, 12-token
+    greedy replies) through the model-level C ABI on a model of the reference
+    fixture's shape (tiny-random Llama: hidden 16, two layers, vocabulary
+    32,000; random f32 weights).  Modes off and on are the reference's; radix
+    also restores the system prompt across conversations from a prefix tree
+    over the model's cache (tvara_model_cache + tvara_radix_*), which the
+    reference's ABI cannot.  Three repetitions, the order alternating; the
+    value is the median prefill speedup of on over off."""
+    import shutil
+    import tempfile
+
+    from tvara_amd import gguf_writer, native, radix, workloads
+
+    spec = gguf_writer.tiny_random_llama()
+    tmp = Path(tempfile.mkdtemp(prefix="tvara-conv-"))
+    try:
+        path = spec.write(tmp / "tiny-random-llama.gguf")
+        m = native.NativeModel(path, max_blocks=256, block_tokens=16)
+        traces = workloads.conversation_traces(vocab=m.vocab_size)
+        cache = m.cache()
+        tree_for = lambda: radix.RadixCache(cache, CONV_ISOLATION)  # noqa: E731
+        conversation_runs(m, traces, 1, ("off", "on", "radix"), tree_for)  # warm-up
+        summary, equal = conversation_summary(conversation_runs(m, traces, 3, ("off", "on", "radix"), tree_for))
+        m.close()
+        on = summary["on"]
+        log(f"conversations: off {summary['off']['prefill_seconds_median'] * 1e3:.1f} ms, on "
+            f"{on['prefill_seconds_median'] * 1e3:.1f} ms ({on['prefill_speedup']}x), radix "
+            f"{summary['radix']['prefill_seconds_median'] * 1e3:.1f} ms ({summary['radix']['prefill_speedup']}x); "
+            f"outputs equal {equal}")
+        result = {
+            "metric": "prefix reuse on the reference's conversation traces: prefill speedup, cache on vs off, "
+                      "1 MI355X",
+            "value": on["prefill_speedup"], "unit": "x", "n_gpus": 1, "steps": 3, "warmup": 1,
+            "ms_per_step": round(on["prefill_seconds_median"] * 1e3, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "the reference's seeded traces (numpy PCG64, seed 262); random f32 weights of the fixture's "
+                    "shape",
+            "config": {"workload": "conversations-4x5-tiny-random-llama", "conversations": 4, "turns": 5,
+                       "reply_tokens": 12, "layers": spec.layers, "hidden": spec.hidden, "heads": spec.heads,
+                       "kv_heads": spec.kv_heads, "vocab": spec.vocab},
+            "modes": summary, "outputs_equal": equal,
+            "reference_published": CONV_PUBLISHED,
+            "roofline": {"bound": "latency", "achieved": None, "peak": None, "unit": "s", "frac": None,
+                         "traffic": None, "traffic_source": "none: a 16-wide model is launch-bound",
+                         "kernel": "whole prefill calls (hidden 16: token by token)"},
+            "cpu_baseline": None,
+        }
+        if ref_ready(args) and (ROOT / "oracle" / "_ref" / "libtvara_ref_capi.so").exists():
+            refso = ROOT / "oracle" / "_ref" / "libtvara_ref_capi.so"
+
+            def job():  # may run after this function returned: a file of its own
+                jtmp = Path(tempfile.mkdtemp(prefix="tvara-conv-ref-"))
+                try:
+                    r = native.NativeModel(spec.write(jtmp / "tiny-random-llama.gguf"), library=str(refso),
+                                           max_blocks=256, block_tokens=16)
+                    ref, ref_equal = conversation_summary(conversation_runs(r, traces, 3, ("off", "on")))
+                    r.close()
+                finally:
+                    shutil.rmtree(jtmp, ignore_errors=True)
+                assert ref["on"]["reused_prompt_tokens"] == on["reused_prompt_tokens"]
+                return {"value": ref["on"]["prefill_speedup"], "unit": "x", "cores": 1, "kind": "reference",
+                        "sample": "the same traces through the reference's C ABI and CPU executor (oracle/_ref), "
+                                  "modes off and on, 3 repetitions",
+                        "modes": ref, "outputs_equal": ref_equal, "host": host_info()}
+
+            baseline(result, job)
+        return result
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 # ------------------------------------------------------------------ model
 
 PREFILL_PROMPT = 2048
@@ -870,6 +998,8 @@ def run_one(args, key):
         return bench_model(args)
     if key == "prefix":
         return bench_prefix(args)
+    if key == "conv":
+        return bench_conversations(args)
     w = {"c1": workloads.decode_c1, "c2": workloads.decode_c2, "c5": workloads.decode_c5,
          "gqa8": workloads.decode_gqa8, "gqa8q8": lambda: workloads.decode_gqa8(q8=True),
          "gqa16": workloads.decode_gqa16, "gqa16q8": lambda: workloads.decode_gqa16(q8=True),
@@ -886,7 +1016,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="all",
                     choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c4f32", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2", "phi3",
-                             "tiny", "tinyq8", "t176", "llama1b", "prefix"],
+                             "tiny", "tinyq8", "t176", "llama1b", "prefix", "conv"],
                     help="one configuration; `all` (the default) runs c1, t176, c3, c3cow, c4, c5, prefix and llama1b, "
                          "one JSON line each, then the c2 headline line last")
     ap.add_argument("--no-cpu-baseline", action="store_true")

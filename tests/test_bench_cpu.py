@@ -57,3 +57,23 @@ def test_prefix_driver_replays_the_reference_workload(ref):
         assert (r["requests"], r["hits"], r["saved_prefill_tokens"], r["requested_tokens"]) == (10000, 7500, 60000,
                                                                                                  80000), (kind, r)
         assert len(r["runs_ns"]) == 2 and min(r["runs_ns"]) > 0
+
+
+def test_conversation_traces_are_the_references(ref, tmp_path):
+    """The conversation traces replayed through the reference's own C ABI and
+    CPU executor (oracle/_ref) on a model of its fixture's shape give the
+    counts its tool recorded (bench/results/prefix-cache-traces.json: 3,675
+    prompt tokens, 2,765 reused, 16 of 20 turns), and cache on/off give the
+    same replies and logits, as that tool checks."""
+    from tvara_amd import gguf_writer, native
+
+    refso = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "libtvara_ref_capi.so"
+    m = native.NativeModel(gguf_writer.tiny_random_llama().write(tmp_path / "tiny.gguf"), library=str(refso),
+                           max_blocks=256, block_tokens=16)
+    traces = workloads.conversation_traces(vocab=m.vocab_size)
+    summary, equal = bench.conversation_summary(bench.conversation_runs(m, traces, 1, ("off", "on")))
+    m.close()
+    assert equal
+    assert (summary["on"]["prompt_tokens"], summary["on"]["reused_prompt_tokens"], summary["on"]["turn_hits"]) == \
+        (3675, 2765, 16)
+    assert (summary["off"]["prompt_tokens"], summary["off"]["reused_prompt_tokens"]) == (3675, 0)

@@ -386,6 +386,42 @@ def test_decode_batch_on_a_fork_copies_on_write(tmp_path, ref_capi):
     assert ok, err
 
 
+def test_conversation_replay_reuses_prefixes(tmp_path, ref_capi):
+    # the reference's conversation traces (tools/run_prefix_cache_traces.py)
+    # on a model of its fixture's shape (hidden 16: token by token): modes
+    # off, on and radix give the same replies and bit-identical prompt logits;
+    # on reuses the reference's 2,765 of 3,675 prompt tokens, radix also the
+    # 64-token system prompt of the three later conversations; the first
+    # prompt's logits are within the bar of the reference executor's
+    from tvara_amd import radix, workloads
+
+    spec = gf.tiny_random_llama()
+    path = spec.write(tmp_path / "tiny.gguf")
+    mine = native.NativeModel(path, max_blocks=256, block_tokens=16)
+    traces = workloads.conversation_traces(vocab=mine.vocab_size)
+    cache = mine.cache()
+    out = {}
+    for mode in ("off", "on", "radix"):
+        say("conversations", mode)
+        tree = radix.RadixCache(cache, "tiny/test") if mode == "radix" else None
+        out[mode] = [t for trace in workloads.replay_conversations(mine, traces, mode, tree=tree) for t in trace]
+        if tree is not None:
+            tree.close()
+        assert cache.sequence_ids() == []
+    for mode, reused in (("off", 0), ("on", 2765), ("radix", 2765 + 3 * 64)):
+        assert sum(t["prompt_tokens"] for t in out[mode]) == 3675
+        assert sum(t["reused_tokens"] for t in out[mode]) == reused, mode
+    for a, b, c in zip(out["off"], out["on"], out["radix"]):
+        assert a["reply"] == b["reply"] == c["reply"]
+        assert np.array_equal(a["logits"], b["logits"]) and np.array_equal(a["logits"], c["logits"])
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=256, block_tokens=16)
+    s = ref.new_sequence()
+    ok, err = close(out["off"][0]["logits"], ref.decode_batch(s, traces[0]["system"] + traces[0]["users"][0])[-1])
+    assert ok, err
+    ref.close()
+    mine.close()
+
+
 class _SerialBackend:
     """The reference's NativeSchedulerBackend loop (scheduler.py:201-210),
     over any NativeModel (here the reference's own library)."""

@@ -403,13 +403,15 @@ void DeviceModel::layer_stack(size_t n, const Attend& attend) {
     float* part = at(bpart_, 0);
     auto* halves = static_cast<_Float16*>(bhalves_.ptr);
     float* unscale = at(bunscale_, 0);
+    // a Q8_0 product reads its input as halves, an f32 one as f32 rows
     auto halves_for = [&](const Weight& w) { return w.q8 ? halves : nullptr; };
+    auto rows_for = [&](const Weight& w, float* rows) { return w.q8 ? nullptr : rows; };
     const Weight& logits_w = has_output_ ? output_ : embedding_;
     step_events_.ensure();
     // Per layer: the products write split sums, and each epilogue finishes
     // what follows its product (RoPE; the residual add with the next
     // RMSNorm; SwiGLU) and writes the next product's input.
-    launch_resid_norm(nullptr, 0, x, at(layers_[0].attn_norm, 0), N, H, c.rms_epsilon, norm,
+    launch_resid_norm(nullptr, 0, x, at(layers_[0].attn_norm, 0), N, H, c.rms_epsilon, rows_for(layers_[0].qkv, norm),
                       halves_for(layers_[0].qkv), unscale, s);
     for (size_t l = 0; l < c.layers; ++l) {
         Layer& L = layers_[l];
@@ -422,15 +424,18 @@ void DeviceModel::layer_stack(size_t n, const Attend& attend) {
         if (l + 1 == c.layers) TVARA_HIP(hipEventRecord(step_events_.attn, s));
         if (L.out.q8) launch_split_halves(attn, N, H, halves, unscale, s);
         launch_batch_product(L.out, attn, halves, unscale, N, part, s);
-        launch_resid_norm(part, batch_splits(L.out), x, at(L.ffn_norm, 0), N, H, c.rms_epsilon, norm,
-                          halves_for(L.gate_up), unscale, s);
+        launch_resid_norm(part, batch_splits(L.out), x, at(L.ffn_norm, 0), N, H, c.rms_epsilon,
+                          rows_for(L.gate_up, norm), halves_for(L.gate_up), unscale, s);
         launch_batch_product(L.gate_up, norm, halves, unscale, N, part, s);
-        launch_swiglu_epilogue(part, batch_splits(L.gate_up), N, I, gate, halves_for(L.down), unscale, s,
-                               L.gate_up.interleaved);
+        launch_swiglu_epilogue(part, batch_splits(L.gate_up), N, I, rows_for(L.down, gate), halves_for(L.down), unscale,
+                               s, L.gate_up.interleaved);
         launch_batch_product(L.down, gate, halves, unscale, N, part, s);
+        // after the last layer the rows stay too: the logits of chosen rows
+        // are taken from them
         const bool last = l + 1 == c.layers;
         launch_resid_norm(part, batch_splits(L.down), x, last ? at(final_norm_, 0) : at(layers_[l + 1].attn_norm, 0), N,
-                          H, c.rms_epsilon, norm, halves_for(last ? logits_w : layers_[l + 1].qkv), unscale, s);
+                          H, c.rms_epsilon, last ? norm : rows_for(layers_[l + 1].qkv, norm),
+                          halves_for(last ? logits_w : layers_[l + 1].qkv), unscale, s);
     }
 }
 

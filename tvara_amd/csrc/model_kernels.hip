@@ -564,14 +564,29 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Write element k of vector j (already scaled by the vector's power of two)
-__device__ __forceinline__ void put_halves(_Float16* halves, int groups, int j, int k, float v) {
-    const _Float16 hi = static_cast<_Float16>(v);
-    const _Float16 lo = static_cast<_Float16>(v - static_cast<float>(hi));
-    const int lane = (j % 16) + 16 * ((k % 32) / 8);
-    const size_t at = ((static_cast<size_t>(j / 16) * groups + k / 32) * 2 * 64 + lane) * 8 + k % 8;
-    halves[at] = hi;
-    halves[at + 64 * 8] = lo;
+// Elements k0 .. k0 + 7 of vector j (k0 % 8 == 0, already scaled): one
+// 16-byte store each for the hi and the lo halves
+__device__ __forceinline__ void put_halves8(_Float16* halves, int groups, int j, int k0, const float (&v)[8]) {
+    half8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        hi[i] = static_cast<_Float16>(v[i]);
+        lo[i] = static_cast<_Float16>(v[i] - static_cast<float>(hi[i]));
+    }
+    const int lane = (j % 16) + 16 * ((k0 % 32) / 8);
+    const size_t at = ((static_cast<size_t>(j / 16) * groups + k0 / 32) * 2 * 64 + lane) * 8;
+    *reinterpret_cast<half8*>(halves + at) = hi;
+    *reinterpret_cast<half8*>(halves + at + 64 * 8) = lo;
+}
+
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+
+__device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
 // the power of two that brings max |x| into [2^13, 2^14) (1 for 0 or a
@@ -596,18 +611,43 @@ __device__ __forceinline__ float block_max(float m, float* scratch) {
     return r;
 }
 
+// The per-vector epilogues run a workgroup per vector; a thread takes
+// eight consecutive elements a chunk (float4 loads, 16-byte halves stores),
+// at most kEpiChunks chunks: rows of up to 16,384 at 1,024 threads.
+constexpr int kEpiChunks = 2;
+
+// threads for a row of h elements: one chunk each up to 1,024 threads
+inline int epi_threads(int h) { return std::min(1024, std::max(64, ((h / 8 + 63) / 64) * 64)); }
+
 // halves of vector j = blockIdx.x (a row of cols floats)
-__global__ __launch_bounds__(256) void split_halves_kernel(const float* x, int cols, int groups, _Float16* halves,
-                                                            float* unscale) {
-    __shared__ float part[4];
-    const int j = blockIdx.x;
+__global__ __launch_bounds__(1024) void split_halves_kernel(const float* x, int cols, int groups, _Float16* halves,
+                                                             float* unscale) {
+    __shared__ float part[16];
+    const int j = blockIdx.x, T = blockDim.x;
     const float* xr = x + static_cast<size_t>(j) * cols;
+    float v[kEpiChunks][8];
     float m = 0.f;
-    for (int k = threadIdx.x; k < cols; k += 256) m = fmaxf(m, fabsf(xr[k]));
+#pragma unroll
+    for (int c = 0; c < kEpiChunks; ++c) {
+        const int e0 = 8 * (static_cast<int>(threadIdx.x) + T * c);
+        if (e0 < cols) {
+            load8(xr + e0, v[c]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[c][i]));
+        }
+    }
     const int shift = halves_shift(block_max(m, part));
     const float up = ldexpf(1.f, shift);
     if (threadIdx.x == 0) unscale[j] = ldexpf(1.f, -shift);
-    for (int k = threadIdx.x; k < cols; k += 256) put_halves(halves, groups, j, k, xr[k] * up);
+#pragma unroll
+    for (int c = 0; c < kEpiChunks; ++c) {
+        const int e0 = 8 * (static_cast<int>(threadIdx.x) + T * c);
+        if (e0 < cols) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[c][i] *= up;
+            put_halves8(halves, groups, j, e0, v[c]);
+        }
+    }
 }
 
 // eight int8 (two dwords) to eight fp16: each byte b, offset by 128, becomes
@@ -633,7 +673,7 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint2 q) {
 struct Q8BatchArgs {
     const uint4* q;
     const uint16_t* d;
-    const uint4* halves;  // 8 fp16 per lane, see put_halves
+    const uint4* halves;  // 8 fp16 per lane, see put_halves8
     const float* unscale;
     int rows, tiles, groups, pairs;  // tiles: one past the last row tile of this launch
     int tile0;                       // its first row tile (blockIdx.x counts from it)
@@ -815,6 +855,22 @@ __device__ __forceinline__ float split_total(const float* p, int splits, size_t 
     return split_sum<8>(p, splits, stride, at);
 }
 
+// the split sums of eight consecutive elements at p + at (16-byte aligned),
+// in split order from 0.f, four splits' loads requested at a time
+__device__ __forceinline__ void split_total8(const float* p, int splits, size_t stride, size_t at, float (&s)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = 0.f;
+    for (int k0 = 0; k0 < splits; k0 += 4) {
+        float v[4][8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) load8(p + static_cast<size_t>(min(k0 + k, splits - 1)) * stride + at, v[k]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s[i] = k0 + k < splits ? s[i] + v[k][i] : s[i];
+    }
+}
+
 // Q|K|V rows of vector j: q and k rotated by row j's (cos, sin)
 // (model.hpp:63-72), v copied; one thread per rotation pair or v element
 __global__ void qkv_epilogue_kernel(const float* p, int splits, int n, int qheads, int kheads, int dim, int interleaved,
@@ -844,79 +900,55 @@ __global__ void qkv_epilogue_kernel(const float* p, int splits, int n, int qhead
     }
 }
 
-// one workgroup per vector; rows up to kEpiThreads * kEpiPerThread = 16,384
-// are held in registers
-constexpr int kEpiThreads = 1024, kEpiPerThread = 16;
-
 // Vector j = blockIdx.x: x += the product's sum (the residual add, when p is
 // given), then RMSNorm with w (model.hpp:54-61: sum of squares in double,
-// scale rounded to float, (x * s) * w) into `norm` and, when `halves` is
-// given, into the next product's fp16 halves.  The row is kept in LDS
-// (dynamic, h floats).
-__global__ __launch_bounds__(kEpiThreads) void resid_norm_kernel(const float* p, int splits, float* x, const float* w, int n,
-                                                         int h, float eps, float* norm, _Float16* halves, int groups,
-                                                         float* unscale) {
-    extern __shared__ float row[];
-    __shared__ double part[kEpiThreads / 64];
-    __shared__ float mpart[kEpiThreads / 64];
-    const int j = blockIdx.x;
+// scale rounded to float, (x * s) * w) into `norm` (when given) and, when
+// `halves` is given, into the next product's fp16 halves.  A thread keeps
+// its chunks in registers between the passes.
+__global__ __launch_bounds__(1024) void resid_norm_kernel(const float* p, int splits, float* x, const float* w, int n,
+                                                          int h, float eps, float* norm, _Float16* halves, int groups,
+                                                          float* unscale) {
+    __shared__ double part[16];
+    __shared__ float mpart[16];
+    const int j = blockIdx.x, T = blockDim.x;
     float* xr = x + static_cast<size_t>(j) * h;
     const size_t stride = static_cast<size_t>(n) * h;
+    float y[kEpiChunks][8], wv[kEpiChunks][8];
     double sq = 0;
-    for (int e = threadIdx.x; e < h; e += kEpiThreads) {
-        float y = xr[e];
-        if (p) {
-            y = __fadd_rn(y, split_total(p, splits, stride, static_cast<size_t>(j) * h + e));
-            xr[e] = y;
+#pragma unroll
+    for (int c = 0; c < kEpiChunks; ++c) {
+        const int e0 = 8 * (static_cast<int>(threadIdx.x) + T * c);
+        if (e0 < h) {
+            load8(xr + e0, y[c]);
+            load8(w + e0, wv[c]);
+            if (p) {
+                float t[8];
+                split_total8(p, splits, stride, static_cast<size_t>(j) * h + e0, t);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) y[c][i] = __fadd_rn(y[c][i], t[i]);
+                store8(xr + e0, y[c]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sq += static_cast<double>(y[c][i]) * y[c][i];
         }
-        row[e] = y;
-        sq += static_cast<double>(y) * y;
     }
     for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = sq;
     __syncthreads();
     double t = 0;
-    for (int wv = 0; wv < kEpiThreads / 64; ++wv) t += part[wv];
+    for (int wave = 0; wave < T / 64; ++wave) t += part[wave];
     const float inv = static_cast<float>(1.0 / sqrt(t / static_cast<double>(h) + static_cast<double>(eps)));
     float mx = 0.f;
-    for (int e = threadIdx.x; e < h; e += kEpiThreads) {
-        const float v = __fmul_rn(__fmul_rn(row[e], inv), w[e]);
-        norm[static_cast<size_t>(j) * h + e] = v;
-        row[e] = v;
-        mx = fmaxf(mx, fabsf(v));
-    }
-    if (!halves) return;
-    const int shift = halves_shift(block_max(mx, mpart));
-    const float up = ldexpf(1.f, shift);
-    if (threadIdx.x == 0) unscale[j] = ldexpf(1.f, -shift);
-    for (int e = threadIdx.x; e < h; e += kEpiThreads) put_halves(halves, groups, j, e, row[e] * up);
-}
-
-// Vector j = blockIdx.x of the fused gate|up product: gate * (sigmoid(gate)
-// * up) (model.hpp:111-116) into `out` and, when given, the next product's
-// halves
-__global__ __launch_bounds__(kEpiThreads) void swiglu_epilogue_kernel(const float* p, int splits, int n, int inter, float* out,
-                                                              _Float16* halves, int groups, float* unscale,
-                                                              int interleaved) {
-    __shared__ float mpart[kEpiThreads / 64];
-    const int j = blockIdx.x;
-    const size_t stride = static_cast<size_t>(n) * 2 * inter, base = static_cast<size_t>(j) * 2 * inter;
-    float val[kEpiPerThread];
-    float mx = 0.f;
 #pragma unroll
-    for (int m = 0; m < kEpiPerThread; ++m) {
-        const int e = threadIdx.x + kEpiThreads * m;
-        val[m] = 0.f;
-        if (e < inter) {
-            const size_t ge = interleaved ? base + 2 * e : base + e, ue = interleaved ? ge + 1 : base + inter + e;
-            const float g = split_total(p, splits, stride, ge);
-            const float u = split_total(p, splits, stride, ue);
-            const float small = expf(-fabsf(g));
-            const float one = __fadd_rn(1.f, small);
-            const float sig = g >= 0 ? __fdiv_rn(1.f, one) : __fdiv_rn(small, one);
-            val[m] = __fmul_rn(g, __fmul_rn(sig, u));
-            out[static_cast<size_t>(j) * inter + e] = val[m];
-            mx = fmaxf(mx, fabsf(val[m]));
+    for (int c = 0; c < kEpiChunks; ++c) {
+        const int e0 = 8 * (static_cast<int>(threadIdx.x) + T * c);
+        if (e0 < h) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                y[c][i] = __fmul_rn(__fmul_rn(y[c][i], inv), wv[c][i]);
+                mx = fmaxf(mx, fabsf(y[c][i]));
+            }
+            if (norm) store8(norm + static_cast<size_t>(j) * h + e0, y[c]);
         }
     }
     if (!halves) return;
@@ -924,9 +956,68 @@ __global__ __launch_bounds__(kEpiThreads) void swiglu_epilogue_kernel(const floa
     const float up = ldexpf(1.f, shift);
     if (threadIdx.x == 0) unscale[j] = ldexpf(1.f, -shift);
 #pragma unroll
-    for (int m = 0; m < kEpiPerThread; ++m) {
-        const int e = threadIdx.x + kEpiThreads * m;
-        if (e < inter) put_halves(halves, groups, j, e, val[m] * up);
+    for (int c = 0; c < kEpiChunks; ++c) {
+        const int e0 = 8 * (static_cast<int>(threadIdx.x) + T * c);
+        if (e0 < h) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) y[c][i] *= up;
+            put_halves8(halves, groups, j, e0, y[c]);
+        }
+    }
+}
+
+// Vector j = blockIdx.x of the fused gate|up product: gate * (sigmoid(gate)
+// * up) (model.hpp:111-116) into `out` (when given) and, when given, the next
+// product's halves
+__global__ __launch_bounds__(1024) void swiglu_epilogue_kernel(const float* p, int splits, int n, int inter, float* out,
+                                                               _Float16* halves, int groups, float* unscale,
+                                                               int interleaved) {
+    __shared__ float mpart[16];
+    const int j = blockIdx.x, T = blockDim.x;
+    const size_t stride = static_cast<size_t>(n) * 2 * inter, base = static_cast<size_t>(j) * 2 * inter;
+    float val[kEpiChunks][8];
+    float mx = 0.f;
+#pragma unroll
+    for (int c = 0; c < kEpiChunks; ++c) {
+        const int e0 = 8 * (static_cast<int>(threadIdx.x) + T * c);
+        if (e0 < inter) {
+            float g[8], u[8];
+            if (interleaved) {  // rows 2e (gate), 2e + 1 (up)
+                float a[8], b[8];
+                split_total8(p, splits, stride, base + 2 * static_cast<size_t>(e0), a);
+                split_total8(p, splits, stride, base + 2 * static_cast<size_t>(e0) + 8, b);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    g[i] = a[2 * i], u[i] = a[2 * i + 1];
+                    g[4 + i] = b[2 * i], u[4 + i] = b[2 * i + 1];
+                }
+            } else {
+                split_total8(p, splits, stride, base + e0, g);
+                split_total8(p, splits, stride, base + inter + e0, u);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float small = expf(-fabsf(g[i]));
+                const float one = __fadd_rn(1.f, small);
+                const float sig = g[i] >= 0 ? __fdiv_rn(1.f, one) : __fdiv_rn(small, one);
+                val[c][i] = __fmul_rn(g[i], __fmul_rn(sig, u[i]));
+                mx = fmaxf(mx, fabsf(val[c][i]));
+            }
+            if (out) store8(out + static_cast<size_t>(j) * inter + e0, val[c]);
+        }
+    }
+    if (!halves) return;
+    const int shift = halves_shift(block_max(mx, mpart));
+    const float up = ldexpf(1.f, shift);
+    if (threadIdx.x == 0) unscale[j] = ldexpf(1.f, -shift);
+#pragma unroll
+    for (int c = 0; c < kEpiChunks; ++c) {
+        const int e0 = 8 * (static_cast<int>(threadIdx.x) + T * c);
+        if (e0 < inter) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) val[c][i] *= up;
+            put_halves8(halves, groups, j, e0, val[c]);
+        }
     }
 }
 
@@ -1211,7 +1302,9 @@ void launch_batch_product_tiles(const Weight& w, int tile0, int tile1, const _Fl
 }
 
 void launch_split_halves(const float* x, int n, int cols, _Float16* halves, float* unscale, hipStream_t s) {
-    launch("model_split_halves", split_halves_kernel, dim3(n), dim3(256), 0, s, x, cols, cols / 32, halves, unscale);
+    if (cols % 32 || cols > 1024 * 8 * kEpiChunks) throw std::invalid_argument("batched decode width above 16384");
+    launch("model_split_halves", split_halves_kernel, dim3(n), dim3(epi_threads(cols)), 0, s, x, cols, cols / 32, halves,
+           unscale);
     TVARA_HIP(hipGetLastError());
 }
 
@@ -1225,17 +1318,17 @@ void launch_qkv_epilogue(const float* p, int splits, int n, int qheads, int khea
 
 void launch_resid_norm(const float* p, int splits, float* x, const float* w, int n, int h, float eps, float* norm,
                        _Float16* halves, float* unscale, hipStream_t s) {
-    if (h > kEpiThreads * kEpiPerThread) throw std::invalid_argument("batched decode width above 16384");
-    launch("model_resid_norm", resid_norm_kernel, dim3(n), dim3(kEpiThreads), static_cast<size_t>(h) * sizeof(float), s,
-           p, splits, x, w, n, h, eps, norm, halves, h / 32, unscale);
+    if (h % 32 || h > 1024 * 8 * kEpiChunks) throw std::invalid_argument("batched decode width above 16384");
+    launch("model_resid_norm", resid_norm_kernel, dim3(n), dim3(epi_threads(h)), 0, s, p, splits, x, w, n, h, eps, norm,
+           halves, h / 32, unscale);
     TVARA_HIP(hipGetLastError());
 }
 
 void launch_swiglu_epilogue(const float* p, int splits, int n, int inter, float* out, _Float16* halves,
                             float* unscale, hipStream_t s, bool interleaved) {
-    if (inter > kEpiThreads * kEpiPerThread) throw std::invalid_argument("batched decode width above 16384");
-    launch("model_swiglu_epilogue", swiglu_epilogue_kernel, dim3(n), dim3(kEpiThreads), 0, s, p, splits, n, inter, out,
-           halves, inter / 32, unscale, interleaved ? 1 : 0);
+    if (inter % 32 || inter > 1024 * 8 * kEpiChunks) throw std::invalid_argument("batched decode width above 16384");
+    launch("model_swiglu_epilogue", swiglu_epilogue_kernel, dim3(n), dim3(epi_threads(inter)), 0, s, p, splits, n, inter,
+           out, halves, inter / 32, unscale, interleaved ? 1 : 0);
     TVARA_HIP(hipGetLastError());
 }
 

@@ -190,6 +190,18 @@ class LlamaSpec:
         return path
 
 
+def tiny_random_llama(**kw):
+    """The shape of the reference's arithmetic fixture, Hugging Face's
+    tiny-random-LlamaForCausalLM (docs/reference-model.md:3-6: hidden 16, two
+    layers; 4 / 4 heads, FFN 64, vocabulary 32,000), exported with the split
+    RoPE layout as tools/convert_reference_gguf.py:47 writes it, with random
+    f32 weights."""
+    args = dict(vocab=32000, hidden=16, intermediate=64, layers=2, heads=4, kv_heads=4, context=2048,
+                rms_epsilon=1e-6, rope_layout="split", seed=13)
+    args.update(kw)
+    return LlamaSpec(**args)
+
+
 def llama32_1b(**kw):
     """The Llama-3.2-1B shape (16 layers, hidden 2048, 32 / 8 heads, FFN 8192,
     vocabulary 128,256, tied embedding) with random Q8_0 weights."""

@@ -15,10 +15,13 @@ kv_c3      KV-management stress: 256 sequences share a 1,024-token prefix
 prefill_c4 8 sequences x (2,048 cached + 512-token causal chunk), 32/8 heads, d=64.
 decode_c5  16 sequences x 32,768 tokens, Llama-3-8B attention: 32/8 heads,
            d=128, Q8_0 blocks.
+conversations  the reference's seeded multi-turn conversation traces replayed
+           through a model, with and without prefix reuse.
 """
 
 from __future__ import annotations
 
+import time
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -303,3 +306,96 @@ def run_kv_stress(cache, w: KVStress, on_phase=None):
     if on_phase:
         on_phase("rollback", seqs)
     return seqs
+
+
+# ------------------------------------------------------------ conversations
+
+def conversation_traces(seed=262, conversations=4, turns=5, vocab=32000):
+    """The reference's conversation traces (tools/run_prefix_cache_traces.py:22-33,
+    defaults :93-98): a 64-token system prompt shared by every conversation,
+    then `turns` user turns of 16-48 random token ids.  The ids come from the
+    same numpy generator calls in the same order, so the traces are the
+    reference's own."""
+    rng = np.random.default_rng(seed)
+    system = rng.integers(1, vocab, 64).tolist()
+    traces = []
+    for _ in range(conversations):
+        users = []
+        for _ in range(turns):
+            length = int(rng.integers(16, 49))
+            users.append(rng.integers(1, vocab, length).tolist())
+        traces.append({"system": system, "users": users})
+    return traces
+
+
+def replay_conversations(model, traces, mode, reply_tokens=12, tree=None, clock=None):
+    """Replays the traces through `model` (a tvara_amd.native.NativeModel) as
+    run_trace does (tools/run_prefix_cache_traces.py:53-91): per turn the
+    prompt (the history plus the user turn) is prefilled and reply_tokens
+    greedy tokens follow, all but the last fed back.  Modes:
+
+    off    every turn prefills its whole prompt in a fresh sequence;
+    on     a conversation keeps its live sequence between turns, so only the
+           new suffix is prefilled (the reference's cache-on mode);
+    radix  as on, and a conversation's first turn restores the shared system
+           prompt from `tree` (a tvara_amd.radix.RadixCache over the model's
+           cache), the first conversation inserting it.
+
+    Prefills go through NativeModel.prefill (one chunked pass per 512 tokens
+    on this library).  Returns per trace the list of turns: prompt and
+    reused token counts, prefill seconds, the prompt's last logits and the
+    reply."""
+    clock = clock or time.perf_counter
+    if mode not in ("off", "on", "radix") or (mode == "radix" and tree is None):
+        raise ValueError("mode is off, on or radix (with a tree)")
+    results = []
+    for trace in traces:
+        system = list(trace["system"])
+        history, turns, sequence, fed = list(system), [], None, []
+        try:
+            for user in trace["users"]:
+                history += user
+                seconds = 0.0
+                if mode != "off" and sequence is not None and history[: len(fed)] == fed:
+                    suffix, reused = history[len(fed):], len(fed)
+                else:
+                    if sequence is not None:
+                        model.drop_sequence(sequence)
+                    sequence, fed, reused = None, [], 0
+                    if mode == "radix":
+                        start = clock()
+                        node, matched = tree.lookup(system)
+                        if matched == len(system) and tree.node(node)["kv_length"] is not None:
+                            sequence, reused = tree.reuse(system)
+                            fed = system[:reused]
+                        else:
+                            sequence = model.new_sequence()
+                            model.prefill(sequence, system)
+                            tree.attach(tree.insert(system), sequence)
+                            fed = list(system)
+                        seconds += clock() - start
+                    else:
+                        sequence = model.new_sequence()
+                    suffix = history[len(fed):]
+                start = clock()
+                logits = model.prefill(sequence, suffix)
+                seconds += clock() - start
+                fed += suffix
+                reply = []
+                for index in range(reply_tokens):
+                    token = int(np.asarray(logits if index == 0 else step).argmax())
+                    reply.append(token)
+                    if index + 1 < reply_tokens:
+                        step = model.logits(sequence, token)
+                fed += reply[:-1]
+                history += reply
+                turns.append({"prompt_tokens": len(history) - len(reply), "reused_tokens": reused,
+                              "prefill_seconds": seconds, "logits": logits, "reply": reply})
+                if mode == "off":
+                    model.drop_sequence(sequence)
+                    sequence, fed = None, []
+        finally:
+            if sequence is not None:
+                model.drop_sequence(sequence)
+        results.append(turns)
+    return results
