@@ -79,9 +79,14 @@ def build_cmake(verbose: bool = False, jobs: int | None = None) -> Path:
     return LIBRARY
 
 
+# per-source flags, as CMakeLists.txt sets them
+SOURCE_FLAGS = {"model_kernels.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path, obj: Path, verbose: bool):
     lang = ["-x", "hip"] if src.suffix == ".hip" else []
-    return _run([HIPCC, *FLAGS, *lang, "-c", str(src), "-o", str(obj)], verbose).stderr
+    extra = SOURCE_FLAGS.get(src.name, [])
+    return _run([HIPCC, *FLAGS, *extra, *lang, "-c", str(src), "-o", str(obj)], verbose).stderr
 
 
 def build_hipcc(verbose: bool = False, jobs: int | None = None) -> Path:

@@ -695,6 +695,20 @@ struct Q8BatchArgs {
 // the activations of chunk c + 1 are requested after chunk c's barrier.
 // Prefetches are unconditional (clamped to the last chunk) so that the
 // compiler keeps them ahead of the arithmetic.
+//
+// Every operand is read through a buffer descriptor: a thread keeps a fixed
+// byte offset per load slot and a chunk adds one scalar offset, so the loads
+// cost no vector address arithmetic.  The weight and scale views cover this
+// workgroup's row tiles only and the activation view this wave's vector
+// tile; reads past a view return zero.  The groups past the split's end (a
+// last chunk of fewer than four) read their activations past the view, so
+// they multiply zeros and add exactly nothing.
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 buffer descriptor, dword 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t view(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferWord3);
+}
+
 template <int NT, int RT>
 __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
     constexpr int P = 2, CG = 2 * P;                 // pairs and groups per chunk
@@ -705,30 +719,43 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
     constexpr int DPT = (DW + NTH - 1) / NTH;        // per thread
     __shared__ half8 ws[2][CG][RT][64];
     __shared__ uint32_t wd[2][RT][P][16];
-    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gbeg = static_cast<int>(blockIdx.y) * a.groups_per_split;
     const int gend = min(a.groups, gbeg + a.groups_per_split);
-    const int pbeg = gbeg / 2, plast = (gend - 1) / 2;
+    const int pbeg = gbeg / 2;
     const int nchunks = (gend - gbeg + CG - 1) / CG;
     const int t0 = a.tile0 + static_cast<int>(blockIdx.x) * RT;
-    const u32x4* xsrc = reinterpret_cast<const u32x4*>(a.halves) + static_cast<size_t>(a.vt0 + wave) * a.groups * 2 * 64;
-    const uint32_t* dsrc = reinterpret_cast<const uint32_t*>(a.d);
+    const int tiles_here = min(RT, a.tiles - t0);
+    const __amdgpu_buffer_rsrc_t qv =
+        view(a.q + static_cast<size_t>(t0) * a.pairs * 64, static_cast<uint32_t>(tiles_here * a.pairs) * 1024u);
+    const __amdgpu_buffer_rsrc_t dv = view(reinterpret_cast<const uint32_t*>(a.d) + static_cast<size_t>(t0) * a.pairs * 16,
+                                           static_cast<uint32_t>(tiles_here * a.pairs) * 64u);
+    const uint32_t xbytes = static_cast<uint32_t>(a.groups) * 2048u;
+    const __amdgpu_buffer_rsrc_t xv = view(a.halves + static_cast<size_t>(a.vt0 + wave) * a.groups * 2 * 64, xbytes);
+    // byte offsets of this thread's load slots within a chunk
+    uint32_t qoff[WPT], doff[DPT];
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+        const int e = min(tid + NTH * i, RAW - 1);
+        const int r = (e >> 6) / P, p = (e >> 6) % P;
+        qoff[i] = static_cast<uint32_t>(((r * a.pairs + p) * 64 + (e & 63)) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) {
+        const int e = min(tid + NTH * i, DW - 1);
+        const int r = e / (P * 16), p = (e / 16) % P;
+        doff[i] = static_cast<uint32_t>(((r * a.pairs + p) * 16 + (e & 15)) * 4);
+    }
+    const uint32_t xoff = static_cast<uint32_t>(lane) * 16u;
 
     auto load_raw = [&](int chunk, uint4 (&raw)[WPT], uint32_t (&dr)[DPT]) {
+        const int pc = pbeg + chunk * P;
 #pragma unroll
-        for (int i = 0; i < WPT; ++i) {
-            const int e = min(tid + NTH * i, RAW - 1);
-            const int r = (e >> 6) / P, p = (e >> 6) % P;
-            const int t = min(t0 + r, a.tiles - 1), pp = min(pbeg + chunk * P + p, plast);
-            raw[i] = a.q[(static_cast<size_t>(t) * a.pairs + pp) * 64 + (e & 63)];
-        }
+        for (int i = 0; i < WPT; ++i)
+            raw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(qv, qoff[i], pc * 1024, 0));
 #pragma unroll
-        for (int i = 0; i < DPT; ++i) {
-            const int e = min(tid + NTH * i, DW - 1);
-            const int r = e / (P * 16), p = (e / 16) % P;
-            const int t = min(t0 + r, a.tiles - 1), pp = min(pbeg + chunk * P + p, plast);
-            dr[i] = dsrc[(static_cast<size_t>(t) * a.pairs + pp) * 16 + (e & 15)];
-        }
+        for (int i = 0; i < DPT; ++i) dr[i] = __builtin_amdgcn_raw_buffer_load_b32(dv, doff[i], pc * 64, 0);
     };
     auto stage = [&](int buf, const uint4 (&raw)[WPT], const uint32_t (&dr)[DPT]) {
 #pragma unroll
@@ -748,15 +775,16 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
     auto load_x = [&](int chunk, u32x4 (&x)[CG][2]) {
 #pragma unroll
         for (int c = 0; c < CG; ++c) {
-            const int g = min(gbeg + chunk * CG + c, gend - 1);
-            x[c][0] = xsrc[(static_cast<size_t>(g) * 2) * 64 + lane];
-            x[c][1] = xsrc[(static_cast<size_t>(g) * 2 + 1) * 64 + lane];
+            const int g = gbeg + chunk * CG + c;
+            const int so = g < gend ? g * 2048 : static_cast<int>(xbytes);  // past the split: zeros
+            x[c][0] = __builtin_amdgcn_raw_buffer_load_b128(xv, xoff, so, 0);
+            x[c][1] = __builtin_amdgcn_raw_buffer_load_b128(xv, xoff + 1024u, so, 0);
         }
     };
     float4v acc[RT];
 #pragma unroll
     for (int r = 0; r < RT; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](int chunk, int buf, const u32x4 (&x)[CG][2]) {
+    auto compute = [&](int buf, const u32x4 (&x)[CG][2]) {
         uint32_t dd[RT][P];
 #pragma unroll
         for (int r = 0; r < RT; ++r)
@@ -764,7 +792,6 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
             for (int p = 0; p < P; ++p) dd[r][p] = wd[buf][r][p][lane & 15];
 #pragma unroll
         for (int c = 0; c < CG; ++c) {
-            const bool live = gbeg + chunk * CG + c < gend;  // uniform across the workgroup
             const half8 xh = __builtin_bit_cast(half8, x[c][0]), xl = __builtin_bit_cast(half8, x[c][1]);
             half8 w[RT];
 #pragma unroll
@@ -777,8 +804,7 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
             for (int r = 0; r < RT; ++r) cc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, w[r], cc[r], 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
-                const float d =
-                    live ? half_bits_to_float(static_cast<uint16_t>(dd[r][c / 2] >> (c % 2 ? 16 : 0))) : 0.f;
+                const float d = half_bits_to_float(static_cast<uint16_t>(dd[r][c / 2] >> (c % 2 ? 16 : 0)));
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[r][i] = fmaf(d, cc[r][i], acc[r][i]);
             }
@@ -797,13 +823,13 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
     __syncthreads();
     for (int k = 0;; k += 2) {
         load_raw(min(k + 2, nchunks - 1), rA, dA);
-        compute(k, 0, xA);
+        compute(0, xA);
         stage(1, rB, dB);
         __syncthreads();
         if (k + 1 >= nchunks) break;
         load_x(min(k + 2, nchunks - 1), xA);
         load_raw(min(k + 3, nchunks - 1), rB, dB);
-        compute(k + 1, 1, xB);
+        compute(1, xB);
         stage(0, rA, dA);
         __syncthreads();
         if (k + 2 >= nchunks) break;
