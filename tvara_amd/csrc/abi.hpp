@@ -12,8 +12,13 @@
 
 namespace tvara_amd::abi {
 
+// The message is meaningful only while the status says a call failed, so
+// clearing (every call) touches the status alone: a trivially constructed
+// thread-local, read without the wrapper a std::string needs, and in the
+// initial-exec model (4 bytes of the static TLS block, a thread-pointer
+// relative access instead of a __tls_get_addr call).
 extern thread_local std::string error_message;
-extern thread_local int error_status;
+extern thread_local int error_status __attribute__((tls_model("initial-exec")));
 
 inline int failed(int status, const char* what) {
     error_message = what;
@@ -21,10 +26,7 @@ inline int failed(int status, const char* what) {
     return status;
 }
 
-inline void clear() {
-    error_message.clear();
-    error_status = TVARA_OK;
-}
+inline void clear() { error_status = TVARA_OK; }
 
 template <class F>
 int guard(F&& f) {
