@@ -224,6 +224,44 @@ def test_bf16_c4_shape(device, oracle, make, fmt):
     say("c4 bf16 vs f32 path (max rel, rms):", err)
 
 
+@pytest.mark.parametrize("make,fmt", [(workloads.prefill_c4, "f32"), (workloads.prefill_8b, "f32"),
+                                      (workloads.prefill_c4, "q8_0")], ids=["d64", "d128", "d64-q8_0"])
+def test_c4_every_row_against_reference(device, oracle, ref, make, fmt):
+    # every one of the batch's 8 x 512 rows, on both paths, against the
+    # reference's own fused_prompt_attention (attention.hpp:85-89, built from
+    # its sources in oracle/_ref) run over the same K/V on the host's threads:
+    # the f32 path within the f32 bar, the bf16 path within its derived bars
+    import os
+
+    w = make()
+    say("prefill every row", w.name, fmt)
+    g = (1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks())
+    q8 = fmt == "q8_0"
+    dev = device.PagedCache(*g, fmt=device.Q8_0 if q8 else device.F32)
+    ds = workloads.fill_prefill(dev, w)
+    q = np.concatenate([w.chunk_queries(i) for i in range(w.sequences)])
+    args = (ds, [w.prefix] * w.sequences, [w.chunk] * w.sequences, 0, w.heads, w.context)
+    got = attention.prefill_batch(dev, q, *args, precision="bf16").reshape(w.sequences, w.chunk, -1)
+    f32 = attention.prefill_batch(dev, q, *args, precision="f32").reshape(w.sequences, w.chunk, -1)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rc = ref.RefCache(*g)
+    want = np.empty_like(f32)
+    for i in range(w.sequences):
+        k, v = w.keys(i), w.values(i)
+        if q8:  # the reference holds the dequantised values the Q8_0 blocks store
+            k = oracle.dequantize_q8_0(oracle.quantize_q8_0(k)).reshape(k.shape)
+            v = oracle.dequantize_q8_0(oracle.quantize_q8_0(v)).reshape(v.shape)
+        s = rc.create_sequence()
+        rc.append_many(s, k, v)
+        want[i] = rc.prompt_batch(w.chunk_queries(i), s, 0, w.prefix, w.chunk, w.heads, w.context, 16,
+                                  threads).reshape(w.chunk, -1)
+        rc.drop(s)
+    assert refmath.close(f32, want, TOL_F32), refmath.max_rel(f32, want)
+    ok, err = bf16_ok(got, want, LONG_ROWS)
+    assert ok, err
+    say("every row: f32 max rel", refmath.max_rel(f32, want), "bf16 (max rel, rms)", err)
+
+
 @pytest.mark.parametrize("precision", ["bf16", "f32"])
 def test_prefill_plan_matches_call(device, oracle, precision):
     # a resident plan launched on two layers gives the one-shot call's bytes,
