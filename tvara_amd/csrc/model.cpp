@@ -261,7 +261,7 @@ void DeviceModel::ensure_batch(size_t n) {
     const ModelConfig& c = cfg_;
     const size_t H = c.hidden, I = c.intermediate, KV = c.kv_width(), L = c.layers, F = sizeof(float);
     if (!part_rows_) {
-        auto note = [&](const Weight& w) { part_rows_ = std::max(part_rows_, static_cast<size_t>(batch_splits(w)) * w.rows); };
+        auto note = [&](const Weight& w) { part_rows_ = std::max(part_rows_, static_cast<size_t>(batch_splits_max(w)) * w.rows); };
         for (const Layer& l : layers_) {
             note(l.qkv);
             note(l.out);
@@ -418,22 +418,22 @@ void DeviceModel::layer_stack(size_t n, const Attend& attend) {
         float* kl = at(bk_, l * n * c.kv_width());
         float* vl = at(bv_, l * n * c.kv_width());
         launch_batch_product(L.qkv, norm, halves, unscale, N, part, s);
-        launch_qkv_epilogue(part, batch_splits(L.qkv), N, static_cast<int>(c.heads), static_cast<int>(c.kv_heads), D,
+        launch_qkv_epilogue(part, batch_splits(L.qkv, N), N, static_cast<int>(c.heads), static_cast<int>(c.kv_heads), D,
                             c.interleaved_rope, at(brope_, 0), q, kl, vl, s);
         attend(static_cast<int>(l), q, kl, vl, attn);
         if (l + 1 == c.layers) TVARA_HIP(hipEventRecord(step_events_.attn, s));
         if (L.out.q8) launch_split_halves(attn, N, H, halves, unscale, s);
         launch_batch_product(L.out, attn, halves, unscale, N, part, s);
-        launch_resid_norm(part, batch_splits(L.out), x, at(L.ffn_norm, 0), N, H, c.rms_epsilon,
+        launch_resid_norm(part, batch_splits(L.out, N), x, at(L.ffn_norm, 0), N, H, c.rms_epsilon,
                           rows_for(L.gate_up, norm), halves_for(L.gate_up), unscale, s);
         launch_batch_product(L.gate_up, norm, halves, unscale, N, part, s);
-        launch_swiglu_epilogue(part, batch_splits(L.gate_up), N, I, rows_for(L.down, gate), halves_for(L.down), unscale,
+        launch_swiglu_epilogue(part, batch_splits(L.gate_up, N), N, I, rows_for(L.down, gate), halves_for(L.down), unscale,
                                s, L.gate_up.interleaved);
         launch_batch_product(L.down, gate, halves, unscale, N, part, s);
         // after the last layer the rows stay too: the logits of chosen rows
         // are taken from them
         const bool last = l + 1 == c.layers;
-        launch_resid_norm(part, batch_splits(L.down), x, last ? at(final_norm_, 0) : at(layers_[l + 1].attn_norm, 0), N,
+        launch_resid_norm(part, batch_splits(L.down, N), x, last ? at(final_norm_, 0) : at(layers_[l + 1].attn_norm, 0), N,
                           H, c.rms_epsilon, last ? norm : rows_for(layers_[l + 1].qkv, norm),
                           halves_for(last ? logits_w : layers_[l + 1].qkv), unscale, s);
     }
@@ -454,7 +454,7 @@ DeviceModel::LogitsBands DeviceModel::launch_logits(size_t n, size_t row0) {
     LogitsBands b;
     const int vocab = static_cast<int>(c.vocab);
     constexpr int kBands = StepEvents::kBands;
-    b.banded = logits_w.q8 && batch_splits(logits_w) == 1 && n * c.vocab * sizeof(float) >= (size_t(8) << 20);
+    b.banded = logits_w.q8 && batch_splits(logits_w, N) == 1 && n * c.vocab * sizeof(float) >= (size_t(8) << 20);
     if (b.banded) {
         const int tiles = logits_w.tiles(), per = (tiles + kBands - 1) / kBands;
         for (int t = 0; t < tiles; t += per) {
@@ -463,12 +463,12 @@ DeviceModel::LogitsBands DeviceModel::launch_logits(size_t n, size_t row0) {
             b.bounds[b.bands++] = static_cast<size_t>(t) * 16;
         }
         b.bounds[b.bands] = c.vocab;
-    } else if (batch_splits(logits_w) == 1) {
+    } else if (batch_splits(logits_w, N) == 1) {
         launch_batch_product(logits_w, norm, halves, unscale, N, at(blogits_, 0), s);
     } else {
         float* part = at(bpart_, 0);
         launch_batch_product(logits_w, norm, halves, unscale, N, part, s);
-        launch_split_sum(part, batch_splits(logits_w), N, vocab, at(blogits_, 0), s);
+        launch_split_sum(part, batch_splits(logits_w, N), N, vocab, at(blogits_, 0), s);
     }
     return b;
 }

@@ -64,7 +64,9 @@ void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg,
 // weights read the vectors as fp16 halves (launch_split_halves or an
 // epilogue below writes them, with a power-of-two unscale per vector), f32
 // weights read x [n][cols].
-int batch_splits(const Weight& w);
+int batch_splits(const Weight& w, int n);
+// the most splits any n gives (the size of a partial-sum buffer)
+int batch_splits_max(const Weight& w);
 void launch_batch_product(const Weight& w, const float* x, const _Float16* halves, const float* unscale, int n,
                           float* out, hipStream_t s);
 // the rows of row tiles [tile0, tile1) of an unsplit Q8_0 product (out as for

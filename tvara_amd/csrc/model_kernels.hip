@@ -679,6 +679,7 @@ struct Q8BatchArgs {
     int tile0;                       // its first row tile (blockIdx.x counts from it)
     int n, vt0;                      // vectors in this launch, first vector tile
     int n_total;
+    int n_total_tiles;  // vector tiles the halves hold
     int groups_per_split;
     float* out;  // [gridDim.y][n_total][rows]
 };
@@ -848,6 +849,151 @@ __global__ __launch_bounds__(256) void batch_q8_kernel(const Q8BatchArgs a) {
             const int row = (t0 + r) * 16 + (lane & 15);
             if (t0 + r < a.tiles && row < a.rows) out[static_cast<size_t>(j) * a.rows + row] = acc[r][i] * us;
         }
+    }
+}
+
+// Weight-stationary form of the same product, for any number of vectors in
+// one launch.  A workgroup of four waves owns RT row tiles over one K split
+// of a.groups_per_split groups (a multiple of four): it first converts the
+// split's int8 weights and scales into LDS, eight loads a thread requested
+// before the first conversion, and then each wave multiplies them against
+// its vector tiles in turn (tiles w, w + 4, ...), UG groups a step, the
+// activation halves of the next step (the next tile's first, at a tile's
+// end) in flight while a step is summed.  No barrier follows the staging.
+// The arithmetic per group is the chunked kernel's, so the sums are the
+// same.  LDS: groups_per_split * RT KiB of fp16 weights, then the scales.
+template <int RT, int UG>
+__global__ __launch_bounds__(256) void batch_q8_ws_kernel(const Q8BatchArgs a) {
+    extern __shared__ half8 wsh[];  // [groups_per_split][RT][64], then scales [RT][pairs][16] dwords
+    const int gps = a.groups_per_split, pps = gps / 2;
+    uint32_t* wsd = reinterpret_cast<uint32_t*>(wsh + static_cast<size_t>(gps) * RT * 64);
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gbeg = static_cast<int>(blockIdx.y) * gps;
+    const int gend = min(a.groups, gbeg + gps);
+    const int pbeg = gbeg / 2;
+    // every slot of the split's share is staged, the pairs past its end too
+    // (the next split's bytes, or zeros past the view): each weight and
+    // scale a dead group meets is finite, so its zero activations add zero
+    const int np = pps;
+    const int t0 = a.tile0 + static_cast<int>(blockIdx.x) * RT;
+    const int tiles_here = min(RT, a.tiles - t0);
+    const __amdgpu_buffer_rsrc_t qv =
+        view(a.q + static_cast<size_t>(t0) * a.pairs * 64, static_cast<uint32_t>(tiles_here * a.pairs) * 1024u);
+    const __amdgpu_buffer_rsrc_t dv = view(reinterpret_cast<const uint32_t*>(a.d) + static_cast<size_t>(t0) * a.pairs * 16,
+                                           static_cast<uint32_t>(tiles_here * a.pairs) * 64u);
+    // ---- staging: RT x np pairs x 64 lanes of int8, eight loads a thread a round
+    {
+        constexpr int B = 8;
+        const int units = RT * np * 64;
+        for (int e0 = tid; e0 < units; e0 += 256 * B) {
+            uint4 raw[B];
+#pragma unroll
+            for (int i = 0; i < B; ++i) {
+                const int e = e0 + 256 * i;  // past `units`: a read past the view (zeros), not stored
+                const int l = e & 63, rp = e >> 6, r = rp / np, p = rp - r * np;
+                raw[i] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                               qv, static_cast<uint32_t>(((r * a.pairs + p) * 64 + l) * 16), pbeg * 1024, 0));
+            }
+#pragma unroll
+            for (int i = 0; i < B; ++i) {
+                const int e = e0 + 256 * i;
+                if (e >= units) break;
+                const int l = e & 63, rp = e >> 6, r = rp / np, p = rp - r * np;
+                wsh[((2 * p) * RT + r) * 64 + l] = i8x8_to_half8(make_uint2(raw[i].x, raw[i].y));
+                wsh[((2 * p + 1) * RT + r) * 64 + l] = i8x8_to_half8(make_uint2(raw[i].z, raw[i].w));
+            }
+        }
+        const int dunits = RT * np * 16;
+        for (int e = tid; e < dunits; e += 256) {
+            const int row = e & 15, rp = e >> 4, r = rp / np, p = rp - r * np;
+            wsd[(r * pps + p) * 16 + row] = __builtin_amdgcn_raw_buffer_load_b32(
+                dv, static_cast<uint32_t>(((r * a.pairs + p) * 16 + row) * 4), pbeg * 64, 0);
+        }
+    }
+    __syncthreads();
+
+    // ---- products: this wave's vector tiles (w, w + 4, ...), UG groups a
+    // unit, one stream of (tile, unit) steps double-buffered across tiles
+    const int ntv = (a.n + 15) / 16;
+    const uint32_t xbytes = static_cast<uint32_t>(a.n_total_tiles) * static_cast<uint32_t>(a.groups) * 2048u;
+    const __amdgpu_buffer_rsrc_t xv = view(a.halves, xbytes);
+    const uint32_t xoff = static_cast<uint32_t>(lane) * 16u;
+    const int nunits = (gend - gbeg + UG - 1) / UG;
+    const int mytiles = wave < ntv ? (ntv - 1 - wave) / 4 + 1 : 0;
+    const int steps = mytiles * nunits;
+    auto load_x = [&](int k, u32x4 (&x)[UG][2]) {  // step k (clamped by the caller)
+        const int vt = wave + 4 * (k / nunits), u = k % nunits;
+#pragma unroll
+        for (int c = 0; c < UG; ++c) {
+            const int g = gbeg + UG * u + c;
+            const int so = g < gend ? ((a.vt0 + vt) * a.groups + g) * 2048 : static_cast<int>(xbytes);
+            x[c][0] = __builtin_amdgcn_raw_buffer_load_b128(xv, xoff, so, 0);
+            x[c][1] = __builtin_amdgcn_raw_buffer_load_b128(xv, xoff + 1024u, so, 0);
+        }
+    };
+    float4v acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
+    float* out = a.out + static_cast<size_t>(blockIdx.y) * a.n_total * a.rows;
+    auto step = [&](int k, const u32x4 (&x)[UG][2]) {
+        const int u = k % nunits;
+        uint32_t dd[RT][UG / 2];
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int p = 0; p < UG / 2; ++p)
+                dd[r][p] = wsd[(r * pps + min((UG / 2) * u + p, pps - 1)) * 16 + (lane & 15)];
+#pragma unroll
+        for (int c = 0; c < UG; ++c) {
+            const int gl = min(UG * u + c, gps - 1);  // a group past the split reads a staged one: its x is zero
+            const half8 xh = __builtin_bit_cast(half8, x[c][0]), xl = __builtin_bit_cast(half8, x[c][1]);
+            half8 w[RT];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) w[r] = wsh[(gl * RT + r) * 64 + lane];
+            float4v cc[RT];
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+                cc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, w[r], float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) cc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, w[r], cc[r], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const float d = half_bits_to_float(static_cast<uint16_t>(dd[r][c / 2] >> (c % 2 ? 16 : 0)));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[r][i] = fmaf(d, cc[r][i], acc[r][i]);
+            }
+        }
+        if (u + 1 < nunits) return;
+        // the tile's last unit: lane l holds row l%16 of each row tile for
+        // vectors 4(l/16) + i of vector tile vt
+        const int vt = wave + 4 * (k / nunits);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int jl = vt * 16 + 4 * (lane >> 4) + i;
+            if (jl >= a.n) continue;
+            const int j = a.vt0 * 16 + jl;
+            const float us = a.unscale[j];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const int row = (t0 + r) * 16 + (lane & 15);
+                if (t0 + r < a.tiles && row < a.rows) out[static_cast<size_t>(j) * a.rows + row] = acc[r][i] * us;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RT; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
+    };
+    if (steps == 0) return;
+    u32x4 xa[UG][2], xb[UG][2];
+    load_x(0, xa);
+    for (int k = 0;; k += 2) {
+        load_x(min(k + 1, steps - 1), xb);
+        step(k, xa);
+        if (k + 1 >= steps) break;
+        load_x(min(k + 2, steps - 1), xa);
+        step(k + 1, xb);
+        if (k + 2 >= steps) break;
     }
 }
 
@@ -1246,13 +1392,87 @@ F32Plan f32_plan(int rows, int cols) {
     p.splits = (chunks + p.per - 1) / p.per;
     return p;
 }
+
+// Weight-stationary plan: RT row tiles per workgroup (four from 1,024 row
+// tiles up, else two) and the K split that keeps a workgroup's fp16 weights
+// within 64 KiB of LDS, split further (in steps of four groups, never below
+// eight) while the launch has fewer than 512 workgroups.
+struct WsPlan {
+    int rt, gps, gx, splits;
+    size_t lds;
+};
+WsPlan ws_plan(const Weight& w) {
+    WsPlan p{};
+    const int tiles = w.tiles(), groups = w.groups();
+    p.rt = tiles >= 1024 ? 4 : 2;
+    p.gx = (tiles + p.rt - 1) / p.rt;
+    const int cap = 64 / p.rt;  // groups of fp16 weights in 64 KiB
+    int splits = (groups + cap - 1) / cap;
+    while (p.gx * splits < 512 && (groups + splits) / (splits + 1) >= 8) ++splits;
+    p.gps = (groups + splits - 1) / splits;
+    p.gps = (p.gps + 3) / 4 * 4;
+    if (p.gps > cap) p.gps = cap / 4 * 4;
+    p.splits = (groups + p.gps - 1) / p.gps;
+    p.lds = static_cast<size_t>(p.gps) * p.rt * 1024 + static_cast<size_t>(p.rt) * (p.gps / 2) * 64;
+    return p;
+}
+
+// The weight-stationary kernel from 128 vectors (matrices under 1,024 row
+// tiles) or 256 (under 4,096); the chunked kernel otherwise.  MI355X,
+// Llama-3.2-1B shapes, weights from HBM: QKV / output / gate|up / down at 512
+// vectors 35.6 / 28.8 / 117 / 70.8 us against 59.9 / 51.0 / 138.5 / 100.6;
+// at 128 vectors 13.5 / 11.0 / 48.3 / 23.9 against 16.2 / 13.4 / 37.6 /
+// 26.8; at 64 vectors, and for the 8,016-tile logits at every size, the
+// chunked kernel is faster (gate|up 18.9 against 32.2 us at 64; logits 841
+// against 862-891 us at 512).
+bool ws_for(const Weight& w, int n) {
+    const int t = w.tiles();
+    return w.q8 && t < 4096 && (n >= 256 || (n >= 128 && t < 1024));
+}
+
+void launch_ws(const Weight& w, const WsPlan& p, int tile0, int tile1, const _Float16* halves, const float* unscale,
+               int n, float* out, hipStream_t s) {
+    Q8BatchArgs a{};
+    a.q = static_cast<const uint4*>(w.q.ptr);
+    a.d = static_cast<const uint16_t*>(w.d.ptr);
+    a.halves = reinterpret_cast<const uint4*>(halves);
+    a.unscale = unscale;
+    a.rows = w.rows;
+    a.tiles = tile1;
+    a.tile0 = tile0;
+    a.groups = w.groups();
+    a.pairs = w.pairs();
+    a.n = n;
+    a.vt0 = 0;
+    a.n_total = n;
+    a.n_total_tiles = (n + 15) / 16;
+    a.groups_per_split = p.gps;
+    a.out = out;
+    if (static_cast<double>(a.n_total_tiles) * a.groups * 2048 >= 2147483648.0)
+        throw std::invalid_argument("batched product input above 2 GiB");
+    const dim3 grid((tile1 - tile0 + p.rt - 1) / p.rt, p.splits);
+    if (p.rt == 4)
+        launch("model_matvec_q8", batch_q8_ws_kernel<4, 4>, grid, dim3(256), p.lds, s, a);
+    else
+        launch("model_matvec_q8", batch_q8_ws_kernel<2, 4>, grid, dim3(256), p.lds, s, a);
+}
 }  // namespace
 
-int batch_splits(const Weight& w) { return w.q8 ? q8_plan(w).splits : f32_plan(w.rows, w.cols).splits; }
+int batch_splits(const Weight& w, int n) {
+    if (!w.q8) return f32_plan(w.rows, w.cols).splits;
+    return ws_for(w, n) ? ws_plan(w).splits : q8_plan(w).splits;
+}
+
+int batch_splits_max(const Weight& w) {
+    if (!w.q8) return f32_plan(w.rows, w.cols).splits;
+    return std::max(ws_plan(w).splits, q8_plan(w).splits);
+}
 
 void launch_batch_product(const Weight& w, const float* x, const _Float16* halves, const float* unscale, int n,
                           float* out, hipStream_t s) {
-    if (w.q8) {
+    if (ws_for(w, n)) {
+        launch_ws(w, ws_plan(w), 0, w.tiles(), halves, unscale, n, out, s);
+    } else if (w.q8) {
         const Q8Plan p = q8_plan(w);
         for (int j0 = 0; j0 < n; j0 += 64) {
             const int nj = std::min(64, n - j0);
@@ -1298,9 +1518,14 @@ void launch_batch_product(const Weight& w, const float* x, const _Float16* halve
 
 void launch_batch_product_tiles(const Weight& w, int tile0, int tile1, const _Float16* halves, const float* unscale,
                                 int n, float* out, hipStream_t s) {
-    const Q8Plan p = q8_plan(w);
-    if (!w.q8 || p.splits != 1 || tile0 < 0 || tile0 >= tile1 || tile1 > w.tiles())
+    if (!w.q8 || batch_splits(w, n) != 1 || tile0 < 0 || tile0 >= tile1 || tile1 > w.tiles())
         throw std::invalid_argument("row-tile range of a batched product needs an unsplit Q8_0 matrix");
+    if (ws_for(w, n)) {
+        launch_ws(w, ws_plan(w), tile0, tile1, halves, unscale, n, out, s);
+        TVARA_HIP(hipGetLastError());
+        return;
+    }
+    const Q8Plan p = q8_plan(w);
     for (int j0 = 0; j0 < n; j0 += 64) {
         const int nj = std::min(64, n - j0);
         Q8BatchArgs a{};
