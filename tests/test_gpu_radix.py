@@ -66,8 +66,10 @@ def test_isolation_and_lifetime(device):
 
 def test_model_prefix_reuse_is_bit_exact(tmp_path):
     # test_radix.cpp's model fixture: a 3-token stem decoded once, attached,
-    # then reused for six requests; each cached decode equals the cold decode
-    # of the whole prompt bit for bit
+    # then reused for six requests; each cached decode equals, bit for bit,
+    # the cold decode of the prompt through the same calls (the stem as one
+    # decode_batch, then the tail), and the whole prompt as one chunked
+    # decode_batch within the logit bar
     spec = gf.LlamaSpec(layers=2)
     m = native.NativeModel(spec.write(tmp_path / "m.gguf"), max_blocks=32, block_tokens=4)
     cache = m.cache()
@@ -82,8 +84,13 @@ def test_model_prefix_reuse_is_bit_exact(tmp_path):
         assert length == 3 and cache.length(restored) == 3
         cached = m.logits(restored, tail)
         cold_seq = m.new_sequence()
-        cold = m.decode_batch(cold_seq, stem + [tail])[-1]
+        m.decode_batch(cold_seq, stem)
+        cold = m.logits(cold_seq, tail)
         assert np.array_equal(cached.view(np.uint32), cold.view(np.uint32)), tail
+        whole_seq = m.new_sequence()
+        whole = m.decode_batch(whole_seq, stem + [tail])[-1]
+        assert np.all(np.abs(whole - cold) <= 1e-4 * (1 + np.abs(cold))), tail
+        m.drop_sequence(whole_seq)
         for layer in range(spec.layers):
             for value in (False, True):
                 assert np.array_equal(cache.read_all(restored, layer, value), cache.read_all(cold_seq, layer, value))
