@@ -443,7 +443,10 @@ def bench_prefill(args, w, precision="bf16"):
     chunks.  bf16: the MFMA kernel.  f32 (the reference's arithmetic, within
     1e-4): every chunk row runs as a decode row whose visible length stops at
     its own position (attention.hpp:85-89), through the decode kernels and the
-    split merge; its dominant kernel is priced against the fp32 peak."""
+    split merge; its dominant kernel is priced against the fp32 peak.  f32x3
+    (within the same 1e-4): the MFMA tiles with every operand split into two
+    bf16 parts and three products per product, priced against a third of the
+    bf16 MFMA peak (the matrix rate left for the algorithmic flops)."""
     import numpy as np
 
     from tvara_amd import attention, hip, kv, workloads
@@ -461,9 +464,9 @@ def bench_prefill(args, w, precision="bf16"):
     for _ in range(args.warmup):
         call()
     plan.check()
-    steps = args.steps if precision == "bf16" else max(1, min(args.steps, 20))
+    steps = args.steps if precision != "f32" else max(1, min(args.steps, 20))
     ms_per_step = timed_steps(call, steps)
-    kernel = "paged_prefill_bf16" if precision == "bf16" else "paged_decode"
+    kernel = {"bf16": "paged_prefill_bf16", "f32x3": "paged_prefill_x3"}.get(precision, "paged_decode")
     kt = kernel_times(call, steps, [kernel, "paged_decode_merge"])
     kernel_ms, _ = kt[kernel]
     merge_ms, merges = kt["paged_decode_merge"]
@@ -472,18 +475,21 @@ def bench_prefill(args, w, precision="bf16"):
     tfs = w.flops() / (kernel_ms * 1e-3) / 1e12
     log(f"prefill ({precision}) kernel {kernel_ms * 1e3:.1f} us, call {ms_per_step * 1e3:.1f} us, {tfs:.1f} TFLOP/s")
     del plan, cache, q, out
-    peak = MFMA_BF16_PEAK_TFS if precision == "bf16" else FP32_PEAK_TFS
-    name = w.name if precision == "bf16" else w.name + "-f32"
+    peak = {"bf16": MFMA_BF16_PEAK_TFS, "f32x3": round(MFMA_BF16_PEAK_TFS / 3, 1)}.get(precision, FP32_PEAK_TFS)
+    name = w.name if precision == "bf16" else w.name + "-" + precision
+    metric = {
+        "bf16": "paged chunked prefill attn: achieved TFLOP/s (MFMA utilisation), 1 MI355X",
+        "f32x3": "paged chunked prefill attn, f32-accurate (three bf16 products): achieved TFLOP/s, 1 MI355X",
+    }.get(precision, "paged chunked prefill attn, f32 (reference arithmetic): achieved TFLOP/s, 1 MI355X")
     result = {
-        "metric": "paged chunked prefill attn: achieved TFLOP/s (MFMA utilisation), 1 MI355X"
-        if precision == "bf16" else "paged chunked prefill attn, f32 (reference arithmetic): achieved TFLOP/s, 1 MI355X",
+        "metric": metric,
         "value": round(w.flops() / (ms_per_step * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": precision, "data": "synthetic: K/V/q ~ N(0,1)",
         "config": {"workload": name, "sequences": w.sequences, "prefix": w.prefix, "chunk": w.chunk,
                    "heads": w.heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
                    "kv": "q8_0" if w.q8 else "f32", "precision": precision},
-        "roofline": {"bound": "mfma" if precision == "bf16" else "fp32", "achieved": round(tfs, 2), "peak": peak,
+        "roofline": {"bound": "fp32" if precision == "f32" else "mfma", "achieved": round(tfs, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(tfs / peak, 4), **hbm_traffic(name, kernel),
                      "kernel": kernel, "kernel_avg_us": round(kernel_ms * 1e3, 3),
                      "merge_avg_us": round(merge_ms * 1e3, 3) if merges else 0.0, "algorithmic_flops": w.flops()},
@@ -988,10 +994,11 @@ def compact(r):
 def run_one(args, key):
     from tvara_amd import workloads
 
-    if key in ("c4", "c4d128", "c4q8", "c4f32"):
+    if key in ("c4", "c4d128", "c4q8", "c4f32", "c4x3", "c4x3d128"):
         make = {"c4": workloads.prefill_c4, "c4d128": workloads.prefill_8b, "c4q8": workloads.prefill_c4_q8,
-                "c4f32": workloads.prefill_c4}
-        return bench_prefill(args, make[key](), "f32" if key == "c4f32" else "bf16")
+                "c4f32": workloads.prefill_c4, "c4x3": workloads.prefill_c4, "c4x3d128": workloads.prefill_8b}
+        precision = {"c4f32": "f32", "c4x3": "f32x3", "c4x3d128": "f32x3"}.get(key, "bf16")
+        return bench_prefill(args, make[key](), precision)
     if key in ("c3", "c3cow"):
         return bench_kv(args, key == "c3cow")
     if key == "llama1b":
@@ -1015,7 +1022,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c4f32", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2", "phi3",
+                    choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c4f32", "c4x3", "c4x3d128", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2", "phi3",
                              "tiny", "tinyq8", "t176", "llama1b", "prefix", "conv"],
                     help="one configuration; `all` (the default) runs c1, t176, c3, c3cow, c4, c5, prefix and llama1b, "
                          "one JSON line each, then the c2 headline line last")

@@ -289,6 +289,10 @@ CHUNK_SPECS = {
     "q8_0-tied-ragged": dict(matrix_type=gf.T_Q8_0, embed_type=gf.T_Q8_0, output=False, vocab=100, hidden=96,
                              intermediate=160, heads=3, kv_heads=1, context=1200),
     "f16-split": dict(matrix_type=gf.T_F16, rope_layout="split", context=1200),
+    # head_dim 64 and 128: with blocks of 16 tokens the passes' attention runs
+    # on the three-product MFMA tiles, with blocks of 4 on the f32 rows
+    "q8_0-d64": dict(matrix_type=gf.T_Q8_0, hidden=256, intermediate=512, heads=4, kv_heads=2, context=1200),
+    "f32-d128": dict(hidden=256, intermediate=256, heads=2, kv_heads=1, context=1200),
 }
 
 

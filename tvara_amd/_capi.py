@@ -114,7 +114,7 @@ SIGNATURES = {
 
 OK, ERROR, INVALID, EXHAUSTED, LOGIC = 0, -1, -2, -3, -4
 KV_F32, KV_Q8_0 = 0, 1
-ATTN_F32, ATTN_BF16 = 0, 1
+ATTN_F32, ATTN_BF16, ATTN_F32X3 = 0, 1, 2
 
 
 class NativeError(RuntimeError):

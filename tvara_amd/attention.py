@@ -20,7 +20,7 @@ from ._capi import InvalidArgument
 _fp = C.POINTER(C.c_float)
 _sz = C.c_size_t
 _NO_CAP = (1 << 64) - 1
-_PRECISION = {"f32": _capi.ATTN_F32, "bf16": _capi.ATTN_BF16}
+_PRECISION = {"f32": _capi.ATTN_F32, "bf16": _capi.ATTN_BF16, "f32x3": _capi.ATTN_F32X3}
 
 
 def _f32(a):

@@ -243,7 +243,7 @@ int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t 
         if (!count) return;
         if (!sequences || !start || !rows || !queries || !out) throw std::invalid_argument("invalid causal prompt chunk");
         if (layer >= c.geometry().layers) throw std::invalid_argument("invalid fused attention shape");
-        if (precision != TVARA_ATTN_F32 && precision != TVARA_ATTN_BF16)
+        if (precision != TVARA_ATTN_F32 && precision != TVARA_ATTN_BF16 && precision != TVARA_ATTN_F32X3)
             throw std::invalid_argument("unknown attention precision");
         tvara_amd::PrefillPlan& plan = cache->prefill_plan;
         std::vector<uint64_t> key =

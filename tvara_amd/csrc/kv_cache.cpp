@@ -696,7 +696,7 @@ void PrefillPlan::build(DeviceCache* c, const uint64_t* sequences, size_t n, siz
     cache = c;
     const Geometry& g = c->geometry();
     if (!sequences || !start || !rows || !n) throw std::invalid_argument("invalid causal prompt chunk");
-    if (prec != 0 && prec != 1) throw std::invalid_argument("unknown attention precision");
+    if (prec != 0 && prec != 1 && prec != 2) throw std::invalid_argument("unknown attention precision");
     if (n > static_cast<size_t>(std::numeric_limits<int>::max())) throw std::invalid_argument("attention batch too large");
     heads = static_cast<int>(h);
     group = static_cast<int>(h / g.kv_heads);
@@ -740,6 +740,8 @@ void PrefillPlan::build(DeviceCache* c, const uint64_t* sequences, size_t n, siz
         throw std::invalid_argument(
             "bf16 prefill needs f32 or Q8_0 blocks of 16 to 1,024 tokens (a power of two, under 2 GiB) and head_dim "
             "64 or 128");
+    if (prec == 2 && !prefill_x3_supported(c->layout(), group / kv_share))
+        throw std::invalid_argument("the three-product prefill needs f32 blocks");
     std::vector<int32_t> tab;
     std::vector<int4> sq(n);
     size_t row0 = 0;
@@ -783,10 +785,37 @@ void PrefillPlan::launch(int layer, const float* q, float* out, hipStream_t s) {
     a.q = q;
     a.out = out;
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
-    a.err = static_cast<int*>(err.ptr);
-    launch_prefill_bf16(a, count, max_rows, s);
+    a.err = pinned_err ? static_cast<int*>(flag.ptr) : static_cast<int*>(err.ptr);
+    launch_prefill_bf16(a, count, max_rows, s, precision == 2);
     cache->leave(s);
     last_stream = s;
+}
+
+void PrefillPlan::use_pinned_error() {
+    if (precision == 0) {
+        rows_plan.use_pinned_error();
+        return;
+    }
+    if (pinned_err) return;
+    *static_cast<volatile int*>(flag.acquire(sizeof(int))) = 0;
+    pinned_err = true;
+}
+
+void PrefillPlan::check_after(hipEvent_t after) {
+    if (precision == 0) {
+        rows_plan.check_after(after);
+        return;
+    }
+    if (!pinned_err) {
+        check();
+        return;
+    }
+    TVARA_HIP(hipEventSynchronize(after));
+    auto* f = static_cast<volatile int*>(flag.ptr);
+    if (*f) {
+        *f = 0;
+        throw std::invalid_argument("invalid online attention input");
+    }
 }
 
 void PrefillPlan::check() {
@@ -794,10 +823,19 @@ void PrefillPlan::check() {
         rows_plan.check();
         return;
     }
-    int flag = 0;
-    TVARA_HIP(hipMemcpyAsync(&flag, err.ptr, sizeof(int), hipMemcpyDeviceToHost, last_stream));
+    if (pinned_err) {
+        TVARA_HIP(hipStreamSynchronize(last_stream));
+        auto* f = static_cast<volatile int*>(flag.ptr);
+        if (*f) {
+            *f = 0;
+            throw std::invalid_argument("invalid online attention input");
+        }
+        return;
+    }
+    int bad = 0;
+    TVARA_HIP(hipMemcpyAsync(&bad, err.ptr, sizeof(int), hipMemcpyDeviceToHost, last_stream));
     TVARA_HIP(hipStreamSynchronize(last_stream));
-    if (flag) {
+    if (bad) {
         TVARA_HIP(hipMemsetAsync(err.ptr, 0, sizeof(int), last_stream));
         TVARA_HIP(hipStreamSynchronize(last_stream));
         throw std::invalid_argument("invalid online attention input");

@@ -218,7 +218,8 @@ struct AttnPlan {
 // Chunked-prefill plan: sequences[i] attends its prompt rows start[i] ..
 // start[i] + rows[i] - 1 causally (fused_prompt_attention,
 // attention.hpp:85-89).  precision 0 = f32 rows through the decode kernels,
-// 1 = the bf16 MFMA tile kernel.  Block tables stay resident, so a plan built
+// 1 = the bf16 MFMA tile kernel, 2 = the tile kernel with three bf16
+// products per product (f32 blocks).  Block tables stay resident, so a plan built
 // once per chunk serves every layer.
 struct PrefillPlan {
     DeviceCache* cache = nullptr;
@@ -228,14 +229,22 @@ struct PrefillPlan {
     size_t total_rows = 0;
     AttnPlan rows_plan;
     DeviceBuffer tables, seqs, err;
+    // the tile kernels set the error flag in pinned host memory instead
+    // (use_pinned_error: no copy back before a check)
+    PinnedBuffer flag;
+    bool pinned_err = false;
     hipStream_t last_stream = nullptr;
     PrefillPlan() = default;
     PrefillPlan(const PrefillPlan&) = delete;
     PrefillPlan& operator=(const PrefillPlan&) = delete;
     void build(DeviceCache* c, const uint64_t* sequences, size_t count, size_t heads, size_t context,
                const size_t* start, const size_t* rows, int precision);
+    void use_pinned_error();
     void launch(int layer, const float* q, float* out, hipStream_t s);
     void check();
+    // the same, waiting only for `after` (an event recorded after the last
+    // launch) when the flag is pinned
+    void check_after(hipEvent_t after);
 };
 
 // ModelConfig::validate (model.hpp:13-19), the part attention depends on

@@ -511,6 +511,7 @@ void DeviceModel::decode_chunk(uint64_t sequence, const uint32_t* tokens, size_t
     const int heads = static_cast<int>(c.heads);
     std::vector<size_t> positions(rows);
     std::vector<uint64_t> seq_of_row(rows, sequence);
+    const bool tiles = prefill_x3_supported(cache_->layout(), 1);
     for (size_t c0 = 0; c0 < n; c0 += rows) {
         const size_t m = std::min(rows, n - c0);
         positions.resize(m);
@@ -523,21 +524,35 @@ void DeviceModel::decode_chunk(uint64_t sequence, const uint32_t* tokens, size_t
         const RowOp* slots = cache_->reserve_tokens(sequence, m);
         // row j sees the cached tokens and the chunk up to itself
         // (fused_prompt_attention, attention.hpp:85-89)
-        for (size_t j = 0; j < m; ++j) positions[j] += 1;
-        AttnPlan& plan = batch_plan_;
-        plan.build(cache_.get(), seq_of_row, positions, {}, heads, 0);
-        layer_stack(m, [&](int l, const float* q, float* kl, float* vl, float* attn) {
-            cache_->write_layer_rows(slots, m, l, kl, vl);
-            plan.launch(l, q, nullptr, nullptr, attn, s);
-        });
+        std::function<void(hipEvent_t)> check;
+        Attend attend;
+        if (tiles) {
+            const size_t start = position + c0;
+            chunk_plan_.build(cache_.get(), &sequence, 1, c.heads, c.context, &start, &m, 2);
+            chunk_plan_.use_pinned_error();
+            attend = [&](int l, const float* q, float* kl, float* vl, float* attn) {
+                cache_->write_layer_rows(slots, m, l, kl, vl);
+                chunk_plan_.launch(l, q, attn, s);
+            };
+            check = [&](hipEvent_t e) { chunk_plan_.check_after(e); };
+        } else {
+            for (size_t j = 0; j < m; ++j) positions[j] += 1;
+            batch_plan_.build(cache_.get(), seq_of_row, positions, {}, heads, 0);
+            attend = [&](int l, const float* q, float* kl, float* vl, float* attn) {
+                cache_->write_layer_rows(slots, m, l, kl, vl);
+                batch_plan_.launch(l, q, nullptr, nullptr, attn, s);
+            };
+            check = [&](hipEvent_t e) { batch_plan_.check_after(e); };
+        }
+        layer_stack(m, attend);
         const bool last = c0 + m == n;
         if (last_only && !last) {
-            plan.check_after(step_events_.attn);
+            check(step_events_.attn);
             continue;
         }
         const size_t out_rows = last_only ? 1 : m;
         const LogitsBands bands = launch_logits(out_rows, m - out_rows);
-        plan.check_after(step_events_.attn);
+        check(step_events_.attn);
         copy_logits(bands, out_rows, last_only ? logits_host : logits_host + c0 * c.vocab);
     }
 }

@@ -128,8 +128,12 @@ public:
     // up to kChunkRows tokens (the batched products, each layer's K/V written
     // into the cache, then the rows' causal attention over it): the logits of
     // n decode() calls, of every token or, with last_only, of the last one
-    // only.  On failure the sequence may hold part of the tokens; the caller
-    // truncates it.
+    // only.  The attention runs as MFMA tiles with every f32 operand split
+    // into two bf16 parts (three products each, about 2^-15 relative error per
+    // term) where the cache layout allows it (f32 blocks of 16 to 1,024
+    // tokens, head_dim 64 or 128), else as f32 rows through the decode
+    // kernels.  On failure the sequence may hold part of the tokens; the
+    // caller truncates it.
     void decode_chunk(uint64_t sequence, const uint32_t* tokens, size_t n, float* logits_host, bool last_only);
     static constexpr size_t kChunkRows = 512;
 
@@ -146,8 +150,9 @@ private:
     std::string metadata_;
     std::unique_ptr<DeviceCache> cache_;
     // the attention plans of a step, rebuilt per token into the same device
-    // region (no allocation once it is large enough)
+    // region (no allocation once it is large enough), and of a chunk pass
     AttnPlan step_plan_, batch_plan_;
+    PrefillPlan chunk_plan_;
     Weight embedding_, output_;
     DeviceBuffer final_norm_;
     bool has_output_ = false;

@@ -62,7 +62,13 @@ constexpr int kBufferWord3 = 0x00020000;
 // to bf16 when staged; otherwise f32 blocks.
 // TPB: 16 for blocks of 16 tokens (block arithmetic folded at compile time),
 // 0 for any power of two from 16 to 1,024 read from the layout
-template <int D, int G, int kWaves, bool kQ8, int TPB>
+// kX3: f32 inputs carried as three bf16 products.  Q, K, V and the
+// probabilities are each split as x = hi + lo (hi = bf16(x), lo = bf16(x -
+// hi): 16 significant bits), and every product takes hi*hi + hi*lo + lo*hi in
+// f32 (the dropped lo*lo is below 2^-16 of the product), so a score or an
+// output carries about 2^-15 relative error per term against the 2^-8 of one
+// bf16 product.  LDS holds the lo planes of K and V beside the hi ones.
+template <int D, int G, int kWaves, bool kQ8, int TPB, bool kX3 = false>
 __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const PrefillArgs a) {
     constexpr int PW = kRows / G;        // chunk positions per wave; rows PW*G .. 31 are padding (G = 3, 5, 6, 7)
     constexpr int QT = kWaves * PW;      // chunk positions per workgroup
@@ -77,6 +83,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     static_assert(SP >= 1 && SP * KPP == kKeys, "the staging map covers whole key rows");
     __shared__ __attribute__((aligned(16))) __bf16 klds[2][kKeys * KSTR];
     __shared__ __attribute__((aligned(16))) __bf16 vlds[2][kKeys * VSTR];
+    __shared__ __attribute__((aligned(16))) __bf16 klo[kX3 ? 2 : 1][kX3 ? kKeys * KSTR : 8];
+    __shared__ __attribute__((aligned(16))) __bf16 vlo[kX3 ? 2 : 1][kX3 ? kKeys * VSTR : 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r16 = lane & 15;
@@ -105,7 +113,9 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     const int32_t* tab = a.tables + sd.x;
 
     // Q^T as the B operand: row n = 16*nt + r16, columns 32*kc + 8*g .. +7
+    // (kX3: qlo the residual's bf16)
     bf16x8 qop[2][KC];
+    bf16x8 qlo[kX3 ? 2 : 1][kX3 ? KC : 1];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int r = 16 * nt + r16, pos = pw0 + r / G, head = kh * G + r % G;
@@ -118,9 +128,15 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                 x1 = *reinterpret_cast<const float4*>(qp + 4);
             }
             const float s = a.qscale;
-            const bf16x4 lo = to_bf16(make_float4(x0.x * s, x0.y * s, x0.z * s, x0.w * s));
-            const bf16x4 hi = to_bf16(make_float4(x1.x * s, x1.y * s, x1.z * s, x1.w * s));
+            const f32x4 y0 = {x0.x * s, x0.y * s, x0.z * s, x0.w * s}, y1 = {x1.x * s, x1.y * s, x1.z * s, x1.w * s};
+            const bf16x4 lo = to_bf16(y0);
+            const bf16x4 hi = to_bf16(y1);
             qop[nt][kc] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if constexpr (kX3) {
+                const bf16x4 l0 = to_bf16(y0 - __builtin_convertvector(lo, f32x4));
+                const bf16x4 l1 = to_bf16(y1 - __builtin_convertvector(hi, f32x4));
+                qlo[nt][kc] = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+            }
         }
     }
 
@@ -213,8 +229,16 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
         }
 #pragma unroll
         for (int p = 0; p < SP; ++p) {
-            *reinterpret_cast<bf16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = to_bf16(values(kreg[p]));
-            *reinterpret_cast<bf16x4*>(&vlds[buf][(KPP * p + skey) * VSTR + col]) = to_bf16(values(vreg[p]));
+            const f32x4 kv = values(kreg[p]), vv = values(vreg[p]);
+            const bf16x4 kb = to_bf16(kv), vb = to_bf16(vv);
+            *reinterpret_cast<bf16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = kb;
+            *reinterpret_cast<bf16x4*>(&vlds[buf][(KPP * p + skey) * VSTR + col]) = vb;
+            if constexpr (kX3) {
+                *reinterpret_cast<bf16x4*>(&klo[buf][(KPP * p + skey) * KSTR + col]) =
+                    to_bf16(kv - __builtin_convertvector(kb, f32x4));
+                *reinterpret_cast<bf16x4*>(&vlo[buf][(KPP * p + skey) * VSTR + col]) =
+                    to_bf16(vv - __builtin_convertvector(vb, f32x4));
+            }
         }
     };
 
@@ -248,21 +272,44 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) s[mt][nt] = f32x4{c0, c0, c0, c0};
             }
-            // every K operand of the tile is read before the first product, so
-            // the reads' latency is paid once
-            bf16x8 kop[KC][4];
+            if constexpr (kX3) {
+                // per 32-column step: the hi and lo K operands, then hi*hi,
+                // hi*lo and lo*hi into each score tile
 #pragma unroll
-            for (int kc = 0; kc < KC; ++kc)
+                for (int kc = 0; kc < KC; ++kc) {
+                    bf16x8 khi[4], klw[4];
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt)
-                    kop[kc][mt] = *reinterpret_cast<const bf16x8*>(&klds[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
+                    for (int mt = 0; mt < 4; ++mt) {
+                        khi[mt] = *reinterpret_cast<const bf16x8*>(&klds[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
+                        klw[mt] = *reinterpret_cast<const bf16x8*>(&klo[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
+                    }
 #pragma unroll
-            for (int kc = 0; kc < KC; ++kc)
+                    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) {
-                    s[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[kc][mt], qop[0][kc], s[mt][0], 0, 0, 0);
-                    s[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[kc][mt], qop[1][kc], s[mt][1], 0, 0, 0);
+                        for (int nt = 0; nt < 2; ++nt) {
+                            s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi[mt], qop[nt][kc], s[mt][nt], 0, 0, 0);
+                            s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi[mt], qlo[nt][kc], s[mt][nt], 0, 0, 0);
+                            s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klw[mt], qop[nt][kc], s[mt][nt], 0, 0, 0);
+                        }
                 }
+            } else {
+                // every K operand of the tile is read before the first product, so
+                // the reads' latency is paid once
+                bf16x8 kop[KC][4];
+#pragma unroll
+                for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+                        kop[kc][mt] =
+                            *reinterpret_cast<const bf16x8*>(&klds[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
+#pragma unroll
+                for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        s[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[kc][mt], qop[0][kc], s[mt][0], 0, 0, 0);
+                        s[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[kc][mt], qop[1][kc], s[mt][1], 0, 0, 0);
+                    }
+            }
             // the causal mask only on tiles that reach past a row's own position
             if (kbase + kKeys - 1 > start + pw0) {
 #pragma unroll
@@ -319,24 +366,63 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                 const bf16x4 hi = to_bf16(make_float4(p[1][0], p[1][1], p[1][2], p[1][3]));
                 return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             };
-            bf16x8 pop0[2];
-            pop0[0] = probs(0, 0);
-            pop0[1] = probs(0, 1);
             // V^T operand by transposing LDS reads (ds_read_b64_tr_b16): within
             // each 16-lane group, lane i receives element i%4 of the chunk that
             // lane 4j + i/4 addresses, as its element j; lane 16g + 4j + q
             // addresses key row 4g + j (+16 for the second half), columns
             // 16dt + 4q, so lane (g, i) gets column 16dt + i of keys 4g + j
+            auto vread = [&](const __bf16* plane, int kc, int dt) {
+                const __bf16* vrow = plane + (32 * kc + 4 * g + (r16 >> 2)) * VSTR + 16 * dt + 4 * (r16 & 3);
+                const bf16x4 lo = tr16_read(vrow);
+                const bf16x4 hi = tr16_read(vrow + 16 * VSTR);
+                return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            };
+            if constexpr (kX3) {
+                // probabilities as hi + lo; O += Vh Ph + Vh Pl + Vl Ph and the
+                // normaliser sums Ph + Pl
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) {
+                    bf16x8 ph[2], pl[2];
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+                        f32x4 p0, p1;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            p0[i] = fast_exp2(s[2 * kc][nt][i]);
+                            p1[i] = fast_exp2(s[2 * kc + 1][nt][i]);
+                        }
+                        const bf16x4 h0 = to_bf16(p0), h1 = to_bf16(p1);
+                        const bf16x4 l0 = to_bf16(p0 - __builtin_convertvector(h0, f32x4));
+                        const bf16x4 l1 = to_bf16(p1 - __builtin_convertvector(h1, f32x4));
+                        ph[nt] = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+                        pl[nt] = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+                    }
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) {
+                        const bf16x8 vh = vread(vlds[buf], kc, dt), vl = vread(vlo[buf], kc, dt);
+#pragma unroll
+                        for (int nt = 0; nt < 2; ++nt) {
+                            acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[nt], acc[dt][nt], 0, 0, 0);
+                            acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[nt], acc[dt][nt], 0, 0, 0);
+                            acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[nt], acc[dt][nt], 0, 0, 0);
+                        }
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+                        acc[DT][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, ph[nt], acc[DT][nt], 0, 0, 0);
+                        acc[DT][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pl[nt], acc[DT][nt], 0, 0, 0);
+                    }
+                }
+                return;
+            }
+            bf16x8 pop0[2];
+            pop0[0] = probs(0, 0);
+            pop0[1] = probs(0, 1);
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc) {
                 bf16x8 vop[DT];
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const __bf16* vrow = &vlds[buf][(32 * kc + 4 * g + (r16 >> 2)) * VSTR + 16 * dt + 4 * (r16 & 3)];
-                    const bf16x4 lo = tr16_read(vrow);
-                    const bf16x4 hi = tr16_read(vrow + 16 * VSTR);
-                    vop[dt] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                }
+                for (int dt = 0; dt < DT; ++dt) vop[dt] = vread(vlds[buf], kc, dt);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt)
                     acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[dt], pop0[kc], acc[dt][0], 0, 0, 0);
@@ -775,8 +861,11 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_pipe_kernel(const Prefill
 // rows per workgroup, over 64-key tiles (eight waves of the plain kernel
 // measured 158 against 225 us for four on the 8 x (2,048 + 512) chunk;
 // 128-key tiles 177 us).
+//
+// x3 (three bf16 products per product, f32 blocks) always takes the plain
+// kernel.
 template <int D, int G, int TPB>
-void launch_gt(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
+void launch_gt(const PrefillArgs& a, int nseqs, int max_rows, bool x3, hipStream_t s) {
     const char* env = std::getenv("TVARA_PREFILL_PIPE");
     const bool pipe = env ? std::atoi(env) != 0 : D == 64;
     const bool q8 = a.lay.format == kQ8;
@@ -786,7 +875,9 @@ void launch_gt(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
     b.pairs = nseqs * a.lay.kv_heads;
     const int groups8 = (b.pairs + 7) / 8;  // ids = 8 XCDs x chunk tiles x pair groups
     const dim3 grid(8 * groups8 * b.chunk_tiles), block(64 * W);
-    if (pipe) {
+    if (x3) {
+        launch("paged_prefill_x3", prefill_bf16_kernel<D, G, W, false, TPB, true>, grid, block, 0, s, b);
+    } else if (pipe) {
         if (q8)
             launch("paged_prefill_bf16", prefill_pipe_kernel<D, G, W, 2, true, TPB>, grid, block, 0, s, b);
         else
@@ -801,11 +892,13 @@ void launch_gt(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
 // blocks of 16 tokens fold the block arithmetic at compile time; other
 // powers of two read it from the layout
 template <int G>
-void launch_g(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
+void launch_g(const PrefillArgs& a, int nseqs, int max_rows, bool x3, hipStream_t s) {
     if (a.lay.head_dim == 128)
-        a.lay.tpb == 16 ? launch_gt<128, G, 16>(a, nseqs, max_rows, s) : launch_gt<128, G, 0>(a, nseqs, max_rows, s);
+        a.lay.tpb == 16 ? launch_gt<128, G, 16>(a, nseqs, max_rows, x3, s)
+                        : launch_gt<128, G, 0>(a, nseqs, max_rows, x3, s);
     else
-        a.lay.tpb == 16 ? launch_gt<64, G, 16>(a, nseqs, max_rows, s) : launch_gt<64, G, 0>(a, nseqs, max_rows, s);
+        a.lay.tpb == 16 ? launch_gt<64, G, 16>(a, nseqs, max_rows, x3, s)
+                        : launch_gt<64, G, 0>(a, nseqs, max_rows, x3, s);
 }
 
 }  // namespace
@@ -817,21 +910,27 @@ bool prefill_bf16_supported(const BlockLayout& lay, int group) {
            lay.stride < (size_t(1) << 31) && group >= 1 && group <= 8;
 }
 
-void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s) {
+bool prefill_x3_supported(const BlockLayout& lay, int group) {
+    return lay.format == kF32 && prefill_bf16_supported(lay, group);
+}
+
+void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s, bool x3) {
     if (!prefill_bf16_supported(a.lay, a.group))
         throw std::invalid_argument(
             "bf16 prefill needs f32 or Q8_0 blocks of 16 to 1,024 tokens (a power of two, under 2 GiB), "
             "head_dim 64 or 128, and a GQA slice of 1-8 heads");
+    if (x3 && !prefill_x3_supported(a.lay, a.group))
+        throw std::invalid_argument("the three-product prefill needs f32 blocks");
     if (nseqs <= 0 || max_rows <= 0) return;
     switch (a.group) {
-        case 1: launch_g<1>(a, nseqs, max_rows, s); break;
-        case 2: launch_g<2>(a, nseqs, max_rows, s); break;
-        case 3: launch_g<3>(a, nseqs, max_rows, s); break;
-        case 4: launch_g<4>(a, nseqs, max_rows, s); break;
-        case 5: launch_g<5>(a, nseqs, max_rows, s); break;
-        case 6: launch_g<6>(a, nseqs, max_rows, s); break;
-        case 7: launch_g<7>(a, nseqs, max_rows, s); break;
-        default: launch_g<8>(a, nseqs, max_rows, s); break;
+        case 1: launch_g<1>(a, nseqs, max_rows, x3, s); break;
+        case 2: launch_g<2>(a, nseqs, max_rows, x3, s); break;
+        case 3: launch_g<3>(a, nseqs, max_rows, x3, s); break;
+        case 4: launch_g<4>(a, nseqs, max_rows, x3, s); break;
+        case 5: launch_g<5>(a, nseqs, max_rows, x3, s); break;
+        case 6: launch_g<6>(a, nseqs, max_rows, x3, s); break;
+        case 7: launch_g<7>(a, nseqs, max_rows, x3, s); break;
+        default: launch_g<8>(a, nseqs, max_rows, x3, s); break;
     }
     TVARA_HIP(hipGetLastError());
 }
