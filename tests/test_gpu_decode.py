@@ -700,3 +700,52 @@ def test_zero_query_counts_every_token(device, oracle, monkeypatch, fmt_name, di
         want = want.reshape(kv_heads, dim)
         for h in range(heads):
             assert np.allclose(got[i, h], want[h // group], rtol=1e-6, atol=1e-6), (i, n, h)
+
+
+@pytest.mark.parametrize("dim,kv_heads,group", [(64, 8, 4), (64, 3, 3), (128, 8, 4), (64, 2, 8), (128, 2, 3),
+                                                (32, 4, 2), (64, 1, 16)])
+def test_wave_split_chunks_count_every_token(device, oracle, dim, kv_heads, group):
+    # Launches of at most 32 (row, KV head) pairs run wave splits: one
+    # workgroup per pair when a row is short, else chunks of one memory round
+    # trip a wave whose partials the merge kernel combines.  q = 0 and integer
+    # V make every output the exact mean of the row's V rows and its tail, so
+    # a token dropped or counted twice by a chunk boundary, an empty trailing
+    # chunk (rows shorter than the longest) or the tail's early request shows
+    # (the bar is 1e-6, a token moves the mean by at least 1/(2n)).
+    heads, tpb = kv_heads * group, 16
+    vkv = kv_heads * (2 if group > 8 else 1)  # groups above eight run as two slices
+    for lengths in ([8192], [1], [40], [700], [2049, 31, 600, 8192, 1, 5000][:max(1, 32 // vkv)]):
+        g = (1, kv_heads, dim, tpb, sum((n + tpb - 1) // tpb for n in lengths) + 4)
+        dev = device.PagedCache(*g)
+        w = kv_heads * dim
+        rng = np.random.default_rng(7 * dim + kv_heads + group + len(lengths))
+        seqs, vals = [], []
+        for i, n in enumerate(lengths):
+            v = rng.integers(-4, 5, size=(n, w)).astype(np.float32)
+            s = dev.create_sequence()
+            dev.append_many(s, synth.normal(17, f"k{i}", n * w).reshape(n, w), v)
+            seqs.append(s)
+            vals.append(v)
+        rows = len(lengths)
+        tv = rng.integers(-4, 5, size=(rows, w)).astype(np.float32)
+        tk = synth.normal(17, "tk", rows * w).reshape(rows, w)
+        plan = attention.DecodePlan(dev, seqs, heads, 1 << 20, with_tail=True)
+        say("wave-split chunks", dim, kv_heads, group, lengths, "items", plan.items, "split", plan.split_tokens)
+        if max(lengths) == 8192 and dim * group <= 512:
+            assert plan.items > 8 * rows  # several chunks a row
+        got = attention.decode_batch(dev, np.zeros((rows, heads * dim), np.float32), seqs, 0, heads, 1 << 20,
+                                     tail_keys=tk, tail_values=tv).reshape(rows, heads, dim)
+        for i, n in enumerate(lengths):
+            want = ((vals[i].astype(np.float64).sum(axis=0) + tv[i]) / (n + 1)).reshape(kv_heads, dim)
+            for h in range(heads):
+                assert np.allclose(got[i, h], want[h // group], rtol=1e-6, atol=1e-6), (lengths, i, h)
+
+
+@pytest.mark.parametrize("dim,kv_heads,group", [(64, 8, 4), (128, 8, 4), (64, 3, 3), (64, 2, 7)])
+@pytest.mark.parametrize("length", [33, 700, 2048, 8192])
+def test_wave_split_chunks_against_reference(device, oracle, dim, kv_heads, group, length):
+    # one row (the single-sequence model step) with its tail, N(0,1) inputs,
+    # through one or many chunks, against the oracle within the f32 bar
+    say("wave-split row", dim, kv_heads, group, length)
+    got, want = _single(device, oracle, kv_heads * group, kv_heads, dim, 16, length, seed=length + dim, tail=True)
+    assert refmath.close(got, want, TOL), refmath.max_rel(got, want)

@@ -106,7 +106,8 @@ struct DecodeArgs {
     // for kernels that merge a row's splits in its last workgroup (zero between
     // launches; null: merge_kernel merges)
     int* row_done;
-    int wave_splits;  // > 0: each row's splits are the waves of one workgroup per (row, KV head)
+    int wave_splits;  // > 0: each row's splits are the waves of ws_chunks workgroups per (row, KV head)
+    int ws_chunks;    // wave splits: workgroups per (row, KV head); above 1 they leave partials per chunk
     int row_major;    // 1: decode_rows_kernel (one eight-wave workgroup per work item)
     // Query groups above eight run as slices: lay.kv_heads and group describe
     // kv_share virtual KV heads per KV head, and virtual head v reads the K/V
@@ -161,7 +162,14 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
                    const WorkOrder* order, hipStream_t s);
 int decode_waves(int kv_heads, int group, int format, int head_dim);
 int decode_slots(int kv_heads, int group, int format, int head_dim);  // waves' worth of work per work item
-int wave_split_waves(int rows, int kv_heads, int group, int format, int head_dim, int tpb, size_t max_tokens);
+// waves == 0: the usual decomposition
+struct WaveSplitShape {
+    int waves = 0;    // splits per chunk, the waves of its workgroup
+    int chunks = 0;   // workgroups per (row, KV head)
+    size_t tokens = 0;  // tokens per split (a whole number of blocks)
+};
+WaveSplitShape wave_split_shape(int rows, int kv_heads, int group, int format, int head_dim, int tpb,
+                                size_t max_tokens, int cus);
 int decode_budget_per_cu(int group, int format, int head_dim);
 // Shapes the row-major f32 kernel takes (head_dim 64, 16-token blocks, 4, 8
 // or 16 KV heads, up to eight query heads each); plans of such a shape whose

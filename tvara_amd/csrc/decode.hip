@@ -284,7 +284,19 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
                 L = fmaf(wt, ml0[w * 2 * G + G + h], L);
                 sum = fmaf(wt, r[0] + r[G * D] + r[2 * G * D] + r[3 * G * D], sum);
             }
-            outw[o] = sum / L;
+            if (a.ws_chunks > 1) {
+                // the chunk's partial, [chunk][heads] for merge_wave_kernel
+                // (chunk = row * chunks + c, the workgroup's id over KV heads)
+                const size_t at = static_cast<size_t>(blockIdx.x / a.lay.kv_heads) * a.heads +
+                                  static_cast<size_t>(kh) * G + h;
+                a.part_acc[at * D + (o - h * D)] = sum;
+                if (o == h * D) {
+                    a.part_ml[2 * at] = M;
+                    a.part_ml[2 * at + 1] = L;
+                }
+            } else {
+                outw[o] = sum / L;
+            }
         }
         if (__any(st.bad) && lane == 0) *a.err = 1;
         return;
@@ -392,6 +404,19 @@ __global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(c
                 q[h][4 * m + 3] = x.w;
             }
     }
+    // wave splits: the row's uncommitted K/V (attention.hpp:80) is requested
+    // with the query, not after the last tile, so it costs no round trip of
+    // its own
+    const bool tok = tail && tg == 0;
+    float4 tka[kWS ? NV : 1], tva[kWS ? NV : 1];
+    if constexpr (kWS) {
+        const size_t toff = static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kh / a.kv_share) * D + 4 * c;
+#pragma unroll
+        for (int m = 0; m < NV; ++m) {
+            tka[m] = tok ? *reinterpret_cast<const float4*>(a.tail_k + toff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+            tva[m] = tok ? *reinterpret_cast<const float4*>(a.tail_v + toff + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
     float acc[G][E];
 #pragma unroll
     for (int h = 0; h < G; ++h)
@@ -484,15 +509,19 @@ __global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(c
         process(ka, va, ok);
     }
     if (tail) {  // the current token's uncommitted K/V is the last position (attention.hpp:80)
-        const bool ok = tg == 0;
-        const float* tk = a.tail_k + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kvh) * D + 4 * c;
-        const float* tv = a.tail_v + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kvh) * D + 4 * c;
+        if constexpr (kWS) {
+            process(tka, tva, tok);
+        } else {
+            const bool ok = tg == 0;
+            const float* tk = a.tail_k + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kvh) * D + 4 * c;
+            const float* tv = a.tail_v + static_cast<size_t>(it.x) * kvw + static_cast<size_t>(kvh) * D + 4 * c;
 #pragma unroll
-        for (int m = 0; m < NV; ++m) {
-            ka[m] = ok ? *reinterpret_cast<const float4*>(tk + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
-            va[m] = ok ? *reinterpret_cast<const float4*>(tv + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int m = 0; m < NV; ++m) {
+                ka[m] = ok ? *reinterpret_cast<const float4*>(tk + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+                va[m] = ok ? *reinterpret_cast<const float4*>(tv + 4 * LPT * m) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            process(ka, va, ok);
         }
-        process(ka, va, ok);
     }
     finish_split<D, G, LPT, E, kWS>(a, acc, st, lane, wave, nwaves, kh, item, item - t0 / a.split_tokens, it.x,
                                     nsplit, [](int cc, int e4) { return 4 * cc + 4 * LPT * e4; });
@@ -1691,8 +1720,8 @@ void launch_f32_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
     const size_t lds = (static_cast<size_t>(waves) * 4 * G * D + waves * 2 * G) * sizeof(float);
     WorkOrder o;
     o.n = 0;
-    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, true>, dim3(nrows * a.lay.kv_heads), dim3(64 * waves), lds,
-           s, a, o);
+    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, true>, dim3(nrows * a.ws_chunks * a.lay.kv_heads),
+           dim3(64 * waves), lds, s, a, o);
 }
 
 template <int D>
@@ -1893,20 +1922,56 @@ static int waves_for(const DecodeArgs& a) {
     return decode_waves(a.lay.kv_heads, a.group, a.lay.format, a.lay.head_dim);
 }
 
-// Wave splits (one workgroup per (row, KV head), its waves the row's splits):
-// f32 blocks, the fast shapes that fit 512-thread workgroups, and launches of
-// at most 32 (row, KV head) pairs.  Returns the waves (splits per row), 0 for
-// the usual decomposition.
-int wave_split_waves(int rows, int kv_heads, int group, int format, int head_dim, int tpb, size_t max_tokens) {
-    if (const char* env = std::getenv("TVARA_WAVE_SPLITS"); env && std::atoi(env) == 0) return 0;
-    if (format != kF32 || !decode_f32_blocks(tpb) || (head_dim != 32 && head_dim != 64 && head_dim != 128)) return 0;
-    if (group > 8 || (head_dim == 128 && group > 4)) return 0;
-    if (static_cast<size_t>(rows) * kv_heads > 32 || max_tokens > 1024) return 0;
-    // one split of at least 64 tokens a wave, at most eight waves, the
-    // partials of every wave in 64 KiB of LDS
+// Wave splits, for launches of at most 32 (row, KV head) pairs on f32 blocks
+// and the fast shapes that fit 512-thread workgroups: a workgroup per (row,
+// KV head, chunk) whose waves take consecutive splits of the chunk, merged
+// in LDS; with more than one chunk a row's chunks leave partials that
+// merge_wave_kernel combines.  Such launches are latency-bound: the usual
+// decomposition puts a (row, KV head) pair's waves on one CU, and a wave
+// that holds more tokens than it has in flight (two tiles) pays a memory
+// round trip per two tiles.  So a row of up to two round trips a wave over
+// eight waves stays one workgroup; a longer one is cut into chunks of one
+// round trip a wave (eight waves), as many as fill the CUs once, beyond
+// which the splits grow (MI355X, one Llama-3.2-1B row, 32/8 heads: 2,048
+// tokens 25.1 against about 6 us, 8,192 tokens 70.2 against about 9 us).
+WaveSplitShape wave_split_shape(int rows, int kv_heads, int group, int format, int head_dim, int tpb,
+                                size_t max_tokens, int cus) {
+    WaveSplitShape none{};
+    if (const char* env = std::getenv("TVARA_WAVE_SPLITS"); env && std::atoi(env) == 0) return none;
+    if (format != kF32 || !decode_f32_blocks(tpb) || (head_dim != 32 && head_dim != 64 && head_dim != 128)) return none;
+    if (group > 8 || (head_dim == 128 && group > 4)) return none;
+    const size_t pairs = static_cast<size_t>(rows) * kv_heads;
+    if (pairs > 32 || max_tokens == 0) return none;
+    // tokens a wave has in flight (two tiles of 64 / LPT tokens, LPT as
+    // dispatch_ws); at most eight waves, their partials in 64 KiB of LDS
+    const int lpt = head_dim == 128 || group > 4 ? 8 : 4;
+    const size_t flight = 2 * (64 / lpt);
     const size_t per_wave = (4 * static_cast<size_t>(group) * head_dim + 2 * group) * sizeof(float);
-    const int w = static_cast<int>(std::min<size_t>({8, (max_tokens + 63) / 64, 65536 / per_wave}));
-    return w >= 2 ? w : 0;
+    const size_t wmax = std::min<size_t>(8, 65536 / per_wave);
+    if (wmax < 1) return none;
+    auto blocks_of = [&](size_t t) {
+        const size_t b = static_cast<size_t>(tpb);
+        return (std::max<size_t>(t, 16) + b - 1) / b * b;
+    };
+    WaveSplitShape w{};
+    if (max_tokens <= 2 * wmax * flight) {
+        w.waves = static_cast<int>(std::min(wmax, (max_tokens + flight - 1) / flight));
+        w.chunks = 1;
+        w.tokens = blocks_of((max_tokens + w.waves - 1) / w.waves);
+    } else {
+        size_t t = blocks_of(flight);
+        if (const char* env = std::getenv("TVARA_WS_TOKENS")) t = blocks_of(std::strtoull(env, nullptr, 10));
+        auto chunks = [&](size_t sp) { return (max_tokens + wmax * sp - 1) / (wmax * sp); };
+        while (pairs * chunks(t) > static_cast<size_t>(cus) && t < kMaxSplitTokens) t = blocks_of(2 * t);
+        w.waves = static_cast<int>(wmax);
+        w.chunks = static_cast<int>(chunks(t));
+        w.tokens = t;
+    }
+    // the kernels keep a split's block ids in one register per lane
+    if (w.tokens > kMaxSplitTokens || w.tokens / tpb > static_cast<size_t>(kMaxSplitBlocks)) return none;
+    // every chunk of a row's waves must cover the row
+    if (static_cast<size_t>(w.waves) * w.chunks * w.tokens < max_tokens) return none;
+    return w;
 }
 
 // the largest decode launch whose splits are merged in the kernel
@@ -1947,6 +2012,13 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
         : a.lay.head_dim == 128 ? dispatch_ws<128>(a, nrows, s)
                                 : dispatch_ws<32>(a, nrows, s);
         TVARA_HIP(hipGetLastError());
+        if (a.ws_chunks > 1) {  // the chunks' partials: (first chunk, chunks) per row
+            if (!inline_rows || nrows > kInlineRows) throw std::logic_error("wave-split decode: rows not inline");
+            DecodeArgs b = a;
+            b.row_done = nullptr;
+            launch_merge(b, inline_rows, nrows, s);
+            TVARA_HIP(hipGetLastError());
+        }
         return;
     }
     if (a.row_major) {  // the plan chose the row-major kernel: merge_kernel merges

@@ -388,14 +388,18 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     if (!split) {
         if (const char* env = std::getenv("TVARA_SPLIT_TOKENS")) split = std::strtoull(env, nullptr, 10);
     }
-    // A launch too small to fill the GPU gives every row one split per wave of
-    // a workgroup per (row, KV head), merged in LDS (wave_split_waves).
+    // A launch of few (row, KV head) pairs gives every row wave splits: the
+    // waves of ws_chunks workgroups per (row, KV head), merged in LDS and
+    // across chunks by the merge kernel (wave_split_shape).
     size_t max_n = 0;
     for (size_t n : cached) max_n = std::max(max_n, n);
-    wave_splits = split ? 0
-                        : wave_split_waves(rows, vkv, vgroup, c->format(), static_cast<int>(g.head_dim),
-                                           static_cast<int>(g.tokens_per_block), max_n);
-    if (wave_splits) split = round_up((max_n + wave_splits - 1) / wave_splits, align);
+    const WaveSplitShape ws =
+        split ? WaveSplitShape{}
+              : wave_split_shape(rows, vkv, vgroup, c->format(), static_cast<int>(g.head_dim),
+                                 static_cast<int>(g.tokens_per_block), max_n, c->compute_units());
+    wave_splits = ws.waves;
+    ws_chunks = ws.waves ? ws.chunks : 1;
+    if (wave_splits) split = ws.tokens;
     // The row-major f32 kernel (decode_rows_shape) runs one workgroup per
     // item.  Its split starts from the shortest whose items fit one workgroup
     // per CU and grows in steps of 64 tokens while at least 80% of the CUs
@@ -474,11 +478,13 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
     for (int r = 0; r < rows; ++r) {
         const size_t n = cached[r];
         const int tail = tail_rows.empty() ? 0 : (tail_rows[r] ? 1 : 0);
-        const int nsplit = wave_splits ? wave_splits : static_cast<int>(std::max<size_t>(1, (n + split - 1) / split));
+        const int nsplit = wave_splits ? wave_splits * ws_chunks
+                                       : static_cast<int>(std::max<size_t>(1, (n + split - 1) / split));
         const int first = static_cast<int>(its.size());
         const int32_t base = offset[seq_of_row[r]];
         ent[r] = make_int4(base, static_cast<int>(n), tail | (nsplit << 1), first);
-        if (inline_ok) inline_rows.r[r] = make_int2(first, nsplit);
+        // wave splits merge a row's chunks (partials r * chunks ..), not its splits
+        if (inline_ok) inline_rows.r[r] = wave_splits ? make_int2(r * ws_chunks, ws_chunks) : make_int2(first, nsplit);
         for (int s = 0; s < nsplit; ++s) {
             its.push_back(make_int2(r, s));
             const int t0 = static_cast<int>(std::min(n, s * split)), t1 = static_cast<int>(std::min(n, (s + 1) * split));
@@ -486,7 +492,7 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
             const int nb = listed ? (t1 - t0 + tpb - 1) / tpb : 0;
             for (int j = 0; j < kMaxSplitBlocks; ++j) work_ids.push_back(j < nb ? tab[base + t0 / tpb + j] : 0);
         }
-        need_merge |= nsplit > 1 && !wave_splits;
+        need_merge |= wave_splits ? ws_chunks > 1 : nsplit > 1;
         kv_bytes += static_cast<size_t>(static_cast<double>(n + tail) * g.kv_width() * 2 * bytes_per_element);
     }
     items = static_cast<int>(its.size());
@@ -631,6 +637,7 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.part_ml = dev.part_ml;
     a.row_done = need_merge ? dev.row_done : nullptr;
     a.wave_splits = wave_splits;
+    a.ws_chunks = ws_chunks;
     a.row_major = row_major ? 1 : 0;
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
     a.err = pinned_err ? static_cast<int*>(flag.ptr) : dev.err;

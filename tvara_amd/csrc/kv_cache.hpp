@@ -144,7 +144,8 @@ struct AttnPlan {
     // three at 80) run as kv_share slices of group / kv_share heads, each a
     // virtual KV head
     int kv_share = 1;
-    int wave_splits = 0;  // > 0: splits per row = waves of one workgroup per (row, KV head)
+    int wave_splits = 0;  // > 0: a row's splits are the waves of ws_chunks workgroups per (row, KV head)
+    int ws_chunks = 1;
     bool row_major = false;  // the launch runs decode_rows_kernel (one workgroup per item)
     bool need_merge = false, with_tail = false, inline_ok = false;
     size_t kv_bytes = 0;  // algorithmic K/V bytes one launch reads
