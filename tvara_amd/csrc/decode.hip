@@ -1954,6 +1954,9 @@ WaveSplitShape wave_split_shape(int rows, int kv_heads, int group, int format, i
         return (std::max<size_t>(t, 16) + b - 1) / b * b;
     };
     WaveSplitShape w{};
+    // (one workgroup of two round trips a wave measured as fast as two
+    // chunks of one, 7.4 against 7.5 us plus the merge for the SmolLM2-135M
+    // row, and faster than them from 384 tokens up to 512)
     if (max_tokens <= 2 * wmax * flight) {
         w.waves = static_cast<int>(std::min(wmax, (max_tokens + flight - 1) / flight));
         w.chunks = 1;
