@@ -405,7 +405,7 @@ __device__ __forceinline__ void write_segment(const MatvecSegment* seg, int nseg
 // bounds).
 template <int W, int RT>
 __global__ __launch_bounds__(W * 64) void matvec_q8_kernel(const Q8MatvecArgs a) {
-    constexpr int U = 4;
+    constexpr int U = 2;
     extern __shared__ float vs[];  // cols floats
     __shared__ double red[W][RT][16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1320,15 +1320,18 @@ void launch_matvec_q8(const Weight& w, const float* v, const MatvecSegment* seg,
     a.rope_dim = rope_dim;
     a.rope_rows = rope_rows;
     a.swiglu = w.interleaved ? 1 : 0;
-    // two tiles per workgroup (sharing the staged input) when there are
-    // many.  Waves per workgroup: one step of pairs each (four), at most
-    // sixteen; launches of a thousand workgroups and more take two (MI355X,
-    // Llama-3.2-1B shapes: 3,072 x 2,048 rows in 6.2 us at eight waves
-    // against 7.4 at sixteen; 8,192 columns in 9.1 us at sixteen; the
-    // 128,256-row logits in 58 us at two waves against 65 at one)
-    const int rt = a.tiles >= 1024 ? 2 : 1;
+    // two tiles per workgroup (sharing the staged input) for the largest
+    // matrices.  Waves per workgroup: up to about sixteen waves per CU over
+    // the launch (4,096), at most sixteen, at least two when there is work
+    // for two, and at least two group pairs a wave (MI355X, Llama-3.2-1B shapes, two pairs a step:
+    // 16,384 x 2,048 gate|up in 11.2 us at one tile and four waves against
+    // 12.3 at two tiles and eight; 2,048 x 8,192 down 8.6 us at sixteen;
+    // 3,072 x 2,048 QKV 6.1-6.2 us at eight or sixteen; the 128,256-row
+    // logits in 58 us at two waves against 65 at one)
+    const int rt = a.tiles >= 4096 ? 2 : 1;
     const int wgs = (a.tiles + rt - 1) / rt;
-    const int want = wgs >= 1024 ? 2 : std::max(1, std::min(16, (a.pairs + 3) / 4));
+    int want = 1;
+    while (want < 16 && 2 * want * 2 <= a.pairs && (want < 2 || wgs * want * 2 <= 4096)) want *= 2;
     const dim3 grid(wgs);
     // the input, and the norm weights beside it when the product normalises
     const size_t lds = static_cast<size_t>(w.cols) * sizeof(float) * (norm_w ? 2 : 1);
