@@ -923,8 +923,8 @@ __global__ __launch_bounds__(256) void batch_q8_ws_kernel(const Q8BatchArgs a) {
     const int nunits = (gend - gbeg + UG - 1) / UG;
     const int mytiles = wave < ntv ? (ntv - 1 - wave) / 4 + 1 : 0;
     const int steps = mytiles * nunits;
-    auto load_x = [&](int k, u32x4 (&x)[UG][2]) {  // step k (clamped by the caller)
-        const int vt = wave + 4 * (k / nunits), u = k % nunits;
+    auto load_x = [&](int jt, int u, u32x4 (&x)[UG][2]) {
+        const int vt = wave + 4 * jt;
 #pragma unroll
         for (int c = 0; c < UG; ++c) {
             const int g = gbeg + UG * u + c;
@@ -937,8 +937,7 @@ __global__ __launch_bounds__(256) void batch_q8_ws_kernel(const Q8BatchArgs a) {
 #pragma unroll
     for (int r = 0; r < RT; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
     float* out = a.out + static_cast<size_t>(blockIdx.y) * a.n_total * a.rows;
-    auto step = [&](int k, const u32x4 (&x)[UG][2]) {
-        const int u = k % nunits;
+    auto step = [&](int jt, int u, const u32x4 (&x)[UG][2]) {
         uint32_t dd[RT][UG / 2];
 #pragma unroll
         for (int r = 0; r < RT; ++r)
@@ -968,7 +967,7 @@ __global__ __launch_bounds__(256) void batch_q8_ws_kernel(const Q8BatchArgs a) {
         if (u + 1 < nunits) return;
         // the tile's last unit: lane l holds row l%16 of each row tile for
         // vectors 4(l/16) + i of vector tile vt
-        const int vt = wave + 4 * (k / nunits);
+        const int vt = wave + 4 * jt;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int jl = vt * 16 + 4 * (lane >> 4) + i;
@@ -985,14 +984,33 @@ __global__ __launch_bounds__(256) void batch_q8_ws_kernel(const Q8BatchArgs a) {
         for (int r = 0; r < RT; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
     };
     if (steps == 0) return;
+    // the (tile, unit) of the next step to load and of the step to compute,
+    // counted up rather than divided out of a flat index (8% of the
+    // product's time at 256-512 vectors went to the divisions)
     u32x4 xa[UG][2], xb[UG][2];
-    load_x(0, xa);
+    int jn = 0, un = 0, jc = 0, uc = 0;
+    auto next_load = [&](u32x4 (&x)[UG][2]) {
+        const bool past = jn >= mytiles;
+        load_x(past ? mytiles - 1 : jn, past ? nunits - 1 : un, x);
+        if (++un == nunits) {
+            un = 0;
+            ++jn;
+        }
+    };
+    auto next_step = [&](const u32x4 (&x)[UG][2]) {
+        step(jc, uc, x);
+        if (++uc == nunits) {
+            uc = 0;
+            ++jc;
+        }
+    };
+    next_load(xa);
     for (int k = 0;; k += 2) {
-        load_x(min(k + 1, steps - 1), xb);
-        step(k, xa);
+        next_load(xb);
+        next_step(xa);
         if (k + 1 >= steps) break;
-        load_x(min(k + 2, steps - 1), xa);
-        step(k + 1, xb);
+        next_load(xa);
+        next_step(xb);
         if (k + 2 >= steps) break;
     }
 }
