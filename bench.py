@@ -495,9 +495,43 @@ def bench_prefill(args, w, precision="bf16"):
                      "merge_avg_us": round(merge_ms * 1e3, 3) if merges else 0.0, "algorithmic_flops": w.flops()},
         "cpu_baseline": None,
     }
+    if precision == "bf16" and not w.q8:
+        result["f32_accurate_x3"] = x3_beside(args, w)
     if ref_ready(args) and not w.q8:
         baseline(result, lambda: cpu_prefill(w))
     return result
+
+
+def x3_beside(args, w):
+    """The same chunks through the three-product tiles (TVARA_ATTN_F32X3,
+    within the f32 bar), reported beside the bf16 line: kernel time from the
+    library's HIP events, algorithmic TFLOP/s and their fraction of a third of
+    the bf16 MFMA peak (three products per product)."""
+    import numpy as np
+
+    from tvara_amd import attention, hip, kv, workloads
+
+    cache = kv.PagedCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks(), fmt=kv.F32)
+    seqs = workloads.fill_prefill(cache, w)
+    q = hip.DeviceArray.from_numpy(np.concatenate([w.chunk_queries(i) for i in range(w.sequences)]))
+    out = hip.DeviceArray(q.shape)
+    plan = attention.PrefillPlan(cache, seqs, [w.prefix] * w.sequences, [w.chunk] * w.sequences, w.heads, w.context,
+                                 "f32x3")
+    call = lambda: plan.launch(0, q.ptr, out.ptr)  # noqa: E731
+    for _ in range(max(1, args.warmup // 4)):
+        call()
+    plan.check()
+    steps = max(1, args.steps // 4)
+    kernel_ms, _ = kernel_times(call, steps, ["paged_prefill_x3"])["paged_prefill_x3"]
+    plan.check()
+    assert np.isfinite(out.numpy()).all()
+    del plan, cache, q, out
+    tfs = w.flops() / (kernel_ms * 1e-3) / 1e12
+    peak = MFMA_BF16_PEAK_TFS / 3
+    log(f"prefill (f32x3) kernel {kernel_ms * 1e3:.1f} us, {tfs:.1f} TFLOP/s")
+    return {"kernel": "paged_prefill_x3", "kernel_avg_us": round(kernel_ms * 1e3, 3), "achieved": round(tfs, 2),
+            "unit": "TFLOP/s", "peak": round(peak, 1), "frac": round(tfs / peak, 4), "steps": steps,
+            "bar": "1e-4 * (1 + |ref|), the f32 path's"}
 
 
 # -------------------------------------------------------------- KV stress
@@ -981,7 +1015,7 @@ def compact(r):
         if k in r["roofline"]:
             out["roofline"][k] = r["roofline"][k]
     for k in ("latency_us", "reference_published", "decode_tokens_per_s", "model_decode_tokens_per_s",
-              "prompt_prefill"):
+              "prompt_prefill", "f32_accurate_x3"):
         if k in r:
             out[k] = r[k]
     if cpu:

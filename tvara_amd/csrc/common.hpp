@@ -88,6 +88,20 @@ struct WorkOrder {
     uint16_t item[kOrderedItems];
 };
 
+// A wave-split launch of few work items passes every item's descriptor and
+// block ids in its kernel arguments, so no dependent load precedes its K/V
+// reads (n == 0: the kernel reads them from the plan in HBM).  Slot
+// chunk * kWsInlineWaves + wave holds an item, kWsInlinePer ids a slot: a
+// launch of up to eight (row, chunk) workgroups whose splits span at most
+// four blocks.
+constexpr int kWsInlineWaves = 8, kWsInlinePer = 4;
+constexpr int kWsInlineItems = 64, kWsInlineIds = kWsInlineItems * kWsInlinePer;
+struct WsItems {
+    int n;  // items
+    int4 item[kWsInlineItems];
+    int32_t ids[kWsInlineIds];
+};
+
 struct DecodeArgs {
     const char* pool;
     BlockLayout lay;
@@ -159,7 +173,7 @@ void launch_q8_to_canonical(const char* pool, const BlockLayout& lay, int64_t id
 void launch_canonical_to_q8(char* pool, const BlockLayout& lay, int64_t id, const uint8_t* in, hipStream_t s);
 // decode.hip
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
-                   const WorkOrder* order, hipStream_t s);
+                   const WorkOrder* order, hipStream_t s, const WsItems* ws_items = nullptr);
 int decode_waves(int kv_heads, int group, int format, int head_dim);
 int decode_slots(int kv_heads, int group, int format, int head_dim);  // waves' worth of work per work item
 // waves == 0: the usual decomposition

@@ -286,9 +286,8 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
             }
             if (a.ws_chunks > 1) {
                 // the chunk's partial, [chunk][heads] for merge_wave_kernel
-                // (chunk = row * chunks + c, the workgroup's id over KV heads)
-                const size_t at = static_cast<size_t>(blockIdx.x / a.lay.kv_heads) * a.heads +
-                                  static_cast<size_t>(kh) * G + h;
+                // (chunk = row * chunks + c = blockIdx.x)
+                const size_t at = static_cast<size_t>(blockIdx.x) * a.heads + static_cast<size_t>(kh) * G + h;
                 a.part_acc[at * D + (o - h * D)] = sum;
                 if (o == h * D) {
                     a.part_ml[2 * at] = M;
@@ -367,21 +366,39 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
 // the workgroup has waves), merged in LDS: no second launch and no global
 // round trip, for launches too small to fill the GPU.
 template <int D, int G, int LPT, int NB, bool kWS>
-__global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(const DecodeArgs a,
-                                                                                const WorkOrder order) {
+__global__ __launch_bounds__(G > 4 && !kWS ? 128 : 512) void decode_f32_kernel(
+    const DecodeArgs a, const std::conditional_t<kWS, WsItems, WorkOrder> order) {
     constexpr int E = D / LPT, NV = E / 4, TT = 64 / LPT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int groups = kWS ? 1 : a.lay.kv_heads / nwaves;
     // the launch order (a kernel argument, so no dependent load) maps this
     // workgroup to its work item
     const int slot = static_cast<int>(blockIdx.x) / groups;
-    const int item = kWS ? (static_cast<int>(blockIdx.x) / a.lay.kv_heads) * nwaves + wave
-                         : (order.n ? static_cast<int>(order.item[slot]) : slot);
-    const int kh = kWS ? static_cast<int>(blockIdx.x) % a.lay.kv_heads
-                       : (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
-    // the item's descriptor and block ids come in two independent loads
-    const int4 it = a.work[item];  // row, first token, end token, tail | splits << 1
-    const int bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
+    // wave splits: blockIdx.x is the (row, chunk), blockIdx.y the KV head
+    int item;
+    if constexpr (kWS)
+        item = static_cast<int>(blockIdx.x) * nwaves + wave;
+    else
+        item = order.n ? static_cast<int>(order.item[slot]) : slot;
+    const int kh = kWS ? static_cast<int>(blockIdx.y) : (static_cast<int>(blockIdx.x) % groups) * nwaves + wave;
+    // the item's descriptor and block ids: from the kernel arguments (wave
+    // splits of few items, at fixed strides so that no argument read comes
+    // first), else in two independent loads
+    bool inl = false;
+    if constexpr (kWS) inl = order.n != 0;
+    int4 it;  // row, first token, end token, tail | splits << 1
+    int bids = 0;
+    if constexpr (kWS) {
+        if (inl) {
+            const int at = static_cast<int>(blockIdx.x) * kWsInlineWaves + __builtin_amdgcn_readfirstlane(wave);
+            it = order.item[at];
+            bids = order.ids[at * kWsInlinePer + (lane & (kWsInlinePer - 1))];
+        }
+    }
+    if (!inl) {
+        it = a.work[item];
+        bids = a.work_blocks[static_cast<size_t>(item) * kMaxSplitBlocks + lane];
+    }
     const int nsplit = it.w >> 1;
     const bool tail = (it.w & 1) != 0;
     const int t0 = it.y, t1 = it.z;
@@ -1715,31 +1732,29 @@ bool dispatch_rows(const DecodeArgs& a, int nitems, const WorkOrder& order, hipS
 }
 
 template <int D, int G, int LPT>
-void launch_f32_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
+void launch_f32_ws(const DecodeArgs& a, int nrows, const WsItems& items, hipStream_t s) {
     const int waves = a.wave_splits;
     const size_t lds = (static_cast<size_t>(waves) * 4 * G * D + waves * 2 * G) * sizeof(float);
-    WorkOrder o;
-    o.n = 0;
-    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, true>, dim3(nrows * a.ws_chunks * a.lay.kv_heads),
-           dim3(64 * waves), lds, s, a, o);
+    launch("paged_decode", decode_f32_kernel<D, G, LPT, 2, true>, dim3(nrows * a.ws_chunks, a.lay.kv_heads),
+           dim3(64 * waves), lds, s, a, items);
 }
 
 template <int D>
-void dispatch_ws(const DecodeArgs& a, int nrows, hipStream_t s) {
+void dispatch_ws(const DecodeArgs& a, int nrows, const WsItems& it, hipStream_t s) {
     constexpr int LPT = D == 128 ? 8 : 4;
     switch (a.group) {
-        case 1: launch_f32_ws<D, 1, LPT>(a, nrows, s); return;
-        case 2: launch_f32_ws<D, 2, LPT>(a, nrows, s); return;
-        case 3: launch_f32_ws<D, 3, LPT>(a, nrows, s); return;
-        case 4: launch_f32_ws<D, 4, LPT>(a, nrows, s); return;
+        case 1: launch_f32_ws<D, 1, LPT>(a, nrows, it, s); return;
+        case 2: launch_f32_ws<D, 2, LPT>(a, nrows, it, s); return;
+        case 3: launch_f32_ws<D, 3, LPT>(a, nrows, it, s); return;
+        case 4: launch_f32_ws<D, 4, LPT>(a, nrows, it, s); return;
         default: break;
     }
     if constexpr (D != 128) {
         switch (a.group) {
-            case 5: launch_f32_ws<D, 5, 8>(a, nrows, s); return;
-            case 6: launch_f32_ws<D, 6, 8>(a, nrows, s); return;
-            case 7: launch_f32_ws<D, 7, 8>(a, nrows, s); return;
-            case 8: launch_f32_ws<D, 8, 8>(a, nrows, s); return;
+            case 5: launch_f32_ws<D, 5, 8>(a, nrows, it, s); return;
+            case 6: launch_f32_ws<D, 6, 8>(a, nrows, it, s); return;
+            case 7: launch_f32_ws<D, 7, 8>(a, nrows, it, s); return;
+            case 8: launch_f32_ws<D, 8, 8>(a, nrows, it, s); return;
             default: break;
         }
     }
@@ -2002,7 +2017,7 @@ bool decode_fast_path(const DecodeArgs& a) {
 }
 
 void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, const RowSplits* inline_rows,
-                   const WorkOrder* order, hipStream_t s) {
+                   const WorkOrder* order, hipStream_t s, const WsItems* ws_items) {
     static const WorkOrder identity = [] {
         WorkOrder o;
         o.n = 0;
@@ -2011,9 +2026,15 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
     const WorkOrder& ord = order ? *order : identity;
     if (nitems <= 0) return;
     if (a.wave_splits) {  // the plan chose wave splits (wave_split_shape): merged in LDS
-        a.lay.head_dim == 64    ? dispatch_ws<64>(a, nrows, s)
-        : a.lay.head_dim == 128 ? dispatch_ws<128>(a, nrows, s)
-                                : dispatch_ws<32>(a, nrows, s);
+        static const WsItems none = [] {
+            WsItems w{};
+            w.n = 0;
+            return w;
+        }();
+        const WsItems& it = ws_items ? *ws_items : none;
+        a.lay.head_dim == 64    ? dispatch_ws<64>(a, nrows, it, s)
+        : a.lay.head_dim == 128 ? dispatch_ws<128>(a, nrows, it, s)
+                                : dispatch_ws<32>(a, nrows, it, s);
         TVARA_HIP(hipGetLastError());
         if (a.ws_chunks > 1) {  // the chunks' partials: (first chunk, chunks) per row
             if (!inline_rows || nrows > kInlineRows) throw std::logic_error("wave-split decode: rows not inline");

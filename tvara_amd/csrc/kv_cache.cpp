@@ -496,6 +496,23 @@ void AttnPlan::compute(DeviceCache* c, const std::vector<uint64_t>& seq_of_row, 
         kv_bytes += static_cast<size_t>(static_cast<double>(n + tail) * g.kv_width() * 2 * bytes_per_element);
     }
     items = static_cast<int>(its.size());
+    ws_items.n = 0;
+    if (wave_splits) {
+        // item chunk * waves + w goes to slot chunk * kWsInlineWaves + w
+        const int per = static_cast<int>((split + tpb - 1) / tpb);
+        const int chunks = rows * ws_chunks;
+        if (chunks * kWsInlineWaves <= kWsInlineItems && per <= kWsInlinePer && wave_splits <= kWsInlineWaves) {
+            for (int ch = 0; ch < chunks; ++ch)
+                for (int w = 0; w < wave_splits; ++w) {
+                    const int i = ch * wave_splits + w, at = ch * kWsInlineWaves + w;
+                    ws_items.item[at] = work[i];
+                    for (int j = 0; j < kWsInlinePer; ++j)
+                        ws_items.ids[at * kWsInlinePer + j] =
+                            j < per ? work_ids[static_cast<size_t>(i) * kMaxSplitBlocks + j] : 0;
+                }
+            ws_items.n = items;
+        }
+    }
     order.n = 0;
     const bool one_group = row_major || decode_waves(vkv, vgroup, c->format(), static_cast<int>(g.head_dim)) == vkv;
     if (!wave_splits && one_group && c->format() == kF32 && items <= kOrderedItems && c->xcds() > 1 &&
@@ -641,7 +658,8 @@ void AttnPlan::launch(int layer, const float* q, const float* tail_k, const floa
     a.row_major = row_major ? 1 : 0;
     a.qscale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(cache->geometry().head_dim)));
     a.err = pinned_err ? static_cast<int*>(flag.ptr) : dev.err;
-    launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, order.n ? &order : nullptr, s);
+    launch_decode(a, items, rows, need_merge, inline_ok ? &inline_rows : nullptr, order.n ? &order : nullptr, s,
+                  ws_items.n ? &ws_items : nullptr);
     cache->leave(s);
     last_stream = s;
 }

@@ -150,6 +150,7 @@ struct AttnPlan {
     bool need_merge = false, with_tail = false, inline_ok = false;
     size_t kv_bytes = 0;  // algorithmic K/V bytes one launch reads
     RowSplits inline_rows{};  // (first item, splits) per row when rows <= kInlineRows
+    WsItems ws_items{};       // wave splits of few items: the items for the kernel arguments
     WorkOrder order{};        // launch order of the items (n == 0: item order)
     // host image
     std::vector<int32_t> h_tables;
