@@ -285,19 +285,47 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, float (&acc)[G
                 sum = fmaf(wt, r[0] + r[G * D] + r[2 * G * D] + r[3 * G * D], sum);
             }
             if (a.ws_chunks > 1) {
-                // the chunk's partial, [chunk][heads] for merge_wave_kernel
-                // (chunk = row * chunks + c = blockIdx.x)
+                // the chunk's partial, [chunk][heads] (chunk = row * chunks +
+                // c = blockIdx.x), for merge_wave_kernel or, with row_done
+                // set, the row's last chunk in this launch (agent-scope
+                // stores, as below)
                 const size_t at = static_cast<size_t>(blockIdx.x) * a.heads + static_cast<size_t>(kh) * G + h;
-                a.part_acc[at * D + (o - h * D)] = sum;
+                float* pa = a.part_acc + at * D + (o - h * D);
+                if (a.row_done)
+                    __hip_atomic_store(pa, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else
+                    *pa = sum;
                 if (o == h * D) {
-                    a.part_ml[2 * at] = M;
-                    a.part_ml[2 * at + 1] = L;
+                    if (a.row_done) {
+                        __hip_atomic_store(a.part_ml + 2 * at, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(a.part_ml + 2 * at + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    } else {
+                        a.part_ml[2 * at] = M;
+                        a.part_ml[2 * at + 1] = L;
+                    }
                 }
             } else {
                 outw[o] = sum / L;
             }
         }
         if (__any(st.bad) && lane == 0) *a.err = 1;
+        if (a.ws_chunks > 1 && a.row_done) {
+            // the (row, KV head)'s last chunk merges them all, in chunk order,
+            // as the split merge below does
+            __shared__ int last_chunk;
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                int* done = a.row_done + static_cast<size_t>(row) * a.lay.kv_heads + kh;
+                const int prev = __hip_atomic_fetch_add(done, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+                last_chunk = prev == a.ws_chunks - 1;
+                if (last_chunk) __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            if (last_chunk && wave == 0) merge_row_splits<D, G>(a, lane, kh, row * a.ws_chunks, row, a.ws_chunks);
+        }
         return;
     }
     const size_t head0 = static_cast<size_t>(kh) * G;
@@ -1996,6 +2024,14 @@ WaveSplitShape wave_split_shape(int rows, int kv_heads, int group, int format, i
 // (TVARA_INKERNEL_MERGE_MAX overrides it for tuning)
 constexpr int kInKernelMergeMaxWorkgroups = 128;
 
+static int in_kernel_merge_max() {
+    static const int max_wgs = [] {
+        const char* env = std::getenv("TVARA_INKERNEL_MERGE_MAX");
+        return env ? std::atoi(env) : kInKernelMergeMaxWorkgroups;
+    }();
+    return max_wgs;
+}
+
 bool decode_f32_blocks(int tpb) { return tpb >= 16 && tpb <= 1024 && (tpb & (tpb - 1)) == 0; }
 
 bool decode_rows_shape(int kv_heads, int group, int format, int head_dim, int tpb) {
@@ -2032,14 +2068,21 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
             return w;
         }();
         const WsItems& it = ws_items ? *ws_items : none;
-        a.lay.head_dim == 64    ? dispatch_ws<64>(a, nrows, it, s)
-        : a.lay.head_dim == 128 ? dispatch_ws<128>(a, nrows, it, s)
-                                : dispatch_ws<32>(a, nrows, it, s);
+        // chunk partials: merged by the (row, KV head)'s last chunk in
+        // launches of at most 64 workgroups, else by the merge kernel
+        // (MI355X, one Llama-3.2-1B row: 1,024 tokens 10.4 -> 9.5 us and
+        // 2,048 tokens 10.4 -> 9.8 us in 64 workgroups; 4,096 tokens 10.7
+        // against 11.1 us in 128)
+        DecodeArgs b = a;
+        const bool in_kernel = a.ws_chunks > 1 && a.row_done &&
+                               nrows * a.ws_chunks * a.lay.kv_heads <= std::min(64, in_kernel_merge_max());
+        if (!in_kernel) b.row_done = nullptr;
+        b.lay.head_dim == 64    ? dispatch_ws<64>(b, nrows, it, s)
+        : b.lay.head_dim == 128 ? dispatch_ws<128>(b, nrows, it, s)
+                                : dispatch_ws<32>(b, nrows, it, s);
         TVARA_HIP(hipGetLastError());
-        if (a.ws_chunks > 1) {  // the chunks' partials: (first chunk, chunks) per row
+        if (a.ws_chunks > 1 && !in_kernel) {  // (first chunk, chunks) per row
             if (!inline_rows || nrows > kInlineRows) throw std::logic_error("wave-split decode: rows not inline");
-            DecodeArgs b = a;
-            b.row_done = nullptr;
             launch_merge(b, inline_rows, nrows, s);
             TVARA_HIP(hipGetLastError());
         }
@@ -2066,12 +2109,8 @@ void launch_decode(const DecodeArgs& a, int nitems, int nrows, bool need_merge, 
     const bool fast = decode_fast_path(a);
     const int wgs = fast ? nitems * (decode_slots(a.lay.kv_heads, a.group, a.lay.format, a.lay.head_dim) / waves_for(a))
                          : nitems * a.heads;
-    static const int max_wgs = [] {
-        const char* env = std::getenv("TVARA_INKERNEL_MERGE_MAX");
-        return env ? std::atoi(env) : kInKernelMergeMaxWorkgroups;
-    }();
-    const bool in_kernel =
-        fast && a.row_done && !q8_mma_shape(a.group, a.lay.format, a.lay.head_dim) && wgs <= max_wgs;
+    const bool in_kernel = fast && a.row_done && !q8_mma_shape(a.group, a.lay.format, a.lay.head_dim) &&
+                           wgs <= in_kernel_merge_max();
     DecodeArgs b = a;
     if (!in_kernel) b.row_done = nullptr;
     bool merged = false;
