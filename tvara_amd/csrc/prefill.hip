@@ -74,8 +74,13 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     constexpr int QT = kWaves * PW;      // chunk positions per workgroup
     constexpr int KC = D / 32;           // K-dimension chunks of S^T
     constexpr int DT = D / 16;           // output column tiles
-    constexpr int KSTR = D + 8;          // LDS row pitch of K (bf16): 144 B, conflict-free b128 operand reads
-    constexpr int VSTR = D + 16;         // LDS row pitch of V (bf16): 160 B, conflict-free transposing reads
+    // LDS row pitches of K and V (bf16): 160 B at d=64, 288 B at d=128.  With
+    // these SQ_LDS_BANK_CONFLICT reads zero on the C4 batch; a K pitch of
+    // D + 8 put 28% of the LDS-active cycles in bank conflicts, D + 24 44%
+    // (the kernel time moved by under 2%: the LDS reads are latency-, not
+    // conflict-bound)
+    constexpr int KSTR = D + 16;
+    constexpr int VSTR = D + 16;
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
     constexpr int LPR = D / 4;                // staging lanes per key row (4 columns each)
     constexpr int KPP = 64 * kWaves / LPR;    // keys per staging pass
@@ -520,7 +525,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_pipe_kernel(const Prefill
     constexpr int QT = kWaves * PW;
     constexpr int KC = D / 32;
     constexpr int DT = D / 16;
-    constexpr int KSTR = D + 8;
+    constexpr int KSTR = D + 16;  // as prefill_bf16_kernel
     constexpr int VSTR = D + 16;
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
     constexpr int LPR = D / 4;
