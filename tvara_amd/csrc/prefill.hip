@@ -325,7 +325,11 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                         for (int i = 0; i < 4; ++i)
                             if (kbase + 16 * mt + 4 * g + i > lim[nt]) s[mt][nt][i] = -INFINITY;
             }
-            float rmax[2];
+            // each lane's own maximum decides the rescale (some lane's exceeds
+            // the threshold exactly when some row's does); the cross-lane row
+            // maximum is taken only on the first tile and the rare tile that
+            // raises m, as the pipelined kernel does
+            float lmax[2];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 float mx = -INFINITY;
@@ -333,21 +337,22 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nt][i]);
-                rmax[nt] = cross_row_max(mx);
+                lmax[nt] = mx;
             }
             if (first) {
                 // every row sees key 0 here, so its maximum is finite
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
-                    m[nt] = rmax[nt];
+                    const float rmax = cross_row_max(lmax[nt]);
+                    m[nt] = rmax;
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt) s[mt][nt] -= rmax[nt];
+                    for (int mt = 0; mt < 4; ++mt) s[mt][nt] -= rmax;
                 }
-            } else if (__any(rmax[0] > kThreshold || rmax[1] > kThreshold)) {
-                // rmax is relative to m: raise m where the tile exceeds it
+            } else if (__any(lmax[0] > kThreshold || lmax[1] > kThreshold)) {
+                // the row maximum is relative to m: raise m where the tile exceeds it
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
-                    const float up = fmaxf(rmax[nt], 0.f);
+                    const float up = fmaxf(cross_row_max(lmax[nt]), 0.f);
                     const float alpha = fast_exp2(-up);
                     m[nt] += up;
 #pragma unroll
