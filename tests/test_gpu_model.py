@@ -293,6 +293,8 @@ CHUNK_SPECS = {
     # on the three-product MFMA tiles, with blocks of 4 on the f32 rows
     "q8_0-d64": dict(matrix_type=gf.T_Q8_0, hidden=256, intermediate=512, heads=4, kv_heads=2, context=1200),
     "f32-d128": dict(hidden=256, intermediate=256, heads=2, kv_heads=1, context=1200),
+    # sixteen query heads per KV head: the tiles run as two slices of eight
+    "q8_0-d64-g16": dict(matrix_type=gf.T_Q8_0, hidden=1024, intermediate=512, heads=16, kv_heads=1, context=1200),
 }
 
 
