@@ -335,6 +335,29 @@ def test_decode_batch_chunks_match_reference(tmp_path, ref_capi, name, block_tok
     say(name, block_tokens, "worst relative logit error", worst)
 
 
+def test_chunk_attention_rows_switch(tmp_path, ref_capi, monkeypatch):
+    # TVARA_CHUNK_ATTENTION=rows: the chunked pass attends through the f32 rows
+    # (the reference's arithmetic) where the three-product tiles would run;
+    # both stay within the bar, and the rows come closer
+    spec = gf.LlamaSpec(**CHUNK_SPECS["q8_0-d64"])
+    path = spec.write(tmp_path / "m.gguf")
+    ref = native.NativeModel(path, library=ref_capi, max_blocks=1200 // 16 + 8, block_tokens=16)
+    tokens = [int(t) for t in np.random.default_rng(5).integers(0, spec.vocab, 600)]
+    sr = ref.new_sequence()
+    want = ref.decode_batch(sr, tokens)
+    errs = {}
+    for choice in ("tiles", "rows"):
+        monkeypatch.setenv("TVARA_CHUNK_ATTENTION", choice)
+        mine = native.NativeModel(path, max_blocks=1200 // 16 + 8, block_tokens=16)
+        got = mine.decode_batch(mine.new_sequence(), tokens)
+        ok, err = close(got, want)
+        assert ok, (choice, err)
+        errs[choice] = err
+        mine.close()
+    say("chunk attention worst relative logit error", errs)
+    assert errs["rows"] < errs["tiles"]
+
+
 def test_prefill_matches_reference_last_logits(tmp_path, ref_capi):
     # tvara_sequence_prefill: the last token's logits of a chunked pass, with
     # decode_batch's checks, messages and rollback

@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <stdexcept>
@@ -511,7 +512,11 @@ void DeviceModel::decode_chunk(uint64_t sequence, const uint32_t* tokens, size_t
     const int heads = static_cast<int>(c.heads);
     std::vector<size_t> positions(rows);
     std::vector<uint64_t> seq_of_row(rows, sequence);
-    const bool tiles = prefill_x3_supported(cache_->layout(), 1);
+    // TVARA_CHUNK_ATTENTION=rows (read on every call) keeps the f32 rows, the
+    // reference's arithmetic, for every layout
+    const char* choice = std::getenv("TVARA_CHUNK_ATTENTION");
+    const bool rows_only = choice && std::strcmp(choice, "rows") == 0;
+    const bool tiles = !rows_only && prefill_x3_supported(cache_->layout(), 1);
     for (size_t c0 = 0; c0 < n; c0 += rows) {
         const size_t m = std::min(rows, n - c0);
         positions.resize(m);
