@@ -47,8 +47,12 @@ extern "C" {
 /* attention precisions for tvara_attn_prefill */
 #define TVARA_ATTN_F32 0  /* reference semantics: one fused_paged_attention per row */
 #define TVARA_ATTN_BF16 1 /* bf16 MFMA tiles, f32 accumulation */
-/* MFMA tiles on f32 inputs split as bf16 hi + lo, three products each
- * (hi*hi + hi*lo + lo*hi): about 2^-15 relative error per term; f32 blocks */
+/* MFMA tiles on f32 inputs split as hi + lo, three products each
+ * (hi*hi + hi*lo + lo*hi): queries and keys as fp16 parts (about 2^-22
+ * relative error per score term; a key beyond the fp16 range, 65,504, or a
+ * query beyond it once multiplied by log2(e)/sqrt(head_dim) makes the call
+ * fail as a non-finite input does), values and probabilities as bf16
+ * parts (about 2^-16 per output term); f32 blocks */
 #define TVARA_ATTN_F32X3 2
 
 typedef struct tvara_model tvara_model;
@@ -301,7 +305,8 @@ TVARA_API int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences
  * Q8_0 blocks of a power of two from 16 to 1,024 tokens and head_dim 64 or
  * 128, any number of query heads per KV head; other shapes fail with
  * TVARA_INVALID); TVARA_ATTN_F32X3 runs the same tiles with every operand as a
- * bf16 pair (f32 blocks only). */
+ * hi/lo pair (f32 blocks only; keys, and scaled queries, within the fp16
+ * range). */
 TVARA_API int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t layer,
                                  size_t heads, size_t context, const size_t* start, const size_t* rows,
                                  const float* queries, float* out, int precision, int device_ptrs);

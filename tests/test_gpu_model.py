@@ -358,6 +358,25 @@ def test_chunk_attention_rows_switch(tmp_path, ref_capi, monkeypatch):
     assert errs["rows"] < errs["tiles"]
 
 
+def test_chunk_tiles_beyond_fp16_take_the_rows(tmp_path, monkeypatch):
+    # attention norms of 2e5 put queries and keys past the fp16 range (65,504)
+    # that the three-product tiles carry them in: the tiles flag the pass and it
+    # runs again on the f32 rows, whose logits these are, bit for bit
+    spec = gf.LlamaSpec(**CHUNK_SPECS["f32-d128"], attn_norm_scale=2e5)
+    path = spec.write(tmp_path / "m.gguf")
+    tokens = [int(t) for t in np.random.default_rng(8).integers(0, spec.vocab, 300)]
+    got = {}
+    for choice in ("tiles", "rows"):
+        monkeypatch.setenv("TVARA_CHUNK_ATTENTION", choice)
+        mine = native.NativeModel(path, max_blocks=1200 // 16 + 8, block_tokens=16)
+        sm = mine.new_sequence()
+        got[choice] = mine.decode_batch(sm, tokens)
+        assert mine.cache().length(sm) == len(tokens)
+        mine.close()
+    assert np.isfinite(got["rows"]).all()
+    assert np.array_equal(got["tiles"], got["rows"])
+
+
 def test_prefill_matches_reference_last_logits(tmp_path, ref_capi):
     # tvara_sequence_prefill: the last token's logits of a chunked pass, with
     # decode_batch's checks, messages and rollback

@@ -404,6 +404,38 @@ def test_bf16_rejections(device):
         assert np.all(np.isfinite(f32))
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+def test_x3_range(device, dim):
+    # f32x3 carries queries and keys as fp16 parts: a visible key beyond the
+    # fp16 range (65,504), or a query beyond it once multiplied by
+    # log2(e)/sqrt(head_dim) (1e6 at both widths), makes scores non-finite and
+    # the launch fails as a non-finite input does; the f32 rows take the same
+    # inputs
+    heads, kv_heads = 4, 2
+    w = kv_heads * dim
+    x = synth.normal(2, "x", 20 * w).reshape(20, w)
+    q = synth.normal(2, "q", 4 * heads * dim).reshape(4, -1)
+    for where in ("key", "query"):
+        dev = device.PagedCache(1, kv_heads, dim, 16, 8)
+        s = dev.create_sequence()
+        k, qq = x.copy(), q.copy()
+        if where == "key":
+            k[5, 7] = 7e4
+        else:
+            qq[2, dim + 3] = -1e6
+        dev.append_many(s, k, x)
+        say("prefill x3 range", dim, where)
+        with pytest.raises(device.InvalidArgument):
+            attention.prefill_batch(dev, qq, [s], [10], [4], 0, heads, 4096, precision="f32x3")
+        f32 = attention.prefill_batch(dev, qq, [s], [10], [4], 0, heads, 4096, precision="f32")
+        assert np.isfinite(f32).all()
+        # within the range the launch goes through
+        k[5, 7], qq[2, dim + 3] = 6e4, -6e4
+        dev.block_write(dev.physical_block(s, 5), dev.kv_offset(0, 0, 5), k[5])
+        got = attention.prefill_batch(dev, qq, [s], [10], [4], 0, heads, 4096, precision="f32x3")
+        assert np.isfinite(got).all()
+
+
 @pytest.mark.parametrize("precision", ["bf16", "f32", "f32x3"])
 @pytest.mark.parametrize("dim", [64, 128])
 def test_chunk_invariant_under_future_tokens(device, precision, dim):

@@ -527,38 +527,56 @@ void DeviceModel::decode_chunk(uint64_t sequence, const uint32_t* tokens, size_t
         // copied on write); every layer writes its K/V rows into their slots
         // before its attention reads them
         const RowOp* slots = cache_->reserve_tokens(sequence, m);
-        // row j sees the cached tokens and the chunk up to itself
-        // (fused_prompt_attention, attention.hpp:85-89)
-        std::function<void(hipEvent_t)> check;
-        Attend attend;
-        if (tiles) {
-            const size_t start = position + c0;
-            chunk_plan_.build(cache_.get(), &sequence, 1, c.heads, c.context, &start, &m, 2);
-            chunk_plan_.use_pinned_error();
-            attend = [&](int l, const float* q, float* kl, float* vl, float* attn) {
-                cache_->write_layer_rows(slots, m, l, kl, vl);
-                chunk_plan_.launch(l, q, attn, s);
-            };
-            check = [&](hipEvent_t e) { chunk_plan_.check_after(e); };
-        } else {
-            for (size_t j = 0; j < m; ++j) positions[j] += 1;
-            batch_plan_.build(cache_.get(), seq_of_row, positions, {}, heads, 0);
-            attend = [&](int l, const float* q, float* kl, float* vl, float* attn) {
-                cache_->write_layer_rows(slots, m, l, kl, vl);
-                batch_plan_.launch(l, q, nullptr, nullptr, attn, s);
-            };
-            check = [&](hipEvent_t e) { batch_plan_.check_after(e); };
-        }
-        layer_stack(m, attend);
-        const bool last = c0 + m == n;
-        if (last_only && !last) {
-            check(step_events_.attn);
-            continue;
-        }
+        const bool last = c0 + m == n, logits = !(last_only && !last);
         const size_t out_rows = last_only ? 1 : m;
-        const LogitsBands bands = launch_logits(out_rows, m - out_rows);
-        check(step_events_.attn);
-        copy_logits(bands, out_rows, last_only ? logits_host : logits_host + c0 * c.vocab);
+        // One pass over the layers, the logits and their copy.  A pass on the
+        // tiles returns false when their flag is raised: a query or key beyond
+        // the fp16 range (or a non-finite input); the chunk is then staged
+        // again and takes the f32 rows, which rewrite the same slots.
+        auto pass = [&](bool on_tiles) {
+            // row j sees the cached tokens and the chunk up to itself
+            // (fused_prompt_attention, attention.hpp:85-89)
+            std::function<void(hipEvent_t)> check;
+            Attend attend;
+            if (on_tiles) {
+                const size_t start = position + c0;
+                chunk_plan_.build(cache_.get(), &sequence, 1, c.heads, c.context, &start, &m, 2);
+                chunk_plan_.use_pinned_error();
+                attend = [&](int l, const float* q, float* kl, float* vl, float* attn) {
+                    cache_->write_layer_rows(slots, m, l, kl, vl);
+                    chunk_plan_.launch(l, q, attn, s);
+                };
+                check = [&](hipEvent_t e) { chunk_plan_.check_after(e); };
+            } else {
+                std::vector<size_t> lengths(m);
+                for (size_t j = 0; j < m; ++j) lengths[j] = positions[j] + 1;
+                batch_plan_.build(cache_.get(), seq_of_row, lengths, {}, heads, 0);
+                attend = [&](int l, const float* q, float* kl, float* vl, float* attn) {
+                    cache_->write_layer_rows(slots, m, l, kl, vl);
+                    batch_plan_.launch(l, q, nullptr, nullptr, attn, s);
+                };
+                check = [&](hipEvent_t e) { batch_plan_.check_after(e); };
+            }
+            layer_stack(m, attend);
+            LogitsBands bands;
+            if (logits) bands = launch_logits(out_rows, m - out_rows);
+            if (on_tiles) {
+                try {
+                    check(step_events_.attn);
+                } catch (const std::invalid_argument&) {
+                    TVARA_HIP(hipStreamSynchronize(s));
+                    return false;
+                }
+            } else {
+                check(step_events_.attn);
+            }
+            if (logits) copy_logits(bands, out_rows, last_only ? logits_host : logits_host + c0 * c.vocab);
+            return true;
+        };
+        if (!pass(tiles)) {
+            stage_rows(tokens + c0, positions.data(), m);
+            pass(false);
+        }
     }
 }
 

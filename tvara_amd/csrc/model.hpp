@@ -129,11 +129,12 @@ public:
     // into the cache, then the rows' causal attention over it): the logits of
     // n decode() calls, of every token or, with last_only, of the last one
     // only.  The attention runs as MFMA tiles with every f32 operand split
-    // into two bf16 parts (three products each, about 2^-15 relative error per
-    // term) where the cache layout allows it (f32 blocks of 16 to 1,024
-    // tokens, head_dim 64 or 128), else as f32 rows through the decode
-    // kernels.  On failure the sequence may hold part of the tokens; the
-    // caller truncates it.
+    // into two parts (queries and keys fp16, values and probabilities bf16;
+    // three products each) where the cache layout allows it (f32 blocks of 16
+    // to 1,024 tokens, head_dim 64 or 128), else as f32 rows through the
+    // decode kernels; a pass whose queries or keys leave the fp16 range runs
+    // again on the rows.  On failure the sequence may hold part of the
+    // tokens; the caller truncates it.
     void decode_chunk(uint64_t sequence, const uint32_t* tokens, size_t n, float* logits_host, bool last_only);
     static constexpr size_t kChunkRows = 512;
 

@@ -33,6 +33,8 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kThreshold = 8.0f;
 constexpr int kRows = 32, kKeys = 64;
@@ -62,12 +64,17 @@ constexpr int kBufferWord3 = 0x00020000;
 // to bf16 when staged; otherwise f32 blocks.
 // TPB: 16 for blocks of 16 tokens (block arithmetic folded at compile time),
 // 0 for any power of two from 16 to 1,024 read from the layout
-// kX3: f32 inputs carried as three bf16 products.  Q, K, V and the
-// probabilities are each split as x = hi + lo (hi = bf16(x), lo = bf16(x -
-// hi): 16 significant bits), and every product takes hi*hi + hi*lo + lo*hi in
-// f32 (the dropped lo*lo is below 2^-16 of the product), so a score or an
-// output carries about 2^-15 relative error per term against the 2^-8 of one
-// bf16 product.  LDS holds the lo planes of K and V beside the hi ones.
+// kX3: f32 inputs carried as three products of split operands.  The score
+// operands Q and K are split into fp16 parts, x = hi + lo (hi = fp16(x),
+// lo = fp16(x - hi): 22 significant bits, lo subnormal for small x, which the
+// MFMA keeps), V and the probabilities into bf16 parts (16 bits, the range of
+// f32), and every product takes hi*hi + hi*lo + lo*hi in f32.  A score then
+// carries about 2^-22 relative error per term (bf16 parts gave 2^-15, which
+// exceeded the 1e-4 bar on rows whose scores spread over tens of units) and
+// the output about 2^-16 per term.  Keys, and queries once scaled by
+// log2(e)/sqrt(D), must lie within the fp16 range (65,504): beyond it a score
+// is not finite and the launch fails as a non-finite input does.  LDS holds the lo planes of K and V beside the hi
+// ones.
 template <int D, int G, int kWaves, bool kQ8, int TPB, bool kX3 = false>
 __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const PrefillArgs a) {
     constexpr int PW = kRows / G;        // chunk positions per wave; rows PW*G .. 31 are padding (G = 3, 5, 6, 7)
@@ -134,13 +141,18 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
             }
             const float s = a.qscale;
             const f32x4 y0 = {x0.x * s, x0.y * s, x0.z * s, x0.w * s}, y1 = {x1.x * s, x1.y * s, x1.z * s, x1.w * s};
-            const bf16x4 lo = to_bf16(y0);
-            const bf16x4 hi = to_bf16(y1);
-            qop[nt][kc] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             if constexpr (kX3) {
-                const bf16x4 l0 = to_bf16(y0 - __builtin_convertvector(lo, f32x4));
-                const bf16x4 l1 = to_bf16(y1 - __builtin_convertvector(hi, f32x4));
-                qlo[nt][kc] = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+                // fp16 parts (11 + 11 significant bits; the MFMA keeps fp16
+                // subnormals), kept in the bf16x8 registers as bits
+                const f16x4 h0 = __builtin_convertvector(y0, f16x4), h1 = __builtin_convertvector(y1, f16x4);
+                const f16x4 l0 = __builtin_convertvector(y0 - __builtin_convertvector(h0, f32x4), f16x4);
+                const f16x4 l1 = __builtin_convertvector(y1 - __builtin_convertvector(h1, f32x4), f16x4);
+                qop[nt][kc] = __builtin_bit_cast(bf16x8, f16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]});
+                qlo[nt][kc] = __builtin_bit_cast(bf16x8, f16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]});
+            } else {
+                const bf16x4 lo = to_bf16(y0);
+                const bf16x4 hi = to_bf16(y1);
+                qop[nt][kc] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
         }
     }
@@ -235,14 +247,18 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
 #pragma unroll
         for (int p = 0; p < SP; ++p) {
             const f32x4 kv = values(kreg[p]), vv = values(vreg[p]);
-            const bf16x4 kb = to_bf16(kv), vb = to_bf16(vv);
-            *reinterpret_cast<bf16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = kb;
+            const bf16x4 vb = to_bf16(vv);
             *reinterpret_cast<bf16x4*>(&vlds[buf][(KPP * p + skey) * VSTR + col]) = vb;
             if constexpr (kX3) {
-                *reinterpret_cast<bf16x4*>(&klo[buf][(KPP * p + skey) * KSTR + col]) =
-                    to_bf16(kv - __builtin_convertvector(kb, f32x4));
+                // K as fp16 parts (the score operands), V as bf16 parts
+                const f16x4 kh = __builtin_convertvector(kv, f16x4);
+                *reinterpret_cast<f16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = kh;
+                *reinterpret_cast<f16x4*>(&klo[buf][(KPP * p + skey) * KSTR + col]) =
+                    __builtin_convertvector(kv - __builtin_convertvector(kh, f32x4), f16x4);
                 *reinterpret_cast<bf16x4*>(&vlo[buf][(KPP * p + skey) * VSTR + col]) =
                     to_bf16(vv - __builtin_convertvector(vb, f32x4));
+            } else {
+                *reinterpret_cast<bf16x4*>(&klds[buf][(KPP * p + skey) * KSTR + col]) = to_bf16(kv);
             }
         }
     };
@@ -282,19 +298,21 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
                 // hi*lo and lo*hi into each score tile
 #pragma unroll
                 for (int kc = 0; kc < KC; ++kc) {
-                    bf16x8 khi[4], klw[4];
+                    f16x8 khi[4], klw[4];
 #pragma unroll
                     for (int mt = 0; mt < 4; ++mt) {
-                        khi[mt] = *reinterpret_cast<const bf16x8*>(&klds[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
-                        klw[mt] = *reinterpret_cast<const bf16x8*>(&klo[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
+                        khi[mt] = *reinterpret_cast<const f16x8*>(&klds[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
+                        klw[mt] = *reinterpret_cast<const f16x8*>(&klo[buf][(16 * mt + r16) * KSTR + 32 * kc + 8 * g]);
                     }
 #pragma unroll
                     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                         for (int nt = 0; nt < 2; ++nt) {
-                            s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi[mt], qop[nt][kc], s[mt][nt], 0, 0, 0);
-                            s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi[mt], qlo[nt][kc], s[mt][nt], 0, 0, 0);
-                            s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klw[mt], qop[nt][kc], s[mt][nt], 0, 0, 0);
+                            const f16x8 qh = __builtin_bit_cast(f16x8, qop[nt][kc]);
+                            const f16x8 ql = __builtin_bit_cast(f16x8, qlo[nt][kc]);
+                            s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi[mt], qh, s[mt][nt], 0, 0, 0);
+                            s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi[mt], ql, s[mt][nt], 0, 0, 0);
+                            s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(klw[mt], qh, s[mt][nt], 0, 0, 0);
                         }
                 }
             } else {

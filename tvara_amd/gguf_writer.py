@@ -139,6 +139,7 @@ class LlamaSpec:
     embed_type: int = T_F32
     norm_type: int = T_F32
     seed: int = 7
+    attn_norm_scale: float = 1.0          # multiplies the attention norms' weights
     extra: list = field(default_factory=list)  # more metadata (key, type, value)
 
     def metadata(self):
@@ -164,6 +165,8 @@ class LlamaSpec:
 
         def norm(name):
             w = (1.0 + 0.1 * _rng(s, name).standard_normal(h)).astype(np.float32)
+            if name.endswith("attn_norm.weight"):
+                w = (w * np.float32(self.attn_norm_scale)).astype(np.float32)
             if self.norm_type == T_F16:
                 return (name, [h], T_F16, w.astype("<f2").tobytes())
             return (name, [h], T_F32, w.astype("<f4").tobytes())
