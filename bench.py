@@ -479,7 +479,7 @@ def bench_prefill(args, w, precision="bf16"):
     name = w.name if precision == "bf16" else w.name + "-" + precision
     metric = {
         "bf16": "paged chunked prefill attn: achieved TFLOP/s (MFMA utilisation), 1 MI355X",
-        "f32x3": "paged chunked prefill attn, f32-accurate (three bf16 products): achieved TFLOP/s, 1 MI355X",
+        "f32x3": "paged chunked prefill attn, f32-accurate (three-product tiles): achieved TFLOP/s, 1 MI355X",
     }.get(precision, "paged chunked prefill attn, f32 (reference arithmetic): achieved TFLOP/s, 1 MI355X")
     result = {
         "metric": metric,

@@ -890,7 +890,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_pipe_kernel(const Prefill
 // measured 158 against 225 us for four on the 8 x (2,048 + 512) chunk;
 // 128-key tiles 177 us).
 //
-// x3 (three bf16 products per product, f32 blocks) always takes the plain
+// x3 (three products per product, f32 blocks) always takes the plain
 // kernel.
 template <int D, int G, int TPB>
 void launch_gt(const PrefillArgs& a, int nseqs, int max_rows, bool x3, hipStream_t s) {
