@@ -35,7 +35,8 @@ triad bandwidth.
 
 Other shapes, one line each with --workload: c4d128, c4q8 and c4f32 (the
 chunks at head_dim 128, over Q8_0 blocks, and in f32 through the decode
-kernels), gqa8 / gqa8q8 (Llama-3-70B, eight query
+kernels), c4x3 / c4x3d128 / c4q8x3 (the three-product tiles at f32
+accuracy), gqa8 / gqa8q8 (Llama-3-70B, eight query
 heads per KV head), gqa16 / gqa16q8 (Llama-3.1-405B, sixteen, run as two
 slices), tiny / tinyq8 (TinyLlama-1.1B), gemma2 (head_dim 256), phi3
 (head_dim 96).
@@ -445,8 +446,8 @@ def bench_prefill(args, w, precision="bf16"):
     its own position (attention.hpp:85-89), through the decode kernels and the
     split merge; its dominant kernel is priced against the fp32 peak.  f32x3
     (within the same 1e-4): the MFMA tiles with every operand split into two
-    bf16 parts and three products per product, priced against a third of the
-    bf16 MFMA peak (the matrix rate left for the algorithmic flops)."""
+    16-bit parts and three products per product, priced against a third of
+    the 16-bit MFMA peak (the matrix rate left for the algorithmic flops)."""
     import numpy as np
 
     from tvara_amd import attention, hip, kv, workloads
@@ -495,7 +496,7 @@ def bench_prefill(args, w, precision="bf16"):
                      "merge_avg_us": round(merge_ms * 1e3, 3) if merges else 0.0, "algorithmic_flops": w.flops()},
         "cpu_baseline": None,
     }
-    if precision == "bf16" and not w.q8:
+    if precision == "bf16":
         result["f32_accurate_x3"] = x3_beside(args, w)
     if ref_ready(args) and not w.q8:
         baseline(result, lambda: cpu_prefill(w))
@@ -506,12 +507,14 @@ def x3_beside(args, w):
     """The same chunks through the three-product tiles (TVARA_ATTN_F32X3,
     within the f32 bar), reported beside the bf16 line: kernel time from the
     library's HIP events, algorithmic TFLOP/s and their fraction of a third of
-    the bf16 MFMA peak (three products per product)."""
+    the 16-bit MFMA peak (three products per product), over the same blocks
+    (f32 or Q8_0)."""
     import numpy as np
 
     from tvara_amd import attention, hip, kv, workloads
 
-    cache = kv.PagedCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks(), fmt=kv.F32)
+    cache = kv.PagedCache(1, w.kv_heads, w.head_dim, w.tokens_per_block, w.pool_blocks(),
+                          fmt=kv.Q8_0 if w.q8 else kv.F32)
     seqs = workloads.fill_prefill(cache, w)
     q = hip.DeviceArray.from_numpy(np.concatenate([w.chunk_queries(i) for i in range(w.sequences)]))
     out = hip.DeviceArray(q.shape)
@@ -1028,10 +1031,11 @@ def compact(r):
 def run_one(args, key):
     from tvara_amd import workloads
 
-    if key in ("c4", "c4d128", "c4q8", "c4f32", "c4x3", "c4x3d128"):
+    if key in ("c4", "c4d128", "c4q8", "c4f32", "c4x3", "c4x3d128", "c4q8x3"):
         make = {"c4": workloads.prefill_c4, "c4d128": workloads.prefill_8b, "c4q8": workloads.prefill_c4_q8,
-                "c4f32": workloads.prefill_c4, "c4x3": workloads.prefill_c4, "c4x3d128": workloads.prefill_8b}
-        precision = {"c4f32": "f32", "c4x3": "f32x3", "c4x3d128": "f32x3"}.get(key, "bf16")
+                "c4f32": workloads.prefill_c4, "c4x3": workloads.prefill_c4, "c4x3d128": workloads.prefill_8b,
+                "c4q8x3": workloads.prefill_c4_q8}
+        precision = {"c4f32": "f32", "c4x3": "f32x3", "c4x3d128": "f32x3", "c4q8x3": "f32x3"}.get(key, "bf16")
         return bench_prefill(args, make[key](), precision)
     if key in ("c3", "c3cow"):
         return bench_kv(args, key == "c3cow")
@@ -1056,7 +1060,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c4f32", "c4x3", "c4x3d128", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2", "phi3",
+                    choices=["all", "c1", "c2", "c3", "c3cow", "c4", "c4d128", "c4q8", "c4f32", "c4x3", "c4x3d128", "c4q8x3", "c5", "gqa8", "gqa8q8", "gqa16", "gqa16q8", "gemma2", "phi3",
                              "tiny", "tinyq8", "t176", "llama1b", "prefix", "conv"],
                     help="one configuration; `all` (the default) runs c1, t176, c3, c3cow, c4, c5, prefix and llama1b, "
                          "one JSON line each, then the c2 headline line last")

@@ -52,7 +52,8 @@ extern "C" {
  * relative error per score term; a key beyond the fp16 range, 65,504, or a
  * query beyond it once multiplied by log2(e)/sqrt(head_dim) makes the call
  * fail as a non-finite input does), values and probabilities as bf16
- * parts (about 2^-16 per output term); f32 blocks */
+ * parts (about 2^-16 per output term); the bf16 tiles' blocks (f32 or Q8_0,
+ * dequantised as d * q when staged) */
 #define TVARA_ATTN_F32X3 2
 
 typedef struct tvara_model tvara_model;
@@ -305,7 +306,7 @@ TVARA_API int tvara_attn_decode(tvara_kv_cache* cache, const uint64_t* sequences
  * Q8_0 blocks of a power of two from 16 to 1,024 tokens and head_dim 64 or
  * 128, any number of query heads per KV head; other shapes fail with
  * TVARA_INVALID); TVARA_ATTN_F32X3 runs the same tiles with every operand as a
- * hi/lo pair (f32 blocks only; keys, and scaled queries, within the fp16
+ * hi/lo pair (the same blocks; keys, and scaled queries, within the fp16
  * range). */
 TVARA_API int tvara_attn_prefill(tvara_kv_cache* cache, const uint64_t* sequences, size_t count, size_t layer,
                                  size_t heads, size_t context, const size_t* start, const size_t* rows,

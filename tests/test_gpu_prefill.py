@@ -3,12 +3,14 @@ fused_prompt_attention (attention.hpp:85-89, FP64).
 
 f32 path: |gpu - ref| <= 1e-4 * (1 + |ref|).
 
-f32x3 path (the MFMA tiles with every operand split as bf16 hi + lo and three
-products, hi*hi + hi*lo + lo*hi): each operand carries 16 significant bits
-and the dropped lo*lo term is below 2^-16 of its product, so every rounding
-term above shrinks by 2^7 against the bf16 path: the short-row worst case
-becomes ~8e-2 / 128 ~ 6e-4 at |ref| ~ 5, within the f32 bar's 1e-4 * (1 +
-|ref|), and the long rows sit two orders below it.  The f32 bar applies.
+f32x3 path (the MFMA tiles with every operand split as hi + lo and three
+products, hi*hi + hi*lo + lo*hi): the score operands q*log2(e)/sqrt(d) and K
+as fp16 parts (22 significant bits), V and the probabilities as bf16 parts
+(16 bits), the dropped lo*lo term below 2^-16 of its product, so every
+rounding term below shrinks by 2^7 or more against the bf16 path: the
+short-row worst case becomes ~8e-2 / 128 ~ 6e-4 at |ref| ~ 5, within the f32
+bar's 1e-4 * (1 + |ref|), and the long rows sit two orders below it.  The
+f32 bar applies.
 
 bf16 MFMA path.  q*log2(e)/sqrt(d), K, V and the probabilities P are rounded
 to bf16 (unit roundoff u = 2^-9); products and sums are f32.  To first order
@@ -119,13 +121,16 @@ def test_bf16_block_sizes(device, oracle, tpb, dim, fmt):
     assert ok, err
 
 
+@pytest.mark.parametrize("fmt", ["f32", "q8_0"])
 @pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8, 10, 16])
-def test_f32x3_small_shapes(device, oracle, group, dim):
+def test_f32x3_small_shapes(device, oracle, group, dim, fmt):
+    # Q8_0 blocks: d * q dequantised when staged, against the oracle over the
+    # dequantised values the blocks hold
     heads, kv_heads = 2 * group, 2
     specs = [(137, 100, 37), (64, 0, 64), (20, 3, 17), (1, 0, 1)]
-    say("prefill f32x3 group", group, "dim", dim)
-    dev, ref, ds, rs, qs = build(device, oracle, heads, kv_heads, dim, specs, seed=50 + group)
+    say("prefill f32x3 group", group, "dim", dim, fmt)
+    dev, ref, ds, rs, qs = build(device, oracle, heads, kv_heads, dim, specs, seed=50 + group, q8=fmt == "q8_0")
     starts = [s for _, s, _ in specs]
     counts = [r for _, _, r in specs]
     got = attention.prefill_batch(dev, np.concatenate(qs), ds, starts, counts, 0, heads, 4096, precision="f32x3")
@@ -135,13 +140,15 @@ def test_f32x3_small_shapes(device, oracle, group, dim):
     assert refmath.close(got, want, TOL_F32), refmath.max_rel(got, want)
 
 
+@pytest.mark.parametrize("fmt", ["f32", "q8_0"])
 @pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("tpb", [32, 64, 128, 1024])
-def test_f32x3_block_sizes(device, oracle, tpb, dim):
+def test_f32x3_block_sizes(device, oracle, tpb, dim, fmt):
     heads, kv_heads = 8, 2
     specs = [(1100, 900, 200), (300, 0, 300), (20, 3, 17)]
-    say("prefill f32x3 tpb", tpb, "dim", dim)
-    dev, ref, ds, rs, qs = build(device, oracle, heads, kv_heads, dim, specs, seed=60 + tpb + dim, tpb=tpb)
+    say("prefill f32x3 tpb", tpb, "dim", dim, fmt)
+    dev, ref, ds, rs, qs = build(device, oracle, heads, kv_heads, dim, specs, seed=60 + tpb + dim, tpb=tpb,
+                                 q8=fmt == "q8_0")
     starts = [s for _, s, _ in specs]
     counts = [r for _, _, r in specs]
     got = attention.prefill_batch(dev, np.concatenate(qs), ds, starts, counts, 0, heads, 4096, precision="f32x3")
@@ -150,14 +157,18 @@ def test_f32x3_block_sizes(device, oracle, tpb, dim):
     assert refmath.close(got, want, TOL_F32), refmath.max_rel(got, want)
 
 
-def test_f32x3_refuses_q8_0_blocks(device):
-    dev = device.PagedCache(1, 2, 64, 16, 8, fmt=device.Q8_0)
-    s = dev.create_sequence()
-    x = synth.normal(1, "x", 20 * 128).reshape(20, 128)
-    dev.append_many(s, x, x)
-    q = synth.normal(1, "q", 4 * 4 * 64).reshape(4, -1)
-    with pytest.raises(device.InvalidArgument):
-        attention.prefill_batch(dev, q, [s], [10], [4], 0, 4, 64, precision="f32x3")
+def test_f32x3_refusals(device):
+    # the three-product tiles take the bf16 tiles' shapes: head_dim 64 or 128
+    # and power-of-two blocks of 16 to 1,024 tokens; the f32 rows take the rest
+    for dim, tpb in [(32, 16), (64, 24)]:
+        dev = device.PagedCache(1, 2, dim, tpb, 8, fmt=device.Q8_0)
+        s = dev.create_sequence()
+        x = synth.normal(1, "x", 20 * 2 * dim).reshape(20, -1)
+        dev.append_many(s, x, x)
+        q = synth.normal(1, "q", 4 * 4 * dim).reshape(4, -1)
+        with pytest.raises(device.InvalidArgument):
+            attention.prefill_batch(dev, q, [s], [10], [4], 0, 4, 64, precision="f32x3")
+        assert np.isfinite(attention.prefill_batch(dev, q, [s], [10], [4], 0, 4, 64, precision="f32")).all()
 
 
 def bf16_rne(x):
@@ -291,7 +302,7 @@ def test_c4_every_row_against_reference(device, oracle, ref, make, fmt):
     args = (ds, [w.prefix] * w.sequences, [w.chunk] * w.sequences, 0, w.heads, w.context)
     got = attention.prefill_batch(dev, q, *args, precision="bf16").reshape(w.sequences, w.chunk, -1)
     f32 = attention.prefill_batch(dev, q, *args, precision="f32").reshape(w.sequences, w.chunk, -1)
-    x3 = None if q8 else attention.prefill_batch(dev, q, *args, precision="f32x3").reshape(f32.shape)
+    x3 = attention.prefill_batch(dev, q, *args, precision="f32x3").reshape(f32.shape)
     threads = max(1, min(16, os.cpu_count() or 1))
     rc = ref.RefCache(*g)
     want = np.empty_like(f32)
@@ -309,9 +320,8 @@ def test_c4_every_row_against_reference(device, oracle, ref, make, fmt):
     ok, err = bf16_ok(got, want, LONG_ROWS)
     assert ok, err
     say("every row: f32 max rel", refmath.max_rel(f32, want), "bf16 (max rel, rms)", err)
-    if x3 is not None:
-        say("every row: f32x3 max rel", refmath.max_rel(x3, want))
-        assert refmath.close(x3, want, TOL_F32), refmath.max_rel(x3, want)
+    say("every row: f32x3 max rel", refmath.max_rel(x3, want))
+    assert refmath.close(x3, want, TOL_F32), refmath.max_rel(x3, want)
 
 
 @pytest.mark.parametrize("precision", ["bf16", "f32", "f32x3"])
@@ -471,8 +481,6 @@ def test_zero_query_averages_every_visible_key(device, oracle, group, dim, fmt, 
     # tiling, the GQA row mapping and the paged block walk are checked exactly
     # (the bf16 bars above cannot see a single key among thousands).  The f32
     # path (decode kernels, split merges) is exact here too.
-    if precision == "f32x3" and fmt == "q8_0":
-        pytest.skip("the three-product tiles read f32 blocks only")
     heads, kv_heads = 2 * group, 2
     w = kv_heads * dim
     specs = [(1100, 1000, 100), (300, 0, 300), (77, 60, 17), (2100, 1600, 500)]

@@ -195,7 +195,8 @@ bool decode_f32_blocks(int tpb);
 constexpr size_t kRowMajorMinWorkgroups = 128;
 // prefill.hip
 bool prefill_bf16_supported(const BlockLayout& lay, int group);
-// x3: the f32-accurate variant (three products per product of split operands), f32 blocks
+// x3: the f32-accurate variant (three products per product of split
+// operands), on the blocks the bf16 tiles take
 bool prefill_x3_supported(const BlockLayout& lay, int group);
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s, bool x3 = false);
 

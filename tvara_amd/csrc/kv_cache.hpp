@@ -221,7 +221,7 @@ struct AttnPlan {
 // start[i] + rows[i] - 1 causally (fused_prompt_attention,
 // attention.hpp:85-89).  precision 0 = f32 rows through the decode kernels,
 // 1 = the bf16 MFMA tile kernel, 2 = the tile kernel with three products
-// per product of split operands (f32 blocks).  Block tables stay resident, so a plan built
+// per product of split operands (f32 or Q8_0 blocks).  Block tables stay resident, so a plan built
 // once per chunk serves every layer.
 struct PrefillPlan {
     DeviceCache* cache = nullptr;

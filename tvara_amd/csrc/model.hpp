@@ -130,7 +130,7 @@ public:
     // n decode() calls, of every token or, with last_only, of the last one
     // only.  The attention runs as MFMA tiles with every f32 operand split
     // into two parts (queries and keys fp16, values and probabilities bf16;
-    // three products each) where the cache layout allows it (f32 blocks of 16
+    // three products each) where the cache layout allows it (blocks of 16
     // to 1,024 tokens, head_dim 64 or 128), else as f32 rows through the
     // decode kernels; a pass whose queries or keys leave the fp16 range runs
     // again on the rows.  On failure the sequence may hold part of the

@@ -125,7 +125,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_bf16_kernel(const Prefill
     const int32_t* tab = a.tables + sd.x;
 
     // Q^T as the B operand: row n = 16*nt + r16, columns 32*kc + 8*g .. +7
-    // (kX3: qlo the residual's bf16)
+    // (kX3: qop and qlo the fp16 parts)
     bf16x8 qop[2][KC];
     bf16x8 qlo[kX3 ? 2 : 1][kX3 ? KC : 1];
 #pragma unroll
@@ -890,8 +890,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_pipe_kernel(const Prefill
 // measured 158 against 225 us for four on the 8 x (2,048 + 512) chunk;
 // 128-key tiles 177 us).
 //
-// x3 (three products per product, f32 blocks) always takes the plain
-// kernel.
+// x3 (three products per product) always takes the plain kernel, over f32
+// or Q8_0 blocks (d * q dequantised when staged, then split).
 template <int D, int G, int TPB>
 void launch_gt(const PrefillArgs& a, int nseqs, int max_rows, bool x3, hipStream_t s) {
     const char* env = std::getenv("TVARA_PREFILL_PIPE");
@@ -904,7 +904,10 @@ void launch_gt(const PrefillArgs& a, int nseqs, int max_rows, bool x3, hipStream
     const int groups8 = (b.pairs + 7) / 8;  // ids = 8 XCDs x chunk tiles x pair groups
     const dim3 grid(8 * groups8 * b.chunk_tiles), block(64 * W);
     if (x3) {
-        launch("paged_prefill_x3", prefill_bf16_kernel<D, G, W, false, TPB, true>, grid, block, 0, s, b);
+        if (q8)
+            launch("paged_prefill_x3", prefill_bf16_kernel<D, G, W, true, TPB, true>, grid, block, 0, s, b);
+        else
+            launch("paged_prefill_x3", prefill_bf16_kernel<D, G, W, false, TPB, true>, grid, block, 0, s, b);
     } else if (pipe) {
         if (q8)
             launch("paged_prefill_bf16", prefill_pipe_kernel<D, G, W, 2, true, TPB>, grid, block, 0, s, b);
@@ -938,17 +941,13 @@ bool prefill_bf16_supported(const BlockLayout& lay, int group) {
            lay.stride < (size_t(1) << 31) && group >= 1 && group <= 8;
 }
 
-bool prefill_x3_supported(const BlockLayout& lay, int group) {
-    return lay.format == kF32 && prefill_bf16_supported(lay, group);
-}
+bool prefill_x3_supported(const BlockLayout& lay, int group) { return prefill_bf16_supported(lay, group); }
 
 void launch_prefill_bf16(const PrefillArgs& a, int nseqs, int max_rows, hipStream_t s, bool x3) {
     if (!prefill_bf16_supported(a.lay, a.group))
         throw std::invalid_argument(
             "bf16 prefill needs f32 or Q8_0 blocks of 16 to 1,024 tokens (a power of two, under 2 GiB), "
             "head_dim 64 or 128, and a GQA slice of 1-8 heads");
-    if (x3 && !prefill_x3_supported(a.lay, a.group))
-        throw std::invalid_argument("the three-product prefill needs f32 blocks");
     if (nseqs <= 0 || max_rows <= 0) return;
     switch (a.group) {
         case 1: launch_g<1>(a, nseqs, max_rows, x3, s); break;
