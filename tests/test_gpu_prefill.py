@@ -157,6 +157,39 @@ def test_f32x3_block_sizes(device, oracle, tpb, dim, fmt):
     assert refmath.close(got, want, TOL_F32), refmath.max_rel(got, want)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+def test_f32x3_sharp_scores(device, oracle, dim):
+    # queries and keys of N(0, 36) put the scores' standard deviation near 36:
+    # a score's error enters the softmax's exponent unscaled, so score
+    # operands carried in two bf16 parts (16 bits) leave 4.1e-4 on these rows
+    # at d=64 (a float64 simulation of the split products), over the f32 bar;
+    # with fp16 parts (22 bits) the same simulation gives 1.1e-5
+    heads, kv_heads = 8, 2
+    w = kv_heads * dim
+    specs = [(700, 500, 200), (130, 0, 130)]
+    nb = sum((n + 15) // 16 for n, _, _ in specs) + 4
+    dev = device.PagedCache(1, kv_heads, dim, 16, nb)
+    ref = oracle.Cache(1, kv_heads, dim, 16, nb)
+    ds, rs, qs = [], [], []
+    for i, (n, _, rows) in enumerate(specs):
+        k = (6.0 * synth.normal(90, f"k{i}", n * w)).astype(np.float32).reshape(n, w)
+        v = synth.normal(90, f"v{i}", n * w).reshape(n, w)
+        sd, sr = dev.create_sequence(), ref.create_sequence()
+        dev.append_many(sd, k, v)
+        ref.append_many(sr, k, v)
+        ds.append(sd)
+        rs.append(sr)
+        qs.append((6.0 * synth.normal(90, f"q{i}", rows * heads * dim)).astype(np.float32).reshape(rows, -1))
+    starts = [s for _, s, _ in specs]
+    counts = [r for _, _, r in specs]
+    say("prefill f32x3 sharp", dim)
+    got = attention.prefill_batch(dev, np.concatenate(qs), ds, starts, counts, 0, heads, 4096, precision="f32x3")
+    want = np.concatenate([ref.fused_prompt_attention(q, s, 0, st, c, heads, 4096).reshape(c, -1)
+                           for q, s, st, c in zip(qs, rs, starts, counts)])
+    say("f32x3 sharp max rel", refmath.max_rel(got, want))
+    assert refmath.close(got, want, TOL_F32), refmath.max_rel(got, want)
+
+
 def test_f32x3_refusals(device):
     # the three-product tiles take the bf16 tiles' shapes: head_dim 64 or 128
     # and power-of-two blocks of 16 to 1,024 tokens; the f32 rows take the rest
