@@ -74,7 +74,7 @@ def log(*a):
 
 def host_threads():
     """Host threads the CPU baseline uses: what the process may run on,
-    capped at 16 (a one-GPU box's CPU share)."""
+    capped at 16 (the host threads a machine grants one GPU's job)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -1071,7 +1071,7 @@ def main():
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(the path shards by sequence or KV head with no exchange; see the design notes)", file=sys.stderr)
         sys.exit(2)
     if args.split_tokens:
