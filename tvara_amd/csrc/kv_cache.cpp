@@ -765,8 +765,6 @@ void PrefillPlan::build(DeviceCache* c, const uint64_t* sequences, size_t n, siz
         throw std::invalid_argument(
             "bf16 prefill needs f32 or Q8_0 blocks of 16 to 1,024 tokens (a power of two, under 2 GiB) and head_dim "
             "64 or 128");
-    if (prec == 2 && !prefill_x3_supported(c->layout(), group / kv_share))
-        throw std::invalid_argument("the three-product prefill needs f32 blocks");
     std::vector<int32_t> tab;
     std::vector<int4> sq(n);
     size_t row0 = 0;
